@@ -1,0 +1,294 @@
+/*
+ * styx_hip.h -- C ABI of libstyx_hip.so, the MI355X (gfx950) backend of the
+ * styx / moe-stream MoE decode hot path.
+ *
+ * It replaces the Rust crate crates/vk-backend (Vulkan) of aDirtyScoundrel/styx
+ * as the engine's GPU boundary, and exports a C++ port of the engine API of
+ * crates/model/src/moe.rs (MoeModel) on top of it.  Plain C types only: opaque
+ * handles, pointers and sizes.  Every call returns 0 (STYX_OK) or a negative
+ * status; styx_last_error() gives the thread's last message.  Nothing aborts
+ * across the boundary.  Handles are owned by the caller and freed explicitly
+ * (the reference's Buffer/Pipeline/Batch have no Drop either,
+ * crates/vk-backend/src/lib.rs:18-52); a gpu must outlive its children.
+ *
+ * Threading: one batch / model per thread; all work of a gpu runs in order on
+ * its compute stream.
+ */
+#ifndef STYX_HIP_H
+#define STYX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ----------------------------------------------------------- status ---- */
+enum {
+    STYX_OK = 0,
+    STYX_E_INVALID = -1,      /* bad argument (reference: assert!/Err) */
+    STYX_E_HIP = -2,          /* HIP runtime error */
+    STYX_E_OOM = -3,
+    STYX_E_IO = -4,
+    STYX_E_FORMAT = -5,       /* GGUF / tensor layout rejected */
+    STYX_E_STATE = -6,        /* call out of order (e.g. KV full) */
+    STYX_E_UNSUPPORTED = -7,
+};
+/* Thread-local message of the last failing call (never NULL). */
+const char *styx_last_error(void);
+
+/* ggml type ids (crates/gguf-rs/src/lib.rs:242-332) used on this path. */
+enum { STYX_F32 = 0, STYX_F16 = 1, STYX_Q8_0 = 8, STYX_Q4_K = 12, STYX_Q5_K = 13, STYX_Q6_K = 14 };
+#define STYX_SKIP 0xFFFFFFFFu
+
+/* ----------------------------------------------------------- device ---- */
+typedef struct styx_gpu styx_gpu;
+/* Gpu::new (crates/vk-backend/src/lib.rs:356): opens HIP device `device`. */
+int styx_gpu_new(int device, styx_gpu **out);
+/* Drop for Gpu (lib.rs:1602-1611): waits for the device, frees the stream. */
+void styx_gpu_free(styx_gpu *gpu);
+/* Gpu::vram_bytes (lib.rs:534). */
+uint64_t styx_gpu_hbm_bytes(const styx_gpu *gpu);
+/* Gpu::device_name (lib.rs:336-353). */
+const char *styx_gpu_name(const styx_gpu *gpu);
+/* Gpu::wait_idle-equivalent: block until all queued work has finished. */
+int styx_gpu_sync(styx_gpu *gpu);
+
+/* ---------------------------------------------------------- buffers ---- */
+typedef struct styx_buf styx_buf;
+enum {
+    STYX_BUF_DEVICE = 0,       /* HBM (create_buffer, lib.rs:568) */
+    STYX_BUF_HOST_PINNED = 1,  /* pinned host memory mapped for the GPU
+                                  (create_buffer_host / _host_shared,
+                                  lib.rs:756, 802) */
+};
+int styx_buf_new(styx_gpu *gpu, uint64_t bytes, int kind, styx_buf **out);
+/* destroy_buffer (lib.rs:1517). */
+void styx_buf_free(styx_buf *buf);
+uint64_t styx_buf_size(const styx_buf *buf);
+/* Device address of the buffer (Gpu::device_address, lib.rs:1136). */
+void *styx_buf_device_ptr(const styx_buf *buf);
+/* Gpu::upload (lib.rs:1033) / download (lib.rs:1175): synchronous copies. */
+int styx_upload(styx_gpu *gpu, styx_buf *dst, uint64_t off, const void *src, uint64_t n);
+int styx_download(styx_gpu *gpu, const styx_buf *src, uint64_t off, void *dst, uint64_t n);
+/* Gpu::copy_region (lib.rs:1192): device-side copy, synchronous. */
+int styx_copy_region(styx_gpu *gpu, const styx_buf *src, uint64_t soff, styx_buf *dst,
+                     uint64_t doff, uint64_t n);
+
+/* ------------------------------------------------ kernels and batches ---- */
+/* Gpu::create_pipeline (lib.rs:1222) and Batch (lib.rs:44-231).  A kernel is
+ * named by the reference pipeline it replaces; bindings and push constants
+ * keep the reference's order and byte layout (crates/vk-backend/src/ops.rs,
+ * the shaders' push blocks), and (gx, gy, gz) is the reference's workgroup
+ * grid, so engine code ports call for call.  Names:
+ *   topk_softmax_f32, moe_reduce_f32, gather_slabs_f32, attn_decode_f32,
+ *   matvec_strided_f32, add_flat_f32, axpy_sig_f32, swiglu_f32,
+ *   mul_mat_vec_id_{q8_0,q4_k,q5_k,q6_k}_f32_f32 (weights in GGUF layout).
+ * styx_kernel_names() lists what this build provides. */
+typedef struct styx_kernel styx_kernel;
+int styx_kernel_get(styx_gpu *gpu, const char *name, const uint32_t *spec, int n_spec,
+                    styx_kernel **out);
+void styx_kernel_free(styx_kernel *k);
+/* Comma-separated kernel names accepted by styx_kernel_get. */
+const char *styx_kernel_names(void);
+
+typedef struct {
+    const styx_buf *buf;
+    uint64_t offset;   /* bytes */
+    uint64_t range;    /* bytes, or UINT64_MAX for the rest (vk::WHOLE_SIZE) */
+} styx_binding;
+
+typedef struct styx_batch styx_batch;
+/* Gpu::create_batch (lib.rs:1530) / destroy_batch (lib.rs:1567). */
+int styx_batch_new(styx_gpu *gpu, styx_batch **out);
+void styx_batch_free(styx_batch *b);
+/* Batch::begin (lib.rs:56). */
+int styx_batch_begin(styx_batch *b);
+/* Batch::dispatch_ranges_barrier (lib.rs:115-197).  Work runs in recording
+ * order on one stream, so every dispatch is ordered after the previous one
+ * whatever `barrier` says. */
+int styx_batch_dispatch(styx_batch *b, const styx_kernel *k, const styx_binding *binds,
+                        int n_binds, const void *push, uint32_t push_len, uint32_t gx,
+                        uint32_t gy, uint32_t gz, int barrier);
+/* Batch::submit (lib.rs:200-231): run the recorded work and wait for it. */
+int styx_batch_submit(styx_batch *b);
+
+/* ------------------------------------------------------- hot-path ops ---- */
+/* Direct entry points of the gfx950 kernels (device pointers, enqueued on
+ * the gpu's stream; call styx_gpu_sync to wait).  Weights are in the split
+ * layout produced by styx_op_to_split unless stated otherwise. */
+
+/* GGUF block layout -> split layout (and back) for nmat matrices of
+ * nblocks blocks each (an expert tensor is nmat = n_expert slabs). */
+int styx_op_to_split(styx_gpu *gpu, int type, const void *src, void *dst, int64_t nblocks,
+                     int64_t nmat);
+int styx_op_from_split(styx_gpu *gpu, int type, const void *src, void *dst, int64_t nblocks,
+                       int64_t nmat);
+/* Dequantize rows [r0, r0+nrows) of a split matrix with nrows_total rows
+ * to f32, in the reference's evaluation order (bit-exact dequant). */
+int styx_op_dequant_rows(styx_gpu *gpu, int type, const void *w, int64_t nrows_total,
+                         int ncols, int64_t r0, int64_t nrows, float *out);
+/* y = W . xn (add: y += W . xn), xn = norm_w ? rmsnorm(x, eps) * norm_w : x.
+ * mul_mat_vec_{t}_f32_f32 + rms_norm_f32 (crates/model/src/moe.rs:1523-1551,
+ * 1746-1766). */
+int styx_op_matvec(styx_gpu *gpu, int type, const void *w, int nrows, int ncols,
+                   const float *x, const float *norm_w, float eps, float *y, int add);
+/* Fused ffn_norm + router (matvec_strided_f32) + topk_softmax_f32
+ * (crates/model/src/moe.rs:1974-2016).  W [E][H] f32, bias [E] or NULL,
+ * remap/pmap [E] or NULL (NULL remap = every expert resident at its own
+ * index), arena_mode: cold experts get arena slot layer*k+s.  Writes
+ * xn [H], logits [E], weights [k], ids [64]. */
+int styx_op_router_topk(styx_gpu *gpu, const float *x, const float *norm_w, float eps,
+                        const float *W, const float *bias, int E, int H, int k, int renorm,
+                        const uint32_t *remap, const uint32_t *pmap, int arena_mode, int layer,
+                        float *xn, float *logits, float *weights, int32_t *ids);
+/* topk_softmax_f32 alone (shaders/topk_softmax_f32.comp). */
+int styx_op_topk_softmax(styx_gpu *gpu, const float *logits, int n, int k, int renorm,
+                         const uint32_t *remap, const uint32_t *pmap, int arena_mode, int layer,
+                         float *weights, int32_t *ids);
+/* Expert slab sources selected per slot by the id row (moe.rs:1649-1700). */
+typedef struct {
+    const void *hot;    int64_t hot_slab;    /* HBM tensor / hot buffer */
+    const void *arena;  int64_t arena_slab;  /* HBM arena slots */
+    const void *host;   int64_t host_slab;   /* pinned host tensor */
+} styx_expert_src;
+/* gu[0][s] = Wg[e_s] . xn, gu[1][s] = Wu[e_s] . xn  (mul_mat_vec_id_*,
+ * ne11 = 1, moe.rs:2023-2038).  gu is [2][k][F]. */
+int styx_op_moe_gate_up(styx_gpu *gpu, int type_gate, int type_up, const styx_expert_src *gate,
+                        const styx_expert_src *up, const int32_t *ids, const float *xn, float *gu,
+                        int H, int F, int k);
+/* x += sum_s w_s * Wd[e_s] . swiglu(gu[0][s], gu[1][s])  (swiglu_f32 +
+ * mul_mat_vec_id ne11=k + moe_reduce_f32, moe.rs:2025-2062).  partial:
+ * [k][H] f32 scratch. */
+int styx_op_moe_down_reduce(styx_gpu *gpu, int type_down, const styx_expert_src *down,
+                            const int32_t *ids, const float *weights, const float *gu, float *x,
+                            float *partial, int H, int F, int k);
+/* Decode attention over the paged KV cache with fused per-head q/k RMSNorm,
+ * NEOX rope and K/V append at *pos (attn_decode_f32.comp, moe.rs:1875-1964).
+ * q [nh*hd], k/v [nkv*hd] raw projections; q_norm/k_norm [hd] or NULL;
+ * inv_freq [hd/2] f64; kpool/vpool [pages][page_tokens][nkv*hd];
+ * page_table [ceil(n_ctx/page_tokens)]; part: styx_op_attn_part_floats(). */
+int styx_op_attn_decode(styx_gpu *gpu, const float *q, const float *k, const float *v,
+                        const float *q_norm, const float *k_norm, float eps,
+                        const double *inv_freq, float *kpool, float *vpool,
+                        const int32_t *page_table, int page_tokens, const int32_t *pos,
+                        float *out, float *part, int nh, int nkv, int hd, int chunk,
+                        int max_chunks, float scale);
+int64_t styx_op_attn_part_floats(int nh, int nkv, int hd, int max_chunks);
+/* gather_slabs_f32 (shaders/gather_slabs_f32.comp:40-86): for slot s < k
+ * with expert ids[s] != SKIP copy that expert's slab of each of the three
+ * tensors into arena slot layer*k+s.  Slab sizes multiples of 16. */
+int styx_op_gather_slabs(styx_gpu *gpu, const void *const src[3], const int64_t src_slab[3],
+                         void *const dst[3], const int64_t dst_slab[3], const int32_t *ids,
+                         int k, int layer);
+/* Greedy argmax, ties -> highest index (generate_moe.rs:29).  scratch:
+ * 64 f32 + 64 u32. */
+int styx_op_argmax(styx_gpu *gpu, const float *v, int n, uint32_t *out, float *scratch_val,
+                   uint32_t *scratch_idx);
+/* Seeded synthetic data: N(0, sigma) values quantized to GGUF blocks of
+ * `type` (n values), or f32 N(mean, sigma). */
+int styx_op_gen_quant(styx_gpu *gpu, int type, uint64_t seed, float sigma, void *dst, int64_t n);
+int styx_op_gen_f32(styx_gpu *gpu, uint64_t seed, float mean, float sigma, float *dst, int64_t n);
+
+/* ------------------------------------------------------------- GGUF ----- */
+/* Gguf::open (crates/gguf-rs/src/lib.rs:41-120): parse the header of a GGUF
+ * v2/v3 file and write a JSON summary {version, data_start, metadata: [keys],
+ * tensors: [{name, dims, type, offset, size_bytes}]} into out.  Rejections
+ * carry the reference's messages (lib.rs:46-332).  Needs no GPU. */
+int styx_gguf_inspect(const char *path, char *out, uint64_t cap);
+
+/* ------------------------------------------------------------ engine ---- */
+/* C++ port of crates/model/src/moe.rs MoeModel (qwen3moe). */
+typedef struct styx_moe styx_moe;
+
+typedef struct {
+    int n_ctx;               /* max context; 0 = 4096 (moe.rs:705) */
+    int use_graph;           /* replay each token as one HIP graph */
+    int64_t expert_budget_mb;/* <0: all experts in HBM; >=0: experts in
+                                pinned host memory, this much HBM for hot
+                                slabs (MOE_EXPERTS_VRAM_MB, moe.rs:692-767) */
+    const char *expert_hist; /* popularity CSV "layer,expert,hits"
+                                (MOE_EXPERT_HIST, moe.rs:774-813) or NULL */
+    int arena;               /* cold experts: 1 gather into the HBM arena
+                                in-stream, 0 read in place from host */
+    int repin_interval;      /* MOE_REPIN_INTERVAL (moe.rs:1450-1508); 0 off */
+    int repin_max;           /* MOE_REPIN_MAX; 0 = 2 */
+    int record_hidden;       /* keep the residual after every layer */
+    int time_kernels;        /* HIP events around the expert kernels */
+} styx_moe_opts;
+
+typedef struct {
+    int n_layers, n_embd, n_heads, n_kv_heads, head_dim;
+    int n_expert, n_expert_used, n_ff_exp, n_ff_shexp, n_vocab, n_ctx;
+    float rms_eps, rope_base;
+    int norm_topk;
+    uint64_t slab_bytes;     /* gate+up+down bytes of one (layer,expert) */
+    uint64_t expert_bytes_hbm, expert_bytes_host;
+} styx_moe_hparams;
+
+typedef struct {
+    int n_layers, n_embd, n_heads, n_kv_heads, head_dim;
+    int n_expert, n_expert_used, n_ff_exp, n_ff_shexp, n_vocab;
+    float rms_eps, rope_base;
+    int attn_type, embd_type, head_type;
+    int exp_type[3];         /* gate, up, down (used when exp_mix == 0) */
+    int exp_mix;             /* 1: type(l, role) = [q4_K,q5_K,q6_K][(l+role)%3] */
+    float sigma;             /* weight std, e.g. 0.02 */
+    uint64_t seed;
+    float router_zipf_s;     /* >0: router bias -s*ln(rank), seeded ranks */
+} styx_moe_synth_cfg;
+
+/* MoeModel::load (moe.rs:536-1408) from a GGUF file. */
+int styx_moe_load(styx_gpu *gpu, const char *path, const styx_moe_opts *opts, styx_moe **out);
+/* Build a seeded synthetic model directly in HBM (no file). */
+int styx_moe_synth(styx_gpu *gpu, const styx_moe_synth_cfg *cfg, const styx_moe_opts *opts,
+                   styx_moe **out);
+void styx_moe_free(styx_moe *m);
+/* MoeModel.hp / slab_bytes (moe.rs:373-499). */
+int styx_moe_get_hparams(const styx_moe *m, styx_moe_hparams *out);
+/* MoeModel::forward_token (moe.rs:1780-2157): logits [n_vocab] (may be
+ * NULL to skip the download). */
+int styx_moe_forward_token(styx_moe *m, uint32_t token, float *logits);
+/* generate_moe main loop (crates/model/examples/generate_moe.rs:44-67):
+ * token-at-a-time prefill of the prompt, then n_predict greedy tokens
+ * (the first from the prefill's logits), argmax on the device. */
+int styx_moe_generate(styx_moe *m, const uint32_t *prompt, int n_prompt, int n_predict,
+                      uint32_t *out_tokens, double *prefill_s, double *decode_s);
+/* Continue greedy decoding from the current state: n_steps forward passes,
+ * each on the previous argmax token (generate_moe.rs:58-67 loop body);
+ * out[i] = the token produced by step i. */
+int styx_moe_decode(styx_moe *m, int n_steps, uint32_t *out);
+/* Turn HIP-event timing of every kernel launch on or off (launches are then
+ * enqueued one by one instead of replayed as a graph). */
+int styx_moe_set_timing(styx_moe *m, int on);
+/* MoeModel::last_expert_ids (moe.rs:2387-2402): [n_layers][k]. */
+int styx_moe_last_expert_ids(styx_moe *m, uint32_t *out);
+/* MoeModel::last_hot_cold (moe.rs:1512-1521): [n_layers][2] (hot, cold). */
+int styx_moe_last_hot_cold(styx_moe *m, uint32_t *out);
+/* MoeModel::reset (moe.rs:1410-1412). */
+int styx_moe_reset(styx_moe *m);
+/* Total slab swaps done by repinning (MoeModel.repin_swaps). */
+uint64_t styx_moe_repin_swaps(const styx_moe *m);
+/* Residuals of the last token: [n_layers+1][n_embd] (needs record_hidden). */
+int styx_moe_last_hidden(styx_moe *m, float *out);
+/* Copy a tensor's bytes in GGUF layout (the model's own data). */
+int styx_moe_export_tensor(styx_moe *m, const char *name, void *dst, uint64_t cap,
+                           uint64_t *size, int *type, int64_t dims[4], int *n_dims);
+/* Names of all tensors, '\n'-separated, into buf (size cap). */
+int styx_moe_tensor_names(styx_moe *m, char *buf, uint64_t cap);
+/* Per-kernel event timing when opts.time_kernels: name, launches, total
+ * milliseconds, algorithmic bytes summed over launches. */
+typedef struct {
+    char name[32];
+    uint64_t launches;
+    double total_ms;
+    double bytes;
+} styx_kernel_stat;
+int styx_moe_kernel_stats(styx_moe *m, styx_kernel_stat *out, int cap, int *n);
+int styx_moe_kernel_stats_reset(styx_moe *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

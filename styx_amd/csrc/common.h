@@ -1,0 +1,99 @@
+// common.h -- shared host/device definitions for libstyx_hip.
+//
+// Block formats are GGUF's (crates/gguf-rs/src/lib.rs:242-332).  In HBM the
+// engine keeps every quant matrix in a "split" layout: the same bytes as the
+// GGUF blocks, regrouped per matrix into aligned regions (quants, high bits,
+// scales, f16 factors) so that every lane issues 16-byte loads.  The regrouping
+// is a byte permutation: dequantized values are bit-identical.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace styx {
+
+enum QType : int { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14 };
+
+constexpr uint32_t SKIP = 0xFFFFFFFFu;
+constexpr int MAX_TOPK = 16;
+constexpr int MAX_EXPERTS = 512;
+constexpr int IDS_ROW = 64;  // int32 per layer id row (256 B), moe.rs:1114-1168
+
+__host__ __device__ inline int blk_elems(int t)
+{
+    return t == T_Q8_0 ? 32 : (t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 256 : 1;
+}
+__host__ __device__ inline int blk_bytes(int t)
+{
+    switch (t) {
+    case T_F32: return 4;
+    case T_F16: return 2;
+    case T_Q8_0: return 34;
+    case T_Q4_K: return 144;
+    case T_Q5_K: return 176;
+    case T_Q6_K: return 210;
+    default: return 0;
+    }
+}
+__host__ __device__ inline bool is_quant(int t)
+{
+    return t == T_Q8_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K;
+}
+// Work units per block: one q8_0 block (32 values) or a quarter K-block (64 values).
+__host__ __device__ inline int units_per_blk(int t) { return t == T_Q8_0 ? 1 : 4; }
+
+// Split layout: up to 4 regions per matrix, each an array over (row, block)
+// of a fixed per-block byte size, row-major.
+struct Split {
+    int nreg;
+    int sz[4];    // bytes per block in region r
+    int src[4];   // byte offset of region r's bytes inside a GGUF block
+};
+
+__host__ __device__ inline Split split_of(int t)
+{
+    Split s{};
+    switch (t) {
+    case T_Q8_0:  // qs[32] | d
+        s.nreg = 2; s.sz[0] = 32; s.src[0] = 2; s.sz[1] = 2; s.src[1] = 0;
+        break;
+    case T_Q4_K:  // qs[128] | {d, dmin, scales[12]}
+        s.nreg = 2; s.sz[0] = 128; s.src[0] = 16; s.sz[1] = 16; s.src[1] = 0;
+        break;
+    case T_Q5_K:  // qs[128] | qh[32] | {d, dmin, scales[12]}
+        s.nreg = 3; s.sz[0] = 128; s.src[0] = 48; s.sz[1] = 32; s.src[1] = 16;
+        s.sz[2] = 16; s.src[2] = 0;
+        break;
+    case T_Q6_K:  // ql[128] | qh[64] | scales[16] | d
+        s.nreg = 4; s.sz[0] = 128; s.src[0] = 0; s.sz[1] = 64; s.src[1] = 128;
+        s.sz[2] = 16; s.src[2] = 192; s.sz[3] = 2; s.src[3] = 208;
+        break;
+    default:  // f32 / f16: one region, identity
+        s.nreg = 1; s.sz[0] = blk_bytes(t); s.src[0] = 0;
+        break;
+    }
+    return s;
+}
+
+// Byte offset of region r inside a matrix of nblocks (rows*blocks-per-row) blocks.
+__host__ __device__ inline int64_t region_off(const Split &s, int r, int64_t nblocks)
+{
+    int64_t o = 0;
+    for (int i = 0; i < r; i++) o += (int64_t)s.sz[i] * nblocks;
+    return o;
+}
+
+// Map GGUF byte index (block b, byte i) of a matrix with nblocks blocks to its
+// split-layout byte index.
+__host__ __device__ inline int64_t split_index(const Split &s, int64_t nblocks, int64_t b, int i)
+{
+    for (int r = 0; r < s.nreg; r++) {
+        if (i >= s.src[r] && i < s.src[r] + s.sz[r]) {
+            return region_off(s, r, nblocks) + b * s.sz[r] + (i - s.src[r]);
+        }
+    }
+    return -1;
+}
+
+}  // namespace styx

@@ -1,0 +1,188 @@
+// dispatch.cpp -- pipelines by name and command batches: the
+// Gpu::create_pipeline / Batch surface of crates/vk-backend/src/lib.rs
+// (44-231, 1222-1312) over one HIP stream.  A batch records dispatches
+// (kernel, resolved bindings, push bytes, grid) and runs them in order on
+// submit, then waits -- the reference's submit + fence.
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "refk.h"
+#include "runtime.h"
+
+using namespace styx;
+
+struct styx_kernel {
+    styx_gpu *gpu = nullptr;
+    int kid = 0;
+    int n_bindings = 0;
+    uint32_t push_bytes = 0;
+    std::vector<uint32_t> spec;  // (id, value) pairs
+    std::string name;
+};
+
+struct styx_batch {
+    styx_gpu *gpu = nullptr;
+    bool recording = false;
+    struct Cmd {
+        const styx_kernel *k;
+        std::vector<void *> ptr;
+        std::vector<uint8_t> push;
+        uint32_t gx, gy, gz;
+    };
+    std::vector<Cmd> cmds;
+};
+
+namespace {
+
+struct KDef {
+    const char *name;
+    int kid;
+    int n_bindings;
+    uint32_t push_bytes;
+};
+
+// binding counts and push sizes as created at crates/model/src/moe.rs:644-690
+const KDef kdefs[] = {
+    {"topk_softmax_f32", RK_TOPK, 5, 12},
+    {"moe_reduce_f32", RK_MOE_REDUCE, 3, 8},
+    {"gather_slabs_f32", RK_GATHER, 7, 36},
+    {"attn_decode_f32", RK_ATTN, 4, 20},
+    {"matvec_strided_f32", RK_MATVEC_STRIDED, 3, 8},
+    {"add_flat_f32", RK_ADD, 3, 4},
+    {"axpy_sig_f32", RK_AXPY_SIG, 3, 4},
+    {"swiglu_f32", RK_SWIGLU, 3, 108},
+    {"rms_norm_f32", RK_RMS_NORM, 3, 116},
+    {"mul_mat_vec_q8_0_f32_f32", RK_MMV_BASE + 0, 5, 52},
+    {"mul_mat_vec_q4_k_f32_f32", RK_MMV_BASE + 1, 5, 52},
+    {"mul_mat_vec_q5_k_f32_f32", RK_MMV_BASE + 2, 5, 52},
+    {"mul_mat_vec_q6_k_f32_f32", RK_MMV_BASE + 3, 5, 52},
+    {"mul_mat_vec_id_q8_0_f32_f32", RK_MMV_BASE + 4, 6, 48},
+    {"mul_mat_vec_id_q4_k_f32_f32", RK_MMV_BASE + 5, 6, 48},
+    {"mul_mat_vec_id_q5_k_f32_f32", RK_MMV_BASE + 6, 6, 48},
+    {"mul_mat_vec_id_q6_k_f32_f32", RK_MMV_BASE + 7, 6, 48},
+};
+
+}  // namespace
+
+extern "C" {
+
+const char *styx_kernel_names(void)
+{
+    static std::string names;
+    if (names.empty())
+        for (const auto &d : kdefs) {
+            if (!names.empty()) names += ",";
+            names += d.name;
+        }
+    return names.c_str();
+}
+
+int styx_kernel_get(styx_gpu *gpu, const char *name, const uint32_t *spec, int n_spec,
+                    styx_kernel **out)
+{
+    if (!gpu || !name || !out || n_spec < 0 || (n_spec && !spec))
+        return fail(STYX_E_INVALID, "styx_kernel_get: bad argument");
+    for (const auto &d : kdefs) {
+        if (std::strcmp(d.name, name) != 0) continue;
+        styx_kernel *k = new styx_kernel();
+        k->gpu = gpu;
+        k->kid = d.kid;
+        k->n_bindings = d.n_bindings;
+        k->push_bytes = d.push_bytes;
+        k->spec.assign(spec, spec + 2 * n_spec);
+        k->name = name;
+        gpu->live_children++;
+        *out = k;
+        return STYX_OK;
+    }
+    return fail(STYX_E_UNSUPPORTED, std::string("styx_kernel_get: no kernel named ") + name);
+}
+
+void styx_kernel_free(styx_kernel *k)
+{
+    if (!k) return;
+    styx_gpu *g = k->gpu;
+    delete k;
+    gpu_release(g);
+}
+
+int styx_batch_new(styx_gpu *gpu, styx_batch **out)
+{
+    if (!gpu || !out) return fail(STYX_E_INVALID, "styx_batch_new: bad argument");
+    styx_batch *b = new styx_batch();
+    b->gpu = gpu;
+    gpu->live_children++;
+    *out = b;
+    return STYX_OK;
+}
+
+void styx_batch_free(styx_batch *b)
+{
+    if (!b) return;
+    styx_gpu *g = b->gpu;
+    delete b;
+    gpu_release(g);
+}
+
+int styx_batch_begin(styx_batch *b)
+{
+    if (!b) return fail(STYX_E_INVALID, "styx_batch_begin: NULL batch");
+    if (b->recording) return fail(STYX_E_STATE, "styx_batch_begin: batch already recording");
+    b->cmds.clear();
+    b->recording = true;
+    return STYX_OK;
+}
+
+int styx_batch_dispatch(styx_batch *b, const styx_kernel *k, const styx_binding *binds,
+                        int n_binds, const void *push, uint32_t push_len, uint32_t gx,
+                        uint32_t gy, uint32_t gz, int barrier)
+{
+    (void)barrier;  // one in-order stream: every dispatch follows the previous one
+    if (!b || !k) return fail(STYX_E_INVALID, "styx_batch_dispatch: NULL batch or kernel");
+    if (!b->recording) return fail(STYX_E_STATE, "styx_batch_dispatch: batch not begun");
+    if (n_binds != k->n_bindings)
+        return fail(STYX_E_INVALID, k->name + ": expected " + std::to_string(k->n_bindings) +
+                                        " bindings, got " + std::to_string(n_binds));
+    if (push_len != k->push_bytes || (push_len && !push))
+        return fail(STYX_E_INVALID, k->name + ": push constants must be " +
+                                        std::to_string(k->push_bytes) + " bytes");
+    if (gx == 0 || gy == 0 || gz == 0) return fail(STYX_E_INVALID, k->name + ": empty grid");
+    styx_batch::Cmd c;
+    c.k = k;
+    for (int i = 0; i < n_binds; i++) {
+        const styx_binding &bd = binds[i];
+        if (!bd.buf) return fail(STYX_E_INVALID, k->name + ": NULL buffer in binding");
+        if (bd.offset % 64 || bd.offset > bd.buf->size)
+            return fail(STYX_E_INVALID, k->name + ": binding offset must be 64-byte aligned "
+                                                  "and inside the buffer (lib.rs:98-100)");
+        c.ptr.push_back((char *)bd.buf->ptr + bd.offset);
+    }
+    c.push.assign((const uint8_t *)push, (const uint8_t *)push + push_len);
+    c.gx = gx;
+    c.gy = gy;
+    c.gz = gz;
+    b->cmds.push_back(std::move(c));
+    return STYX_OK;
+}
+
+int styx_batch_submit(styx_batch *b)
+{
+    if (!b) return fail(STYX_E_INVALID, "styx_batch_submit: NULL batch");
+    if (!b->recording) return fail(STYX_E_STATE, "styx_batch_submit: batch not begun");
+    b->recording = false;
+    STYX_HIP(hipSetDevice(b->gpu->device));
+    for (auto &c : b->cmds) {
+        const uint32_t *spec = c.k->spec.empty() ? nullptr : c.k->spec.data();
+        hipError_t e = refk_launch(b->gpu->stream, c.k->kid, c.ptr.data(), c.push.data(), c.gx,
+                                   c.gy, c.gz, spec, (int)c.k->spec.size() / 2);
+        if (e == hipErrorInvalidValue)
+            return fail(STYX_E_INVALID, c.k->name + ": unsupported parameters");
+        if (e != hipSuccess) return hip_fail(e, c.k->name.c_str());
+    }
+    b->cmds.clear();
+    STYX_HIP(hipStreamSynchronize(b->gpu->stream));
+    return STYX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,1281 @@
+// engine.cpp -- C++ port of the qwen3moe MoeModel of crates/model/src/moe.rs
+// on the gfx950 kernels: load (GGUF or seeded synthetic), placement and
+// residency, per-token decode (one HIP graph per token), greedy generation,
+// telemetry.
+//
+// Per layer the token runs 6 kernels (7 with an in-stream slab gather):
+//   qkv matvec (+attn_norm) | attention (+q/k norm, rope, KV append) |
+//   o-proj (+residual) | router+topk (+ffn_norm) | expert gate/up |
+//   expert down (+swiglu, +weighted reduce into the residual)
+// against 21 dispatches per layer in the reference (moe.rs:1845-2062).
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <functional>
+#include <memory>
+#include <numeric>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "gguf.h"
+#include "kernels.h"
+#include "runtime.h"
+
+namespace styx {
+hipError_t launch_swiglu(hipStream_t st, const float *g, const float *u, float *h, int n);
+}  // namespace styx
+
+using namespace styx;
+
+namespace {
+
+constexpr int KV_PAGE_TOKENS = 512;  // moe.rs:501-503
+
+#define CK(call)                                                          \
+    do {                                                                  \
+        hipError_t _e = (call);                                           \
+        if (_e == hipErrorInvalidValue)                                   \
+            return fail(STYX_E_INVALID, std::string(#call) + ": unsupported shape or type"); \
+        if (_e != hipSuccess) return hip_fail(_e, #call);                 \
+    } while (0)
+
+uint64_t fnv1a64(const std::string &s)
+{
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (unsigned char c : s) {
+        h ^= c;
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}
+
+uint64_t splitmix(uint64_t &s)
+{
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+struct Mat {
+    std::string name;
+    int type = 0;
+    int rows = 0, cols = 0;   // per expert for expert tensors
+    int nmat = 1;             // experts
+    int64_t slab = 0;         // bytes per matrix
+    uint8_t *dev = nullptr;   // HBM copy (split layout), or null
+    uint8_t *host = nullptr;  // pinned host copy (split layout), or null
+    uint8_t *host_dev = nullptr;
+    uint8_t *hot = nullptr;   // hot slabs in HBM (host-resident experts)
+    std::vector<int64_t> gguf_dims;
+    int64_t bytes() const { return slab * nmat; }
+};
+
+struct Layer {
+    float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *ffn_norm = nullptr;
+    float *router = nullptr, *router_bias = nullptr, *gate_inp_sh = nullptr;
+    Mat wq, wk, wv, wo, gate, up, down, gsh, ush, dsh;
+    bool host_experts = false;
+    std::vector<uint32_t> remap;       // expert -> hot slot or SKIP
+    uint32_t *remap_dev = nullptr;
+    std::vector<uint32_t> slot_experts;
+    std::vector<uint64_t> hits;
+};
+
+struct KStat {
+    std::string name;
+    uint64_t launches = 0;
+    double ms = 0, bytes = 0;
+};
+
+}  // namespace
+
+struct styx_moe {
+    styx_gpu *gpu = nullptr;
+    styx_moe_opts opts{};
+    // hparams
+    int L = 0, H = 0, nh = 0, nkv = 0, hd = 0, E = 0, K = 0, F = 0, Fsh = 0, V = 0, n_ctx = 0;
+    float eps = 1e-6f, rope_base = 10000.0f;
+    int norm_topk = 1;
+    uint64_t slab_bytes = 0, exp_hbm = 0, exp_host = 0;
+    std::vector<Layer> layers;
+    Mat embd, head;
+    float *out_norm = nullptr;
+    // f32 tensors for export: name -> (device ptr, count, dims)
+    struct F32T {
+        std::string name;
+        float *p;
+        int64_t n;
+        std::vector<int64_t> dims;
+    };
+    std::vector<F32T> f32s;
+    // activations / state
+    float *x = nullptr, *q = nullptr, *kk = nullptr, *vv = nullptr, *attn = nullptr,
+          *xn = nullptr, *rlog = nullptr, *wts = nullptr, *gu = nullptr, *partial = nullptr,
+          *logits = nullptr, *hidden = nullptr, *sh_g = nullptr, *sh_u = nullptr, *sh_y = nullptr,
+          *attn_part = nullptr, *am_val = nullptr;
+    int32_t *ids = nullptr, *d_pos = nullptr;
+    uint32_t *d_tok = nullptr, *am_idx = nullptr, *hist = nullptr;
+    uint32_t *h_stage = nullptr;  // pinned: tok, pos
+    // KV
+    float *kpool = nullptr, *vpool = nullptr;
+    int32_t *d_pt = nullptr;
+    std::vector<int32_t> h_pt;
+    int pages_per_layer = 0, next_page = 0, chunk = 64, max_chunks = 1;
+    double *inv_freq = nullptr;
+    // arena
+    uint8_t *arena[3] = {nullptr, nullptr, nullptr};
+    int64_t arena_slab[3] = {0, 0, 0};
+    bool any_host = false;
+    // graphs
+    hipGraphExec_t g_fwd = nullptr, g_gen = nullptr;
+    int n_past = 0;
+    uint64_t repin_swaps = 0;
+    std::vector<void *> dev_allocs, host_allocs;
+    // timing
+    std::vector<KStat> stats;
+    std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> pending;
+    std::vector<hipEvent_t> ev_pool;
+    size_t ev_next = 0;
+
+    ~styx_moe();
+    int alloc(void **p, size_t n);
+    int alloc_host(void **p, size_t n);
+    template <typename T> int dalloc(T **p, size_t count)
+    {
+        return alloc((void **)p, sizeof(T) * count);
+    }
+    int setup_runtime();
+    int place_experts(const std::vector<std::vector<std::pair<uint32_t, uint64_t>>> *hist);
+    int enqueue_token(bool gen);
+    int run_token(bool gen);
+    int ensure_pages(int upto_pos);
+    int build_graphs();
+    void maybe_repin();
+    int stat_id(const char *name);
+    hipEvent_t ev();
+    int collect_stats();
+};
+
+styx_moe::~styx_moe()
+{
+    if (gpu) {
+        hipSetDevice(gpu->device);
+        hipStreamSynchronize(gpu->stream);
+    }
+    if (g_fwd) hipGraphExecDestroy(g_fwd);
+    if (g_gen) hipGraphExecDestroy(g_gen);
+    for (auto e : ev_pool) hipEventDestroy(e);
+    for (void *p : dev_allocs) hipFree(p);
+    for (void *p : host_allocs) hipHostFree(p);
+    if (gpu) gpu_release(gpu);
+}
+
+int styx_moe::alloc(void **p, size_t n)
+{
+    *p = nullptr;
+    if (n == 0) n = 16;
+    hipError_t e = hipMalloc(p, n);
+    if (e != hipSuccess) return hip_fail(e, ("hipMalloc(" + std::to_string(n) + ")").c_str());
+    dev_allocs.push_back(*p);
+    return STYX_OK;
+}
+
+int styx_moe::alloc_host(void **p, size_t n)
+{
+    *p = nullptr;
+    hipError_t e = hipHostMalloc(p, n, hipHostMallocMapped | hipHostMallocPortable);
+    if (e != hipSuccess) return hip_fail(e, ("hipHostMalloc(" + std::to_string(n) + ")").c_str());
+    host_allocs.push_back(*p);
+    return STYX_OK;
+}
+
+hipEvent_t styx_moe::ev()
+{
+    if (ev_next == ev_pool.size()) {
+        hipEvent_t e;
+        hipEventCreate(&e);
+        ev_pool.push_back(e);
+    }
+    return ev_pool[ev_next++];
+}
+
+int styx_moe::stat_id(const char *name)
+{
+    for (size_t i = 0; i < stats.size(); i++)
+        if (stats[i].name == name) return (int)i;
+    stats.push_back(KStat{name, 0, 0, 0});
+    return (int)stats.size() - 1;
+}
+
+int styx_moe::collect_stats()
+{
+    if (pending.empty()) return STYX_OK;
+    STYX_HIP(hipStreamSynchronize(gpu->stream));
+    for (auto &p : pending) {
+        float ms = 0;
+        STYX_HIP(hipEventElapsedTime(&ms, p.second.first, p.second.second));
+        stats[p.first].ms += ms;
+        stats[p.first].launches++;
+    }
+    pending.clear();
+    ev_next = 0;
+    return STYX_OK;
+}
+
+// ------------------------------------------------------------ runtime ----
+int styx_moe::setup_runtime()
+{
+    const int kv_dim = nkv * hd, q_dim = nh * hd;
+    if (n_ctx <= 0) n_ctx = 4096;
+    STYX_HIP(hipSetDevice(gpu->device));
+    if (int r = dalloc(&x, H)) return r;
+    if (int r = dalloc(&xn, H)) return r;
+    if (int r = dalloc(&q, q_dim)) return r;
+    if (int r = dalloc(&kk, kv_dim)) return r;
+    if (int r = dalloc(&vv, kv_dim)) return r;
+    if (int r = dalloc(&attn, q_dim)) return r;
+    if (int r = dalloc(&rlog, E)) return r;
+    if (int r = dalloc(&wts, (size_t)L * 16)) return r;
+    if (int r = dalloc(&ids, (size_t)L * 64)) return r;
+    if (int r = dalloc(&gu, (size_t)2 * K * F)) return r;
+    if (int r = dalloc(&partial, (size_t)K * H)) return r;
+    if (int r = dalloc(&logits, V)) return r;
+    if (int r = dalloc(&hidden, (size_t)(L + 1) * H)) return r;
+    if (int r = dalloc(&am_val, 64)) return r;
+    if (int r = dalloc(&am_idx, 64)) return r;
+    if (int r = dalloc(&d_pos, 1)) return r;
+    if (int r = dalloc(&d_tok, 1)) return r;
+    if (int r = dalloc(&hist, (size_t)n_ctx + 1)) return r;
+    if (Fsh > 0) {
+        if (int r = dalloc(&sh_g, Fsh)) return r;
+        if (int r = dalloc(&sh_u, Fsh)) return r;
+        if (int r = dalloc(&sh_y, H)) return r;
+    }
+    STYX_HIP(hipMemsetAsync(ids, 0xFF, sizeof(int32_t) * L * 64, gpu->stream));
+    STYX_HIP(hipMemsetAsync(d_pos, 0, 4, gpu->stream));
+    STYX_HIP(hipMemsetAsync(d_tok, 0, 4, gpu->stream));
+    void *hs;
+    if (int r = alloc_host(&hs, 64)) return r;
+    h_stage = (uint32_t *)hs;
+    // paged KV: pool sized for n_ctx on every layer, pages handed out lazily
+    pages_per_layer = (n_ctx + KV_PAGE_TOKENS - 1) / KV_PAGE_TOKENS;
+    const size_t pool = (size_t)L * pages_per_layer * KV_PAGE_TOKENS * kv_dim;
+    if (int r = dalloc(&kpool, pool)) return r;
+    if (int r = dalloc(&vpool, pool)) return r;
+    if (int r = dalloc(&d_pt, (size_t)L * pages_per_layer)) return r;
+    h_pt.assign((size_t)L * pages_per_layer, -1);
+    STYX_HIP(hipMemsetAsync(d_pt, 0, sizeof(int32_t) * L * pages_per_layer, gpu->stream));
+    next_page = 0;
+    // attention split: ~64 chunks over the full context, 32-token multiples
+    chunk = std::max(64, (n_ctx / 64 + 31) / 32 * 32);
+    max_chunks = (n_ctx + chunk - 1) / chunk;
+    const int64_t pf = styx_op_attn_part_floats(nh, nkv, hd, max_chunks);
+    if (int r = dalloc(&attn_part, (size_t)pf)) return r;
+    // rope table in f64: base^(-2i/hd) = theta_scale^i (ops2.rs:426-442)
+    std::vector<double> invf(hd / 2);
+    const double ts = std::pow((double)rope_base, -2.0 / (double)hd);
+    for (int i = 0; i < hd / 2; i++) invf[i] = std::pow(ts, (double)i);
+    if (int r = dalloc(&inv_freq, hd / 2)) return r;
+    STYX_HIP(hipMemcpyAsync(inv_freq, invf.data(), sizeof(double) * invf.size(),
+                            hipMemcpyHostToDevice, gpu->stream));
+    STYX_HIP(hipStreamSynchronize(gpu->stream));
+    return STYX_OK;
+}
+
+int styx_moe::ensure_pages(int upto_pos)
+{
+    const int last = std::min(upto_pos, n_ctx - 1) / KV_PAGE_TOKENS;
+    for (int l = 0; l < L; l++) {
+        bool dirty = false;
+        for (int p = 0; p <= last; p++) {
+            int32_t &e = h_pt[(size_t)l * pages_per_layer + p];
+            if (e < 0) {
+                e = next_page++;
+                dirty = true;
+            }
+        }
+        if (dirty)
+            STYX_HIP(hipMemcpyAsync(d_pt + (size_t)l * pages_per_layer,
+                                    h_pt.data() + (size_t)l * pages_per_layer,
+                                    sizeof(int32_t) * (last + 1), hipMemcpyHostToDevice,
+                                    gpu->stream));
+    }
+    STYX_HIP(hipStreamSynchronize(gpu->stream));
+    return STYX_OK;
+}
+
+// Placement of expert tensors (moe.rs:692-880).  All experts stay in HBM
+// unless opts.expert_budget_mb >= 0; then every expert tensor lives in
+// pinned host memory and the budget buys HBM copies of the hottest
+// (layer, expert) slabs from the popularity list, or -- without a list --
+// whole layers in order.
+int styx_moe::place_experts(const std::vector<std::vector<std::pair<uint32_t, uint64_t>>> *hist)
+{
+    for (auto &ly : layers) {
+        ly.remap.assign(E, SKIP);
+        ly.hits.assign(E, 0);
+        ly.slot_experts.clear();
+    }
+    any_host = false;
+    exp_hbm = exp_host = 0;
+    if (opts.expert_budget_mb < 0) {
+        for (auto &ly : layers) {
+            for (int e = 0; e < E; e++) ly.remap[e] = (uint32_t)e;
+            ly.slot_experts.resize(E);
+            std::iota(ly.slot_experts.begin(), ly.slot_experts.end(), 0u);
+            ly.host_experts = false;
+            exp_hbm += ly.gate.bytes() + ly.up.bytes() + ly.down.bytes();
+        }
+        return STYX_OK;
+    }
+    any_host = true;
+    uint64_t left = (uint64_t)opts.expert_budget_mb << 20;
+    std::vector<std::vector<uint32_t>> hot(L);
+    if (hist) {
+        // global ranking by hits, stable on ties (moe.rs:774-813)
+        struct Ent { uint64_t hits; int layer; uint32_t e; size_t ord; };
+        std::vector<Ent> ents;
+        size_t ord = 0;
+        for (int l = 0; l < L && l < (int)hist->size(); l++)
+            for (auto &p : (*hist)[l]) ents.push_back({p.second, l, p.first, ord++});
+        std::stable_sort(ents.begin(), ents.end(),
+                         [](const Ent &a, const Ent &b) { return a.hits > b.hits; });
+        for (auto &en : ents) {
+            if (en.e >= (uint32_t)E) continue;
+            const auto &ly = layers[en.layer];
+            const uint64_t cost = ly.gate.slab + ly.up.slab + ly.down.slab;
+            if (left < cost) break;
+            left -= cost;
+            hot[en.layer].push_back(en.e);
+        }
+    } else {
+        for (int l = 0; l < L; l++) {
+            const auto &ly = layers[l];
+            const uint64_t cost = ly.gate.bytes() + ly.up.bytes() + ly.down.bytes();
+            if (left < cost) break;
+            left -= cost;
+            for (int e = 0; e < E; e++) hot[l].push_back((uint32_t)e);
+        }
+    }
+    for (int l = 0; l < L; l++) {
+        auto &ly = layers[l];
+        auto &ord = hot[l];
+        std::sort(ord.begin(), ord.end());
+        ly.host_experts = true;
+        ly.slot_experts = ord;
+        for (size_t i = 0; i < ord.size(); i++) ly.remap[ord[i]] = (uint32_t)i;
+        for (Mat *m : {&ly.gate, &ly.up, &ly.down}) {
+            exp_host += m->bytes();
+            if (ord.empty()) continue;
+            if (int r = alloc((void **)&m->hot, (size_t)ord.size() * m->slab)) return r;
+            exp_hbm += (uint64_t)ord.size() * m->slab;
+            for (size_t i = 0; i < ord.size(); i++)
+                STYX_HIP(hipMemcpyAsync(m->hot + i * m->slab, m->host + (int64_t)ord[i] * m->slab,
+                                        m->slab, hipMemcpyHostToDevice, gpu->stream));
+        }
+        if (int r = dalloc(&ly.remap_dev, E)) return r;
+        STYX_HIP(hipMemcpyAsync(ly.remap_dev, ly.remap.data(), sizeof(uint32_t) * E,
+                                hipMemcpyHostToDevice, gpu->stream));
+    }
+    // in-stream arena: k slots per tensor, each the largest slab of its kind
+    if (opts.arena) {
+        for (int t = 0; t < 3; t++) {
+            int64_t mx = 0;
+            for (auto &ly : layers) mx = std::max(mx, (t == 0 ? ly.gate : t == 1 ? ly.up : ly.down).slab);
+            arena_slab[t] = mx;
+            if (int r = alloc((void **)&arena[t], (size_t)K * mx)) return r;
+            exp_hbm += (uint64_t)K * mx;
+        }
+    }
+    STYX_HIP(hipStreamSynchronize(gpu->stream));
+    return STYX_OK;
+}
+
+// ------------------------------------------------------------ forward ----
+int styx_moe::enqueue_token(bool gen)
+{
+    hipStream_t st = gpu->stream;
+    const int q_dim = nh * hd;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipStreamIsCapturing(st, &cs);
+    const bool timing = opts.time_kernels != 0 && cs == hipStreamCaptureStatusNone;
+    auto tstart = [&]() -> hipEvent_t {
+        if (!timing) return nullptr;
+        hipEvent_t e = ev();
+        hipEventRecord(e, st);
+        return e;
+    };
+    auto tend = [&](hipEvent_t a, const char *nm, double bytes) {
+        if (!timing) return;
+        hipEvent_t e = ev();
+        hipEventRecord(e, st);
+        const int id = stat_id(nm);
+        stats[id].bytes += bytes;
+        pending.push_back({id, {a, e}});
+    };
+    CK(launch_embed(st, embd.type, embd.dev, V, H, d_tok, x));
+    if (opts.record_hidden) CK(hipMemcpyAsync(hidden, x, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
+    for (int l = 0; l < L; l++) {
+        Layer &ly = layers[l];
+        hipEvent_t e0 = tstart();
+        if (ly.wq.type == ly.wk.type && ly.wq.type == ly.wv.type) {
+            DenseSeg s[3] = {{ly.wq.dev, q, ly.wq.rows}, {ly.wk.dev, kk, ly.wk.rows},
+                             {ly.wv.dev, vv, ly.wv.rows}};
+            CK(launch_dense(st, ly.wq.type, H, s, 3, x, ly.attn_norm, eps, 0));
+        } else {
+            DenseSeg a{ly.wq.dev, q, ly.wq.rows}, b{ly.wk.dev, kk, ly.wk.rows},
+                c{ly.wv.dev, vv, ly.wv.rows};
+            CK(launch_dense(st, ly.wq.type, H, &a, 1, x, ly.attn_norm, eps, 0));
+            CK(launch_dense(st, ly.wk.type, H, &b, 1, x, ly.attn_norm, eps, 0));
+            CK(launch_dense(st, ly.wv.type, H, &c, 1, x, ly.attn_norm, eps, 0));
+        }
+        tend(e0, "qkv", (double)(ly.wq.bytes() + ly.wk.bytes() + ly.wv.bytes()) + 4.0 * H);
+        e0 = tstart();
+        AttnArgs aa{};
+        aa.q = q;
+        aa.k = kk;
+        aa.v = vv;
+        aa.q_norm = ly.q_norm;
+        aa.k_norm = ly.k_norm;
+        aa.eps = eps;
+        aa.inv_freq = inv_freq;
+        aa.kpool = kpool;
+        aa.vpool = vpool;
+        aa.page_table = d_pt + (size_t)l * pages_per_layer;
+        aa.page_tokens = KV_PAGE_TOKENS;
+        aa.pos = d_pos;
+        aa.out = attn;
+        aa.part = attn_part;
+        aa.nh = nh;
+        aa.nkv = nkv;
+        aa.hd = hd;
+        aa.chunk = chunk;
+        aa.max_chunks = max_chunks;
+        aa.scale = 1.0f / std::sqrt((float)hd);
+        CK(launch_attn_decode(st, aa));
+        tend(e0, "attn", (double)(n_past + 1) * nkv * hd * 8.0);
+        e0 = tstart();
+        DenseSeg so{ly.wo.dev, x, H};
+        CK(launch_dense(st, ly.wo.type, q_dim, &so, 1, attn, nullptr, 0.0f, 1));
+        tend(e0, "o_proj", (double)ly.wo.bytes() + 4.0 * q_dim + 8.0 * H);
+        e0 = tstart();
+        RouterArgs ra{};
+        ra.x = x;
+        ra.norm_w = ly.ffn_norm;
+        ra.W = ly.router;
+        ra.bias = ly.router_bias;
+        ra.eps = eps;
+        ra.xn = xn;
+        ra.logits = rlog;
+        ra.E = E;
+        ra.H = H;
+        ra.k = K;
+        CK(launch_router(st, ra));
+        tend(e0, "router", (double)E * H * 4 + 8.0 * H + 4.0 * E);
+        // top-k is recomputed by every consumer workgroup from the logits;
+        // gate_up's first workgroup publishes the id row and weights
+        Route rt{};
+        rt.logits = rlog;
+        rt.E = E;
+        rt.k = K;
+        rt.renorm = norm_topk;
+        rt.remap = ly.host_experts ? ly.remap_dev : nullptr;
+        rt.arena_mode = ly.host_experts && opts.arena ? 1 : 0;
+        rt.layer = 0;
+        rt.wts_out = wts + (size_t)l * 16;
+        rt.ids_out = ids + (size_t)l * 64;
+        const int32_t *lid = ids + (size_t)l * 64;
+        ExpSrc sg{}, su{}, sd{};
+        Mat *ms[3] = {&ly.gate, &ly.up, &ly.down};
+        ExpSrc *ss[3] = {&sg, &su, &sd};
+        for (int t = 0; t < 3; t++) {
+            Mat &m = *ms[t];
+            ExpSrc &s = *ss[t];
+            if (!ly.host_experts) {
+                s.hot = m.dev;
+                s.hot_slab = m.slab;
+            } else {
+                s.hot = m.hot;
+                s.hot_slab = m.slab;
+                s.arena = arena[t];
+                s.arena_slab = arena_slab[t];
+                s.gtt = m.host_dev;
+                s.gtt_slab = m.slab;
+            }
+        }
+        if (ly.host_experts && opts.arena) {
+            e0 = tstart();
+            const uint8_t *src[3] = {ly.gate.host_dev, ly.up.host_dev, ly.down.host_dev};
+            const int64_t sslab[3] = {ly.gate.slab, ly.up.slab, ly.down.slab};
+            Route rg = rt;
+            rg.wts_out = nullptr;
+            rg.ids_out = nullptr;
+            CK(launch_gather(st, src, sslab, arena, arena_slab, nullptr, &rg, K));
+            tend(e0, "gather", 0.0);
+        }
+        const double slabs_gu = (double)K * (ly.gate.slab + ly.up.slab);
+        e0 = tstart();
+        CK(launch_moe_gate_up(st, ly.gate.type, ly.up.type, sg, su, nullptr, &rt, xn, gu, H, F, K));
+        tend(e0, "moe_gate_up", slabs_gu + 4.0 * H + 4.0 * K * F);
+        e0 = tstart();
+        CK(launch_moe_down(st, ly.down.type, sd, lid, wts + (size_t)l * 16, gu, x, partial, H, F,
+                           K));
+        tend(e0, "moe_down_reduce", (double)K * ly.down.slab + 4.0 * K * F + 8.0 * H);
+        if (ly.gsh.dev) {
+            DenseSeg s2[2] = {{ly.gsh.dev, sh_g, Fsh}, {ly.ush.dev, sh_u, Fsh}};
+            if (ly.gsh.type == ly.ush.type) {
+                CK(launch_dense(st, ly.gsh.type, H, s2, 2, xn, nullptr, 0.0f, 0));
+            } else {
+                CK(launch_dense(st, ly.gsh.type, H, &s2[0], 1, xn, nullptr, 0.0f, 0));
+                CK(launch_dense(st, ly.ush.type, H, &s2[1], 1, xn, nullptr, 0.0f, 0));
+            }
+            CK(launch_swiglu(st, sh_g, sh_u, sh_g, Fsh));
+            DenseSeg sd2{ly.dsh.dev, sh_y, H};
+            CK(launch_dense(st, ly.dsh.type, Fsh, &sd2, 1, sh_g, nullptr, 0.0f, 0));
+            CK(launch_axpy_sig_dot(st, ly.gate_inp_sh, xn, sh_y, x, H));
+        }
+        if (opts.record_hidden)
+            CK(hipMemcpyAsync(hidden + (size_t)(l + 1) * H, x, sizeof(float) * H,
+                              hipMemcpyDeviceToDevice, st));
+    }
+    hipEvent_t e0 = tstart();
+    DenseSeg sh{head.dev, logits, V};
+    CK(launch_dense(st, head.type, H, &sh, 1, x, out_norm, eps, 0));
+    tend(e0, "lm_head", (double)head.bytes() + 4.0 * H + 4.0 * V);
+    CK(launch_argmax(st, logits, V, d_tok, am_val, am_idx, d_pos, gen ? 1 : 0, hist));
+    return STYX_OK;
+}
+
+int styx_moe::build_graphs()
+{
+    if (!opts.use_graph) return STYX_OK;
+    for (int gm = 0; gm < 2; gm++) {
+        hipGraph_t g;
+        STYX_HIP(hipStreamBeginCapture(gpu->stream, hipStreamCaptureModeThreadLocal));
+        int r = enqueue_token(gm == 1);
+        hipError_t e = hipStreamEndCapture(gpu->stream, &g);
+        if (r) return r;
+        if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+        hipGraphExec_t ex;
+        e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+        (gm ? g_gen : g_fwd) = ex;
+    }
+    return STYX_OK;
+}
+
+int styx_moe::run_token(bool gen)
+{
+    hipGraphExec_t g = gen ? g_gen : g_fwd;
+    if (g && !opts.time_kernels) {
+        STYX_HIP(hipGraphLaunch(g, gpu->stream));
+        return STYX_OK;
+    }
+    return enqueue_token(gen);
+}
+
+// Online repinning (moe.rs:1450-1508): fold the last token's routing into
+// per-layer hit counters; every repin_interval tokens swap up to repin_max
+// cold slots per layer for outsiders with at least twice the hits.
+void styx_moe::maybe_repin()
+{
+    if (opts.repin_interval <= 0 || !any_host) return;
+    std::vector<int32_t> h((size_t)L * 64);
+    if (hipMemcpy(h.data(), ids, sizeof(int32_t) * h.size(), hipMemcpyDeviceToHost) != hipSuccess)
+        return;
+    for (int l = 0; l < L; l++)
+        for (int s = 0; s < K; s++) {
+            const uint32_t e = (uint32_t)h[(size_t)l * 64 + s];
+            if (e < (uint32_t)E) layers[l].hits[e]++;
+        }
+    if (n_past % opts.repin_interval != 0) return;
+    const int maxsw = opts.repin_max > 0 ? opts.repin_max : 2;
+    for (auto &ly : layers) {
+        const int n_slots = (int)ly.slot_experts.size();
+        if (n_slots == 0 || !ly.host_experts) continue;
+        std::vector<int> res(n_slots);
+        std::iota(res.begin(), res.end(), 0);
+        std::stable_sort(res.begin(), res.end(), [&](int a, int b) {
+            return ly.hits[ly.slot_experts[a]] < ly.hits[ly.slot_experts[b]];
+        });
+        std::vector<uint32_t> out;
+        for (int e = 0; e < E; e++)
+            if (ly.remap[e] == SKIP) out.push_back((uint32_t)e);
+        std::stable_sort(out.begin(), out.end(),
+                         [&](uint32_t a, uint32_t b) { return ly.hits[a] > ly.hits[b]; });
+        bool dirty = false;
+        for (int i = 0; i < maxsw && i < n_slots && i < (int)out.size(); i++) {
+            const int slot = res[i];
+            const uint32_t old = ly.slot_experts[slot], nw = out[i];
+            if (ly.hits[nw] < 2 * std::max<uint64_t>(ly.hits[old], 1)) break;
+            for (Mat *m : {&ly.gate, &ly.up, &ly.down})
+                hipMemcpyAsync(m->hot + (int64_t)slot * m->slab, m->host + (int64_t)nw * m->slab,
+                               m->slab, hipMemcpyHostToDevice, gpu->stream);
+            ly.remap[old] = SKIP;
+            ly.remap[nw] = (uint32_t)slot;
+            ly.slot_experts[slot] = nw;
+            repin_swaps++;
+            dirty = true;
+        }
+        if (dirty)
+            hipMemcpyAsync(ly.remap_dev, ly.remap.data(), sizeof(uint32_t) * E,
+                           hipMemcpyHostToDevice, gpu->stream);
+    }
+    hipStreamSynchronize(gpu->stream);
+}
+
+// ---------------------------------------------------------- model build --
+namespace {
+
+struct TensorSpec {
+    std::string name;
+    int type;
+    std::vector<int64_t> dims;  // GGUF order: dims[0] = columns
+};
+
+int64_t n_elems(const std::vector<int64_t> &d)
+{
+    int64_t n = 1;
+    for (auto v : d) n *= v;
+    return n;
+}
+
+// Source of a tensor's GGUF-layout bytes: either a host pointer (file) or
+// the generator.
+struct Source {
+    const uint8_t *host = nullptr;
+    uint64_t seed = 0;
+    float sigma = 0, mean = 0;
+    const std::vector<float> *values = nullptr;  // explicit f32 values
+};
+
+struct Builder {
+    styx_moe *m;
+    uint8_t *tmp = nullptr;  // staging for GGUF-layout bytes
+    size_t tmp_size = 0;
+
+    int stage(int type, int64_t n, const Source &src)
+    {
+        const int64_t bytes = n / blk_elems(type) * blk_bytes(type);
+        if ((size_t)bytes > tmp_size) return fail(STYX_E_INVALID, "staging buffer too small");
+        hipStream_t st = m->gpu->stream;
+        if (src.host) {
+            STYX_HIP(hipMemcpyAsync(tmp, src.host, bytes, hipMemcpyHostToDevice, st));
+        } else if (src.values) {
+            STYX_HIP(hipMemcpyAsync(tmp, src.values->data(), bytes, hipMemcpyHostToDevice, st));
+        } else if (type == T_F32) {
+            CK(launch_gen_f32(st, src.seed, src.mean, src.sigma, (float *)tmp, n));
+        } else {
+            CK(launch_gen_quant(st, type, src.seed, src.sigma, tmp, n));
+        }
+        return STYX_OK;
+    }
+
+    int f32(const TensorSpec &t, const Source &src, float **out)
+    {
+        const int64_t n = n_elems(t.dims);
+        if (t.type != T_F32) return fail(STYX_E_FORMAT, t.name + ": expected f32");
+        if (int r = m->dalloc(out, n)) return r;
+        if (int r = stage(T_F32, n, src)) return r;
+        STYX_HIP(hipMemcpyAsync(*out, tmp, n * 4, hipMemcpyDeviceToDevice, m->gpu->stream));
+        m->f32s.push_back({t.name, *out, n, t.dims});
+        return STYX_OK;
+    }
+
+    // 2-D matrix or 3-D expert tensor into split layout; host_copy: keep the
+    // split bytes in pinned host memory instead of HBM.
+    int mat(const TensorSpec &t, const Source &src, Mat &o, bool host_copy)
+    {
+        if (!is_quant(t.type)) return fail(STYX_E_FORMAT, t.name + ": matrix type must be q8_0/q4_K/q5_K/q6_K");
+        if (t.dims.size() < 2) return fail(STYX_E_FORMAT, t.name + ": not a matrix");
+        o.name = t.name;
+        o.type = t.type;
+        o.cols = (int)t.dims[0];
+        o.rows = (int)t.dims[1];
+        o.nmat = t.dims.size() > 2 ? (int)t.dims[2] : 1;
+        o.gguf_dims = t.dims;
+        if (o.cols % blk_elems(t.type))
+            return fail(STYX_E_FORMAT, t.name + ": row length not a multiple of the block size");
+        const int64_t nb = (int64_t)o.rows * (o.cols / blk_elems(t.type));
+        o.slab = nb * blk_bytes(t.type);
+        if (o.slab % 16) return fail(STYX_E_FORMAT, t.name + ": slab not a multiple of 16 bytes");
+        const int64_t n = n_elems(t.dims);
+        if (int r = stage(t.type, n, src)) return r;
+        uint8_t *dst;
+        if (int r = m->alloc((void **)&dst, o.bytes())) return r;
+        CK(launch_to_split(m->gpu->stream, t.type, tmp, dst, nb, o.nmat));
+        if (host_copy) {
+            if (int r = m->alloc_host((void **)&o.host, o.bytes())) return r;
+            STYX_HIP(hipMemcpyAsync(o.host, dst, o.bytes(), hipMemcpyDeviceToHost, m->gpu->stream));
+            STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+            void *dp = nullptr;
+            STYX_HIP(hipHostGetDevicePointer(&dp, o.host, 0));
+            o.host_dev = (uint8_t *)dp;
+            STYX_HIP(hipFree(dst));
+            m->dev_allocs.erase(std::find(m->dev_allocs.begin(), m->dev_allocs.end(), (void *)dst));
+        } else {
+            o.dev = dst;
+        }
+        return STYX_OK;
+    }
+};
+
+std::string blk(int l, const char *s) { return "blk." + std::to_string(l) + "." + s + ".weight"; }
+
+// Tensor list of a qwen3moe model (names/dims the loader expects,
+// moe.rs:550-599,1061-1108).
+std::vector<TensorSpec> model_specs(const styx_moe_synth_cfg &c)
+{
+    std::vector<TensorSpec> v;
+    const int64_t H = c.n_embd, qd = (int64_t)c.n_heads * c.head_dim,
+                  kvd = (int64_t)c.n_kv_heads * c.head_dim;
+    v.push_back({"token_embd.weight", c.embd_type, {H, c.n_vocab}});
+    v.push_back({"output_norm.weight", T_F32, {H}});
+    v.push_back({"output.weight", c.head_type, {H, c.n_vocab}});
+    static const int mix[3] = {T_Q4_K, T_Q5_K, T_Q6_K};
+    for (int l = 0; l < c.n_layers; l++) {
+        auto et = [&](int role) { return c.exp_mix ? mix[(l + role) % 3] : c.exp_type[role]; };
+        v.push_back({blk(l, "attn_norm"), T_F32, {H}});
+        v.push_back({blk(l, "attn_q_norm"), T_F32, {c.head_dim}});
+        v.push_back({blk(l, "attn_k_norm"), T_F32, {c.head_dim}});
+        v.push_back({blk(l, "attn_q"), c.attn_type, {H, qd}});
+        v.push_back({blk(l, "attn_k"), c.attn_type, {H, kvd}});
+        v.push_back({blk(l, "attn_v"), c.attn_type, {H, kvd}});
+        v.push_back({blk(l, "attn_output"), c.attn_type, {qd, H}});
+        v.push_back({blk(l, "ffn_norm"), T_F32, {H}});
+        v.push_back({blk(l, "ffn_gate_inp"), T_F32, {H, c.n_expert}});
+        v.push_back({blk(l, "ffn_gate_exps"), et(0), {H, c.n_ff_exp, c.n_expert}});
+        v.push_back({blk(l, "ffn_up_exps"), et(1), {H, c.n_ff_exp, c.n_expert}});
+        v.push_back({blk(l, "ffn_down_exps"), et(2), {c.n_ff_exp, H, c.n_expert}});
+        if (c.n_ff_shexp > 0) {
+            v.push_back({blk(l, "ffn_gate_shexp"), et(0), {H, c.n_ff_shexp}});
+            v.push_back({blk(l, "ffn_up_shexp"), et(1), {H, c.n_ff_shexp}});
+            v.push_back({blk(l, "ffn_down_shexp"), et(2), {c.n_ff_shexp, H}});
+            v.push_back({blk(l, "ffn_gate_inp_shexp"), T_F32, {H}});
+        }
+        if (c.router_zipf_s > 0)
+            v.push_back({"blk." + std::to_string(l) + ".ffn_gate_inp.bias", T_F32, {c.n_expert}});
+    }
+    return v;
+}
+
+int64_t spec_bytes(const TensorSpec &t)
+{
+    return n_elems(t.dims) / blk_elems(t.type) * blk_bytes(t.type);
+}
+
+// Common construction from a list of tensors with their sources.
+int build_model(styx_moe *m, const styx_moe_synth_cfg &c, const std::vector<TensorSpec> &specs,
+                const std::function<Source(const TensorSpec &)> &source,
+                const std::vector<std::vector<std::pair<uint32_t, uint64_t>>> *hist)
+{
+    m->L = c.n_layers;
+    m->H = c.n_embd;
+    m->nh = c.n_heads;
+    m->nkv = c.n_kv_heads;
+    m->hd = c.head_dim;
+    m->E = c.n_expert;
+    m->K = c.n_expert_used;
+    m->F = c.n_ff_exp;
+    m->Fsh = c.n_ff_shexp;
+    m->V = c.n_vocab;
+    m->eps = c.rms_eps;
+    m->rope_base = c.rope_base;
+    m->norm_topk = 1;
+    if (m->K < 1 || m->K > MAX_TOPK) return fail(STYX_E_INVALID, "n_expert_used must be in [1, 16] (moe.rs:587)");
+    if (m->E < m->K || m->E > MAX_EXPERTS) return fail(STYX_E_INVALID, "n_expert must be in [k, 512]");
+    if (m->nkv < 1 || m->nh % m->nkv || m->nh / m->nkv > 16) return fail(STYX_E_INVALID, "bad head counts");
+    if (m->hd % 32 || m->hd > 256) return fail(STYX_E_INVALID, "head_dim must be a multiple of 32, <= 256");
+    if (m->H % 256) return fail(STYX_E_INVALID, "n_embd must be a multiple of 256");
+    if (m->F % 32 || m->F > 8192) return fail(STYX_E_INVALID, "expert FFN width must be a multiple of 32, <= 8192");
+
+    Builder b{m};
+    int64_t mx = 0;
+    for (auto &t : specs) mx = std::max(mx, spec_bytes(t));
+    if (int r = m->alloc((void **)&b.tmp, (size_t)mx)) return r;
+    b.tmp_size = (size_t)mx;
+    const bool host_experts = m->opts.expert_budget_mb >= 0;
+    m->layers.assign(m->L, Layer());
+    for (auto &t : specs) {
+        const Source src = source(t);
+        const std::string &n = t.name;
+        int l = -1;
+        char role[64] = {0};
+        if (sscanf(n.c_str(), "blk.%d.%63[^.]", &l, role) == 2 && l >= 0 && l < m->L) {
+            Layer &ly = m->layers[l];
+            const std::string r = role;
+            int rc = 0;
+            const bool is_bias = n.size() > 5 && n.compare(n.size() - 5, 5, ".bias") == 0;
+            if (r == "attn_norm") rc = b.f32(t, src, &ly.attn_norm);
+            else if (r == "attn_q_norm") rc = b.f32(t, src, &ly.q_norm);
+            else if (r == "attn_k_norm") rc = b.f32(t, src, &ly.k_norm);
+            else if (r == "ffn_norm") rc = b.f32(t, src, &ly.ffn_norm);
+            else if (r == "ffn_gate_inp" && is_bias) rc = b.f32(t, src, &ly.router_bias);
+            else if (r == "ffn_gate_inp") rc = b.f32(t, src, &ly.router);
+            else if (r == "ffn_gate_inp_shexp") rc = b.f32(t, src, &ly.gate_inp_sh);
+            else if (r == "attn_q") rc = b.mat(t, src, ly.wq, false);
+            else if (r == "attn_k") rc = b.mat(t, src, ly.wk, false);
+            else if (r == "attn_v") rc = b.mat(t, src, ly.wv, false);
+            else if (r == "attn_output") rc = b.mat(t, src, ly.wo, false);
+            else if (r == "ffn_gate_exps") rc = b.mat(t, src, ly.gate, host_experts);
+            else if (r == "ffn_up_exps") rc = b.mat(t, src, ly.up, host_experts);
+            else if (r == "ffn_down_exps") rc = b.mat(t, src, ly.down, host_experts);
+            else if (r == "ffn_gate_shexp") rc = b.mat(t, src, ly.gsh, false);
+            else if (r == "ffn_up_shexp") rc = b.mat(t, src, ly.ush, false);
+            else if (r == "ffn_down_shexp") rc = b.mat(t, src, ly.dsh, false);
+            if (rc) return rc;
+        } else if (n == "token_embd.weight") {
+            if (int r = b.mat(t, src, m->embd, false)) return r;
+        } else if (n == "output.weight") {
+            if (int r = b.mat(t, src, m->head, false)) return r;
+        } else if (n == "output_norm.weight") {
+            if (int r = b.f32(t, src, &m->out_norm)) return r;
+        }
+        STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+    }
+    STYX_HIP(hipFree(b.tmp));
+    m->dev_allocs.erase(std::find(m->dev_allocs.begin(), m->dev_allocs.end(), (void *)b.tmp));
+    // completeness / shape checks
+    if (!m->embd.dev || !m->head.dev || !m->out_norm) return fail(STYX_E_FORMAT, "missing token_embd/output/output_norm");
+    for (int l = 0; l < m->L; l++) {
+        Layer &ly = m->layers[l];
+        const std::string p = "blk." + std::to_string(l) + ": ";
+        if (!ly.attn_norm || !ly.ffn_norm || !ly.router || !ly.wq.slab || !ly.wk.slab ||
+            !ly.wv.slab || !ly.wo.slab || !ly.gate.slab || !ly.up.slab || !ly.down.slab)
+            return fail(STYX_E_FORMAT, p + "missing tensor");
+        if (ly.wq.rows != m->nh * m->hd || ly.wk.rows != m->nkv * m->hd || ly.wv.rows != m->nkv * m->hd ||
+            ly.wo.rows != m->H || ly.wo.cols != m->nh * m->hd || ly.wq.cols != m->H)
+            return fail(STYX_E_FORMAT, p + "attention shapes do not match hparams");
+        if (ly.gate.nmat != m->E || ly.gate.rows != m->F || ly.gate.cols != m->H ||
+            ly.up.nmat != m->E || ly.up.rows != m->F || ly.down.nmat != m->E ||
+            ly.down.rows != m->H || ly.down.cols != m->F)
+            return fail(STYX_E_FORMAT, p + "expert shapes do not match hparams");
+        if (blk_elems(ly.gate.type) != blk_elems(ly.up.type))
+            return fail(STYX_E_UNSUPPORTED, p + "gate/up block sizes differ");
+        if (m->Fsh > 0 && (!ly.gsh.dev || !ly.ush.dev || !ly.dsh.dev || !ly.gate_inp_sh))
+            return fail(STYX_E_FORMAT, p + "missing shared-expert tensor");
+        if (!pick_geo(ly.down.type, m->F).G || !pick_geo(ly.gate.type, m->H).G ||
+            !pick_geo(ly.wo.type, m->nh * m->hd).G)
+            return fail(STYX_E_UNSUPPORTED, p + "no kernel geometry for these shapes");
+    }
+    const Layer &l0 = m->layers[0];
+    m->slab_bytes = l0.gate.slab + l0.up.slab + l0.down.slab;
+    if (int r = m->place_experts(hist)) return r;
+    if (int r = m->setup_runtime()) return r;
+    if (int r = m->build_graphs()) return r;
+    return STYX_OK;
+}
+
+int read_hist(const char *path, int L, std::vector<std::vector<std::pair<uint32_t, uint64_t>>> &h)
+{
+    std::ifstream f(path);
+    if (!f) return fail(STYX_E_IO, std::string("cannot read expert histogram ") + path);
+    h.assign(L, {});
+    std::string line;
+    std::getline(f, line);  // header
+    while (std::getline(f, line)) {
+        int l;
+        unsigned e;
+        unsigned long long hits;
+        if (sscanf(line.c_str(), "%d,%u,%llu", &l, &e, &hits) == 3 && l >= 0 && l < L)
+            h[l].push_back({e, hits});
+    }
+    return STYX_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ C ABI --
+extern "C" {
+
+static styx_moe_opts default_opts()
+{
+    styx_moe_opts o{};
+    o.n_ctx = 4096;
+    o.use_graph = 1;
+    o.expert_budget_mb = -1;
+    o.arena = 1;
+    o.repin_max = 2;
+    return o;
+}
+
+int styx_moe_synth(styx_gpu *gpu, const styx_moe_synth_cfg *cfg, const styx_moe_opts *opts,
+                   styx_moe **out)
+{
+    if (!gpu || !cfg || !out) return fail(STYX_E_INVALID, "styx_moe_synth: NULL argument");
+    STYX_HIP(hipSetDevice(gpu->device));
+    auto m = std::make_unique<styx_moe>();
+    m->gpu = gpu;
+    gpu->live_children++;
+    m->opts = opts ? *opts : default_opts();
+    m->n_ctx = m->opts.n_ctx > 0 ? m->opts.n_ctx : 4096;
+    const styx_moe_synth_cfg c = *cfg;
+    auto specs = model_specs(c);
+    // router bias for Zipf-skewed routing: b_e = -s * ln(rank_e), ranks a
+    // seeded permutation per layer
+    std::vector<std::vector<float>> biases(c.n_layers);
+    if (c.router_zipf_s > 0)
+        for (int l = 0; l < c.n_layers; l++) {
+            std::vector<int> rank(c.n_expert);
+            std::iota(rank.begin(), rank.end(), 1);
+            uint64_t s = c.seed ^ fnv1a64("zipf." + std::to_string(l));
+            for (int i = c.n_expert - 1; i > 0; i--) std::swap(rank[i], rank[splitmix(s) % (i + 1)]);
+            biases[l].resize(c.n_expert);
+            for (int e = 0; e < c.n_expert; e++)
+                biases[l][e] = (float)(-(double)c.router_zipf_s * std::log((double)rank[e]));
+        }
+    auto source = [&](const TensorSpec &t) {
+        Source s;
+        s.seed = c.seed ^ fnv1a64(t.name);
+        const bool norm = t.name.find("norm") != std::string::npos;
+        if (t.type == T_F32 && norm) {
+            s.mean = 1.0f;
+            s.sigma = 0.0f;
+        } else {
+            s.sigma = c.sigma;
+        }
+        int l;
+        if (t.name.find(".ffn_gate_inp.bias") != std::string::npos &&
+            sscanf(t.name.c_str(), "blk.%d.", &l) == 1)
+            s.values = &biases[l];
+        return s;
+    };
+    std::vector<std::vector<std::pair<uint32_t, uint64_t>>> hist;
+    if (m->opts.expert_hist) {
+        if (int r = read_hist(m->opts.expert_hist, c.n_layers, hist)) return r;
+    }
+    if (int r = build_model(m.get(), c, specs, source, m->opts.expert_hist ? &hist : nullptr)) return r;
+    *out = m.release();
+    return STYX_OK;
+}
+
+int styx_moe_load(styx_gpu *gpu, const char *path, const styx_moe_opts *opts, styx_moe **out)
+{
+    if (!gpu || !path || !out) return fail(STYX_E_INVALID, "styx_moe_load: NULL argument");
+    STYX_HIP(hipSetDevice(gpu->device));
+    Gguf g;
+    std::string err;
+    if (!gguf_open(path, g, err)) return fail(STYX_E_FORMAT, std::string("gguf: ") + err);
+    std::string arch;
+    if (!g.get_str("general.architecture", arch))
+        return fail(STYX_E_FORMAT, "missing general.architecture");
+    if (arch != "qwen3moe")
+        return fail(STYX_E_UNSUPPORTED, "unsupported architecture '" + arch + "' (qwen3moe only)");
+    styx_moe_synth_cfg c{};
+    uint32_t u;
+    auto need = [&](const std::string &k, int &dst) -> bool {
+        if (!g.get_u32(arch + "." + k, u)) return false;
+        dst = (int)u;
+        return true;
+    };
+    if (!need("block_count", c.n_layers) || !need("embedding_length", c.n_embd) ||
+        !need("attention.head_count", c.n_heads) || !need("attention.head_count_kv", c.n_kv_heads) ||
+        !need("expert_count", c.n_expert) || !need("expert_used_count", c.n_expert_used))
+        return fail(STYX_E_FORMAT, "missing qwen3moe hyperparameter metadata");
+    if (!need("attention.key_length", c.head_dim)) c.head_dim = c.n_embd / c.n_heads;
+    if (!need("expert_feed_forward_length", c.n_ff_exp)) {
+        const GgufTensor *t = g.find("blk.0.ffn_gate_exps.weight");
+        if (!t || t->dims.size() < 2) return fail(STYX_E_FORMAT, "no expert_feed_forward_length and no ffn_gate_exps");
+        c.n_ff_exp = (int)t->dims[1];
+    }
+    if (!g.get_f32(arch + ".attention.layer_norm_rms_epsilon", c.rms_eps) ||
+        !g.get_f32(arch + ".rope.freq_base", c.rope_base))
+        return fail(STYX_E_FORMAT, "missing rms epsilon / rope base");
+    const GgufTensor *te = g.find("token_embd.weight");
+    if (!te || te->dims.size() != 2) return fail(STYX_E_FORMAT, "missing token_embd.weight");
+    c.n_vocab = (int)te->dims[1];
+    if (const GgufTensor *ts = g.find("blk.0.ffn_gate_shexp.weight")) c.n_ff_shexp = (int)ts->dims[1];
+    // map the file
+    int fd = open(path, O_RDONLY);
+    if (fd < 0) return fail(STYX_E_IO, std::string("open ") + path);
+    struct stat stb;
+    fstat(fd, &stb);
+    const size_t len = (size_t)stb.st_size;
+    void *map = mmap(nullptr, len, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (map == MAP_FAILED) return fail(STYX_E_IO, std::string("mmap ") + path);
+    struct Unmap { void *p; size_t n; ~Unmap() { munmap(p, n); } } unmap{map, len};
+    std::vector<TensorSpec> specs;
+    for (auto &t : g.tensors) {
+        if (t.offset + t.size_bytes + g.data_start > len)
+            return fail(STYX_E_FORMAT, t.name + ": tensor data past end of file");
+        TensorSpec s{t.name, (int)t.ggml_type, {}};
+        for (auto d : t.dims) s.dims.push_back((int64_t)d);
+        specs.push_back(s);
+    }
+    auto m = std::make_unique<styx_moe>();
+    m->gpu = gpu;
+    gpu->live_children++;
+    m->opts = opts ? *opts : default_opts();
+    m->n_ctx = m->opts.n_ctx > 0 ? m->opts.n_ctx : 4096;
+    const uint8_t *data = (const uint8_t *)map + g.data_start;
+    auto source = [&](const TensorSpec &t) {
+        Source s;
+        s.host = data + g.find(t.name)->offset;
+        return s;
+    };
+    std::vector<std::vector<std::pair<uint32_t, uint64_t>>> hist;
+    if (m->opts.expert_hist) {
+        if (int r = read_hist(m->opts.expert_hist, c.n_layers, hist)) return r;
+    }
+    if (int r = build_model(m.get(), c, specs, source, m->opts.expert_hist ? &hist : nullptr)) return r;
+    *out = m.release();
+    return STYX_OK;
+}
+
+void styx_moe_free(styx_moe *m) { delete m; }
+
+int styx_moe_get_hparams(const styx_moe *m, styx_moe_hparams *o)
+{
+    if (!m || !o) return fail(STYX_E_INVALID, "styx_moe_get_hparams: NULL argument");
+    o->n_layers = m->L;
+    o->n_embd = m->H;
+    o->n_heads = m->nh;
+    o->n_kv_heads = m->nkv;
+    o->head_dim = m->hd;
+    o->n_expert = m->E;
+    o->n_expert_used = m->K;
+    o->n_ff_exp = m->F;
+    o->n_ff_shexp = m->Fsh;
+    o->n_vocab = m->V;
+    o->n_ctx = m->n_ctx;
+    o->rms_eps = m->eps;
+    o->rope_base = m->rope_base;
+    o->norm_topk = m->norm_topk;
+    o->slab_bytes = m->slab_bytes;
+    o->expert_bytes_hbm = m->exp_hbm;
+    o->expert_bytes_host = m->exp_host;
+    return STYX_OK;
+}
+
+int styx_moe_forward_token(styx_moe *m, uint32_t token, float *logits_out)
+{
+    if (!m) return fail(STYX_E_INVALID, "styx_moe_forward_token: NULL model");
+    if (m->n_past >= m->n_ctx)
+        return fail(STYX_E_STATE, "KV arena full (" + std::to_string(m->n_ctx) + ")");
+    if (token >= (uint32_t)m->V) return fail(STYX_E_INVALID, "token id out of range");
+    STYX_HIP(hipSetDevice(m->gpu->device));
+    if (m->n_past > 0) m->maybe_repin();
+    if (int r = m->ensure_pages(m->n_past)) return r;
+    m->h_stage[0] = token;
+    m->h_stage[1] = (uint32_t)m->n_past;
+    STYX_HIP(hipMemcpyAsync(m->d_tok, &m->h_stage[0], 4, hipMemcpyHostToDevice, m->gpu->stream));
+    STYX_HIP(hipMemcpyAsync(m->d_pos, &m->h_stage[1], 4, hipMemcpyHostToDevice, m->gpu->stream));
+    if (int r = m->run_token(false)) return r;
+    m->n_past++;
+    if (logits_out)
+        STYX_HIP(hipMemcpyAsync(logits_out, m->logits, sizeof(float) * m->V, hipMemcpyDeviceToHost,
+                                m->gpu->stream));
+    STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+    return m->collect_stats();
+}
+
+int styx_moe_decode(styx_moe *m, int n_steps, uint32_t *out)
+{
+    if (!m || n_steps < 0 || (n_steps && !out)) return fail(STYX_E_INVALID, "styx_moe_decode: bad argument");
+    if (m->n_past < 1) return fail(STYX_E_STATE, "styx_moe_decode: no token forwarded yet");
+    if (m->n_past + n_steps > m->n_ctx) return fail(STYX_E_STATE, "styx_moe_decode: exceeds n_ctx");
+    if (n_steps == 0) return STYX_OK;
+    STYX_HIP(hipSetDevice(m->gpu->device));
+    const int start = m->n_past;  // position of the pending (argmax) token
+    if (int r = m->ensure_pages(start + n_steps - 1)) return r;
+    m->h_stage[1] = (uint32_t)start;
+    STYX_HIP(hipMemcpyAsync(m->d_pos, &m->h_stage[1], 4, hipMemcpyHostToDevice, m->gpu->stream));
+    const bool host_work = (m->opts.repin_interval > 0 && m->any_host) || m->opts.time_kernels;
+    for (int i = 0; i < n_steps; i++) {
+        if (host_work && i > 0) {
+            // host bookkeeping between tokens needs the previous token done
+            STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+            m->maybe_repin();
+            if (int r = m->collect_stats()) return r;
+        }
+        if (int r = m->run_token(true)) return r;
+        m->n_past++;
+    }
+    STYX_HIP(hipMemcpyAsync(out, m->hist + start + 1, sizeof(uint32_t) * n_steps,
+                            hipMemcpyDeviceToHost, m->gpu->stream));
+    STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+    return m->collect_stats();
+}
+
+int styx_moe_generate(styx_moe *m, const uint32_t *prompt, int n_prompt, int n_predict,
+                      uint32_t *out, double *prefill_s, double *decode_s)
+{
+    if (!m || !prompt || n_prompt < 1 || n_predict < 1 || !out)
+        return fail(STYX_E_INVALID, "styx_moe_generate: bad argument");
+    if (m->n_past + n_prompt + n_predict - 1 > m->n_ctx)
+        return fail(STYX_E_STATE, "prompt + generation exceeds n_ctx");
+    using clk = std::chrono::steady_clock;
+    const auto t0 = clk::now();
+    for (int i = 0; i < n_prompt; i++)
+        if (int r = styx_moe_forward_token(m, prompt[i], nullptr)) return r;
+    const auto t1 = clk::now();
+    // the first generated token is the prefill's argmax, already on device
+    STYX_HIP(hipMemcpy(out, m->d_tok, 4, hipMemcpyDeviceToHost));
+    if (int r = styx_moe_decode(m, n_predict - 1, out + 1)) return r;
+    const auto t2 = clk::now();
+    if (prefill_s) *prefill_s = std::chrono::duration<double>(t1 - t0).count();
+    if (decode_s) *decode_s = std::chrono::duration<double>(t2 - t1).count();
+    return STYX_OK;
+}
+
+int styx_moe_set_timing(styx_moe *m, int on)
+{
+    if (!m) return fail(STYX_E_INVALID, "styx_moe_set_timing: NULL model");
+    if (int r = m->collect_stats()) return r;
+    m->opts.time_kernels = on ? 1 : 0;
+    return STYX_OK;
+}
+
+int styx_moe_last_expert_ids(styx_moe *m, uint32_t *out)
+{
+    if (!m || !out) return fail(STYX_E_INVALID, "styx_moe_last_expert_ids: NULL argument");
+    std::vector<int32_t> h((size_t)m->L * 64);
+    STYX_HIP(hipMemcpyAsync(h.data(), m->ids, sizeof(int32_t) * h.size(), hipMemcpyDeviceToHost,
+                            m->gpu->stream));
+    STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+    for (int l = 0; l < m->L; l++)
+        for (int s = 0; s < m->K; s++) out[(size_t)l * m->K + s] = (uint32_t)h[(size_t)l * 64 + s];
+    return STYX_OK;
+}
+
+int styx_moe_last_hot_cold(styx_moe *m, uint32_t *out)
+{
+    if (!m || !out) return fail(STYX_E_INVALID, "styx_moe_last_hot_cold: NULL argument");
+    std::vector<uint32_t> ids((size_t)m->L * m->K);
+    if (int r = styx_moe_last_expert_ids(m, ids.data())) return r;
+    for (int l = 0; l < m->L; l++) {
+        uint32_t hot = 0;
+        for (int s = 0; s < m->K; s++) {
+            const uint32_t e = ids[(size_t)l * m->K + s];
+            if (e < (uint32_t)m->E && m->layers[l].remap[e] != SKIP) hot++;
+        }
+        out[2 * l] = hot;
+        out[2 * l + 1] = (uint32_t)m->K - hot;
+    }
+    return STYX_OK;
+}
+
+int styx_moe_reset(styx_moe *m)
+{
+    if (!m) return fail(STYX_E_INVALID, "styx_moe_reset: NULL model");
+    m->n_past = 0;
+    return STYX_OK;
+}
+
+uint64_t styx_moe_repin_swaps(const styx_moe *m) { return m ? m->repin_swaps : 0; }
+
+int styx_moe_last_hidden(styx_moe *m, float *out)
+{
+    if (!m || !out) return fail(STYX_E_INVALID, "styx_moe_last_hidden: NULL argument");
+    if (!m->opts.record_hidden) return fail(STYX_E_STATE, "model was loaded without record_hidden");
+    STYX_HIP(hipMemcpyAsync(out, m->hidden, sizeof(float) * (m->L + 1) * m->H,
+                            hipMemcpyDeviceToHost, m->gpu->stream));
+    STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+    return STYX_OK;
+}
+
+static const Mat *find_mat(const styx_moe *m, const std::string &name)
+{
+    if (name == m->embd.name) return &m->embd;
+    if (name == m->head.name) return &m->head;
+    for (auto &ly : m->layers)
+        for (const Mat *x : {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.gate, &ly.up, &ly.down, &ly.gsh,
+                             &ly.ush, &ly.dsh})
+            if (x->name == name) return x;
+    return nullptr;
+}
+
+int styx_moe_tensor_names(styx_moe *m, char *buf, uint64_t cap)
+{
+    if (!m || !buf) return fail(STYX_E_INVALID, "styx_moe_tensor_names: NULL argument");
+    std::string s;
+    auto add = [&](const std::string &n) {
+        if (!n.empty()) s += n + "\n";
+    };
+    add(m->embd.name);
+    add(m->head.name);
+    for (auto &t : m->f32s) add(t.name);
+    for (auto &ly : m->layers)
+        for (const Mat *x : {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.gate, &ly.up, &ly.down, &ly.gsh,
+                             &ly.ush, &ly.dsh})
+            add(x->name);
+    if (s.size() + 1 > cap) return fail(STYX_E_INVALID, "styx_moe_tensor_names: buffer too small");
+    memcpy(buf, s.c_str(), s.size() + 1);
+    return STYX_OK;
+}
+
+int styx_moe_export_tensor(styx_moe *m, const char *name, void *dst, uint64_t cap, uint64_t *size,
+                           int *type, int64_t dims[4], int *n_dims)
+{
+    if (!m || !name) return fail(STYX_E_INVALID, "styx_moe_export_tensor: NULL argument");
+    STYX_HIP(hipSetDevice(m->gpu->device));
+    for (auto &t : m->f32s) {
+        if (t.name != name) continue;
+        if (size) *size = (uint64_t)t.n * 4;
+        if (type) *type = T_F32;
+        if (n_dims) *n_dims = (int)t.dims.size();
+        if (dims)
+            for (size_t i = 0; i < t.dims.size() && i < 4; i++) dims[i] = t.dims[i];
+        if (!dst) return STYX_OK;
+        if (cap < (uint64_t)t.n * 4) return fail(STYX_E_INVALID, "export: buffer too small");
+        STYX_HIP(hipMemcpy(dst, t.p, (size_t)t.n * 4, hipMemcpyDeviceToHost));
+        return STYX_OK;
+    }
+    const Mat *x = find_mat(m, name);
+    if (!x) return fail(STYX_E_INVALID, std::string("export: no tensor ") + name);
+    if (size) *size = (uint64_t)x->bytes();
+    if (type) *type = x->type;
+    if (n_dims) *n_dims = (int)x->gguf_dims.size();
+    if (dims)
+        for (size_t i = 0; i < x->gguf_dims.size() && i < 4; i++) dims[i] = x->gguf_dims[i];
+    if (!dst) return STYX_OK;
+    if (cap < (uint64_t)x->bytes()) return fail(STYX_E_INVALID, "export: buffer too small");
+    void *tmp = nullptr;
+    STYX_HIP(hipMalloc(&tmp, x->bytes()));
+    const uint8_t *src = x->dev ? x->dev : x->host_dev;
+    const int64_t nb = (int64_t)x->rows * (x->cols / blk_elems(x->type));
+    hipError_t e = launch_from_split(m->gpu->stream, x->type, src, (uint8_t *)tmp, nb, x->nmat);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(dst, tmp, x->bytes(), hipMemcpyDeviceToHost, m->gpu->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->gpu->stream);
+    hipFree(tmp);
+    if (e != hipSuccess) return hip_fail(e, "export");
+    return STYX_OK;
+}
+
+int styx_moe_kernel_stats(styx_moe *m, styx_kernel_stat *out, int cap, int *n)
+{
+    if (!m || !n) return fail(STYX_E_INVALID, "styx_moe_kernel_stats: NULL argument");
+    if (int r = m->collect_stats()) return r;
+    *n = (int)m->stats.size();
+    for (int i = 0; i < cap && i < (int)m->stats.size(); i++) {
+        memset(out[i].name, 0, sizeof(out[i].name));
+        strncpy(out[i].name, m->stats[i].name.c_str(), sizeof(out[i].name) - 1);
+        out[i].launches = m->stats[i].launches;
+        out[i].total_ms = m->stats[i].ms;
+        out[i].bytes = m->stats[i].bytes;
+    }
+    return STYX_OK;
+}
+
+int styx_moe_kernel_stats_reset(styx_moe *m)
+{
+    if (!m) return fail(STYX_E_INVALID, "styx_moe_kernel_stats_reset: NULL model");
+    if (int r = m->collect_stats()) return r;
+    m->stats.clear();
+    return STYX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,145 @@
+// kernels.h -- host-side launch interface of the HIP kernels in libstyx_hip.
+#pragma once
+
+#include "common.h"
+
+namespace styx {
+
+// Lane-group geometry for a matvec over rows of `ncols` values of type t.
+struct Geo {
+    int G;    // lanes per row
+    int UPL;  // units per lane
+    int units;
+};
+Geo pick_geo(int t, int ncols);
+
+// Slab sources of one expert tensor for the three id rows written by the
+// router (hot / arena / host), see topk_softmax_f32.comp:4-17.
+struct ExpSrc {
+    const uint8_t *hot;
+    int64_t hot_slab;
+    const uint8_t *arena;
+    int64_t arena_slab;
+    const uint8_t *gtt;
+    int64_t gtt_slab;
+};
+
+struct DenseSeg {
+    const uint8_t *w;  // split-layout matrix
+    float *y;
+    int rows;
+};
+
+// y_seg = W_seg . xn for up to 3 matrices sharing type/ncols, where
+// xn = norm_w ? rmsnorm(x)*norm_w : x.  add != 0 accumulates into y.
+hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, int nseg,
+                        const float *x, const float *norm_w, float eps, int add);
+
+// Router for one layer (fused ffn_norm): writes xn (f32, for the expert
+// kernels) and logits[E].  launch_router_topk also runs the top-k into
+// weights[k] and the 64-int id row.
+struct RouterArgs {
+    const float *x, *norm_w, *W, *bias;
+    float eps;
+    float *xn, *logits, *wts;
+    int32_t *ids;
+    const uint32_t *remap, *pmap;
+    int E, H, k, renorm, arena_mode, layer;
+};
+hipError_t launch_router(hipStream_t st, const RouterArgs &a);
+hipError_t launch_router_topk(hipStream_t st, const RouterArgs &a);
+
+// Top-k routing recomputed inside a consumer kernel from the router logits
+// (topk_softmax_f32 semantics); the first workgroup publishes weights and
+// the id row.
+struct Route {
+    const float *logits;
+    int E, k, renorm;
+    const uint32_t *remap, *pmap;
+    int arena_mode, layer;
+    float *wts_out;
+    int32_t *ids_out;
+};
+
+// Standalone topk_softmax_f32 over given logits (one workgroup).
+hipError_t launch_topk_softmax(hipStream_t st, const float *logits, int n, int k, int renorm,
+                               const uint32_t *remap, const uint32_t *pmap, int arena_mode,
+                               int layer, float *wts, int32_t *ids);
+
+// gu[0][s] = Wg[e_s] xn, gu[1][s] = Wu[e_s] xn for the k routed slots;
+// routing from `route` (computed in-kernel) or, if null, the id row `ids`.
+hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, const ExpSrc &u,
+                              const int32_t *ids, const Route *route, const float *xn, float *gu,
+                              int H, int F, int k);
+
+// partial[s] = Wd[e_s] swiglu(gu[0][s], gu[1][s]), then
+// x += sum_s w_s * partial[s] in fixed slot order (moe_reduce_f32.comp:11-13).
+hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_t *ids,
+                           const float *wts, const float *gu, float *x, float *partial, int H,
+                           int F, int k);
+
+// Shared-expert gate: x += sigmoid(dot(ginp, xn)) * y  (axpy_sig_f32.comp).
+hipError_t launch_axpy_sig_dot(hipStream_t st, const float *ginp, const float *xn,
+                               const float *y, float *x, int n);
+
+// Decode attention over the paged f32 KV cache with fused per-head q/k
+// RMSNorm, NEOX rope and the K/V append at the current position.
+struct AttnArgs {
+    const float *q, *k, *v;          // raw projections
+    const float *q_norm, *k_norm;    // [hd] or null
+    float eps;
+    const double *inv_freq;          // [hd/2] base^(-2i/hd)
+    float *kpool, *vpool;            // [pages][page_tokens][kv_dim]
+    const int32_t *page_table;       // logical page -> physical page
+    int page_tokens;
+    const int32_t *pos;              // device scalar
+    float *out;                      // [nh*hd]
+    float *part;                     // [nkv][max_chunks][gqa][hd+2]
+    int nh, nkv, hd, chunk, max_chunks;
+    float scale;
+};
+hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a);
+
+// x = dequant(token_embd[tok]) for the token held in device memory.
+hipError_t launch_embed(hipStream_t st, int t, const uint8_t *w, int64_t nrows, int ncols,
+                        const uint32_t *tok, float *x);
+
+// Greedy argmax over logits (ties -> highest index, generate_moe.rs:29),
+// in two kernels through part_val/part_idx (64 entries each).  Writes
+// out_tok; if advance != 0 also pos += 1 and hist[pos] = result.
+hipError_t launch_argmax(hipStream_t st, const float *v, int n, uint32_t *out_tok,
+                         float *part_val, uint32_t *part_idx, int32_t *pos, int advance,
+                         uint32_t *hist);
+
+// gather_slabs_f32 semantics: for slot s<k with arena id != SKIP copy expert
+// ids[s]'s slab of each tensor into arena slot ids[32+s].
+hipError_t launch_gather(hipStream_t st, const uint8_t *const src[3], const int64_t src_slab[3],
+                         uint8_t *const dst[3], const int64_t dst_slab[3],
+                         const int32_t *ids, const Route *route, int k);
+// Plain gather with explicit expert list (reference binding: ids = expert
+// per slot, arena slot layer*k+s).
+hipError_t launch_gather_list(hipStream_t st, const uint8_t *const src[3],
+                              const int64_t src_slab[3], uint8_t *const dst[3],
+                              const int64_t dst_slab[3], const int32_t *ids, int k, int layer);
+
+// GGUF block layout <-> split layout, for nmat matrices of nblocks blocks.
+hipError_t launch_to_split(hipStream_t st, int t, const uint8_t *src, uint8_t *dst,
+                           int64_t nblocks, int64_t nmat);
+hipError_t launch_from_split(hipStream_t st, int t, const uint8_t *src, uint8_t *dst,
+                             int64_t nblocks, int64_t nmat);
+
+// Dequantize rows [r0, r0+nrows) of a split-layout matrix (nrows_total rows)
+// to f32 with the reference evaluation order.
+hipError_t launch_dequant_rows(hipStream_t st, int t, const uint8_t *w, int64_t nrows_total,
+                               int ncols, int64_t r0, int64_t nrows, float *out);
+
+// Seeded synthetic weights: N(0, sigma) quantized to GGUF blocks of type t
+// (or f32), n values.  Deterministic in (seed, index).
+hipError_t launch_gen_quant(hipStream_t st, int t, uint64_t seed, float sigma, uint8_t *dst,
+                            int64_t n);
+hipError_t launch_gen_f32(hipStream_t st, uint64_t seed, float mean, float sigma, float *dst,
+                          int64_t n);
+
+hipError_t launch_fill_u32(hipStream_t st, uint32_t *p, uint32_t v, int64_t n);
+
+}  // namespace styx

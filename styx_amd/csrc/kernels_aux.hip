@@ -1,0 +1,468 @@
+// kernels_aux.hip -- layout conversion, dequant check, embedding, argmax,
+// slab gather and the seeded synthetic-weight generator (gfx950).
+#include "kernels.h"
+#include "qdot.h"
+#include "deq.h"
+#include "topk.h"
+
+#include <algorithm>
+
+namespace styx {
+
+// ------------------------------------------------- GGUF <-> split layout --
+// One thread per block; each region's bytes are moved with byte loops (a
+// load-time operation).
+__global__ void k_to_split(int t, const uint8_t *src, uint8_t *dst, int64_t nblocks, int64_t nmat,
+                           int dir)
+{
+    const Split s = split_of(t);
+    const int bb = blk_bytes(t);
+    const int64_t total = nblocks * nmat;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t m = i / nblocks, b = i - m * nblocks;
+        const uint8_t *gs = (dir ? dst : src);
+        (void)gs;
+        const int64_t mbase = m * nblocks * bb;
+        for (int r = 0; r < s.nreg; r++) {
+            const int64_t so = mbase + b * bb + s.src[r];
+            const int64_t po = mbase + region_off(s, r, nblocks) + b * s.sz[r];
+            if (dir == 0)
+                for (int j = 0; j < s.sz[r]; j++) dst[po + j] = src[so + j];
+            else
+                for (int j = 0; j < s.sz[r]; j++) dst[so + j] = src[po + j];
+        }
+    }
+}
+
+static hipError_t split_launch(hipStream_t st, int t, const uint8_t *src, uint8_t *dst,
+                               int64_t nblocks, int64_t nmat, int dir)
+{
+    if (blk_bytes(t) == 0) return hipErrorInvalidValue;
+    const int64_t total = nblocks * nmat;
+    const int64_t nwg = std::min<int64_t>((total + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_to_split, dim3((unsigned)std::max<int64_t>(nwg, 1)), dim3(256), 0, st, t,
+                       src, dst, nblocks, nmat, dir);
+    return hipGetLastError();
+}
+
+hipError_t launch_to_split(hipStream_t st, int t, const uint8_t *src, uint8_t *dst,
+                           int64_t nblocks, int64_t nmat)
+{
+    return split_launch(st, t, src, dst, nblocks, nmat, 0);
+}
+hipError_t launch_from_split(hipStream_t st, int t, const uint8_t *src, uint8_t *dst,
+                             int64_t nblocks, int64_t nmat)
+{
+    return split_launch(st, t, src, dst, nblocks, nmat, 1);
+}
+
+__global__ void k_dequant_rows(int t, const uint8_t *w, int64_t nrows_total, int ncols,
+                               int64_t r0, int64_t nrows, float *out)
+{
+    const int be = blk_elems(t), nb = ncols / be;
+    const Mat m = mat_at(w, t, nrows_total * nb);
+    const int64_t total = nrows * nb;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / nb, b = i - r * nb;
+        deq_block(t, m, (r0 + r) * nb + b, out + r * ncols + (int64_t)b * be);
+    }
+}
+
+hipError_t launch_dequant_rows(hipStream_t st, int t, const uint8_t *w, int64_t nrows_total,
+                               int ncols, int64_t r0, int64_t nrows, float *out)
+{
+    if (blk_bytes(t) == 0 || ncols % blk_elems(t)) return hipErrorInvalidValue;
+    const int64_t total = nrows * (ncols / blk_elems(t));
+    const int64_t nwg = std::min<int64_t>((total + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_dequant_rows, dim3((unsigned)std::max<int64_t>(nwg, 1)), dim3(256), 0,
+                       st, t, w, nrows_total, ncols, r0, nrows, out);
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------- embedding ----
+__global__ void k_embed(int t, const uint8_t *w, int64_t nrows, int ncols, const uint32_t *tok,
+                        float *x)
+{
+    const int be = blk_elems(t), nb = ncols / be;
+    const Mat m = mat_at(w, t, nrows * nb);
+    const int64_t r = *tok;
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) deq_block(t, m, r * nb + b, x + b * be);
+}
+
+hipError_t launch_embed(hipStream_t st, int t, const uint8_t *w, int64_t nrows, int ncols,
+                        const uint32_t *tok, float *x)
+{
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, t, w, nrows, ncols, tok, x);
+    return hipGetLastError();
+}
+
+// -------------------------------------------------------------- argmax ----
+// Rust f32::total_cmp key; larger key wins, equal keys -> larger index
+// (Iterator::max_by keeps the last maximum, generate_moe.rs:29).
+__device__ __forceinline__ int32_t tkey(float v)
+{
+    int32_t b = __float_as_int(v);
+    return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+}
+
+constexpr int ARGMAX_WG = 64;
+
+// Stage 1: each workgroup reduces a contiguous slice to (key, index).
+__global__ void __launch_bounds__(256) k_argmax_part(const float *v, int n, float *part_key,
+                                                     uint32_t *part_idx)
+{
+    __shared__ int32_t sk[4];
+    __shared__ uint32_t si[4];
+    const int per = (n + gridDim.x - 1) / gridDim.x;
+    const int lo = blockIdx.x * per, hi = min(n, lo + per);
+    int32_t bk = INT32_MIN;
+    uint32_t bi = 0;
+    for (int i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+        const int32_t k = tkey(v[i]);
+        if (k > bk || (k == bk && (uint32_t)i > bi)) {
+            bk = k;
+            bi = i;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const int32_t ok = __shfl_xor(bk, o);
+        const uint32_t oi = __shfl_xor(bi, o);
+        if (ok > bk || (ok == bk && oi > bi)) {
+            bk = ok;
+            bi = oi;
+        }
+    }
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) {
+        sk[w] = bk;
+        si[w] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int j = 1; j < (int)(blockDim.x >> 6); j++)
+            if (sk[j] > bk || (sk[j] == bk && si[j] > bi)) {
+                bk = sk[j];
+                bi = si[j];
+            }
+        part_key[blockIdx.x] = __int_as_float(bk);
+        part_idx[blockIdx.x] = bi;
+    }
+}
+
+// Stage 2: one wave reduces the stage-1 results in fixed order; optionally
+// advances the device position and records the token (greedy decoding).
+__global__ void __launch_bounds__(64) k_argmax_final(const float *part_key,
+                                                     const uint32_t *part_idx, int nparts,
+                                                     uint32_t *out_tok, int32_t *pos, int advance,
+                                                     uint32_t *hist)
+{
+    if (threadIdx.x != 0) return;
+    int32_t k = __float_as_int(part_key[0]);
+    uint32_t idx = part_idx[0];
+    for (int j = 1; j < nparts; j++) {
+        const int32_t kj = __float_as_int(part_key[j]);
+        if (kj > k || (kj == k && part_idx[j] > idx)) {
+            k = kj;
+            idx = part_idx[j];
+        }
+    }
+    *out_tok = idx;
+    if (advance) {
+        const int32_t p = *pos + 1;
+        *pos = p;
+        if (hist) hist[p] = idx;
+    }
+}
+
+hipError_t launch_argmax(hipStream_t st, const float *v, int n, uint32_t *out_tok,
+                         float *part_val, uint32_t *part_idx, int32_t *pos, int advance,
+                         uint32_t *hist)
+{
+    if (n < 1 || (advance && !pos)) return hipErrorInvalidValue;
+    const int nwg = std::min(ARGMAX_WG, std::max(1, n / 1024));
+    hipLaunchKernelGGL(k_argmax_part, dim3(nwg), dim3(256), 0, st, v, n, part_val, part_idx);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(64), 0, st, part_val, part_idx, nwg, out_tok,
+                       pos, advance, hist);
+    return hipGetLastError();
+}
+
+// swiglu_f32 split mode (crates/vk-backend/tests/ops2.rs:305-309): h = g/(1+e^-g)*u
+__global__ void k_swiglu(const float *g, const float *u, float *h, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) h[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+}
+
+hipError_t launch_swiglu(hipStream_t st, const float *g, const float *u, float *h, int n)
+{
+    hipLaunchKernelGGL(k_swiglu, dim3((n + 255) / 256), dim3(256), 0, st, g, u, h, n);
+    return hipGetLastError();
+}
+
+// -------------------------------------------------------------- gather ----
+// shaders/gather_slabs_f32.comp:40-86: slot s with expert e != SKIP copies
+// slab e of each tensor into its arena slot.  16-byte copies; grid
+// (chunks, k, 3).
+constexpr int64_t GATHER_CHUNK = 64 * 1024;
+
+struct GatherK {
+    const uint8_t *src[3];
+    int64_t src_slab[3];
+    uint8_t *dst[3];
+    int64_t dst_slab[3];
+    const int32_t *ids;
+    Route route;  // mode 0 with route.logits: the id row is computed in-kernel
+    int k, layer, mode;  // mode 0: arena row of an id row; 1: expert list
+};
+
+__global__ void __launch_bounds__(256) k_gather(GatherK a)
+{
+    __shared__ int32_t s_ids[IDS_ROW];
+    __shared__ float s_w[MAX_TOPK];
+    const int s = blockIdx.y, t = blockIdx.z;
+    uint32_t e, slot;
+    if (a.mode == 0) {
+        const int32_t *ids = a.route.logits ? route_in_lds(a.route, s_ids, s_w) : a.ids;
+        slot = (uint32_t)ids[32 + s];
+        e = (uint32_t)ids[s];
+        if (slot == SKIP) return;
+    } else {
+        e = (uint32_t)a.ids[s];
+        if (e == SKIP) return;
+        slot = (uint32_t)(a.layer * a.k + s);
+    }
+    const int64_t n16 = a.src_slab[t] / 16;
+    const int64_t c0 = blockIdx.x * (GATHER_CHUNK / 16);
+    const int64_t c1 = min(n16, c0 + GATHER_CHUNK / 16);
+    const uint4 *src = (const uint4 *)(a.src[t] + (int64_t)e * a.src_slab[t]);
+    uint4 *dst = (uint4 *)(a.dst[t] + (int64_t)slot * a.dst_slab[t]);
+    for (int64_t i = c0 + threadIdx.x; i < c1; i += 256) dst[i] = src[i];
+}
+
+static hipError_t gather_launch(hipStream_t st, const uint8_t *const src[3],
+                                const int64_t src_slab[3], uint8_t *const dst[3],
+                                const int64_t dst_slab[3], const int32_t *ids, const Route *route,
+                                int k, int layer, int mode)
+{
+    GatherK a{};
+    if (route) a.route = *route;
+    int64_t mx = 0;
+    for (int t = 0; t < 3; t++) {
+        if (src_slab[t] % 16 || dst_slab[t] % 16 || src_slab[t] > dst_slab[t])
+            return hipErrorInvalidValue;
+        a.src[t] = src[t];
+        a.src_slab[t] = src_slab[t];
+        a.dst[t] = dst[t];
+        a.dst_slab[t] = dst_slab[t];
+        mx = std::max(mx, src_slab[t]);
+    }
+    a.ids = ids;
+    a.k = k;
+    a.layer = layer;
+    a.mode = mode;
+    const int chunks = (int)((mx + GATHER_CHUNK - 1) / GATHER_CHUNK);
+    hipLaunchKernelGGL(k_gather, dim3(std::max(chunks, 1), k, 3), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(hipStream_t st, const uint8_t *const src[3], const int64_t src_slab[3],
+                         uint8_t *const dst[3], const int64_t dst_slab[3], const int32_t *ids,
+                         const Route *route, int k)
+{
+    return gather_launch(st, src, src_slab, dst, dst_slab, ids, route, k, 0, 0);
+}
+
+hipError_t launch_gather_list(hipStream_t st, const uint8_t *const src[3],
+                              const int64_t src_slab[3], uint8_t *const dst[3],
+                              const int64_t dst_slab[3], const int32_t *ids, int k, int layer)
+{
+    return gather_launch(st, src, src_slab, dst, dst_slab, ids, nullptr, k, layer, 1);
+}
+
+// ---------------------------------------------------------- generator ----
+// Counter-based normal samples (splitmix64 + Box-Muller) quantized with
+// simple min/max quantizers into GGUF blocks.  Deterministic in (seed, i).
+__device__ __forceinline__ uint64_t mix64(uint64_t z)
+{
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ float gauss(uint64_t seed, int64_t i)
+{
+    const uint64_t h1 = mix64(seed ^ mix64((uint64_t)i * 2 + 1));
+    const uint64_t h2 = mix64(h1 ^ 0xD1B54A32D192ED03ull);
+    const float u1 = ((float)(h1 >> 40) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+    const float u2 = (float)(h2 >> 40) * (1.0f / 16777216.0f);
+    return sqrtf(-2.0f * logf(u1)) * cosf(6.28318530717958648f * u2);
+}
+
+__device__ __forceinline__ uint16_t to_f16(float f)
+{
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+__device__ void quant_block(int t, const float *x, uint8_t *o)
+{
+    if (t == T_Q8_0) {
+        float am = 0.0f;
+        for (int i = 0; i < 32; i++) am = fmaxf(am, fabsf(x[i]));
+        const uint16_t dh = to_f16(am / 127.0f);
+        const float d = f16f(dh), id = d > 0.0f ? 1.0f / d : 0.0f;
+        o[0] = dh & 0xFF;
+        o[1] = dh >> 8;
+        for (int i = 0; i < 32; i++)
+            o[2 + i] = (uint8_t)(int8_t)fminf(fmaxf(rintf(x[i] * id), -127.0f), 127.0f);
+        return;
+    }
+    if (t == T_Q4_K || t == T_Q5_K) {
+        const float lv = t == T_Q4_K ? 15.0f : 31.0f;
+        float sc[8], mn[8], msc = 0.0f, mmn = 0.0f;
+        for (int j = 0; j < 8; j++) {
+            float lo = 0.0f, hi = -INFINITY;
+            for (int i = 0; i < 32; i++) {
+                lo = fminf(lo, x[32 * j + i]);
+                hi = fmaxf(hi, x[32 * j + i]);
+            }
+            sc[j] = (hi - lo) / lv;
+            mn[j] = -lo;
+            msc = fmaxf(msc, sc[j]);
+            mmn = fmaxf(mmn, mn[j]);
+        }
+        const uint16_t dh = to_f16(msc / 63.0f), mh = to_f16(mmn / 63.0f);
+        const float d = f16f(dh), dmin = f16f(mh);
+        int ls[8], lm[8];
+        for (int j = 0; j < 8; j++) {
+            ls[j] = d > 0.0f ? (int)fminf(rintf(sc[j] / d), 63.0f) : 0;
+            lm[j] = dmin > 0.0f ? (int)fminf(rintf(mn[j] / dmin), 63.0f) : 0;
+        }
+        o[0] = dh & 0xFF; o[1] = dh >> 8; o[2] = mh & 0xFF; o[3] = mh >> 8;
+        uint8_t *s = o + 4;
+        for (int j = 0; j < 4; j++) {
+            s[j] = (uint8_t)(ls[j] | ((ls[j + 4] >> 4) << 6));
+            s[j + 4] = (uint8_t)(lm[j] | ((lm[j + 4] >> 4) << 6));
+            s[j + 8] = (uint8_t)((ls[j + 4] & 0xF) | ((lm[j + 4] & 0xF) << 4));
+        }
+        int q[256];
+        for (int j = 0; j < 8; j++) {
+            const float ds = d * (float)ls[j], ms = dmin * (float)lm[j];
+            for (int i = 0; i < 32; i++) {
+                const float v = ds > 0.0f ? rintf((x[32 * j + i] + ms) / ds) : 0.0f;
+                q[32 * j + i] = (int)fminf(fmaxf(v, 0.0f), lv);
+            }
+        }
+        if (t == T_Q4_K) {
+            uint8_t *qs = o + 16;
+            for (int c = 0; c < 4; c++)
+                for (int l = 0; l < 32; l++)
+                    qs[32 * c + l] = (uint8_t)(q[64 * c + l] | (q[64 * c + 32 + l] << 4));
+        } else {
+            uint8_t *qh = o + 16, *qs = o + 48;
+            for (int l = 0; l < 32; l++) qh[l] = 0;
+            for (int c = 0; c < 4; c++)
+                for (int l = 0; l < 32; l++) {
+                    const int a = q[64 * c + l], b = q[64 * c + 32 + l];
+                    qs[32 * c + l] = (uint8_t)((a & 15) | ((b & 15) << 4));
+                    qh[l] |= (uint8_t)(((a >> 4) << (2 * c)) | ((b >> 4) << (2 * c + 1)));
+                }
+        }
+        return;
+    }
+    if (t == T_Q6_K) {
+        float sc[16], msc = 0.0f;
+        for (int j = 0; j < 16; j++) {
+            float am = 0.0f;
+            for (int i = 0; i < 16; i++) am = fmaxf(am, fabsf(x[16 * j + i]));
+            sc[j] = am / 31.0f;
+            msc = fmaxf(msc, sc[j]);
+        }
+        const uint16_t dh = to_f16(msc / 127.0f);
+        const float d = f16f(dh);
+        int ls[16], q[256];
+        for (int j = 0; j < 16; j++) {
+            ls[j] = d > 0.0f ? (int)fminf(rintf(sc[j] / d), 127.0f) : 0;
+            const float ds = d * (float)ls[j];
+            for (int i = 0; i < 16; i++) {
+                const float v = ds > 0.0f ? rintf(x[16 * j + i] / ds) : 0.0f;
+                q[16 * j + i] = (int)fminf(fmaxf(v, -32.0f), 31.0f) + 32;
+            }
+        }
+        uint8_t *ql = o, *qh = o + 128;
+        int8_t *scs = (int8_t *)(o + 192);
+        for (int n = 0; n < 2; n++)
+            for (int l = 0; l < 32; l++) {
+                const int q1 = q[128 * n + l], q2 = q[128 * n + 32 + l], q3 = q[128 * n + 64 + l],
+                          q4 = q[128 * n + 96 + l];
+                ql[64 * n + l] = (uint8_t)((q1 & 15) | ((q3 & 15) << 4));
+                ql[64 * n + l + 32] = (uint8_t)((q2 & 15) | ((q4 & 15) << 4));
+                qh[32 * n + l] =
+                    (uint8_t)((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
+            }
+        for (int j = 0; j < 16; j++) scs[j] = (int8_t)ls[j];
+        o[208] = dh & 0xFF;
+        o[209] = dh >> 8;
+        return;
+    }
+}
+
+__global__ void __launch_bounds__(64) k_gen_quant(int t, uint64_t seed, float sigma, uint8_t *dst,
+                                                  int64_t nblocks)
+{
+    const int be = blk_elems(t), bb = blk_bytes(t);
+    for (int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; b < nblocks;
+         b += (int64_t)gridDim.x * blockDim.x) {
+        float x[256];
+        for (int i = 0; i < be; i++) x[i] = sigma * gauss(seed, b * be + i);
+        quant_block(t, x, dst + b * bb);
+    }
+}
+
+hipError_t launch_gen_quant(hipStream_t st, int t, uint64_t seed, float sigma, uint8_t *dst,
+                            int64_t n)
+{
+    if (!is_quant(t) || n % blk_elems(t)) return hipErrorInvalidValue;
+    const int64_t nb = n / blk_elems(t);
+    const int64_t nwg = std::min<int64_t>((nb + 63) / 64, 16384);
+    hipLaunchKernelGGL(k_gen_quant, dim3((unsigned)std::max<int64_t>(nwg, 1)), dim3(64), 0, st, t,
+                       seed, sigma, dst, nb);
+    return hipGetLastError();
+}
+
+__global__ void k_gen_f32(uint64_t seed, float mean, float sigma, float *dst, int64_t n)
+{
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = sigma == 0.0f ? mean : mean + sigma * gauss(seed, i);
+}
+
+hipError_t launch_gen_f32(hipStream_t st, uint64_t seed, float mean, float sigma, float *dst,
+                          int64_t n)
+{
+    const int64_t nwg = std::min<int64_t>((n + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_gen_f32, dim3((unsigned)std::max<int64_t>(nwg, 1)), dim3(256), 0, st, seed,
+                       mean, sigma, dst, n);
+    return hipGetLastError();
+}
+
+__global__ void k_fill_u32(uint32_t *p, uint32_t v, int64_t n)
+{
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+hipError_t launch_fill_u32(hipStream_t st, uint32_t *p, uint32_t v, int64_t n)
+{
+    const int64_t nwg = std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::max<int64_t>(nwg, 1)), dim3(256), 0, st, p, v,
+                       n);
+    return hipGetLastError();
+}
+
+}  // namespace styx

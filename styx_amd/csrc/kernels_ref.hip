@@ -1,0 +1,288 @@
+// kernels_ref.hip -- kernels with the reference pipelines' exact interface,
+// for the generic dispatch path (styx_batch_dispatch).  Each takes the
+// bindings and push-constant block of the shader or vendored kernel it
+// stands in for, with the same workgroup grid.  Quant weights are read in
+// GGUF block layout, as the reference uploads them.
+#include "deq.h"
+#include "kernels.h"
+#include "qdot.h"
+#include "refk.h"
+#include "topk.h"
+
+#include <cstring>
+
+namespace styx {
+
+#pragma clang fp contract(off)
+
+// shaders/moe_reduce_f32.comp: x[i] += sum_s w[s]*d[s*ne+i]
+__global__ void __launch_bounds__(256) kr_moe_reduce(const float *d, const float *w, float *x,
+                                                     uint32_t ne, uint32_t k)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= ne) return;
+    float acc = 0.0f;
+    for (uint32_t s = 0; s < k; s++) acc += w[s] * d[s * ne + i];
+    x[i] += acc;
+}
+
+// shaders/add_flat_f32.comp
+__global__ void __launch_bounds__(256) kr_add(const float *a, const float *b, float *d, uint32_t n)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) d[i] = a[i] + b[i];
+}
+
+// shaders/axpy_sig_f32.comp
+__global__ void __launch_bounds__(256) kr_axpy_sig(const float *a, const float *g, float *d,
+                                                   uint32_t n)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const float s = 1.0f / (1.0f + expf(-g[0]));
+    if (i < n) d[i] += s * a[i];
+}
+
+// shaders/matvec_strided_f32.comp: 32 strided partials, halving tree.
+__global__ void __launch_bounds__(32) kr_matvec_strided(const float *A, const float *x, float *d,
+                                                        uint32_t ncols, uint32_t stride)
+{
+    __shared__ float tmp[32];
+    const uint32_t row = blockIdx.x, tid = threadIdx.x;
+    const float *a = A + (int64_t)row * stride;
+    float sum = 0.0f;
+    for (uint32_t c = tid; c < ncols; c += 32) sum += a[c] * x[c];
+    tmp[tid] = sum;
+    __syncthreads();
+    for (uint32_t s = 16; s > 0; s >>= 1) {
+        if (tid < s) tmp[tid] += tmp[tid + s];
+        __syncthreads();
+    }
+    if (tid == 0) d[row] = tmp[0];
+}
+
+// shaders/attn_decode_f32.comp:31-79 (one workgroup of 128 per query head).
+__global__ void __launch_bounds__(128) kr_attn_decode(const float *Q, const float *K,
+                                                      const float *V, float *O, uint32_t n_t,
+                                                      uint32_t hd, uint32_t kv_dim, uint32_t gqa,
+                                                      float scale)
+{
+    __shared__ float sh_q[256];
+    __shared__ float sh_red[128];
+    __shared__ float sh_prob, sh_m, sh_l, sh_corr;
+    const uint32_t h = blockIdx.x, tid = threadIdx.x;
+    const uint32_t kvoff = (h / gqa) * hd, qbase = h * hd;
+    for (uint32_t i = tid; i < hd; i += 128) sh_q[i] = Q[qbase + i];
+    __syncthreads();
+    float acc0 = 0.0f, acc1 = 0.0f, m = -INFINITY, l = 0.0f;
+    for (uint32_t t = 0; t < n_t; t++) {
+        const int64_t krow = (int64_t)t * kv_dim + kvoff;
+        float part = 0.0f;
+        for (uint32_t i = tid; i < hd; i += 128) part += sh_q[i] * K[krow + i];
+        sh_red[tid] = part;
+        __syncthreads();
+        for (uint32_t s = 64; s > 0; s >>= 1) {
+            if (tid < s) sh_red[tid] += sh_red[tid + s];
+            __syncthreads();
+        }
+        if (tid == 0) {
+            const float sc = sh_red[0] * scale;
+            const float m_new = fmaxf(m, sc);
+            const float corr = expf(m - m_new);
+            const float pr = expf(sc - m_new);
+            sh_l = l * corr + pr;
+            sh_m = m_new;
+            sh_prob = pr;
+            sh_corr = corr;
+        }
+        __syncthreads();
+        const float pr = sh_prob, corr = sh_corr;
+        m = sh_m;
+        l = sh_l;
+        if (tid < hd) acc0 = acc0 * corr + pr * V[krow + tid];
+        if (tid + 128 < hd) acc1 = acc1 * corr + pr * V[krow + tid + 128];
+        __syncthreads();
+    }
+    const float inv_l = 1.0f / l;
+    if (tid < hd) O[qbase + tid] = acc0 * inv_l;
+    if (tid + 128 < hd) O[qbase + tid + 128] = acc1 * inv_l;
+}
+
+// swiglu_f32 split mode over n values (GluPush.n).
+__global__ void __launch_bounds__(256) kr_swiglu(const float *g, const float *u, float *d, uint32_t n)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) d[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+}
+
+// rms_norm_f32 (generic_binary_head, do_multiply spec): one row per workgroup.
+__global__ void __launch_bounds__(256) kr_rms_norm(const float *a, const float *w, float *d,
+                                                   uint32_t ncols, uint32_t a_row, uint32_t d_row,
+                                                   float eps, int mul)
+{
+    __shared__ float red[16];
+    const float *x = a + (int64_t)blockIdx.x * a_row;
+    float ss = 0.0f;
+    for (uint32_t c = threadIdx.x; c < ncols; c += 256) ss += x[c] * x[c];
+    ss = block_sum(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)ncols + eps);
+    float *y = d + (int64_t)blockIdx.x * d_row;
+    for (uint32_t c = threadIdx.x; c < ncols; c += 256) y[c] = mul ? (scale * x[c]) * w[c] : scale * x[c];
+}
+
+#pragma clang fp contract(on)
+
+// mul_mat_vec_{t} / mul_mat_vec_id_{t} over GGUF-layout rows: one wave per
+// (row, slot); lanes take blocks, dequantize in reference order and dot.
+struct MmvRef {
+    const uint8_t *A;
+    const float *B;
+    float *D;
+    const int32_t *ids;  // null for the plain matvec
+    int type;
+    uint32_t ncols, stride_a, stride_b, stride_d, batch_stride_a, batch_stride_b, batch_stride_d;
+    uint32_t ne11, expert_i1, nbi1, nrows, num_rows;
+};
+
+__global__ void __launch_bounds__(64) kr_mmv(MmvRef p)
+{
+    const int t = p.type, be = blk_elems(t), bb = blk_bytes(t);
+    const uint32_t slot = blockIdx.y;
+    int64_t a_blk = 0, b_off = 0, d_off = 0;
+    if (p.ids) {
+        // get_offsets() of mul_mat_vec_base (crates/vk-backend/tests/kernels.rs:124-131)
+        const uint32_t e = (uint32_t)p.ids[slot + p.expert_i1 * p.nbi1];
+        if (e == SKIP) return;
+        a_blk = (int64_t)e * (p.batch_stride_a / be);
+        b_off = (int64_t)(slot % p.ne11) * p.stride_b + (int64_t)p.expert_i1 * p.batch_stride_b;
+        d_off = (int64_t)slot * p.stride_d + (int64_t)p.expert_i1 * p.batch_stride_d;
+    }
+    const uint32_t nb = p.ncols / be;
+    for (uint32_t j = 0; j < p.num_rows; j++) {
+        const uint32_t r = blockIdx.x * p.num_rows + j;
+        if (r >= p.nrows) return;
+        float acc = 0.0f;
+        for (uint32_t b = threadIdx.x; b < nb; b += 64) {
+            const uint8_t *blk = p.A + (a_blk + (int64_t)r * p.stride_a + b) * bb;
+            float y[256];
+            deq_block(t, gguf_blk(blk, t), 0, y);
+            const float *x = p.B + b_off + (int64_t)b * be;
+            for (int i = 0; i < be; i++) acc += y[i] * x[i];
+        }
+        acc = wave_sum(acc);
+        if (threadIdx.x == 0) p.D[d_off + r] = acc;
+    }
+}
+
+// topk_softmax_f32 with the shader's bindings (remap/pmap required).
+__global__ void __launch_bounds__(64) kr_topk(const float *logits, float *w, int32_t *ids,
+                                              const uint32_t *remap, const uint32_t *pmap,
+                                              uint32_t n, uint32_t k, uint32_t renorm)
+{
+    topk_wave(logits, (int)n, (int)k, (int)renorm, remap, pmap, 0, 0, w, ids);
+}
+
+hipError_t refk_launch(hipStream_t st, int kid, void *const *ptr, const void *push, uint32_t gx,
+                       uint32_t gy, uint32_t gz, const uint32_t *spec, int n_spec)
+{
+    const uint32_t *pc = (const uint32_t *)push;
+    switch (kid) {
+    case RK_MOE_REDUCE:
+        hipLaunchKernelGGL(kr_moe_reduce, dim3(gx), dim3(256), 0, st, (const float *)ptr[0],
+                           (const float *)ptr[1], (float *)ptr[2], pc[0], pc[1]);
+        break;
+    case RK_ADD:
+        hipLaunchKernelGGL(kr_add, dim3(gx), dim3(256), 0, st, (const float *)ptr[0],
+                           (const float *)ptr[1], (float *)ptr[2], pc[0]);
+        break;
+    case RK_AXPY_SIG:
+        hipLaunchKernelGGL(kr_axpy_sig, dim3(gx), dim3(256), 0, st, (const float *)ptr[0],
+                           (const float *)ptr[1], (float *)ptr[2], pc[0]);
+        break;
+    case RK_MATVEC_STRIDED:
+        hipLaunchKernelGGL(kr_matvec_strided, dim3(gx), dim3(32), 0, st, (const float *)ptr[0],
+                           (const float *)ptr[1], (float *)ptr[2], pc[0], pc[1]);
+        break;
+    case RK_ATTN: {
+        float scale;
+        std::memcpy(&scale, pc + 4, 4);
+        if (pc[1] > 256 || pc[3] == 0) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(kr_attn_decode, dim3(gx), dim3(128), 0, st, (const float *)ptr[0],
+                           (const float *)ptr[1], (const float *)ptr[2], (float *)ptr[3], pc[0],
+                           pc[1], pc[2], pc[3], scale);
+        break;
+    }
+    case RK_SWIGLU:
+        // GluPush: n is the first field
+        hipLaunchKernelGGL(kr_swiglu, dim3((pc[0] + 255) / 256), dim3(256), 0, st,
+                           (const float *)ptr[0], (const float *)ptr[1], (float *)ptr[2], pc[0]);
+        break;
+    case RK_RMS_NORM: {
+        // BinaryPush: ne, src0[8] (ne00..ne03, nb00..nb03), src1[8], dst[8], misalign, param1
+        float eps;
+        std::memcpy(&eps, pc + 26, 4);
+        int mul = 1;
+        for (int i = 0; i + 1 < 2 * n_spec; i += 2)
+            if (spec[i] == 1) mul = spec[i + 1] != 0;
+        hipLaunchKernelGGL(kr_rms_norm, dim3(gx), dim3(256), 0, st, (const float *)ptr[0],
+                           (const float *)ptr[1], (float *)ptr[2], pc[1], pc[6], pc[22], eps, mul);
+        break;
+    }
+    case RK_TOPK:
+        if (pc[0] < 1 || pc[0] > MAX_EXPERTS || pc[1] < 1 || pc[1] > MAX_TOPK)
+            return hipErrorInvalidValue;
+        hipLaunchKernelGGL(kr_topk, dim3(1), dim3(64), 0, st, (const float *)ptr[0],
+                           (float *)ptr[1], (int32_t *)ptr[2], (const uint32_t *)ptr[3],
+                           (const uint32_t *)ptr[4], pc[0], pc[1], pc[2]);
+        break;
+    case RK_GATHER: {
+        // push: dst_vg, dst_vu, dst_vd, src_vg, src_vu, src_vd, layer, k, canary
+        if (pc[8] != 0) return hipErrorInvalidValue;
+        const uint8_t *src[3] = {(const uint8_t *)ptr[0], (const uint8_t *)ptr[1],
+                                 (const uint8_t *)ptr[2]};
+        uint8_t *dst[3] = {(uint8_t *)ptr[3], (uint8_t *)ptr[4], (uint8_t *)ptr[5]};
+        const int64_t ss[3] = {16ll * pc[3], 16ll * pc[4], 16ll * pc[5]};
+        const int64_t ds[3] = {16ll * pc[0], 16ll * pc[1], 16ll * pc[2]};
+        return launch_gather_list(st, src, ss, dst, ds, (const int32_t *)ptr[6], (int)pc[7],
+                                  (int)pc[6]);
+    }
+    default: {
+        if (kid < RK_MMV_BASE || kid >= RK_MMV_BASE + 8) return hipErrorInvalidValue;
+        const int ti = (kid - RK_MMV_BASE) % 4;
+        const bool with_id = kid >= RK_MMV_BASE + 4;
+        static const int types[4] = {T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K};
+        MmvRef p{};
+        p.type = types[ti];
+        p.A = (const uint8_t *)ptr[0];
+        p.B = (const float *)ptr[1];
+        p.D = (float *)ptr[2];
+        p.ncols = pc[0];
+        p.stride_a = pc[1];
+        p.stride_b = pc[2];
+        p.stride_d = pc[3];
+        p.batch_stride_a = pc[4];
+        p.batch_stride_b = pc[5];
+        p.batch_stride_d = pc[6];
+        if (p.ncols % blk_elems(p.type)) return hipErrorInvalidValue;
+        if (with_id) {
+            // MatVecIdPush: ..., fusion_flags, nei0, ne11, expert_i1, nbi1
+            p.ids = (const int32_t *)ptr[5];
+            p.ne11 = pc[9] ? pc[9] : 1;
+            p.expert_i1 = pc[10];
+            p.nbi1 = pc[11];
+            p.nrows = gx;
+            p.num_rows = 1;
+        } else {
+            // MatVecPush: stride_d = nrows (MatVecPush::simple); NUM_ROWS spec id 1
+            p.num_rows = 1;
+            for (int i = 0; i + 1 < 2 * n_spec; i += 2)
+                if (spec[i] == 1) p.num_rows = spec[i + 1] ? spec[i + 1] : 1;
+            p.nrows = p.stride_d;
+        }
+        hipLaunchKernelGGL(kr_mmv, dim3(gx, with_id ? gy : 1, 1), dim3(64), 0, st, p);
+        break;
+    }
+    }
+    return hipGetLastError();
+}
+
+}  // namespace styx

@@ -1,0 +1,455 @@
+// qdot.h -- device-side dequant dot products for the split quant layout.
+//
+// A matvec row is cut into "units": one q8_0 block (32 values) or a quarter of
+// a K-quant block (64 values).  A lane group of G lanes owns a row; lane gl
+// owns units gl, gl+G, ... and keeps the activation values for those units in
+// registers for every row it visits (the activations are the same for all
+// rows).  Activations are held as three int8 limbs per value,
+//     x ~= sx * (a + (b + c/254)/254),   sx = max|x| / 127 per 32 values,
+// which carries ~23 bits -- f32-class accuracy -- and lets the inner loop be
+// one v_dot4c_i32_i8 per 4 quant values per limb, instead of a convert and an
+// FMA per value.  Quant values of every format are small non-negative or
+// signed integers that fit int8 unchanged.
+#pragma once
+
+#include "common.h"
+
+namespace styx {
+
+constexpr float R254 = 1.0f / 254.0f;
+
+__device__ __forceinline__ float f16f(uint32_t h)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c)
+{
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+__device__ __forceinline__ float limbs_to_f(int A, int B, int C)
+{
+    return (float)A + ((float)B + (float)C * R254) * R254;
+}
+
+// ----------------------------------------------------------------------------
+// Activation limbs in LDS: int8 planes A/B/C of n values, sx[n/32], s16[n/16]
+// (plain sums of the f32 values over 16-value runs, for the per-sub-block
+// offset terms).
+// ----------------------------------------------------------------------------
+struct XqLds {
+    int8_t *A, *B, *C;
+    float *sx, *s16;
+};
+
+__host__ __device__ inline size_t xq_lds_bytes(int n)
+{
+    return (size_t)3 * n + (size_t)(n / 32) * 4 + (size_t)(n / 16) * 4;
+}
+
+__device__ inline XqLds xq_carve(uint8_t *lds, int n)
+{
+    XqLds q;
+    q.A = (int8_t *)lds;
+    q.B = q.A + n;
+    q.C = q.B + n;
+    q.sx = (float *)(lds + 3 * (size_t)n);
+    q.s16 = q.sx + n / 32;
+    return q;
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v)
+{
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Block-wide sum (blockDim.x multiple of 64, <= 1024).  All threads get it.
+__device__ inline float block_sum(float v, float *red)
+{
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < nw; i++) t += red[i];
+    return t;
+}
+
+// Build the limb form of xn = norm ? x * rsqrt(mean(x^2)+eps) * w : x
+// (n a multiple of 32, n <= 8 * 32 * blockDim.x).  If xn_out is non-null
+// the normalised f32 vector is also written there (by block 0 only).
+// Thread t owns 8 consecutive values; four threads share one 32-value block.
+__device__ inline void xq_build(const float *__restrict__ x, const float *__restrict__ nw,
+                                float eps, bool norm, int n, XqLds q, float *red,
+                                float *xn_out)
+{
+    float scale = 1.0f;
+    if (norm) {
+        float ss = 0.0f;
+        for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4) {
+            const float4 v = *(const float4 *)(x + i);
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = block_sum(ss, red);
+        scale = 1.0f / sqrtf(ss / (float)n + eps);
+    }
+    const int ngroups = n / 8;
+    for (int g0 = 0; g0 < ngroups; g0 += blockDim.x) {
+        const int g = g0 + threadIdx.x;
+        const bool act = g < ngroups;
+        float v[8];
+        if (act) {
+            const float4 a = *(const float4 *)(x + 8 * g), b = *(const float4 *)(x + 8 * g + 4);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+            if (norm) {
+                const float4 wa = *(const float4 *)(nw + 8 * g), wb = *(const float4 *)(nw + 8 * g + 4);
+                const float w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = (v[i] * scale) * w[i];
+            }
+            if (xn_out && blockIdx.x == 0 && blockIdx.y == 0) {
+                *(float4 *)(xn_out + 8 * g) = make_float4(v[0], v[1], v[2], v[3]);
+                *(float4 *)(xn_out + 8 * g + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = 0.0f;
+        }
+        float am = 0.0f, s8 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            am = fmaxf(am, fabsf(v[i]));
+            s8 += v[i];
+        }
+        // four consecutive lanes share a 32-value block (groups are 4-aligned)
+        am = fmaxf(am, __shfl_xor(am, 1));
+        am = fmaxf(am, __shfl_xor(am, 2));
+        const float s16 = s8 + __shfl_xor(s8, 1);
+        if (!act) continue;
+        const float inv = am > 0.0f ? 127.0f / am : 0.0f;
+        uint32_t pa[2] = {0, 0}, pb[2] = {0, 0}, pc[2] = {0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float y = v[i] * inv;
+            const float a = rintf(y);
+            const float r1 = (y - a) * 254.0f;
+            const float b = rintf(r1);
+            const float c = fminf(fmaxf(rintf((r1 - b) * 254.0f), -127.0f), 127.0f);
+            const int sh = 8 * (i & 3);
+            pa[i >> 2] |= ((uint32_t)(int)a & 0xFFu) << sh;
+            pb[i >> 2] |= ((uint32_t)(int)b & 0xFFu) << sh;
+            pc[i >> 2] |= ((uint32_t)(int)c & 0xFFu) << sh;
+        }
+        *(uint2 *)(q.A + 8 * g) = make_uint2(pa[0], pa[1]);
+        *(uint2 *)(q.B + 8 * g) = make_uint2(pb[0], pb[1]);
+        *(uint2 *)(q.C + 8 * g) = make_uint2(pc[0], pc[1]);
+        if ((g & 3) == 0) q.sx[g >> 2] = am / 127.0f;
+        if ((g & 1) == 0) q.s16[g >> 1] = s16;
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Per-format unit operands.
+//   q8_0 unit  = block b (32 values at 32b).
+//   q4_K/q5_K  = quarter c of block b: values 256b+64c .. +63
+//                (low nibbles -> first 32, high nibbles -> next 32).
+//   q6_K       = quarter u=(n=u>>1, h=u&1) of block b: four runs of 16 values
+//                at 256b + 128n + 16h + 32r, r = 0..3.
+// ----------------------------------------------------------------------------
+template <int T> struct UX;
+template <> struct UX<T_Q8_0> {
+    uint32_t a[8], b[8], c[8];
+    float sx;
+};
+template <> struct UX<T_Q4_K> {
+    uint32_t a[16], b[16], c[16];
+    float sx[2], s[2];
+    int sh;     // byte shift of this quarter's scale pair (0 or 16)
+    int high;   // quarters 2,3 use the 6-bit packed high scales
+};
+template <> struct UX<T_Q5_K> {
+    uint32_t a[16], b[16], c[16];
+    float sx[2], s[2];
+    int sh, high, qsh;  // qsh = 2c: qh bit of the low nibbles
+};
+template <> struct UX<T_Q6_K> {
+    uint32_t a[16], b[16], c[16];
+    float sx[4], s[4];
+    int h, n;
+};
+
+__device__ __forceinline__ void ld_limbs(const XqLds &q, int e, int ndw, uint32_t *a,
+                                         uint32_t *b, uint32_t *c)
+{
+    for (int i = 0; i < ndw; i += 4) {
+        const uint4 va = *(const uint4 *)(q.A + e + 4 * i);
+        const uint4 vb = *(const uint4 *)(q.B + e + 4 * i);
+        const uint4 vc = *(const uint4 *)(q.C + e + 4 * i);
+        a[i] = va.x; a[i + 1] = va.y; a[i + 2] = va.z; a[i + 3] = va.w;
+        b[i] = vb.x; b[i + 1] = vb.y; b[i + 2] = vb.z; b[i + 3] = vb.w;
+        c[i] = vc.x; c[i + 1] = vc.y; c[i + 2] = vc.z; c[i + 3] = vc.w;
+    }
+}
+
+template <int T> __device__ inline void ux_load(UX<T> &u, const XqLds &q, int unit);
+
+template <> __device__ inline void ux_load<T_Q8_0>(UX<T_Q8_0> &u, const XqLds &q, int unit)
+{
+    ld_limbs(q, 32 * unit, 8, u.a, u.b, u.c);
+    u.sx = q.sx[unit];
+}
+
+template <> __device__ inline void ux_load<T_Q4_K>(UX<T_Q4_K> &u, const XqLds &q, int unit)
+{
+    const int b = unit >> 2, c = unit & 3, e = 256 * b + 64 * c;
+    ld_limbs(q, e, 16, u.a, u.b, u.c);
+    u.sx[0] = q.sx[e / 32];
+    u.sx[1] = q.sx[e / 32 + 1];
+    u.s[0] = q.s16[e / 16] + q.s16[e / 16 + 1];
+    u.s[1] = q.s16[e / 16 + 2] + q.s16[e / 16 + 3];
+    u.sh = 16 * (c & 1);
+    u.high = c >> 1;
+}
+
+template <> __device__ inline void ux_load<T_Q5_K>(UX<T_Q5_K> &u, const XqLds &q, int unit)
+{
+    const int b = unit >> 2, c = unit & 3, e = 256 * b + 64 * c;
+    ld_limbs(q, e, 16, u.a, u.b, u.c);
+    u.sx[0] = q.sx[e / 32];
+    u.sx[1] = q.sx[e / 32 + 1];
+    u.s[0] = q.s16[e / 16] + q.s16[e / 16 + 1];
+    u.s[1] = q.s16[e / 16 + 2] + q.s16[e / 16 + 3];
+    u.sh = 16 * (c & 1);
+    u.high = c >> 1;
+    u.qsh = 2 * c;
+}
+
+template <> __device__ inline void ux_load<T_Q6_K>(UX<T_Q6_K> &u, const XqLds &q, int unit)
+{
+    const int b = unit >> 2, n = (unit >> 1) & 1, h = unit & 1;
+    const int e0 = 256 * b + 128 * n + 16 * h;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int e = e0 + 32 * r;
+        ld_limbs(q, e, 4, u.a + 4 * r, u.b + 4 * r, u.c + 4 * r);
+        u.sx[r] = q.sx[e / 32];
+        u.s[r] = q.s16[e / 16];
+    }
+    u.h = h;
+    u.n = n;
+}
+
+// ----------------------------------------------------------------------------
+// Per-format weight operands of one unit, and their byte offsets inside a
+// matrix in split layout.  `blk` = row * nb + block.
+// ----------------------------------------------------------------------------
+template <int T> struct UW;
+template <> struct UW<T_Q8_0> { uint4 q0, q1; uint32_t d; };
+template <> struct UW<T_Q4_K> { uint4 q0, q1, hd; };
+template <> struct UW<T_Q5_K> { uint4 q0, q1, h0, h1, hd; };
+template <> struct UW<T_Q6_K> { uint4 p0, p1, qh; uint2 sc; uint32_t d; };
+
+// Region base pointers of one matrix (rows x nb blocks) in split layout.
+struct Mat {
+    const uint8_t *r0, *r1, *r2, *r3;
+};
+
+__device__ __forceinline__ Mat mat_at(const uint8_t *base, int t, int64_t nblocks)
+{
+    const Split s = split_of(t);
+    Mat m;
+    m.r0 = base;
+    m.r1 = base + region_off(s, 1, nblocks);
+    m.r2 = s.nreg > 2 ? base + region_off(s, 2, nblocks) : nullptr;
+    m.r3 = s.nreg > 3 ? base + region_off(s, 3, nblocks) : nullptr;
+    return m;
+}
+
+__device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return *(const uint4 *)p; }
+
+template <int T> __device__ inline void uw_load(UW<T> &w, const Mat &m, int64_t blk, int sub);
+
+template <> __device__ inline void uw_load<T_Q8_0>(UW<T_Q8_0> &w, const Mat &m, int64_t blk, int)
+{
+    const uint8_t *q = m.r0 + blk * 32;
+    w.q0 = ldg16(q);
+    w.q1 = ldg16(q + 16);
+    w.d = *(const uint16_t *)(m.r1 + blk * 2);
+}
+template <> __device__ inline void uw_load<T_Q4_K>(UW<T_Q4_K> &w, const Mat &m, int64_t blk, int c)
+{
+    const uint8_t *q = m.r0 + blk * 128 + 32 * c;
+    w.q0 = ldg16(q);
+    w.q1 = ldg16(q + 16);
+    w.hd = ldg16(m.r1 + blk * 16);
+}
+template <> __device__ inline void uw_load<T_Q5_K>(UW<T_Q5_K> &w, const Mat &m, int64_t blk, int c)
+{
+    const uint8_t *q = m.r0 + blk * 128 + 32 * c;
+    w.q0 = ldg16(q);
+    w.q1 = ldg16(q + 16);
+    const uint8_t *h = m.r1 + blk * 32;
+    w.h0 = ldg16(h);
+    w.h1 = ldg16(h + 16);
+    w.hd = ldg16(m.r2 + blk * 16);
+}
+template <> __device__ inline void uw_load<T_Q6_K>(UW<T_Q6_K> &w, const Mat &m, int64_t blk, int u)
+{
+    const int n = (u >> 1) & 1, h = u & 1;
+    const uint8_t *ql = m.r0 + blk * 128 + 64 * n + 16 * h;
+    w.p0 = ldg16(ql);
+    w.p1 = ldg16(ql + 32);
+    w.qh = ldg16(m.r1 + blk * 64 + 32 * n + 16 * h);
+    w.sc = *(const uint2 *)(m.r2 + blk * 16 + 8 * n);
+    w.d = *(const uint16_t *)(m.r3 + blk * 2);
+}
+
+__device__ __forceinline__ void u4_to(const uint4 v, uint32_t *o)
+{
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+}
+
+// q4_K / q5_K scale+min pair for quarter c (get_scale_min at 2c, 2c+1;
+// crates/model/src/moe.rs:513-522), from the header dwords y,z,w.
+__device__ __forceinline__ void k4_scales(const uint4 hd, int sh, int high, float &sc_lo,
+                                          float &sc_hi, float &m_lo, float &m_hi)
+{
+    const uint32_t A = (hd.y >> sh) & 0xFFFFu, B = (hd.z >> sh) & 0xFFFFu,
+                   C = (hd.w >> sh) & 0xFFFFu;
+    uint32_t sc2, m2;
+    if (high) {
+        sc2 = (C & 0x0F0Fu) | ((A >> 2) & 0x3030u);
+        m2 = ((C >> 4) & 0x0F0Fu) | ((B >> 2) & 0x3030u);
+    } else {
+        sc2 = A & 0x3F3Fu;
+        m2 = B & 0x3F3Fu;
+    }
+    sc_lo = (float)(sc2 & 0xFFu);
+    sc_hi = (float)(sc2 >> 8);
+    m_lo = (float)(m2 & 0xFFu);
+    m_hi = (float)(m2 >> 8);
+}
+
+// ---------------------------------------------------------------- dots ----
+__device__ __forceinline__ float udot(const UW<T_Q8_0> &w, const UX<T_Q8_0> &x)
+{
+    uint32_t q[8];
+    u4_to(w.q0, q);
+    u4_to(w.q1, q + 4);
+    int A = 0, B = 0, C = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        A = sdot4(q[i], x.a[i], A);
+        B = sdot4(q[i], x.b[i], B);
+        C = sdot4(q[i], x.c[i], C);
+    }
+    return (f16f(w.d) * x.sx) * limbs_to_f(A, B, C);
+}
+
+__device__ __forceinline__ float udot(const UW<T_Q4_K> &w, const UX<T_Q4_K> &x)
+{
+    uint32_t q[8];
+    u4_to(w.q0, q);
+    u4_to(w.q1, q + 4);
+    int Al = 0, Bl = 0, Cl = 0, Ah = 0, Bh = 0, Ch = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t lo = q[i] & 0x0F0F0F0Fu, hi = (q[i] >> 4) & 0x0F0F0F0Fu;
+        Al = sdot4(lo, x.a[i], Al);
+        Bl = sdot4(lo, x.b[i], Bl);
+        Cl = sdot4(lo, x.c[i], Cl);
+        Ah = sdot4(hi, x.a[8 + i], Ah);
+        Bh = sdot4(hi, x.b[8 + i], Bh);
+        Ch = sdot4(hi, x.c[8 + i], Ch);
+    }
+    float scl, sch, ml, mh;
+    k4_scales(w.hd, x.sh, x.high, scl, sch, ml, mh);
+    const float d = f16f(w.hd.x), dmin = f16f(w.hd.x >> 16);
+    return (d * scl) * (x.sx[0] * limbs_to_f(Al, Bl, Cl)) - (dmin * ml) * x.s[0] +
+           (d * sch) * (x.sx[1] * limbs_to_f(Ah, Bh, Ch)) - (dmin * mh) * x.s[1];
+}
+
+__device__ __forceinline__ float udot(const UW<T_Q5_K> &w, const UX<T_Q5_K> &x)
+{
+    uint32_t q[8], qh[8];
+    u4_to(w.q0, q);
+    u4_to(w.q1, q + 4);
+    u4_to(w.h0, qh);
+    u4_to(w.h1, qh + 4);
+    int Al = 0, Bl = 0, Cl = 0, Ah = 0, Bh = 0, Ch = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t hb = qh[i] >> x.qsh;
+        const uint32_t lo = (q[i] & 0x0F0F0F0Fu) | ((hb & 0x01010101u) << 4);
+        const uint32_t hi = ((q[i] >> 4) & 0x0F0F0F0Fu) | ((hb & 0x02020202u) << 3);
+        Al = sdot4(lo, x.a[i], Al);
+        Bl = sdot4(lo, x.b[i], Bl);
+        Cl = sdot4(lo, x.c[i], Cl);
+        Ah = sdot4(hi, x.a[8 + i], Ah);
+        Bh = sdot4(hi, x.b[8 + i], Bh);
+        Ch = sdot4(hi, x.c[8 + i], Ch);
+    }
+    float scl, sch, ml, mh;
+    k4_scales(w.hd, x.sh, x.high, scl, sch, ml, mh);
+    const float d = f16f(w.hd.x), dmin = f16f(w.hd.x >> 16);
+    return (d * scl) * (x.sx[0] * limbs_to_f(Al, Bl, Cl)) - (dmin * ml) * x.s[0] +
+           (d * sch) * (x.sx[1] * limbs_to_f(Ah, Bh, Ch)) - (dmin * mh) * x.s[1];
+}
+
+__device__ __forceinline__ float udot(const UW<T_Q6_K> &w, const UX<T_Q6_K> &x)
+{
+    uint32_t p0[4], p1[4], qh[4];
+    u4_to(w.p0, p0);
+    u4_to(w.p1, p1);
+    u4_to(w.qh, qh);
+    int A[4] = {0, 0, 0, 0}, B[4] = {0, 0, 0, 0}, C[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t v[4] = {
+            (p0[i] & 0x0F0F0F0Fu) | ((qh[i] << 4) & 0x30303030u),
+            (p1[i] & 0x0F0F0F0Fu) | ((qh[i] << 2) & 0x30303030u),
+            ((p0[i] >> 4) & 0x0F0F0F0Fu) | (qh[i] & 0x30303030u),
+            ((p1[i] >> 4) & 0x0F0F0F0Fu) | ((qh[i] >> 2) & 0x30303030u),
+        };
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            A[r] = sdot4(v[r], x.a[4 * r + i], A[r]);
+            B[r] = sdot4(v[r], x.b[4 * r + i], B[r]);
+            C[r] = sdot4(v[r], x.c[4 * r + i], C[r]);
+        }
+    }
+    // scales[8n + h + {0,2,4,6}]: bytes h, h+2 of dwords sc.x (sc[8n..]) and sc.y
+    const int b0 = 8 * x.h, b2 = 8 * x.h + 16;
+    const float s0 = (float)(int8_t)(w.sc.x >> b0), s1 = (float)(int8_t)(w.sc.x >> b2);
+    const float s2 = (float)(int8_t)(w.sc.y >> b0), s3 = (float)(int8_t)(w.sc.y >> b2);
+    const float d = f16f(w.d);
+    float acc = s0 * (x.sx[0] * limbs_to_f(A[0], B[0], C[0]) - 32.0f * x.s[0]);
+    acc += s1 * (x.sx[1] * limbs_to_f(A[1], B[1], C[1]) - 32.0f * x.s[1]);
+    acc += s2 * (x.sx[2] * limbs_to_f(A[2], B[2], C[2]) - 32.0f * x.s[2]);
+    acc += s3 * (x.sx[3] * limbs_to_f(A[3], B[3], C[3]) - 32.0f * x.s[3]);
+    return d * acc;
+}
+
+// Sum over the G lanes of a group; the group leader (gl == 0) gets the total.
+// Groups are consecutive lanes [grp*G, grp*G+G); any 1 <= G <= 64.
+__device__ __forceinline__ float group_sum(float v, int gl, int G)
+{
+    int off = 1;
+    while (off * 2 < G) off *= 2;
+    for (; off > 0; off >>= 1) {
+        const float o = __shfl_down(v, off);
+        if (gl + off < G) v += o;
+    }
+    return v;
+}
+
+}  // namespace styx

@@ -1,0 +1,27 @@
+// refk.h -- ids of the reference-interface kernels (kernels_ref.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace styx {
+
+enum RefKernel {
+    RK_TOPK = 1,
+    RK_MOE_REDUCE,
+    RK_GATHER,
+    RK_ATTN,
+    RK_MATVEC_STRIDED,
+    RK_ADD,
+    RK_AXPY_SIG,
+    RK_SWIGLU,
+    RK_RMS_NORM,
+    RK_MMV_BASE = 32,  // +0..3 mul_mat_vec_{q8_0,q4_k,q5_k,q6_k}, +4..7 the _id forms
+};
+
+// Launch reference kernel `kid` with resolved binding pointers, the raw
+// push-constant block, the reference grid and spec constants (id, value pairs).
+hipError_t refk_launch(hipStream_t st, int kid, void *const *ptr, const void *push, uint32_t gx,
+                       uint32_t gy, uint32_t gz, const uint32_t *spec, int n_spec);
+
+}  // namespace styx

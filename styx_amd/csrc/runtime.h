@@ -1,0 +1,43 @@
+// runtime.h -- host-side objects behind the C ABI handles.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../../include/styx_hip.h"
+
+struct styx_gpu {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string name;
+    uint64_t hbm = 0;
+    int live_children = 0;
+    bool closed = false;  // styx_gpu_free called while children were alive
+};
+
+struct styx_buf {
+    styx_gpu *gpu = nullptr;
+    void *ptr = nullptr;  // device-visible address
+    void *host = nullptr; // host address of a pinned buffer
+    uint64_t size = 0;
+    int kind = STYX_BUF_DEVICE;
+};
+
+namespace styx {
+
+// Thread-local error message helpers.  fail() records the message and
+// returns the status so callers can `return fail(...)`.
+int fail(int status, const std::string &msg);
+int hip_fail(hipError_t e, const char *what);
+void clear_error();
+// Drop one child of gpu; deletes the gpu if it was closed and this was the last.
+void gpu_release(styx_gpu *gpu);
+
+#define STYX_HIP(call)                                      \
+    do {                                                    \
+        hipError_t _e = (call);                             \
+        if (_e != hipSuccess) return ::styx::hip_fail(_e, #call); \
+    } while (0)
+
+}  // namespace styx
