@@ -167,15 +167,20 @@ int styx_op_moe_down_reduce(styx_gpu *gpu, int type_down, const styx_expert_src 
 /* Decode attention over the paged KV cache with fused per-head q/k RMSNorm,
  * NEOX rope and K/V append at *pos (attn_decode_f32.comp, moe.rs:1875-1964).
  * q [nh*hd], k/v [nkv*hd] raw projections; q_norm/k_norm [hd] or NULL;
- * inv_freq [hd/2] f64; kpool/vpool [pages][page_tokens][nkv*hd];
+ * rope [n_pos][hd/2][2] f64 (cos, sin) from styx_rope_table, n_pos > *pos;
+ * kpool/vpool [pages][page_tokens][nkv*hd];
  * page_table [ceil(n_ctx/page_tokens)]; part: styx_op_attn_part_floats(). */
 int styx_op_attn_decode(styx_gpu *gpu, const float *q, const float *k, const float *v,
                         const float *q_norm, const float *k_norm, float eps,
-                        const double *inv_freq, float *kpool, float *vpool,
+                        const double *rope, float *kpool, float *vpool,
                         const int32_t *page_table, int page_tokens, const int32_t *pos,
                         float *out, float *part, int nh, int nkv, int hd, int chunk,
                         int max_chunks, float scale);
 int64_t styx_op_attn_part_floats(int nh, int nkv, int hd, int max_chunks);
+/* Host-side NEOX rope table: out[p][i] = (cos, sin)(p * base^(-2i/hd)) in
+ * f64 for p < n_pos, i < hd/2 (crates/vk-backend/tests/ops2.rs:426-442).
+ * out holds n_pos * hd doubles.  Needs no GPU. */
+void styx_rope_table(float base, int hd, int n_pos, double *out);
 /* gather_slabs_f32 (shaders/gather_slabs_f32.comp:40-86): for slot s < k
  * with expert ids[s] != SKIP copy that expert's slab of each of the three
  * tensors into arena slot layer*k+s.  Slab sizes multiples of 16. */

@@ -76,6 +76,7 @@ def lib() -> C.CDLL:
             "styx_oracle_moe_block": (i, [vp, i, vp, vp, vp, vp, vp]),
             "styx_oracle_forward": (i, [vp, i, C.c_uint32, vp, vp, vp, vp]),
             "styx_oracle_argmax": (C.c_uint32, [vp, i]),
+            "styx_oracle_gather_slabs": (None, [vp, vp, vp, vp, vp, i, i]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(_lib, name)

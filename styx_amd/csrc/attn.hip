@@ -4,15 +4,21 @@
 // per query head, GQA kvh = h / gqa, K/V rows [t][kv_dim]) with the per-head
 // q/k RMSNorm (crates/model/src/moe.rs:1875-1913), NEOX rope
 // (crates/vk-backend/tests/ops2.rs:426-442, angle in f64) and the KV append
-// at the current position (moe.rs:1932-1943) fused in front.
+// at the current position (moe.rs:1932-1943) fused in front.  The rope
+// factors come from a table of (cos, sin) pairs in f64 per position, built
+// on the host with the same formula (styx_rope_table), so the device does
+// the rotation in f64 without evaluating a single trigonometric function.
 //
-// Layout: one workgroup per (context chunk, kv head).  It loads its K/V rows
-// once for all gqa query heads of that kv head (the reference re-reads them
-// per query head), streams them through LDS in 32-token tiles with an online
-// softmax, and writes a partial (m, l, o); k_attn_combine merges the
-// partials in chunk order (a single active chunk writes the output itself).  The current position is read
-// from device memory, so a captured graph serves every step; chunks past the
-// context exit at once.
+// Layout: one workgroup per (context chunk, kv head) serves all gqa query
+// heads of that kv head, so each K/V row comes from HBM once (the reference
+// re-reads it per query head).  Its four waves split the query heads (and,
+// for gqa < 4, the chunk's 16-token tiles); each wave runs its own online
+// softmax over its tiles with no workgroup barrier until the end, where the
+// waves sharing heads merge their (m, l, o) in LDS and one partial per
+// (chunk, head) is written.  k_attn_combine merges the chunk partials of
+// each query head, writes the output and the activation limbs of the o-proj
+// input.  The current position is read from device memory, so a captured
+// graph serves every step; chunks past the context exit at once.
 #include "kernels.h"
 #include "qdot.h"
 
@@ -21,8 +27,8 @@
 namespace styx {
 
 constexpr int AT_WG = 256;
-constexpr int TT = 32;
-constexpr int MAX_OWN = 8;  // outputs (g, i) per thread: gqa*hd <= 2048
+constexpr int AT_WAVES = AT_WG / 64;
+constexpr int TILE = 16;
 
 __device__ __forceinline__ int64_t kv_off(const AttnArgs &a, int t, int kvh, int kv_dim)
 {
@@ -30,195 +36,377 @@ __device__ __forceinline__ int64_t kv_off(const AttnArgs &a, int t, int kvh, int
     return ((int64_t)page * a.page_tokens + (t % a.page_tokens)) * kv_dim + (int64_t)kvh * a.hd;
 }
 
-// RMSNorm(hd) * w, then NEOX rope at pos, of one head held in src; one wave.
-__device__ inline void norm_rope_head(const float *src, const float *w, float eps, int hd,
-                                      const double *inv_freq, int pos, float *dst)
+// One head's RMSNorm(hd) * w and NEOX rope at pos, split into a load phase
+// (every operand of the head issued at once) and a compute phase, so a wave
+// can have all its heads' loads in flight together.  Lane l owns the rope
+// pairs (i, i + hd/2) for i = l + 64 j, j < PPL; cs points at the (cos, sin)
+// row of the position.
+template <int PPL> struct HeadIn {
+    float x0[PPL], x1[PPL], w0[PPL], w1[PPL];
+};
+
+template <int PPL>
+__device__ __forceinline__ void head_load(HeadIn<PPL> &h, const float *src, const float *w, int hd)
 {
     const int lane = threadIdx.x & 63, half = hd / 2;
-    float ss = 0.0f;
-    for (int i = lane; i < hd; i += 64) ss += src[i] * src[i];
-    ss = wave_sum(ss);
-    const float scale = w ? 1.0f / sqrtf(ss / (float)hd + eps) : 1.0f;
-    for (int i = lane; i < half; i += 64) {
-        float x0 = src[i], x1 = src[i + half];
-        if (w) {
-            x0 = (x0 * scale) * w[i];
-            x1 = (x1 * scale) * w[i + half];
-        }
-        const double th = (double)pos * inv_freq[i];
-        const double sn = sin(th), cs = cos(th);
-        dst[i] = (float)((double)x0 * cs - (double)x1 * sn);
-        dst[i + half] = (float)((double)x0 * sn + (double)x1 * cs);
+#pragma unroll
+    for (int j = 0; j < PPL; j++) {
+        const int i = lane + 64 * j;
+        const bool ok = i < half;
+        h.x0[j] = ok ? src[i] : 0.0f;
+        h.x1[j] = ok ? src[i + half] : 0.0f;
+        h.w0[j] = (ok && w) ? w[i] : 1.0f;
+        h.w1[j] = (ok && w) ? w[i + half] : 1.0f;
     }
 }
 
-__global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a)
+template <int PPL>
+__device__ __forceinline__ void cs_load(double2 *cs, const double2 *row, int hd)
 {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < PPL; j++) {
+        const int i = lane + 64 * j;
+        cs[j] = i < hd / 2 ? row[i] : make_double2(1.0, 0.0);
+    }
+}
+
+template <int PPL>
+__device__ __forceinline__ void head_finish(const HeadIn<PPL> &h, const double2 *cs, bool norm,
+                                            float eps, int hd, float *dst)
+{
+    const int lane = threadIdx.x & 63, half = hd / 2;
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PPL; j++) ss += h.x0[j] * h.x0[j] + h.x1[j] * h.x1[j];
+    ss = wave_sum(ss);
+    const float scale = norm ? 1.0f / sqrtf(ss / (float)hd + eps) : 1.0f;
+#pragma unroll
+    for (int j = 0; j < PPL; j++) {
+        const int i = lane + 64 * j;
+        if (i >= half) continue;
+        float x0 = h.x0[j], x1 = h.x1[j];
+        if (norm) {
+            x0 = (x0 * scale) * h.w0[j];
+            x1 = (x1 * scale) * h.w1[j];
+        }
+        const double c = cs[j].x, sn = cs[j].y;
+        dst[i] = (float)((double)x0 * c - (double)x1 * sn);
+        dst[i + half] = (float)((double)x0 * sn + (double)x1 * c);
+    }
+}
+
+__device__ __forceinline__ float max16(float v)
+{
+    for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float sum16(float v)
+{
+    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Wave roles: the four waves of a workgroup split the gqa query heads into
+// NHG head groups of HPW heads (HPW <= MAXH) and, when fewer than four
+// groups exist, also split the chunk's 16-token tiles NTS = 4 / NHG ways.
+// EPL = hd / 64 output values per lane.  Every global load of a tile (its
+// K quarter-rows and all 16 V rows) is issued before any of it is used; the
+// first tile's loads go out before the q heads are normalised and rotated,
+// and each next tile's page-table entries while the current one is computed.
+template <int MAXH, int EPL>
+__global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
+{
+    constexpr int HD = 64 * EPL, PPL = (HD / 2 + 63) / 64, SEG = HD / 4;
     const int c = blockIdx.x, kvh = blockIdx.y;
     const int pos = *a.pos, n_t = pos + 1;
     const int t0 = c * a.chunk;
     if (t0 >= n_t) return;
     const int t1 = min(n_t, t0 + a.chunk);
-    const int gqa = a.nh / a.nkv, hd = a.hd, kv_dim = a.nkv * hd, kp = hd + 4;
-    const int n_active = (n_t + a.chunk - 1) / a.chunk;
+    const int gqa = a.nh / a.nkv, kv_dim = a.nkv * HD;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nts = AT_WAVES / nhg, hg = wave % nhg, ts = wave / nhg;
+    const int g0 = hg * hpw;  // first head (within the kv head's group) of this wave
+    const int tl = lane & (TILE - 1), qd = lane >> 4;  // token in tile, quarter of hd
 
     extern __shared__ __align__(16) float sm[];
-    float *qs = sm;                   // [gqa][hd]
-    float *kt = qs + gqa * hd;        // [TT][hd+4]
-    float *vt = kt + TT * kp;         // [TT][hd]
-    float *sc = vt + TT * hd;         // [gqa][TT]
-    float *knew = sc + gqa * TT;      // [hd]
-    float *vnew = knew + hd;          // [hd]
-    float *mrun = vnew + hd;          // [gqa]
-    float *lrun = mrun + 16;          // [gqa]
-    float *corr = lrun + 16;          // [gqa]
+    // per wave: q [MAXH][HD] | knew [HD] | vnew [HD] | p [MAXH][TILE]
+    constexpr int PWF = MAXH * HD + 2 * HD + MAXH * TILE;
+    float *qs = sm + wave * PWF;
+    float *knew = qs + MAXH * HD;
+    float *vnew = knew + HD;
+    float *my_p = vnew + HD;
 
-    for (int g = wave; g < gqa; g += AT_WG / 64)
-        norm_rope_head(a.q + (int64_t)(kvh * gqa + g) * hd, a.q_norm, a.eps, hd, a.inv_freq, pos,
-                       qs + g * hd);
+    // prologue loads, all independent: this wave's q heads, the rope row,
+    // the new k/v head (in the chunk that holds pos), the first tile's
+    // page-table entry
     const bool owns_pos = t1 == n_t;
-    if (owns_pos && wave == 0) {
-        norm_rope_head(a.k + (int64_t)kvh * hd, a.k_norm, a.eps, hd, a.inv_freq, pos, knew);
-        for (int i = lane; i < hd; i += 64) vnew[i] = a.v[(int64_t)kvh * hd + i];
-    }
-    if (threadIdx.x < 16) {
-        mrun[threadIdx.x] = -INFINITY;
-        lrun[threadIdx.x] = 0.0f;
-    }
-    __syncthreads();
-    if (owns_pos && wave == 0) {
-        const int64_t o = kv_off(a, pos, kvh, kv_dim);
-        for (int i = lane; i < hd; i += 64) {
-            a.kpool[o + i] = knew[i];
-            a.vpool[o + i] = vnew[i];
-        }
-    }
-
-    const int nown = (gqa * hd + AT_WG - 1) / AT_WG;
-    float acc[MAX_OWN];
+    HeadIn<PPL> hq[MAXH], hk;
+    double2 cs[PPL];
+    cs_load<PPL>(cs, a.rope + (int64_t)pos * (HD / 2), HD);
 #pragma unroll
-    for (int j = 0; j < MAX_OWN; j++) acc[j] = 0.0f;
+    for (int i = 0; i < MAXH; i++)
+        if (i < hpw) head_load<PPL>(hq[i], a.q + (int64_t)(kvh * gqa + g0 + i) * HD, a.q_norm, HD);
+    float vn[EPL];
+    if (owns_pos) {
+        head_load<PPL>(hk, a.k + (int64_t)kvh * HD, a.k_norm, HD);
+#pragma unroll
+        for (int e = 0; e < EPL; e++) vn[e] = a.v[(int64_t)kvh * HD + lane * EPL + e];
+    }
+    int tb = t0 + ts * TILE;
+    int64_t row = 0;  // pool offset of token tb + tl's row (this kv head)
+    if (tb + tl < t1) row = kv_off(a, tb + tl, kvh, kv_dim);
 
-    const int hd4 = hd / 4;
-    for (int ts = t0; ts < t1; ts += TT) {
-        const int nt = min(TT, t1 - ts);
-        for (int idx = threadIdx.x; idx < nt * hd4; idx += AT_WG) {
-            const int row = idx / hd4, c4 = idx - row * hd4, t = ts + row;
-            float4 kv, vv;
-            if (t == pos) {
-                kv = *(const float4 *)(knew + 4 * c4);
-                vv = *(const float4 *)(vnew + 4 * c4);
-            } else {
-                const int64_t o = kv_off(a, t, kvh, kv_dim) + 4 * c4;
-                kv = *(const float4 *)(a.kpool + o);
-                vv = *(const float4 *)(a.vpool + o);
-            }
-            *(float4 *)(kt + row * kp + 4 * c4) = kv;
-            *(float4 *)(vt + row * hd + 4 * c4) = vv;
+    float m_run[MAXH], l_run[MAXH], o[MAXH][EPL];
+#pragma unroll
+    for (int g = 0; g < MAXH; g++) {
+        m_run[g] = -INFINITY;
+        l_run[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) o[g][e] = 0.0f;
+    }
+    bool first = true;
+    for (; tb < t1; tb += nts * TILE) {
+        const int t = tb + tl;
+        const bool tv = t < t1;
+        const int nt = min(TILE, t1 - tb);
+        // all of the tile's loads: this lane's K quarter-row, every V row
+        float4 kq[SEG / 4];
+#pragma unroll
+        for (int j = 0; j < SEG / 4; j++)
+            kq[j] = tv ? *(const float4 *)(a.kpool + row + qd * SEG + 4 * j)
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float vv[TILE][EPL];
+#pragma unroll
+        for (int i = 0; i < TILE; i++) {
+            const int64_t ri = __shfl(row, i);  // token tb+i's row, held by lane i
+#pragma unroll
+            for (int e = 0; e < EPL; e++)
+                vv[i][e] = i < nt ? a.vpool[ri + lane * EPL + e] : 0.0f;
         }
-        __syncthreads();
-        for (int p = threadIdx.x; p < gqa * nt; p += AT_WG) {
-            const int g = p / nt, t = p - g * nt;
-            const float4 *qv = (const float4 *)(qs + g * hd);
-            const float4 *kr = (const float4 *)(kt + t * kp);
-            float d = 0.0f;
-            for (int i = 0; i < hd4; i++) {
-                const float4 x = qv[i], y = kr[i];
-                d += x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
+        // next tile's page-table entry while this one is computed
+        const int tn = tb + nts * TILE;
+        if (tn + tl < t1) row = kv_off(a, tn + tl, kvh, kv_dim);
+        if (first) {
+            // q heads (and the new k head) normalised and rotated into this
+            // wave's LDS while the tile's loads are in flight
+#pragma unroll
+            for (int i = 0; i < MAXH; i++)
+                if (i < hpw) head_finish<PPL>(hq[i], cs, a.q_norm != nullptr, a.eps, HD, qs + i * HD);
+            if (owns_pos) {
+                head_finish<PPL>(hk, cs, a.k_norm != nullptr, a.eps, HD, knew);
+#pragma unroll
+                for (int e = 0; e < EPL; e++) vnew[lane * EPL + e] = vn[e];
             }
-            sc[g * TT + t] = d * a.scale;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            first = false;
         }
-        __syncthreads();
-        for (int g = wave; g < gqa; g += AT_WG / 64) {
-            const float s = lane < nt ? sc[g * TT + lane] : -INFINITY;
-            const float mt = wave_max(s);
-            const float m_old = mrun[g], m_new = fmaxf(m_old, mt);
-            const float p = lane < nt ? expf(s - m_new) : 0.0f;
-            const float ps = wave_sum(p);
-            if (lane < nt) sc[g * TT + lane] = p;
+        // the token at pos comes from LDS (its pool row is written below)
+        if (t == pos) {
+#pragma unroll
+            for (int j = 0; j < SEG / 4; j++) kq[j] = *(const float4 *)(knew + qd * SEG + 4 * j);
+        }
+        if (pos >= tb && pos < tb + TILE) {
+            const int ip = pos - tb;
+#pragma unroll
+            for (int i = 0; i < TILE; i++)
+                if (i == ip) {
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) vv[i][e] = vnew[lane * EPL + e];
+                }
+        }
+        // scores: lane (tl, qd) dots quarter qd of K row tb+tl with each head
+        float s[MAXH];
+#pragma unroll
+        for (int g = 0; g < MAXH; g++) {
+            s[g] = 0.0f;
+            if (g < hpw) {
+#pragma unroll
+                for (int j = 0; j < SEG / 4; j++) {
+                    const float4 qv = *(const float4 *)(qs + g * HD + qd * SEG + 4 * j);
+                    s[g] += qv.x * kq[j].x + qv.y * kq[j].y + qv.z * kq[j].z + qv.w * kq[j].w;
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < MAXH; g++) {
+            if (g >= hpw) break;
+            float v = s[g] + __shfl_xor(s[g], 16);
+            v += __shfl_xor(v, 32);
+            v = tv ? v * a.scale : -INFINITY;
+            const float m_new = fmaxf(m_run[g], max16(v));
+            const float p = tv ? expf(v - m_new) : 0.0f;
+            const float corr = expf(m_run[g] - m_new);
+            l_run[g] = l_run[g] * corr + sum16(p);
+            m_run[g] = m_new;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) o[g][e] *= corr;
+            if (qd == 0) my_p[g * TILE + tl] = p;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // o[g][e] += sum_t p[g][t] * V[t][e] for this lane's EPL values
+#pragma unroll
+        for (int g = 0; g < MAXH; g++) {
+            if (g < hpw) {
+#pragma unroll
+                for (int tt = 0; tt < TILE; tt += 4) {
+                    const float4 p4 = *(const float4 *)(my_p + g * TILE + tt);
+#pragma unroll
+                    for (int e = 0; e < EPL; e++)
+                        o[g][e] += p4.x * vv[tt][e] + p4.y * vv[tt + 1][e] + p4.z * vv[tt + 2][e] +
+                                   p4.w * vv[tt + 3][e];
+                }
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if (owns_pos && wave == 0) {
+        const int64_t po = kv_off(a, pos, kvh, kv_dim);
+        for (int e = lane; e < HD; e += 64) {
+            a.kpool[po + e] = knew[e];
+            a.vpool[po + e] = vnew[e];
+        }
+    }
+
+    const int ps = HD + 2;
+    float *part = a.part + ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
+    if (nts == 1) {
+        // every wave owns distinct heads: its running state is the partial
+#pragma unroll
+        for (int g = 0; g < MAXH; g++) {
+            if (g >= hpw) break;
+            float *pg = part + (g0 + g) * ps;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) pg[lane * EPL + e] = o[g][e];
             if (lane == 0) {
-                const float cr = expf(m_old - m_new);
-                corr[g] = cr;
-                lrun[g] = lrun[g] * cr + ps;
-                mrun[g] = m_new;
+                pg[HD] = m_run[g];
+                pg[HD + 1] = l_run[g];
             }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < MAX_OWN; j++) {
-            if (j >= nown) break;
-            const int o = threadIdx.x + j * AT_WG;
-            if (o >= gqa * hd) break;
-            const int g = o / hd, i = o - g * hd;
-            float v = acc[j] * corr[g];
-            for (int t = 0; t < nt; t++) v += sc[g * TT + t] * vt[t * hd + i];
-            acc[j] = v;
-        }
-        __syncthreads();
-    }
-
-    if (n_active == 1) {
-#pragma unroll
-        for (int j = 0; j < MAX_OWN; j++) {
-            const int o = threadIdx.x + j * AT_WG;
-            if (j >= nown || o >= gqa * hd) break;
-            const int g = o / hd;
-            a.out[(int64_t)kvh * gqa * hd + o] = acc[j] * (1.0f / lrun[g]);
         }
         return;
     }
-    const int ps = hd + 2;
-    float *part = a.part + ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
+    // merge the NTS waves of each head group: M = max m_w, L = sum l_w
+    // e^(m_w-M), O likewise (LDS past the per-wave areas)
+    float *mo = sm + AT_WAVES * PWF;          // [AT_WAVES][MAXH][HD]
+    float *mm = mo + AT_WAVES * MAXH * HD;    // [AT_WAVES][MAXH]
+    float *ml = mm + AT_WAVES * MAXH;         // [AT_WAVES][MAXH]
 #pragma unroll
-    for (int j = 0; j < MAX_OWN; j++) {
-        const int o = threadIdx.x + j * AT_WG;
-        if (j >= nown || o >= gqa * hd) break;
-        const int g = o / hd, i = o - g * hd;
-        part[g * ps + i] = acc[j];
+    for (int g = 0; g < MAXH; g++) {
+        if (g >= hpw) break;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) mo[(wave * MAXH + g) * HD + lane * EPL + e] = o[g][e];
+        if (lane == 0) {
+            mm[wave * MAXH + g] = m_run[g];
+            ml[wave * MAXH + g] = l_run[g];
+        }
     }
-    if (threadIdx.x < gqa) {
-        part[threadIdx.x * ps + hd] = mrun[threadIdx.x];
-        part[threadIdx.x * ps + hd + 1] = lrun[threadIdx.x];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < gqa * HD; idx += AT_WG) {
+        const int gg = idx / HD, e = idx - gg * HD;
+        const int hgi = gg / hpw, gi = gg - hgi * hpw;  // head group, head within it
+        float M = -INFINITY;
+        for (int w = 0; w < nts; w++) M = fmaxf(M, mm[(w * nhg + hgi) * MAXH + gi]);
+        float O = 0.0f, L = 0.0f;
+        for (int w = 0; w < nts; w++) {
+            const int wi = (w * nhg + hgi) * MAXH + gi;
+            const float f = expf(mm[wi] - M);
+            O += mo[wi * HD + e] * f;
+            L += ml[wi] * f;
+        }
+        part[gg * ps + e] = O;
+        if (e == 0) {
+            part[gg * ps + HD] = M;
+            part[gg * ps + HD + 1] = L;
+        }
     }
 }
 
 // Merge the per-chunk partials (m, l, o) of one query head in chunk order:
-// M = max m_c, L = sum l_c e^(m_c-M), out = sum o_c e^(m_c-M) / L.
+// M = max m_c, L = sum l_c e^(m_c-M), out = sum o_c e^(m_c-M) / L; then the
+// limbs of this head's slice of the output.
 __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a)
 {
+    extern __shared__ __align__(16) float xs[];  // [hd] output | [max_chunks] factors
+    __shared__ float red[16];
+    __shared__ float s_L;
     const int h = blockIdx.x, gqa = a.nh / a.nkv, hd = a.hd, ps = hd + 2;
     const int n_t = *a.pos + 1;
     const int n_active = (n_t + a.chunk - 1) / a.chunk;
-    if (n_active == 1) return;  // the single chunk wrote the output itself
     const int kvh = h / gqa, g = h - kvh * gqa;
     const float *pk = a.part + (int64_t)kvh * a.max_chunks * gqa * ps + (int64_t)g * ps;
+    float *fc = xs + hd;
+    // chunk statistics in parallel: M, then each chunk's factor e^(m_c - M)
+    float mloc = -INFINITY;
+    for (int cc = threadIdx.x; cc < n_active; cc += blockDim.x) {
+        const float m = pk[(int64_t)cc * gqa * ps + hd];
+        fc[cc] = m;
+        mloc = fmaxf(mloc, m);
+    }
+    mloc = wave_max(mloc);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mloc;
+    __syncthreads();
+    float M = red[0];
+    for (int w = 1; w < (int)blockDim.x / 64; w++) M = fmaxf(M, red[w]);
+    float lloc = 0.0f;
+    for (int cc = threadIdx.x; cc < n_active; cc += blockDim.x) {
+        const float f = expf(fc[cc] - M);
+        fc[cc] = f;
+        lloc += pk[(int64_t)cc * gqa * ps + hd + 1] * f;
+    }
+    const float L = block_sum(lloc, red);
     for (int i = threadIdx.x; i < hd; i += blockDim.x) {
-        float M = -INFINITY;
-        for (int cc = 0; cc < n_active; cc++) M = fmaxf(M, pk[(int64_t)cc * gqa * ps + hd]);
-        float L = 0.0f, O = 0.0f;
-        for (int cc = 0; cc < n_active; cc++) {
-            const float *pp = pk + (int64_t)cc * gqa * ps;
-            const float f = expf(pp[hd] - M);
-            L += pp[hd + 1] * f;
-            O += pp[i] * f;
-        }
-        a.out[(int64_t)h * hd + i] = O / L;
+        float O = 0.0f;
+#pragma unroll 8
+        for (int cc = 0; cc < n_active; cc++) O += pk[(int64_t)cc * gqa * ps + i] * fc[cc];
+        const float v = O / L;
+        a.out[(int64_t)h * hd + i] = v;
+        xs[i] = v;
+    }
+    if (!a.xq.A) return;
+    __syncthreads();
+    xq_build(xs, nullptr, 0.0f, false, hd, xq_shift(a.xq, h * hd), red, nullptr);
+}
+
+template <int MAXH>
+static void launch_k_attn(hipStream_t st, const AttnArgs &a, int nhg, int hpw)
+{
+    const dim3 grid(a.max_chunks, a.nkv);
+    const size_t lds = sizeof(float) * (AT_WAVES * ((size_t)MAXH * a.hd + 2 * a.hd + MAXH * TILE) +
+                                        (size_t)AT_WAVES * MAXH * a.hd + 2 * AT_WAVES * MAXH);
+    switch (a.hd) {
+    case 64: hipLaunchKernelGGL((k_attn<MAXH, 1>), grid, dim3(AT_WG), lds, st, a, nhg, hpw); break;
+    case 128: hipLaunchKernelGGL((k_attn<MAXH, 2>), grid, dim3(AT_WG), lds, st, a, nhg, hpw); break;
+    default: hipLaunchKernelGGL((k_attn<MAXH, 4>), grid, dim3(AT_WG), lds, st, a, nhg, hpw); break;
     }
 }
 
 hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
 {
     const int gqa = a.nkv > 0 ? a.nh / a.nkv : 0;
-    if (gqa < 1 || gqa > 16 || a.nh % a.nkv || a.hd % 4 || a.hd > 256 ||
-        gqa * a.hd > MAX_OWN * AT_WG || a.chunk % TT || a.page_tokens % TT)
+    if (gqa < 1 || gqa > 16 || a.nh % a.nkv || (a.hd != 64 && a.hd != 128 && a.hd != 256) ||
+        a.chunk < TILE || a.chunk % TILE || a.page_tokens < 1 || a.max_chunks < 1)
         return hipErrorInvalidValue;
-    const size_t lds =
-        sizeof(float) * ((size_t)gqa * a.hd + TT * (a.hd + 4) + TT * a.hd + gqa * TT + 2 * a.hd + 48);
-    hipLaunchKernelGGL(k_attn, dim3(a.max_chunks, a.nkv), dim3(AT_WG), lds, st, a);
+    // head groups: the largest of 4, 2, 1 dividing gqa
+    const int nhg = gqa % 4 == 0 ? 4 : gqa % 2 == 0 ? 2 : 1;
+    const int hpw = gqa / nhg;
+    if (hpw <= 1)
+        launch_k_attn<1>(st, a, nhg, hpw);
+    else if (hpw <= 2)
+        launch_k_attn<2>(st, a, nhg, hpw);
+    else if (hpw <= 4)
+        launch_k_attn<4>(st, a, nhg, hpw);
+    else
+        return hipErrorInvalidValue;  // gqa of 5, 7, 9.. above 4 heads per wave
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.max_chunks == 1) return e;
-    hipLaunchKernelGGL(k_attn_combine, dim3(a.nh), dim3(std::min(256, a.hd)), 0, st, a);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.nh), dim3(std::max(64, std::min(256, a.hd))),
+                       (size_t)(a.hd + a.max_chunks) * 4, st, a);
     return hipGetLastError();
 }
 

@@ -1,6 +1,8 @@
 // capi.cpp -- C ABI: device, buffers, transfers and the hot-path ops.
 // (crates/vk-backend/src/lib.rs replacement; see include/styx_hip.h)
+#include <cmath>
 #include <cstring>
+#include <vector>
 #include <string>
 
 #include "kernels.h"
@@ -29,6 +31,7 @@ static void gpu_destroy(styx_gpu *g)
     hipSetDevice(g->device);
     hipStreamSynchronize(g->stream);
     hipStreamDestroy(g->stream);
+    if (g->xq_scratch) hipFree(g->xq_scratch);
     delete g;
 }
 
@@ -67,6 +70,12 @@ int styx_gpu_new(int device, styx_gpu **out)
     if (e != hipSuccess) {
         delete g;
         return hip_fail(e, "hipStreamCreateWithFlags");
+    }
+    e = hipMalloc(&g->xq_scratch, xq_bytes(XQ_MAX));
+    if (e != hipSuccess) {
+        hipStreamDestroy(g->stream);
+        delete g;
+        return hip_fail(e, "hipMalloc(limb scratch)");
     }
     *out = g;
     return STYX_OK;
@@ -223,10 +232,13 @@ int styx_op_matvec(styx_gpu *g, int type, const void *w, int nrows, int ncols, c
                    const float *norm_w, float eps, float *y, int add)
 {
     OP_GPU(g);
-    if (nrows < 1 || ncols < 32 || ncols % 32 || ncols > 16384)
+    if (nrows < 1 || ncols < 32 || ncols % 32 || ncols > XQ_MAX)
         return fail(STYX_E_INVALID, "styx_op_matvec: bad shape");
+    if (!w || !x || !y) return fail(STYX_E_INVALID, "styx_op_matvec: NULL pointer");
+    const Xq q = xq_at(g->xq_scratch, ncols);
+    OP_RUN(launch_xq(g->stream, x, nullptr, norm_w, eps, ncols, q, nullptr), "styx_op_matvec");
     DenseSeg s{(const uint8_t *)w, y, nrows};
-    OP_RUN(launch_dense(g->stream, type, ncols, &s, 1, x, norm_w, eps, add), "styx_op_matvec");
+    OP_RUN(launch_dense(g->stream, type, ncols, &s, 1, q, add), "styx_op_matvec");
     return STYX_OK;
 }
 
@@ -291,7 +303,10 @@ int styx_op_moe_gate_up(styx_gpu *g, int tg, int tu, const styx_expert_src *gate
     OP_GPU(g);
     if (!gate || !up || !ids || !xn || !gu || k < 1 || k > 16 || F < 1)
         return fail(STYX_E_INVALID, "styx_op_moe_gate_up: bad argument");
-    OP_RUN(launch_moe_gate_up(g->stream, tg, tu, to_src(gate), to_src(up), ids, nullptr, xn, gu, H,
+    if (H < 32 || H % 32 || H > XQ_MAX) return fail(STYX_E_INVALID, "styx_op_moe_gate_up: bad H");
+    const Xq q = xq_at(g->xq_scratch, H);
+    OP_RUN(launch_xq(g->stream, xn, nullptr, nullptr, 0.0f, H, q, nullptr), "styx_op_moe_gate_up");
+    OP_RUN(launch_moe_gate_up(g->stream, tg, tu, to_src(gate), to_src(up), ids, nullptr, q, gu, H,
                               F, k),
            "styx_op_moe_gate_up");
     return STYX_OK;
@@ -304,15 +319,24 @@ int styx_op_moe_down_reduce(styx_gpu *g, int td, const styx_expert_src *down, co
     OP_GPU(g);
     if (!down || !ids || !weights || !gu || !x || !partial || k < 1 || k > 16)
         return fail(STYX_E_INVALID, "styx_op_moe_down_reduce: bad argument");
-    if (F > 8192) return fail(STYX_E_INVALID, "styx_op_moe_down_reduce: F > 8192");
-    OP_RUN(launch_moe_down(g->stream, td, to_src(down), ids, weights, gu, x, partial, H, F, k),
+    if (F > XQ_MAX / 2) return fail(STYX_E_INVALID, "styx_op_moe_down_reduce: F > 8192");
+    if (H < 32 || H % 32 || H > XQ_MAX)
+        return fail(STYX_E_INVALID, "styx_op_moe_down_reduce: bad H");
+    OP_RUN(launch_moe_down(g->stream, td, to_src(down), ids, gu, partial, H, F, k),
            "styx_op_moe_down_reduce");
+    ReduceArgs r{};
+    r.partial = partial;
+    r.k = k;
+    r.H = H;
+    r.wts = weights;
+    r.x = x;
+    OP_RUN(launch_reduce_norm(g->stream, r), "styx_op_moe_down_reduce");
     return STYX_OK;
 }
 
 int styx_op_attn_decode(styx_gpu *g, const float *q, const float *k, const float *v,
                         const float *q_norm, const float *k_norm, float eps,
-                        const double *inv_freq, float *kpool, float *vpool,
+                        const double *rope, float *kpool, float *vpool,
                         const int32_t *page_table, int page_tokens, const int32_t *pos,
                         float *out, float *part, int nh, int nkv, int hd, int chunk,
                         int max_chunks, float scale)
@@ -325,7 +349,7 @@ int styx_op_attn_decode(styx_gpu *g, const float *q, const float *k, const float
     a.q_norm = q_norm;
     a.k_norm = k_norm;
     a.eps = eps;
-    a.inv_freq = inv_freq;
+    a.rope = (const double2 *)rope;
     a.kpool = kpool;
     a.vpool = vpool;
     a.page_table = page_table;
@@ -341,6 +365,22 @@ int styx_op_attn_decode(styx_gpu *g, const float *q, const float *k, const float
     a.scale = scale;
     OP_RUN(launch_attn_decode(g->stream, a), "styx_op_attn_decode");
     return STYX_OK;
+}
+
+void styx_rope_table(float base, int hd, int n_pos, double *out)
+{
+    // theta_scale = base^(-2/hd), theta = pos * theta_scale^i, all in f64
+    // (crates/vk-backend/tests/ops2.rs:426-442)
+    if (!out || hd < 2 || n_pos < 1) return;
+    const double ts = std::pow((double)base, -2.0 / (double)hd);
+    std::vector<double> invf(hd / 2);
+    for (int i = 0; i < hd / 2; i++) invf[i] = std::pow(ts, (double)i);
+    for (int p = 0; p < n_pos; p++)
+        for (int i = 0; i < hd / 2; i++) {
+            const double th = (double)p * invf[i];
+            out[((size_t)p * (hd / 2) + i) * 2] = std::cos(th);
+            out[((size_t)p * (hd / 2) + i) * 2 + 1] = std::sin(th);
+        }
 }
 
 int64_t styx_op_attn_part_floats(int nh, int nkv, int hd, int max_chunks)

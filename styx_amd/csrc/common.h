@@ -96,4 +96,48 @@ __host__ __device__ inline int64_t split_index(const Split &s, int64_t nblocks, 
     return -1;
 }
 
+// ----------------------------------------------------------------------------
+// Activation limbs ("xq") of an n-value vector (n a multiple of 32): int8
+// planes A, B, C with x ~= sx * (A + (B + C/254)/254), sx = max|x|/127 per 32
+// values, plus s16 = plain f32 sums over runs of 16 values (for the
+// per-sub-block offset terms of the K-quants).  One contiguous buffer:
+//   A[n] | B[n] | C[n] | sx[n/32] f32 | s16[n/16] f32
+// Written once by the kernel that produces the vector, read by every matvec
+// lane that needs a slice of it.
+// ----------------------------------------------------------------------------
+constexpr int XQ_MAX = 16384;  // longest vector with limbs
+
+struct Xq {
+    int8_t *A, *B, *C;
+    float *sx, *s16;
+};
+
+__host__ __device__ inline size_t xq_bytes(int n)
+{
+    return (size_t)3 * n + (size_t)(n / 32) * 4 + (size_t)(n / 16) * 4;
+}
+
+__host__ __device__ inline Xq xq_at(void *base, int n)
+{
+    Xq q;
+    q.A = (int8_t *)base;
+    q.B = q.A + n;
+    q.C = q.B + n;
+    q.sx = (float *)((uint8_t *)base + 3 * (size_t)n);
+    q.s16 = q.sx + n / 32;
+    return q;
+}
+
+// The same vector seen from element e0 (a multiple of 32) on.
+__host__ __device__ inline Xq xq_shift(const Xq &q, int e0)
+{
+    Xq r;
+    r.A = q.A + e0;
+    r.B = q.B + e0;
+    r.C = q.C + e0;
+    r.sx = q.sx + e0 / 32;
+    r.s16 = q.s16 + e0 / 16;
+    return r;
+}
+
 }  // namespace styx

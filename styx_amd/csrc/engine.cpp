@@ -31,7 +31,6 @@
 #include "runtime.h"
 
 namespace styx {
-hipError_t launch_swiglu(hipStream_t st, const float *g, const float *u, float *h, int n);
 }  // namespace styx
 
 using namespace styx;
@@ -123,6 +122,7 @@ struct styx_moe {
           *xn = nullptr, *rlog = nullptr, *wts = nullptr, *gu = nullptr, *partial = nullptr,
           *logits = nullptr, *hidden = nullptr, *sh_g = nullptr, *sh_u = nullptr, *sh_y = nullptr,
           *attn_part = nullptr, *am_val = nullptr;
+    Xq xq_a{}, xq_o{}, xq_f{}, xq_sh{};  // limbs: layer input, attention out, ffn input, shexp hidden
     int32_t *ids = nullptr, *d_pos = nullptr;
     uint32_t *d_tok = nullptr, *am_idx = nullptr, *hist = nullptr;
     uint32_t *h_stage = nullptr;  // pinned: tok, pos
@@ -131,7 +131,7 @@ struct styx_moe {
     int32_t *d_pt = nullptr;
     std::vector<int32_t> h_pt;
     int pages_per_layer = 0, next_page = 0, chunk = 64, max_chunks = 1;
-    double *inv_freq = nullptr;
+    double *rope = nullptr;  // [n_ctx][hd/2] (cos, sin)
     // arena
     uint8_t *arena[3] = {nullptr, nullptr, nullptr};
     int64_t arena_slab[3] = {0, 0, 0};
@@ -256,6 +256,14 @@ int styx_moe::setup_runtime()
     if (int r = dalloc(&d_pos, 1)) return r;
     if (int r = dalloc(&d_tok, 1)) return r;
     if (int r = dalloc(&hist, (size_t)n_ctx + 1)) return r;
+    uint8_t *xqb = nullptr;
+    const size_t xa = (xq_bytes(H) + 255) & ~(size_t)255, xo = (xq_bytes(q_dim) + 255) & ~(size_t)255;
+    const size_t xs = (xq_bytes(std::max(Fsh, 32)) + 255) & ~(size_t)255;
+    if (int r = dalloc(&xqb, 2 * xa + xo + xs)) return r;
+    xq_a = xq_at(xqb, H);
+    xq_f = xq_at(xqb + xa, H);
+    xq_o = xq_at(xqb + 2 * xa, q_dim);
+    if (Fsh > 0) xq_sh = xq_at(xqb + 2 * xa + xo, Fsh);
     if (Fsh > 0) {
         if (int r = dalloc(&sh_g, Fsh)) return r;
         if (int r = dalloc(&sh_u, Fsh)) return r;
@@ -276,18 +284,21 @@ int styx_moe::setup_runtime()
     h_pt.assign((size_t)L * pages_per_layer, -1);
     STYX_HIP(hipMemsetAsync(d_pt, 0, sizeof(int32_t) * L * pages_per_layer, gpu->stream));
     next_page = 0;
-    // attention split: ~64 chunks over the full context, 32-token multiples
-    chunk = std::max(64, (n_ctx / 64 + 31) / 32 * 32);
+    // attention split: at most ~64 chunks over the full context, 16-token
+    // multiples, at least two tiles per chunk
+    chunk = std::max(32, (n_ctx / 64 + 15) / 16 * 16);
     max_chunks = (n_ctx + chunk - 1) / chunk;
     const int64_t pf = styx_op_attn_part_floats(nh, nkv, hd, max_chunks);
     if (int r = dalloc(&attn_part, (size_t)pf)) return r;
-    // rope table in f64: base^(-2i/hd) = theta_scale^i (ops2.rs:426-442)
-    std::vector<double> invf(hd / 2);
-    const double ts = std::pow((double)rope_base, -2.0 / (double)hd);
-    for (int i = 0; i < hd / 2; i++) invf[i] = std::pow(ts, (double)i);
-    if (int r = dalloc(&inv_freq, hd / 2)) return r;
-    STYX_HIP(hipMemcpyAsync(inv_freq, invf.data(), sizeof(double) * invf.size(),
-                            hipMemcpyHostToDevice, gpu->stream));
+    // rope factors in f64 for every position of the context (ops2.rs:426-442)
+    {
+        std::vector<double> cs((size_t)n_ctx * hd);
+        styx_rope_table(rope_base, hd, n_ctx, cs.data());
+        if (int r = dalloc(&rope, cs.size())) return r;
+        STYX_HIP(hipMemcpyAsync(rope, cs.data(), sizeof(double) * cs.size(), hipMemcpyHostToDevice,
+                                gpu->stream));
+        STYX_HIP(hipStreamSynchronize(gpu->stream));
+    }
     STYX_HIP(hipStreamSynchronize(gpu->stream));
     return STYX_OK;
 }
@@ -423,7 +434,10 @@ int styx_moe::enqueue_token(bool gen)
         stats[id].bytes += bytes;
         pending.push_back({id, {a, e}});
     };
-    CK(launch_embed(st, embd.type, embd.dev, V, H, d_tok, x));
+    // the first layer's q/k/v input: limbs of attn_norm_0(x) (or of the LM
+    // head's output_norm(x) for a model without layers)
+    const float *norm0 = L > 0 ? layers[0].attn_norm : out_norm;
+    CK(launch_embed(st, embd.type, embd.dev, V, H, d_tok, x, norm0, eps, xq_a));
     if (opts.record_hidden) CK(hipMemcpyAsync(hidden, x, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
     for (int l = 0; l < L; l++) {
         Layer &ly = layers[l];
@@ -431,15 +445,15 @@ int styx_moe::enqueue_token(bool gen)
         if (ly.wq.type == ly.wk.type && ly.wq.type == ly.wv.type) {
             DenseSeg s[3] = {{ly.wq.dev, q, ly.wq.rows}, {ly.wk.dev, kk, ly.wk.rows},
                              {ly.wv.dev, vv, ly.wv.rows}};
-            CK(launch_dense(st, ly.wq.type, H, s, 3, x, ly.attn_norm, eps, 0));
+            CK(launch_dense(st, ly.wq.type, H, s, 3, xq_a, 0));
         } else {
             DenseSeg a{ly.wq.dev, q, ly.wq.rows}, b{ly.wk.dev, kk, ly.wk.rows},
                 c{ly.wv.dev, vv, ly.wv.rows};
-            CK(launch_dense(st, ly.wq.type, H, &a, 1, x, ly.attn_norm, eps, 0));
-            CK(launch_dense(st, ly.wk.type, H, &b, 1, x, ly.attn_norm, eps, 0));
-            CK(launch_dense(st, ly.wv.type, H, &c, 1, x, ly.attn_norm, eps, 0));
+            CK(launch_dense(st, ly.wq.type, H, &a, 1, xq_a, 0));
+            CK(launch_dense(st, ly.wk.type, H, &b, 1, xq_a, 0));
+            CK(launch_dense(st, ly.wv.type, H, &c, 1, xq_a, 0));
         }
-        tend(e0, "qkv", (double)(ly.wq.bytes() + ly.wk.bytes() + ly.wv.bytes()) + 4.0 * H);
+        tend(e0, "qkv", (double)(ly.wq.bytes() + ly.wk.bytes() + ly.wv.bytes()) + xq_bytes(H));
         e0 = tstart();
         AttnArgs aa{};
         aa.q = q;
@@ -448,13 +462,14 @@ int styx_moe::enqueue_token(bool gen)
         aa.q_norm = ly.q_norm;
         aa.k_norm = ly.k_norm;
         aa.eps = eps;
-        aa.inv_freq = inv_freq;
+        aa.rope = (const double2 *)rope;
         aa.kpool = kpool;
         aa.vpool = vpool;
         aa.page_table = d_pt + (size_t)l * pages_per_layer;
         aa.page_tokens = KV_PAGE_TOKENS;
         aa.pos = d_pos;
         aa.out = attn;
+        aa.xq = xq_o;
         aa.part = attn_part;
         aa.nh = nh;
         aa.nkv = nkv;
@@ -466,8 +481,8 @@ int styx_moe::enqueue_token(bool gen)
         tend(e0, "attn", (double)(n_past + 1) * nkv * hd * 8.0);
         e0 = tstart();
         DenseSeg so{ly.wo.dev, x, H};
-        CK(launch_dense(st, ly.wo.type, q_dim, &so, 1, attn, nullptr, 0.0f, 1));
-        tend(e0, "o_proj", (double)ly.wo.bytes() + 4.0 * q_dim + 8.0 * H);
+        CK(launch_dense(st, ly.wo.type, q_dim, &so, 1, xq_o, 1));
+        tend(e0, "o_proj", (double)ly.wo.bytes() + xq_bytes(q_dim) + 8.0 * H);
         e0 = tstart();
         RouterArgs ra{};
         ra.x = x;
@@ -476,23 +491,23 @@ int styx_moe::enqueue_token(bool gen)
         ra.bias = ly.router_bias;
         ra.eps = eps;
         ra.xn = xn;
+        ra.xq = xq_f;
         ra.logits = rlog;
         ra.E = E;
         ra.H = H;
         ra.k = K;
         CK(launch_router(st, ra));
         tend(e0, "router", (double)E * H * 4 + 8.0 * H + 4.0 * E);
-        // top-k is recomputed by every consumer workgroup from the logits;
-        // gate_up's first workgroup publishes the id row and weights
+        // top-k ids are ranked by every consumer workgroup from the logits;
+        // gate_up's first workgroup publishes the id row, k_reduce_norm the
+        // weights
         Route rt{};
         rt.logits = rlog;
         rt.E = E;
         rt.k = K;
-        rt.renorm = norm_topk;
         rt.remap = ly.host_experts ? ly.remap_dev : nullptr;
         rt.arena_mode = ly.host_experts && opts.arena ? 1 : 0;
         rt.layer = 0;
-        rt.wts_out = wts + (size_t)l * 16;
         rt.ids_out = ids + (size_t)l * 64;
         const int32_t *lid = ids + (size_t)l * 64;
         ExpSrc sg{}, su{}, sd{};
@@ -518,41 +533,64 @@ int styx_moe::enqueue_token(bool gen)
             const uint8_t *src[3] = {ly.gate.host_dev, ly.up.host_dev, ly.down.host_dev};
             const int64_t sslab[3] = {ly.gate.slab, ly.up.slab, ly.down.slab};
             Route rg = rt;
-            rg.wts_out = nullptr;
             rg.ids_out = nullptr;
             CK(launch_gather(st, src, sslab, arena, arena_slab, nullptr, &rg, K));
             tend(e0, "gather", 0.0);
         }
         const double slabs_gu = (double)K * (ly.gate.slab + ly.up.slab);
         e0 = tstart();
-        CK(launch_moe_gate_up(st, ly.gate.type, ly.up.type, sg, su, nullptr, &rt, xn, gu, H, F, K));
-        tend(e0, "moe_gate_up", slabs_gu + 4.0 * H + 4.0 * K * F);
+        CK(launch_moe_gate_up(st, ly.gate.type, ly.up.type, sg, su, nullptr, &rt, xq_f, gu, H, F,
+                              K));
+        tend(e0, "moe_gate_up", slabs_gu + xq_bytes(H) + 4.0 * E + 4.0 * 2 * K * F);
         e0 = tstart();
-        CK(launch_moe_down(st, ly.down.type, sd, lid, wts + (size_t)l * 16, gu, x, partial, H, F,
-                           K));
-        tend(e0, "moe_down_reduce", (double)K * ly.down.slab + 4.0 * K * F + 8.0 * H);
+        CK(launch_moe_down(st, ly.down.type, sd, lid, gu, partial, H, F, K));
+        tend(e0, "moe_down", (double)K * ly.down.slab + 4.0 * 2 * K * F + 4.0 * K * H);
         if (ly.gsh.dev) {
+            e0 = tstart();
             DenseSeg s2[2] = {{ly.gsh.dev, sh_g, Fsh}, {ly.ush.dev, sh_u, Fsh}};
             if (ly.gsh.type == ly.ush.type) {
-                CK(launch_dense(st, ly.gsh.type, H, s2, 2, xn, nullptr, 0.0f, 0));
+                CK(launch_dense(st, ly.gsh.type, H, s2, 2, xq_f, 0));
             } else {
-                CK(launch_dense(st, ly.gsh.type, H, &s2[0], 1, xn, nullptr, 0.0f, 0));
-                CK(launch_dense(st, ly.ush.type, H, &s2[1], 1, xn, nullptr, 0.0f, 0));
+                CK(launch_dense(st, ly.gsh.type, H, &s2[0], 1, xq_f, 0));
+                CK(launch_dense(st, ly.ush.type, H, &s2[1], 1, xq_f, 0));
             }
-            CK(launch_swiglu(st, sh_g, sh_u, sh_g, Fsh));
+            CK(launch_xq(st, sh_g, sh_u, nullptr, 0.0f, Fsh, xq_sh, nullptr));
             DenseSeg sd2{ly.dsh.dev, sh_y, H};
-            CK(launch_dense(st, ly.dsh.type, Fsh, &sd2, 1, sh_g, nullptr, 0.0f, 0));
-            CK(launch_axpy_sig_dot(st, ly.gate_inp_sh, xn, sh_y, x, H));
+            CK(launch_dense(st, ly.dsh.type, Fsh, &sd2, 1, xq_sh, 0));
+            tend(e0, "shexp", (double)(ly.gsh.bytes() + ly.ush.bytes() + ly.dsh.bytes()));
         }
+        e0 = tstart();
+        ReduceArgs rd{};
+        rd.partial = partial;
+        rd.k = K;
+        rd.H = H;
+        rd.logits = rlog;
+        rd.E = E;
+        rd.renorm = norm_topk;
+        rd.ids = lid;
+        rd.wts_out = wts + (size_t)l * 16;
+        rd.x = x;
+        if (ly.gsh.dev) {
+            rd.sh_y = sh_y;
+            rd.sh_ginp = ly.gate_inp_sh;
+            rd.xn = xn;
+        }
+        rd.norm_w = l + 1 < L ? layers[l + 1].attn_norm : out_norm;
+        rd.eps = eps;
+        rd.xq = xq_a;
+        CK(launch_reduce_norm(st, rd));
+        tend(e0, "reduce_norm", 4.0 * K * H + 8.0 * H + 4.0 * E + xq_bytes(H));
         if (opts.record_hidden)
             CK(hipMemcpyAsync(hidden + (size_t)(l + 1) * H, x, sizeof(float) * H,
                               hipMemcpyDeviceToDevice, st));
     }
     hipEvent_t e0 = tstart();
     DenseSeg sh{head.dev, logits, V};
-    CK(launch_dense(st, head.type, H, &sh, 1, x, out_norm, eps, 0));
-    tend(e0, "lm_head", (double)head.bytes() + 4.0 * H + 4.0 * V);
+    CK(launch_dense(st, head.type, H, &sh, 1, xq_a, 0));
+    tend(e0, "lm_head", (double)head.bytes() + xq_bytes(H) + 4.0 * V);
+    e0 = tstart();
     CK(launch_argmax(st, logits, V, d_tok, am_val, am_idx, d_pos, gen ? 1 : 0, hist));
+    tend(e0, "argmax", 4.0 * V);
     return STYX_OK;
 }
 
@@ -796,9 +834,15 @@ int build_model(styx_moe *m, const styx_moe_synth_cfg &c, const std::vector<Tens
     if (m->K < 1 || m->K > MAX_TOPK) return fail(STYX_E_INVALID, "n_expert_used must be in [1, 16] (moe.rs:587)");
     if (m->E < m->K || m->E > MAX_EXPERTS) return fail(STYX_E_INVALID, "n_expert must be in [k, 512]");
     if (m->nkv < 1 || m->nh % m->nkv || m->nh / m->nkv > 16) return fail(STYX_E_INVALID, "bad head counts");
-    if (m->hd % 32 || m->hd > 256) return fail(STYX_E_INVALID, "head_dim must be a multiple of 32, <= 256");
-    if (m->H % 256) return fail(STYX_E_INVALID, "n_embd must be a multiple of 256");
+    if (m->hd != 64 && m->hd != 128 && m->hd != 256) return fail(STYX_E_INVALID, "head_dim must be 64, 128 or 256");
+    {
+        const int gqa = m->nh / m->nkv, nhg = gqa % 4 == 0 ? 4 : gqa % 2 == 0 ? 2 : 1;
+        if (gqa / nhg > 4) return fail(STYX_E_INVALID, "gqa must split into <= 4 heads per wave");
+    }
+    if (m->H % 256 || m->H > XQ_MAX) return fail(STYX_E_INVALID, "n_embd must be a multiple of 256, <= 16384");
+    if (m->nh * m->hd > XQ_MAX) return fail(STYX_E_INVALID, "n_head * head_dim must be <= 16384");
     if (m->F % 32 || m->F > 8192) return fail(STYX_E_INVALID, "expert FFN width must be a multiple of 32, <= 8192");
+    if (m->Fsh % 32 || m->Fsh > XQ_MAX) return fail(STYX_E_INVALID, "shared expert FFN width must be a multiple of 32, <= 16384");
 
     Builder b{m};
     int64_t mx = 0;

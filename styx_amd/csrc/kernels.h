@@ -30,18 +30,25 @@ struct DenseSeg {
     int rows;
 };
 
-// y_seg = W_seg . xn for up to 3 matrices sharing type/ncols, where
-// xn = norm_w ? rmsnorm(x)*norm_w : x.  add != 0 accumulates into y.
-hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, int nseg,
-                        const float *x, const float *norm_w, float eps, int add);
+// Limbs of x (u == null, norm_w == null), of rmsnorm(x) * norm_w, or of
+// swiglu(x, u) (u != null), n <= XQ_MAX; xn_out (optional) gets the f32
+// vector the limbs encode.  One workgroup.
+hipError_t launch_xq(hipStream_t st, const float *x, const float *u, const float *norm_w,
+                     float eps, int n, const Xq &q, float *xn_out);
 
-// Router for one layer (fused ffn_norm): writes xn (f32, for the expert
-// kernels) and logits[E].  launch_router_topk also runs the top-k into
-// weights[k] and the 64-int id row.
+// y_seg = W_seg . x for up to 3 matrices sharing type/ncols, x given by its
+// limbs.  add != 0 accumulates into y.
+hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, int nseg,
+                        const Xq &xq, int add);
+
+// Router for one layer (fused ffn_norm): writes logits[E] and, from its first
+// workgroup, xn (f32) and its limbs xq (if xq.A).  launch_router_topk also
+// runs the top-k into weights[k] and the 64-int id row.
 struct RouterArgs {
     const float *x, *norm_w, *W, *bias;
     float eps;
     float *xn, *logits, *wts;
+    Xq xq;
     int32_t *ids;
     const uint32_t *remap, *pmap;
     int E, H, k, renorm, arena_mode, layer;
@@ -49,15 +56,14 @@ struct RouterArgs {
 hipError_t launch_router(hipStream_t st, const RouterArgs &a);
 hipError_t launch_router_topk(hipStream_t st, const RouterArgs &a);
 
-// Top-k routing recomputed inside a consumer kernel from the router logits
-// (topk_softmax_f32 semantics); the first workgroup publishes weights and
-// the id row.
+// Top-k ids ranked inside a consumer kernel from the router logits
+// (topk_softmax_f32 selection order); the first workgroup publishes the id
+// row to ids_out.  The weights are formed by k_reduce_norm.
 struct Route {
     const float *logits;
-    int E, k, renorm;
+    int E, k;
     const uint32_t *remap, *pmap;
     int arena_mode, layer;
-    float *wts_out;
     int32_t *ids_out;
 };
 
@@ -66,21 +72,36 @@ hipError_t launch_topk_softmax(hipStream_t st, const float *logits, int n, int k
                                const uint32_t *remap, const uint32_t *pmap, int arena_mode,
                                int layer, float *wts, int32_t *ids);
 
-// gu[0][s] = Wg[e_s] xn, gu[1][s] = Wu[e_s] xn for the k routed slots;
-// routing from `route` (computed in-kernel) or, if null, the id row `ids`.
+// gu[0][s] = Wg[e_s] xn, gu[1][s] = Wu[e_s] xn for the k routed slots, xn
+// given by its limbs; routing from `route` (ranked in-kernel) or, if null,
+// the id row `ids`.
 hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, const ExpSrc &u,
-                              const int32_t *ids, const Route *route, const float *xn, float *gu,
+                              const int32_t *ids, const Route *route, const Xq &xq, float *gu,
                               int H, int F, int k);
 
-// partial[s] = Wd[e_s] swiglu(gu[0][s], gu[1][s]), then
-// x += sum_s w_s * partial[s] in fixed slot order (moe_reduce_f32.comp:11-13).
+// partial[s] = Wd[e_s] swiglu(gu[0][s], gu[1][s]) for the k routed slots.
 hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_t *ids,
-                           const float *wts, const float *gu, float *x, float *partial, int H,
-                           int F, int k);
+                           const float *gu, float *partial, int H, int F, int k);
 
-// Shared-expert gate: x += sigmoid(dot(ginp, xn)) * y  (axpy_sig_f32.comp).
-hipError_t launch_axpy_sig_dot(hipStream_t st, const float *ginp, const float *xn,
-                               const float *y, float *x, int n);
+// One workgroup: w_s from the logits and ids (topk_softmax_f32.comp:29-67)
+// or given; x += sum_s w_s partial[s] (moe_reduce_f32.comp:11-13, fixed slot
+// order); x += sigmoid(sh_ginp . xn) * sh_y if sh_y (axpy_sig_f32.comp);
+// then, if norm_w, the limbs of rmsnorm(x) * norm_w.
+struct ReduceArgs {
+    const float *partial;
+    int k, H;
+    const float *logits;   // null: weights from wts
+    int E, renorm;
+    const int32_t *ids;    // original expert per slot (id row)
+    const float *wts;
+    float *wts_out;        // optional: weights used
+    float *x;
+    const float *sh_y, *sh_ginp, *xn;
+    const float *norm_w;
+    float eps;
+    Xq xq;
+};
+hipError_t launch_reduce_norm(hipStream_t st, const ReduceArgs &a);
 
 // Decode attention over the paged f32 KV cache with fused per-head q/k
 // RMSNorm, NEOX rope and the K/V append at the current position.
@@ -88,21 +109,24 @@ struct AttnArgs {
     const float *q, *k, *v;          // raw projections
     const float *q_norm, *k_norm;    // [hd] or null
     float eps;
-    const double *inv_freq;          // [hd/2] base^(-2i/hd)
+    const double2 *rope;             // [n_pos][hd/2] (cos, sin) of pos * base^(-2i/hd)
     float *kpool, *vpool;            // [pages][page_tokens][kv_dim]
     const int32_t *page_table;       // logical page -> physical page
     int page_tokens;
     const int32_t *pos;              // device scalar
     float *out;                      // [nh*hd]
+    Xq xq;                           // optional limbs of out (o-proj input)
     float *part;                     // [nkv][max_chunks][gqa][hd+2]
-    int nh, nkv, hd, chunk, max_chunks;
+    int nh, nkv, hd, chunk, max_chunks;  // chunk: tokens per workgroup, multiple of 16
     float scale;
 };
 hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a);
 
-// x = dequant(token_embd[tok]) for the token held in device memory.
+// x = dequant(token_embd[tok]) for the token held in device memory, and
+// (if q.A) the limbs of rmsnorm(x) * norm_w (or of x if norm_w is null).
 hipError_t launch_embed(hipStream_t st, int t, const uint8_t *w, int64_t nrows, int ncols,
-                        const uint32_t *tok, float *x);
+                        const uint32_t *tok, float *x, const float *norm_w, float eps,
+                        const Xq &q);
 
 // Greedy argmax over logits (ties -> highest index, generate_moe.rs:29),
 // in two kernels through part_val/part_idx (64 entries each).  Writes

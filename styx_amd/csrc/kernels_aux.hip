@@ -82,19 +82,30 @@ hipError_t launch_dequant_rows(hipStream_t st, int t, const uint8_t *w, int64_t 
 }
 
 // ----------------------------------------------------------- embedding ----
-__global__ void k_embed(int t, const uint8_t *w, int64_t nrows, int ncols, const uint32_t *tok,
-                        float *x)
+// x = dequant(token_embd[tok]) and the limbs of rmsnorm(x) * norm_w for the
+// first layer's q/k/v matvec; one workgroup.
+__global__ void __launch_bounds__(256) k_embed(int t, const uint8_t *w, int64_t nrows, int ncols,
+                                               const uint32_t *tok, float *x, const float *nw,
+                                               float eps, Xq q)
 {
+    extern __shared__ __align__(16) float xs[];  // [ncols]
+    __shared__ float red[16];
     const int be = blk_elems(t), nb = ncols / be;
     const Mat m = mat_at(w, t, nrows * nb);
     const int64_t r = *tok;
-    for (int b = threadIdx.x; b < nb; b += blockDim.x) deq_block(t, m, r * nb + b, x + b * be);
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) deq_block(t, m, r * nb + b, xs + b * be);
+    __syncthreads();
+    for (int i = threadIdx.x; i < ncols; i += blockDim.x) x[i] = xs[i];
+    if (q.A) xq_build(xs, nw, eps, nw != nullptr, ncols, q, red, nullptr);
 }
 
 hipError_t launch_embed(hipStream_t st, int t, const uint8_t *w, int64_t nrows, int ncols,
-                        const uint32_t *tok, float *x)
+                        const uint32_t *tok, float *x, const float *norm_w, float eps,
+                        const Xq &q)
 {
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, t, w, nrows, ncols, tok, x);
+    if (ncols % 32 || ncols > XQ_MAX || ncols % blk_elems(t)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), (size_t)ncols * 4, st, t, w, nrows, ncols,
+                       tok, x, norm_w, eps, q);
     return hipGetLastError();
 }
 
@@ -190,19 +201,6 @@ hipError_t launch_argmax(hipStream_t st, const float *v, int n, uint32_t *out_to
     return hipGetLastError();
 }
 
-// swiglu_f32 split mode (crates/vk-backend/tests/ops2.rs:305-309): h = g/(1+e^-g)*u
-__global__ void k_swiglu(const float *g, const float *u, float *h, int n)
-{
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) h[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
-}
-
-hipError_t launch_swiglu(hipStream_t st, const float *g, const float *u, float *h, int n)
-{
-    hipLaunchKernelGGL(k_swiglu, dim3((n + 255) / 256), dim3(256), 0, st, g, u, h, n);
-    return hipGetLastError();
-}
-
 // -------------------------------------------------------------- gather ----
 // shaders/gather_slabs_f32.comp:40-86: slot s with expert e != SKIP copies
 // slab e of each tensor into its arena slot.  16-byte copies; grid
@@ -222,11 +220,11 @@ struct GatherK {
 __global__ void __launch_bounds__(256) k_gather(GatherK a)
 {
     __shared__ int32_t s_ids[IDS_ROW];
-    __shared__ float s_w[MAX_TOPK];
+    __shared__ float s_lg[MAX_EXPERTS];
     const int s = blockIdx.y, t = blockIdx.z;
     uint32_t e, slot;
     if (a.mode == 0) {
-        const int32_t *ids = a.route.logits ? route_in_lds(a.route, s_ids, s_w) : a.ids;
+        const int32_t *ids = a.route.logits ? route_ids_wg(a.route, s_ids, s_lg) : a.ids;
         slot = (uint32_t)ids[32 + s];
         e = (uint32_t)ids[s];
         if (slot == SKIP) return;

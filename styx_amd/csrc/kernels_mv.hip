@@ -1,26 +1,34 @@
 // kernels_mv.hip -- dequant-matvec kernels of the MoE decode hot path (gfx950).
 //
-//   k_mv_dense      q/k/v, o-proj (+residual), LM head: rows of one or up to
-//                   three split-layout matrices against one activation vector,
-//                   optional fused RMSNorm prologue (rms_norm_f32 semantics,
-//                   crates/model/src/moe.rs:1746-1766) and residual add.
-//   k_router_topk   f32 router matvec (shaders/matvec_strided_f32.comp) with the
-//                   ffn RMSNorm fused in front and topk_softmax_f32 fused behind
-//                   (last-workgroup-done).
+//   k_xq            activation limbs (see qdot.h) of x, rmsnorm(x)*w or
+//                   swiglu(g, u), one workgroup; used where no producer
+//                   kernel writes them itself.
+//   k_mv_dense      q/k/v, o-proj (+residual), LM head, shared expert: rows of
+//                   one or up to three split-layout matrices against one limb
+//                   vector.
+//   k_router        ffn RMSNorm (rms_norm_f32 semantics, moe.rs:1746-1766) +
+//                   f32 router matvec (shaders/matvec_strided_f32.comp); its
+//                   first workgroup also writes the normalised vector and its
+//                   limbs for the expert kernels.
 //   k_gate_up       expert gate and up matvecs for the k routed slots
-//                   (mul_mat_vec_id semantics, ne11 = 1).
-//   k_down          expert down matvec with swiglu fused in its prologue and
-//                   moe_reduce fused behind (last-workgroup-done per row tile):
-//                   x[r] += sum_s w_s * y_s[r], s ascending.
+//                   (mul_mat_vec_id semantics, ne11 = 1), top-k ids ranked
+//                   in-kernel from the router logits.
+//   k_down          expert down matvec, swiglu + limbs of the slot's hidden
+//                   vector built in LDS in front; per-slot rows to partial[s].
+//   k_reduce_norm   topk_softmax weights of the selected ids, moe_reduce
+//                   (x += sum_s w_s y_s, s ascending), the shared-expert
+//                   axpy_sig, then the next RMSNorm and its limbs; one
+//                   workgroup.
 //
-// Every matvec workgroup (256 threads, 4 wave64) first issues nothing but
-// builds the activation limbs in LDS, then each lane group walks rows with
-// 16-byte loads of the split layout (see qdot.h).
+// No kernel waits on another workgroup: every producer writes what its
+// consumers read before the kernel boundary, so there is no device-scope
+// fence or counter anywhere on the path.
 #include "kernels.h"
 #include "qdot.h"
 #include "topk.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace styx {
 
@@ -49,15 +57,20 @@ Geo pick_geo(int t, int ncols)
     return g;
 }
 
-__device__ __forceinline__ const uint8_t *slab_for(const ExpSrc &s, const int32_t *ids, int slot)
+// Slab of one routed slot from its hot / arena / host ids (first non-SKIP).
+__device__ __forceinline__ const uint8_t *slab_pick(const ExpSrc &s, uint32_t h, uint32_t a,
+                                                    uint32_t g)
 {
-    const uint32_t h = (uint32_t)ids[16 + slot];
     if (h != SKIP) return s.hot + (int64_t)h * s.hot_slab;
-    const uint32_t a = (uint32_t)ids[32 + slot];
     if (a != SKIP) return s.arena + (int64_t)a * s.arena_slab;
-    const uint32_t g = (uint32_t)ids[48 + slot];
     if (g != SKIP) return s.gtt + (int64_t)g * s.gtt_slab;
     return nullptr;
+}
+
+__device__ __forceinline__ const uint8_t *slab_for(const ExpSrc &s, const int32_t *ids, int slot)
+{
+    return slab_pick(s, (uint32_t)ids[16 + slot], (uint32_t)ids[32 + slot],
+                     (uint32_t)ids[48 + slot]);
 }
 
 // ---------------------------------------------------------------------------
@@ -85,41 +98,52 @@ __device__ __forceinline__ LaneMap lane_map(int G)
     return m;
 }
 
-template <int T, int UPL, typename Emit>
-__device__ inline void walk_rows(const XqLds &q, const Mat &mat, int nb, int G, int r_begin,
-                                 int r_end, Emit emit)
+// The activation limbs of one lane's units, loaded once and kept in
+// registers for every row the lane visits.
+template <int T, int UPL> struct LaneX {
+    UX<T> x[UPL];
+    int ub[UPL], us[UPL];
+    bool uv[UPL];
+};
+
+template <int T, int UPL>
+__device__ __forceinline__ void lane_x_load(LaneX<T, UPL> &lx, const Xq &q, int nb, int G)
 {
     constexpr int UPB = T == T_Q8_0 ? 1 : 4;
     const LaneMap lm = lane_map(G);
     const int units = nb * UPB;
-    UX<T> x[UPL];
-    int ub[UPL], us[UPL];
-    bool uv[UPL];
 #pragma unroll
     for (int u = 0; u < UPL; u++) {
         const int un = lm.gl + u * G;
-        uv[u] = lm.ok && un < units;
-        ub[u] = un / UPB;
-        us[u] = un % UPB;
-        if (uv[u]) ux_load<T>(x[u], q, un);
+        lx.uv[u] = lm.ok && un < units;
+        lx.ub[u] = un / UPB;
+        lx.us[u] = un % UPB;
+        if (lx.uv[u]) ux_load<T>(lx.x[u], q, un);
     }
+}
+
+template <int T, int UPL, typename Emit>
+__device__ inline void walk_rows_x(const LaneX<T, UPL> &lx, const Mat &mat, int nb, int G,
+                                   int r_begin, int r_end, Emit emit)
+{
+    const LaneMap lm = lane_map(G);
     for (int r = r_begin + lm.gid; r < r_end; r += 2 * lm.ngrp) {
         const int r2 = r + lm.ngrp;
         const bool has2 = r2 < r_end;
         UW<T> w0[UPL], w1[UPL];
 #pragma unroll
         for (int u = 0; u < UPL; u++) {
-            if (uv[u]) {
-                uw_load<T>(w0[u], mat, (int64_t)r * nb + ub[u], us[u]);
-                if (has2) uw_load<T>(w1[u], mat, (int64_t)r2 * nb + ub[u], us[u]);
+            if (lx.uv[u]) {
+                uw_load<T>(w0[u], mat, (int64_t)r * nb + lx.ub[u], lx.us[u]);
+                if (has2) uw_load<T>(w1[u], mat, (int64_t)r2 * nb + lx.ub[u], lx.us[u]);
             }
         }
         float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
         for (int u = 0; u < UPL; u++) {
-            if (uv[u]) {
-                a0 += udot(w0[u], x[u]);
-                if (has2) a1 += udot(w1[u], x[u]);
+            if (lx.uv[u]) {
+                a0 += udot(w0[u], lx.x[u]);
+                if (has2) a1 += udot(w1[u], lx.x[u]);
             }
         }
         a0 = group_sum(a0, lm.gl, G);
@@ -131,45 +155,85 @@ __device__ inline void walk_rows(const XqLds &q, const Mat &mat, int nb, int G, 
     }
 }
 
-template <int T, typename Emit>
-__device__ inline void walk_rows_upl(int upl, const XqLds &q, const Mat &mat, int nb, int G,
-                                     int r_begin, int r_end, Emit emit)
+template <int T, int UPL, typename Emit>
+__device__ inline void walk_rows(const Xq &q, const Mat &mat, int nb, int G, int r_begin,
+                                 int r_end, Emit emit)
+{
+    LaneX<T, UPL> lx;
+    lane_x_load<T, UPL>(lx, q, nb, G);
+    walk_rows_x<T, UPL>(lx, mat, nb, G, r_begin, r_end, emit);
+}
+
+// Units per lane are a compile-time parameter of every matvec kernel: one
+// kernel per (type, UPL) keeps the register file to what that geometry
+// needs (the activation limbs of UPL units live in registers), which sets
+// the occupancy.
+template <int N> using IC = std::integral_constant<int, N>;
+
+template <int T, typename F> static void upl_dispatch(int upl, F f)
 {
     if constexpr (T == T_Q8_0) {
         switch (upl) {
-        case 1: walk_rows<T, 1>(q, mat, nb, G, r_begin, r_end, emit); break;
-        case 2: walk_rows<T, 2>(q, mat, nb, G, r_begin, r_end, emit); break;
-        case 3: walk_rows<T, 3>(q, mat, nb, G, r_begin, r_end, emit); break;
-        default: walk_rows<T, 4>(q, mat, nb, G, r_begin, r_end, emit); break;
+        case 1: f(IC<1>{}); break;
+        case 2: f(IC<2>{}); break;
+        case 3: f(IC<3>{}); break;
+        default: f(IC<4>{}); break;
         }
     } else {
         if (upl == 1)
-            walk_rows<T, 1>(q, mat, nb, G, r_begin, r_end, emit);
+            f(IC<1>{});
         else
-            walk_rows<T, 2>(q, mat, nb, G, r_begin, r_end, emit);
+            f(IC<2>{});
     }
 }
 
-__host__ __device__ inline size_t red_off(int n) { return (xq_lds_bytes(n) + 15) & ~(size_t)15; }
+// Rows per workgroup: about `target` workgroups over `rows` rows, at least
+// two rows per lane group, whole passes of the workgroup's groups.
+static int rows_per_wg(int rows, int G, int target)
+{
+    const int ngrp = WAVES * (64 / G);
+    int rpw = (rows + target - 1) / target;
+    rpw = std::max(rpw, 2 * ngrp);
+    return (rpw + ngrp - 1) / ngrp * ngrp;
+}
+
+// --------------------------------------------------------------- limbs ---
+__global__ void __launch_bounds__(WG) k_xq(const float *x, const float *u, const float *nw,
+                                           float eps, int n, Xq q, float *xn_out)
+{
+    extern __shared__ __align__(16) float hs[];
+    __shared__ float red[16];
+    if (u) {
+        // swiglu_f32 (ops2.rs:305-309)
+        for (int i = threadIdx.x; i < n; i += WG) hs[i] = x[i] / (1.0f + expf(-x[i])) * u[i];
+        __syncthreads();
+        xq_build(hs, nullptr, 0.0f, false, n, q, red, xn_out);
+    } else {
+        xq_build(x, nw, eps, nw != nullptr, n, q, red, xn_out);
+    }
+}
+
+hipError_t launch_xq(hipStream_t st, const float *x, const float *u, const float *norm_w,
+                     float eps, int n, const Xq &q, float *xn_out)
+{
+    if (n < 32 || n % 32 || n > XQ_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_xq, dim3(1), dim3(WG), u ? (size_t)n * 4 : 0, st, x, u, norm_w, eps, n,
+                       q, xn_out);
+    return hipGetLastError();
+}
 
 // ------------------------------------------------------------------ dense --
 struct DenseK {
     const uint8_t *w[3];
     float *y[3];
     int rows[3];
-    int nseg, total, ncols, nb, G, UPL, rpw, add;
-    const float *x, *nw;
-    float eps;
+    int nseg, total, nb, G, UPL, rpw, add;
+    Xq xq;
 };
 
-template <int T>
+template <int T, int UPL>
 __global__ void __launch_bounds__(WG) k_mv_dense(DenseK a)
 {
-    extern __shared__ __align__(16) uint8_t lds[];
-    const XqLds q = xq_carve(lds, a.ncols);
-    float *red = (float *)(lds + red_off(a.ncols));
-    xq_build(a.x, a.nw, a.eps, a.nw != nullptr, a.ncols, q, red, nullptr);
-    __syncthreads();
     const int r_begin = blockIdx.x * a.rpw, r_end = min(a.total, r_begin + a.rpw);
     // segments are walked one after another; each starts a fresh row walk
     int base = 0;
@@ -179,18 +243,18 @@ __global__ void __launch_bounds__(WG) k_mv_dense(DenseK a)
             const Mat mat = mat_at(a.w[s], T, (int64_t)a.rows[s] * a.nb);
             float *y = a.y[s];
             const int add = a.add;
-            walk_rows_upl<T>(a.UPL, q, mat, a.nb, a.G, lo - base, hi - base,
-                             [=](int r, float v) { y[r] = add ? y[r] + v : v; });
+            walk_rows<T, UPL>(a.xq, mat, a.nb, a.G, lo - base, hi - base,
+                              [=](int r, float v) { y[r] = add ? y[r] + v : v; });
         }
         base += a.rows[s];
     }
 }
 
 hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, int nseg,
-                        const float *x, const float *norm_w, float eps, int add)
+                        const Xq &xq, int add)
 {
     const Geo g = pick_geo(t, ncols);
-    if (g.G == 0 || nseg < 1 || nseg > 3) return hipErrorInvalidValue;
+    if (g.G == 0 || nseg < 1 || nseg > 3 || !xq.A) return hipErrorInvalidValue;
     DenseK a{};
     a.total = 0;
     for (int i = 0; i < nseg; i++) {
@@ -200,27 +264,18 @@ hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, 
         a.total += segs[i].rows;
     }
     a.nseg = nseg;
-    a.ncols = ncols;
     a.nb = ncols / blk_elems(t);
     a.G = g.G;
     a.UPL = g.UPL;
     a.add = add;
-    a.x = x;
-    a.nw = norm_w;
-    a.eps = eps;
-    const int ngrp = WAVES * (64 / g.G);
-    // aim for ~1024 workgroups (4 per CU), at least 2 rows per group
-    int rpw = (a.total + 1023) / 1024;
-    rpw = std::max(rpw, 2 * ngrp);
-    rpw = (rpw + ngrp - 1) / ngrp * ngrp;
-    a.rpw = rpw;
-    const int nwg = (a.total + rpw - 1) / rpw;
-    const size_t lds = red_off(ncols) + 64;
+    a.xq = xq;
+    a.rpw = rows_per_wg(a.total, g.G, 1024);
+    const dim3 grid((a.total + a.rpw - 1) / a.rpw);
     switch (t) {
-    case T_Q8_0: hipLaunchKernelGGL(k_mv_dense<T_Q8_0>, dim3(nwg), dim3(WG), lds, st, a); break;
-    case T_Q4_K: hipLaunchKernelGGL(k_mv_dense<T_Q4_K>, dim3(nwg), dim3(WG), lds, st, a); break;
-    case T_Q5_K: hipLaunchKernelGGL(k_mv_dense<T_Q5_K>, dim3(nwg), dim3(WG), lds, st, a); break;
-    case T_Q6_K: hipLaunchKernelGGL(k_mv_dense<T_Q6_K>, dim3(nwg), dim3(WG), lds, st, a); break;
+    case T_Q8_0: upl_dispatch<T_Q8_0>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_mv_dense<T_Q8_0, decltype(u)::value>), grid, dim3(WG), 0, st, a); }); break;
+    case T_Q4_K: upl_dispatch<T_Q4_K>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_mv_dense<T_Q4_K, decltype(u)::value>), grid, dim3(WG), 0, st, a); }); break;
+    case T_Q5_K: upl_dispatch<T_Q5_K>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_mv_dense<T_Q5_K, decltype(u)::value>), grid, dim3(WG), 0, st, a); }); break;
+    case T_Q6_K: upl_dispatch<T_Q6_K>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_mv_dense<T_Q6_K, decltype(u)::value>), grid, dim3(WG), 0, st, a); }); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -246,9 +301,9 @@ hipError_t launch_topk_softmax(hipStream_t st, const float *logits, int n, int k
 
 // ------------------------------------------------------------- router ----
 // ffn RMSNorm fused in front of the f32 router matvec
-// (shaders/matvec_strided_f32.comp); one row per wave.  The top-k is run by
-// each consumer workgroup from these logits (see route_in_lds), so no
-// workgroup ever waits on another inside a kernel.
+// (shaders/matvec_strided_f32.comp); one row per wave.  The top-k ids are
+// ranked by each consumer workgroup from these logits (route_ids_wg) and the
+// weights by k_reduce_norm, so no workgroup ever waits on another.
 constexpr int ROUTER_ROWS = 4;
 
 __global__ void __launch_bounds__(WG) k_router(RouterArgs a)
@@ -256,40 +311,78 @@ __global__ void __launch_bounds__(WG) k_router(RouterArgs a)
     extern __shared__ __align__(16) uint8_t lds[];
     float *xs = (float *)lds;          // normalised x, H floats
     float *red = xs + a.H;             // 16 floats
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = blockIdx.x * ROUTER_ROWS + wave;
+    // the router row, x and the norm weights do not depend on each other:
+    // load the first 2048 columns of all three before any reduction
+    constexpr int PW = 8, PX = 2;  // float4 per lane of W, per thread of x
+    float4 wv[PW], xv[PX], nv[PX];
+    const float *w = a.W + (int64_t)min(r, a.E - 1) * a.H;
+#pragma unroll
+    for (int j = 0; j < PW; j++) {
+        const int c = lane * 4 + 256 * j;
+        wv[j] = c < a.H ? *(const float4 *)(w + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int j = 0; j < PX; j++) {
+        const int i = threadIdx.x * 4 + WG * 4 * j;
+        xv[j] = i < a.H ? *(const float4 *)(a.x + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        nv[j] = i < a.H ? *(const float4 *)(a.norm_w + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     float ss = 0.0f;
-    for (int i = threadIdx.x * 4; i < a.H; i += WG * 4) {
+#pragma unroll
+    for (int j = 0; j < PX; j++)
+        ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+    for (int i = threadIdx.x * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {
         const float4 v = *(const float4 *)(a.x + i);
         ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     }
     ss = block_sum(ss, red);
     const float scale = 1.0f / sqrtf(ss / (float)a.H + a.eps);
-    for (int i = threadIdx.x * 4; i < a.H; i += WG * 4) {
+#pragma unroll
+    for (int j = 0; j < PX; j++) {
+        const int i = threadIdx.x * 4 + WG * 4 * j;
+        if (i < a.H)
+            *(float4 *)(xs + i) = make_float4((xv[j].x * scale) * nv[j].x, (xv[j].y * scale) * nv[j].y,
+                                              (xv[j].z * scale) * nv[j].z, (xv[j].w * scale) * nv[j].w);
+    }
+    for (int i = threadIdx.x * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {
         const float4 v = *(const float4 *)(a.x + i);
-        const float4 w = *(const float4 *)(a.norm_w + i);
-        const float4 o = make_float4((v.x * scale) * w.x, (v.y * scale) * w.y,
-                                     (v.z * scale) * w.z, (v.w * scale) * w.w);
-        *(float4 *)(xs + i) = o;
-        if (blockIdx.x == 0) *(float4 *)(a.xn + i) = o;
+        const float4 nw = *(const float4 *)(a.norm_w + i);
+        *(float4 *)(xs + i) = make_float4((v.x * scale) * nw.x, (v.y * scale) * nw.y,
+                                          (v.z * scale) * nw.z, (v.w * scale) * nw.w);
     }
     __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = blockIdx.x * ROUTER_ROWS + wave;
     if (r < a.E) {
-        const float *w = a.W + (int64_t)r * a.H;
         float acc = 0.0f;
-        for (int c = lane * 4; c < a.H; c += 256) {
-            const float4 wv = *(const float4 *)(w + c);
-            const float4 xv = *(const float4 *)(xs + c);
-            acc += wv.x * xv.x + wv.y * xv.y + wv.z * xv.z + wv.w * xv.w;
+#pragma unroll
+        for (int j = 0; j < PW; j++) {
+            const int c = lane * 4 + 256 * j;
+            if (c < a.H) {
+                const float4 xv4 = *(const float4 *)(xs + c);
+                acc += wv[j].x * xv4.x + wv[j].y * xv4.y + wv[j].z * xv4.z + wv[j].w * xv4.w;
+            }
+        }
+        for (int c = lane * 4 + 256 * PW; c < a.H; c += 256) {
+            const float4 wq = *(const float4 *)(w + c);
+            const float4 xv4 = *(const float4 *)(xs + c);
+            acc += wq.x * xv4.x + wq.y * xv4.y + wq.z * xv4.z + wq.w * xv4.w;
         }
         acc = wave_sum(acc);
         if (lane == 0) a.logits[r] = a.bias ? acc + a.bias[r] : acc;
+    }
+    if (blockIdx.x == 0) {
+        if (a.xq.A)
+            xq_build(xs, nullptr, 0.0f, false, a.H, a.xq, red, a.xn);
+        else if (a.xn)
+            for (int i = threadIdx.x * 4; i < a.H; i += WG * 4)
+                *(float4 *)(a.xn + i) = *(const float4 *)(xs + i);
     }
 }
 
 hipError_t launch_router(hipStream_t st, const RouterArgs &a)
 {
-    if (a.E < 1 || a.E > MAX_EXPERTS || a.H % 4) return hipErrorInvalidValue;
+    if (a.E < 1 || a.E > MAX_EXPERTS || a.H % 32 || a.H > XQ_MAX) return hipErrorInvalidValue;
     const int nwg = (a.E + ROUTER_ROWS - 1) / ROUTER_ROWS;
     hipLaunchKernelGGL(k_router, dim3(nwg), dim3(WG), (size_t)a.H * 4 + 64, st, a);
     return hipGetLastError();
@@ -307,64 +400,66 @@ hipError_t launch_router_topk(hipStream_t st, const RouterArgs &a)
 // ------------------------------------------------------------ gate / up ---
 struct GateUpK {
     ExpSrc src[2];
-    int type[2], G[2], UPL[2];
+    int G;
     const int32_t *ids;   // id row in memory, used when route.logits is null
     Route route;
-    const float *xn;
+    Xq xq;
     float *gu;  // [2][k][F]
-    int H, F, k, nb, rpw;
+    int F, k, nb, rpw;
 };
 
-template <int T>
-__device__ inline void gate_up_body(const GateUpK &a, const XqLds &q, int m, int s,
-                                    const uint8_t *slab)
+// The lane's activation limbs are loaded before the routing so both
+// memory trips overlap.
+template <int T, int UPL>
+__device__ inline void gate_up_body(const GateUpK &a, int m, int s, int32_t *s_ids, float *s_lg)
 {
+    LaneX<T, UPL> lx;
+    lane_x_load<T, UPL>(lx, a.xq, a.nb, a.G);
+    const int32_t *ids = a.route.logits ? route_ids_wg(a.route, s_ids, s_lg) : a.ids;
+    const uint8_t *slab = slab_for(a.src[m], ids, s);
+    if (!slab) return;
     const Mat mat = mat_at(slab, T, (int64_t)a.F * a.nb);
     const int r_begin = blockIdx.x * a.rpw, r_end = min(a.F, r_begin + a.rpw);
     float *y = a.gu + ((int64_t)m * a.k + s) * a.F;
-    walk_rows_upl<T>(a.UPL[m], q, mat, a.nb, a.G[m], r_begin, r_end,
-                     [=](int r, float v) { y[r] = v; });
+    walk_rows_x<T, UPL>(lx, mat, a.nb, a.G, r_begin, r_end, [=](int r, float v) { y[r] = v; });
 }
 
-template <int TG, int TU>
+template <int TG, int TU, int UPL>
 __global__ void __launch_bounds__(WG) k_gate_up(GateUpK a)
 {
-    extern __shared__ __align__(16) uint8_t lds[];
     __shared__ int32_t s_ids[IDS_ROW];
-    __shared__ float s_w[MAX_TOPK];
+    __shared__ float s_lg[MAX_EXPERTS];
     const int s = blockIdx.y, m = blockIdx.z;
-    const int32_t *ids = a.route.logits ? route_in_lds(a.route, s_ids, s_w) : a.ids;
-    const uint8_t *slab = slab_for(a.src[m], ids, s);
-    if (!slab) return;
-    const XqLds q = xq_carve(lds, a.H);
-    float *red = (float *)(lds + red_off(a.H));
-    xq_build(a.xn, nullptr, 0.0f, false, a.H, q, red, nullptr);
-    __syncthreads();
     if (m == 0)
-        gate_up_body<TG>(a, q, 0, s, slab);
+        gate_up_body<TG, UPL>(a, 0, s, s_ids, s_lg);
     else
-        gate_up_body<TU>(a, q, 1, s, slab);
+        gate_up_body<TU, UPL>(a, 1, s, s_ids, s_lg);
 }
 
+// gate and up share the block size, so one geometry serves both
 template <int TG>
-static hipError_t launch_gu_tu(hipStream_t st, int tu, const GateUpK &a, dim3 grid, size_t lds)
+static hipError_t launch_gu_tu(hipStream_t st, int tu, int upl, const GateUpK &a, dim3 grid)
 {
-    switch (tu) {
-    case T_Q8_0: hipLaunchKernelGGL((k_gate_up<TG, T_Q8_0>), grid, dim3(WG), lds, st, a); break;
-    case T_Q4_K: hipLaunchKernelGGL((k_gate_up<TG, T_Q4_K>), grid, dim3(WG), lds, st, a); break;
-    case T_Q5_K: hipLaunchKernelGGL((k_gate_up<TG, T_Q5_K>), grid, dim3(WG), lds, st, a); break;
-    case T_Q6_K: hipLaunchKernelGGL((k_gate_up<TG, T_Q6_K>), grid, dim3(WG), lds, st, a); break;
-    default: return hipErrorInvalidValue;
+    if constexpr (TG == T_Q8_0) {
+        if (tu != T_Q8_0) return hipErrorInvalidValue;
+        upl_dispatch<T_Q8_0>(upl, [&](auto u) { hipLaunchKernelGGL((k_gate_up<TG, T_Q8_0, decltype(u)::value>), grid, dim3(WG), 0, st, a); });
+    } else {
+        switch (tu) {
+        case T_Q4_K: upl_dispatch<T_Q4_K>(upl, [&](auto u) { hipLaunchKernelGGL((k_gate_up<TG, T_Q4_K, decltype(u)::value>), grid, dim3(WG), 0, st, a); }); break;
+        case T_Q5_K: upl_dispatch<T_Q5_K>(upl, [&](auto u) { hipLaunchKernelGGL((k_gate_up<TG, T_Q5_K, decltype(u)::value>), grid, dim3(WG), 0, st, a); }); break;
+        case T_Q6_K: upl_dispatch<T_Q6_K>(upl, [&](auto u) { hipLaunchKernelGGL((k_gate_up<TG, T_Q6_K, decltype(u)::value>), grid, dim3(WG), 0, st, a); }); break;
+        default: return hipErrorInvalidValue;
+        }
     }
     return hipGetLastError();
 }
 
 hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, const ExpSrc &u,
-                              const int32_t *ids, const Route *route, const float *xn, float *gu,
+                              const int32_t *ids, const Route *route, const Xq &xq, float *gu,
                               int H, int F, int k)
 {
-    const Geo gg = pick_geo(tg, H), gv = pick_geo(tu, H);
-    if (!gg.G || !gv.G || blk_elems(tg) != blk_elems(tu) || k < 1 || k > MAX_TOPK)
+    const Geo gg = pick_geo(tg, H);
+    if (!gg.G || blk_elems(tg) != blk_elems(tu) || k < 1 || k > MAX_TOPK || !xq.A)
         return hipErrorInvalidValue;
     if (route && (route->E < k || route->E > MAX_EXPERTS || route->k != k))
         return hipErrorInvalidValue;
@@ -372,40 +467,29 @@ hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, c
     GateUpK a{};
     a.src[0] = g;
     a.src[1] = u;
-    a.type[0] = tg;
-    a.type[1] = tu;
-    a.G[0] = gg.G;
-    a.G[1] = gv.G;
-    a.UPL[0] = gg.UPL;
-    a.UPL[1] = gv.UPL;
+    a.G = gg.G;
     a.ids = ids;
     if (route) a.route = *route;
-    a.xn = xn;
+    a.xq = xq;
     a.gu = gu;
-    a.H = H;
     a.F = F;
     a.k = k;
     a.nb = H / blk_elems(tg);
-    // rows per workgroup: ~1024 workgroups in total over 2*k slot-matrices
-    const int ngrp = WAVES * (64 / std::max(gg.G, gv.G));
-    int rpw = (2 * k * F + 1023) / 1024;
-    rpw = std::max(rpw, 2 * ngrp);
-    rpw = (rpw + ngrp - 1) / ngrp * ngrp;
-    a.rpw = rpw;
-    const dim3 grid((F + rpw - 1) / rpw, k, 2);
-    const size_t lds = red_off(H) + 64;
+    // ~1024 workgroups in total over the 2*k slot matrices
+    a.rpw = rows_per_wg(2 * k * F, gg.G, 1024);
+    const dim3 grid((F + a.rpw - 1) / a.rpw, k, 2);
     switch (tg) {
-    case T_Q8_0: return launch_gu_tu<T_Q8_0>(st, tu, a, grid, lds);
-    case T_Q4_K: return launch_gu_tu<T_Q4_K>(st, tu, a, grid, lds);
-    case T_Q5_K: return launch_gu_tu<T_Q5_K>(st, tu, a, grid, lds);
-    case T_Q6_K: return launch_gu_tu<T_Q6_K>(st, tu, a, grid, lds);
+    case T_Q8_0: return launch_gu_tu<T_Q8_0>(st, tu, gg.UPL, a, grid);
+    case T_Q4_K: return launch_gu_tu<T_Q4_K>(st, tu, gg.UPL, a, grid);
+    case T_Q5_K: return launch_gu_tu<T_Q5_K>(st, tu, gg.UPL, a, grid);
+    case T_Q6_K: return launch_gu_tu<T_Q6_K>(st, tu, gg.UPL, a, grid);
     default: return hipErrorInvalidValue;
     }
 }
 
 // ------------------------------------------------------------- down -------
-// y_s = Wd[e_s] . swiglu(g_s, u_s) for every routed slot s into partial[s];
-// the weighted combine into the residual is k_moe_reduce.
+// partial[s] = Wd[e_s] . swiglu(g_s, u_s) for every routed slot s; the
+// weighted combine into the residual is k_reduce_norm.
 struct DownK {
     ExpSrc src;
     int G, UPL;
@@ -415,51 +499,40 @@ struct DownK {
     int H, F, k, nb, rpw;
 };
 
-template <int T>
+template <int T, int UPL>
 __global__ void __launch_bounds__(WG) k_down(DownK a)
 {
     extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float red[16];
     const int s = blockIdx.y;
     const int r_begin = blockIdx.x * a.rpw, r_end = min(a.H, r_begin + a.rpw);
-    const uint8_t *slab = slab_for(a.src, a.ids, s);
+    // the id row and this slot's gate/up rows are independent loads: issue
+    // both, then swiglu_f32 (ops2.rs:305-309) into LDS
+    int32_t idr[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) idr[j] = a.ids[16 * (j + 1) + s];
+    float *hs = (float *)lds;
+    const float *g = a.gu + (int64_t)s * a.F, *u = a.gu + ((int64_t)a.k + s) * a.F;
+    for (int i = threadIdx.x; i < a.F; i += WG) hs[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+    const uint8_t *slab = slab_pick(a.src, (uint32_t)idr[0], (uint32_t)idr[1], (uint32_t)idr[2]);
     float *part = a.partial + (int64_t)s * a.H;
     if (!slab) {
         for (int r = r_begin + threadIdx.x; r < r_end; r += WG) part[r] = 0.0f;
         return;
     }
-    // swiglu_f32 (ops2.rs:305-309) of this slot's gate/up rows into LDS
-    float *hs = (float *)lds;
-    const float *g = a.gu + (int64_t)s * a.F, *u = a.gu + ((int64_t)a.k + s) * a.F;
-    for (int i = threadIdx.x; i < a.F; i += WG) hs[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
     __syncthreads();
-    uint8_t *qbase = lds + (((size_t)a.F * 4 + 15) & ~(size_t)15);
-    const XqLds q = xq_carve(qbase, a.F);
-    float *red = (float *)(qbase + red_off(a.F));
+    const Xq q = xq_at(lds + (size_t)a.F * 4, a.F);
     xq_build(hs, nullptr, 0.0f, false, a.F, q, red, nullptr);
     __syncthreads();
     const Mat mat = mat_at(slab, T, (int64_t)a.H * a.nb);
-    walk_rows_upl<T>(a.UPL, q, mat, a.nb, a.G, r_begin, r_end,
-                     [=](int r, float v) { part[r] = v; });
-}
-
-// moe_reduce_f32 (shaders/moe_reduce_f32.comp:8-13): x[i] += sum_s w[s]*d[s][i],
-// accumulated from 0 in ascending s.
-__global__ void __launch_bounds__(WG) k_moe_reduce(const float *d, const float *w, float *x,
-                                                   int ne, int k)
-{
-    const int i = blockIdx.x * WG + threadIdx.x;
-    if (i >= ne) return;
-    float acc = 0.0f;
-    for (int s = 0; s < k; s++) acc += w[s] * d[(int64_t)s * ne + i];
-    x[i] += acc;
+    walk_rows<T, UPL>(q, mat, a.nb, a.G, r_begin, r_end, [=](int r, float v) { part[r] = v; });
 }
 
 hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_t *ids,
-                           const float *wts, const float *gu, float *x, float *partial, int H,
-                           int F, int k)
+                           const float *gu, float *partial, int H, int F, int k)
 {
     const Geo g = pick_geo(td, F);
-    if (!g.G || k < 1 || k > MAX_TOPK) return hipErrorInvalidValue;
+    if (!g.G || k < 1 || k > MAX_TOPK || F > XQ_MAX / 2) return hipErrorInvalidValue;
     DownK a{};
     a.src = d;
     a.G = g.G;
@@ -471,44 +544,118 @@ hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_
     a.F = F;
     a.k = k;
     a.nb = F / blk_elems(td);
-    const int ngrp = WAVES * (64 / g.G);
-    int rpw = (k * H + 1023) / 1024;
-    rpw = std::max(rpw, 2 * ngrp);
-    rpw = (rpw + ngrp - 1) / ngrp * ngrp;
-    a.rpw = rpw;
-    const dim3 grid((H + rpw - 1) / rpw, k, 1);
-    const size_t lds = (((size_t)F * 4 + 15) & ~(size_t)15) + red_off(F) + 64;
+    a.rpw = rows_per_wg(k * H, g.G, 1024);
+    const dim3 grid((H + a.rpw - 1) / a.rpw, k, 1);
+    const size_t lds = (size_t)F * 4 + xq_bytes(F);
     switch (td) {
-    case T_Q8_0: hipLaunchKernelGGL(k_down<T_Q8_0>, grid, dim3(WG), lds, st, a); break;
-    case T_Q4_K: hipLaunchKernelGGL(k_down<T_Q4_K>, grid, dim3(WG), lds, st, a); break;
-    case T_Q5_K: hipLaunchKernelGGL(k_down<T_Q5_K>, grid, dim3(WG), lds, st, a); break;
-    case T_Q6_K: hipLaunchKernelGGL(k_down<T_Q6_K>, grid, dim3(WG), lds, st, a); break;
+    case T_Q8_0: upl_dispatch<T_Q8_0>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_down<T_Q8_0, decltype(u)::value>), grid, dim3(WG), lds, st, a); }); break;
+    case T_Q4_K: upl_dispatch<T_Q4_K>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_down<T_Q4_K, decltype(u)::value>), grid, dim3(WG), lds, st, a); }); break;
+    case T_Q5_K: upl_dispatch<T_Q5_K>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_down<T_Q5_K, decltype(u)::value>), grid, dim3(WG), lds, st, a); }); break;
+    case T_Q6_K: upl_dispatch<T_Q6_K>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_down<T_Q6_K, decltype(u)::value>), grid, dim3(WG), lds, st, a); }); break;
     default: return hipErrorInvalidValue;
     }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_moe_reduce, dim3((H + WG - 1) / WG), dim3(WG), 0, st, partial, wts, x, H,
-                       k);
     return hipGetLastError();
 }
 
-// ------------------------------------------------ shared-expert gating ----
-__global__ void __launch_bounds__(WG) k_axpy_sig_dot(const float *ginp, const float *xn,
-                                                     const float *y, float *x, int n)
+// ------------------------------------------------------- reduce + norm ----
+// One workgroup: weights w_s = softmax(logits)[ids[s]] (renormalised over
+// the k picks if renorm) exactly as topk_softmax_f32.comp:29-67 forms them,
+// or taken from a.wts; then
+//   x[i] += sum_s w_s * partial[s][i]      (moe_reduce_f32.comp:8-13)
+//   x[i] += sigmoid(ginp . xn) * sh_y[i]   (axpy_sig_f32.comp, if sh_y)
+// and, if norm_w, the limbs of rmsnorm(x) * norm_w for the next matvec.
+constexpr int RN_WG = 1024;
+
+__global__ void __launch_bounds__(RN_WG) k_reduce_norm(ReduceArgs a)
 {
+    extern __shared__ __align__(16) float xs[];  // H floats
     __shared__ float red[16];
-    float acc = 0.0f;
-    for (int i = threadIdx.x; i < n; i += WG) acc += ginp[i] * xn[i];
-    acc = block_sum(acc, red);
-    const float sg = 1.0f / (1.0f + expf(-acc));
-    for (int i = blockIdx.x * WG + threadIdx.x; i < n; i += gridDim.x * WG) x[i] += sg * y[i];
+    __shared__ float s_w[MAX_TOPK];
+    __shared__ float s_wsum, s_sg;
+    // every load that does not depend on the weights is issued first: the
+    // first RN_WG elements of x and of each slot's partial, the routed
+    // logits, the shared-expert operands
+    const int i0 = threadIdx.x;
+    const bool h0 = i0 < a.H;
+    float p0[MAX_TOPK];
+#pragma unroll
+    for (int s = 0; s < MAX_TOPK; s++)
+        p0[s] = (s < a.k && h0) ? a.partial[(int64_t)s * a.H + i0] : 0.0f;
+    const float x0 = h0 ? a.x[i0] : 0.0f;
+    const float y0 = (a.sh_y && h0) ? a.sh_y[i0] : 0.0f;
+    float lg_own = -INFINITY, lg_pick = 0.0f;
+    if (a.logits) {
+        if (i0 < a.E) lg_own = a.logits[i0];
+        if (i0 < a.k) {
+            const int e = a.ids[i0];
+            lg_pick = (e >= 0 && e < a.E) ? a.logits[e] : -INFINITY;
+        }
+    }
+    if (a.logits) {
+        float mx = lg_own;
+        for (int e = threadIdx.x + RN_WG; e < a.E; e += RN_WG) mx = fmaxf(mx, a.logits[e]);
+        mx = wave_max(mx);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+        __syncthreads();
+        mx = red[0];
+        for (int i = 1; i < RN_WG / 64; i++) mx = fmaxf(mx, red[i]);
+        float se = i0 < a.E ? expf(lg_own - mx) : 0.0f;
+        for (int e = threadIdx.x + RN_WG; e < a.E; e += RN_WG) se += expf(a.logits[e] - mx);
+        se = block_sum(se, red);
+        // each slot's weight in its own thread; the renormalising sum runs in
+        // slot order as in the reference
+        if (i0 < a.k) s_w[i0] = expf(lg_pick - mx) / se;
+        __syncthreads();
+        if (threadIdx.x == 0 && a.renorm) {
+            float wsum = 0.0f;
+            for (int s = 0; s < a.k; s++) wsum += s_w[s];
+            s_wsum = wsum;
+        }
+        __syncthreads();
+        if (i0 < a.k) {
+            const float w = a.renorm ? s_w[i0] / s_wsum : s_w[i0];
+            s_w[i0] = w;  // only this thread touches slot i0 here
+            if (a.wts_out) a.wts_out[i0] = w;
+        }
+    } else if (i0 < a.k) {
+        s_w[i0] = a.wts[i0];
+    }
+    if (a.sh_y) {
+        float d = 0.0f;
+        for (int i = threadIdx.x; i < a.H; i += RN_WG) d += a.sh_ginp[i] * a.xn[i];
+        d = block_sum(d, red);
+        if (threadIdx.x == 0) s_sg = 1.0f / (1.0f + expf(-d));
+    }
+    __syncthreads();
+    if (h0) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int s = 0; s < MAX_TOPK; s++)
+            if (s < a.k) acc += s_w[s] * p0[s];
+        float v = x0 + acc;
+        if (a.sh_y) v = v + s_sg * y0;
+        a.x[i0] = v;
+        xs[i0] = v;
+    }
+    for (int i = i0 + RN_WG; i < a.H; i += RN_WG) {
+        float acc = 0.0f;
+        for (int s = 0; s < a.k; s++) acc += s_w[s] * a.partial[(int64_t)s * a.H + i];
+        float v = a.x[i] + acc;
+        if (a.sh_y) v = v + s_sg * a.sh_y[i];
+        a.x[i] = v;
+        xs[i] = v;
+    }
+    __syncthreads();
+    if (a.norm_w) xq_build(xs, a.norm_w, a.eps, true, a.H, a.xq, red, nullptr);
 }
 
-hipError_t launch_axpy_sig_dot(hipStream_t st, const float *ginp, const float *xn,
-                               const float *y, float *x, int n)
+hipError_t launch_reduce_norm(hipStream_t st, const ReduceArgs &a)
 {
-    hipLaunchKernelGGL(k_axpy_sig_dot, dim3(std::max(1, std::min(32, n / WG))), dim3(WG), 0, st,
-                       ginp, xn, y, x, n);
+    if (a.k < 1 || a.k > MAX_TOPK || a.H < 32 || a.H % 32 || a.H > XQ_MAX ||
+        (a.logits && (a.E < a.k || a.E > MAX_EXPERTS || !a.ids)) || (!a.logits && !a.wts) ||
+        (a.sh_y && (!a.sh_ginp || !a.xn)) || (a.norm_w && !a.xq.A))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_reduce_norm, dim3(1), dim3(RN_WG), (size_t)a.H * 4, st, a);
     return hipGetLastError();
 }
 

@@ -33,32 +33,6 @@ __device__ __forceinline__ float limbs_to_f(int A, int B, int C)
     return (float)A + ((float)B + (float)C * R254) * R254;
 }
 
-// ----------------------------------------------------------------------------
-// Activation limbs in LDS: int8 planes A/B/C of n values, sx[n/32], s16[n/16]
-// (plain sums of the f32 values over 16-value runs, for the per-sub-block
-// offset terms).
-// ----------------------------------------------------------------------------
-struct XqLds {
-    int8_t *A, *B, *C;
-    float *sx, *s16;
-};
-
-__host__ __device__ inline size_t xq_lds_bytes(int n)
-{
-    return (size_t)3 * n + (size_t)(n / 32) * 4 + (size_t)(n / 16) * 4;
-}
-
-__device__ inline XqLds xq_carve(uint8_t *lds, int n)
-{
-    XqLds q;
-    q.A = (int8_t *)lds;
-    q.B = q.A + n;
-    q.C = q.B + n;
-    q.sx = (float *)(lds + 3 * (size_t)n);
-    q.s16 = q.sx + n / 32;
-    return q;
-}
-
 __device__ __forceinline__ float wave_sum(float v)
 {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -84,12 +58,11 @@ __device__ inline float block_sum(float v, float *red)
 }
 
 // Build the limb form of xn = norm ? x * rsqrt(mean(x^2)+eps) * w : x
-// (n a multiple of 32, n <= 8 * 32 * blockDim.x).  If xn_out is non-null
-// the normalised f32 vector is also written there (by block 0 only).
+// (n a multiple of 32).  If xn_out is non-null the normalised f32 vector is
+// also written there.
 // Thread t owns 8 consecutive values; four threads share one 32-value block.
 __device__ inline void xq_build(const float *__restrict__ x, const float *__restrict__ nw,
-                                float eps, bool norm, int n, XqLds q, float *red,
-                                float *xn_out)
+                                float eps, bool norm, int n, Xq q, float *red, float *xn_out)
 {
     float scale = 1.0f;
     if (norm) {
@@ -116,7 +89,7 @@ __device__ inline void xq_build(const float *__restrict__ x, const float *__rest
 #pragma unroll
                 for (int i = 0; i < 8; i++) v[i] = (v[i] * scale) * w[i];
             }
-            if (xn_out && blockIdx.x == 0 && blockIdx.y == 0) {
+            if (xn_out) {
                 *(float4 *)(xn_out + 8 * g) = make_float4(v[0], v[1], v[2], v[3]);
                 *(float4 *)(xn_out + 8 * g + 4) = make_float4(v[4], v[5], v[6], v[7]);
             }
@@ -187,7 +160,7 @@ template <> struct UX<T_Q6_K> {
     int h, n;
 };
 
-__device__ __forceinline__ void ld_limbs(const XqLds &q, int e, int ndw, uint32_t *a,
+__device__ __forceinline__ void ld_limbs(const Xq &q, int e, int ndw, uint32_t *a,
                                          uint32_t *b, uint32_t *c)
 {
     for (int i = 0; i < ndw; i += 4) {
@@ -200,15 +173,15 @@ __device__ __forceinline__ void ld_limbs(const XqLds &q, int e, int ndw, uint32_
     }
 }
 
-template <int T> __device__ inline void ux_load(UX<T> &u, const XqLds &q, int unit);
+template <int T> __device__ inline void ux_load(UX<T> &u, const Xq &q, int unit);
 
-template <> __device__ inline void ux_load<T_Q8_0>(UX<T_Q8_0> &u, const XqLds &q, int unit)
+template <> __device__ inline void ux_load<T_Q8_0>(UX<T_Q8_0> &u, const Xq &q, int unit)
 {
     ld_limbs(q, 32 * unit, 8, u.a, u.b, u.c);
     u.sx = q.sx[unit];
 }
 
-template <> __device__ inline void ux_load<T_Q4_K>(UX<T_Q4_K> &u, const XqLds &q, int unit)
+template <> __device__ inline void ux_load<T_Q4_K>(UX<T_Q4_K> &u, const Xq &q, int unit)
 {
     const int b = unit >> 2, c = unit & 3, e = 256 * b + 64 * c;
     ld_limbs(q, e, 16, u.a, u.b, u.c);
@@ -220,7 +193,7 @@ template <> __device__ inline void ux_load<T_Q4_K>(UX<T_Q4_K> &u, const XqLds &q
     u.high = c >> 1;
 }
 
-template <> __device__ inline void ux_load<T_Q5_K>(UX<T_Q5_K> &u, const XqLds &q, int unit)
+template <> __device__ inline void ux_load<T_Q5_K>(UX<T_Q5_K> &u, const Xq &q, int unit)
 {
     const int b = unit >> 2, c = unit & 3, e = 256 * b + 64 * c;
     ld_limbs(q, e, 16, u.a, u.b, u.c);
@@ -233,7 +206,7 @@ template <> __device__ inline void ux_load<T_Q5_K>(UX<T_Q5_K> &u, const XqLds &q
     u.qsh = 2 * c;
 }
 
-template <> __device__ inline void ux_load<T_Q6_K>(UX<T_Q6_K> &u, const XqLds &q, int unit)
+template <> __device__ inline void ux_load<T_Q6_K>(UX<T_Q6_K> &u, const Xq &q, int unit)
 {
     const int b = unit >> 2, n = (unit >> 1) & 1, h = unit & 1;
     const int e0 = 256 * b + 128 * n + 16 * h;

@@ -14,6 +14,11 @@ struct styx_gpu {
     uint64_t hbm = 0;
     int live_children = 0;
     bool closed = false;  // styx_gpu_free called while children were alive
+    // Activation limbs of the op entry points that take an f32 vector
+    // (matvec, gate/up): built into this buffer in stream order right before
+    // the matvec that reads them.  Calls on one styx_gpu are serialised on
+    // its stream, so one buffer serves them all.
+    void *xq_scratch = nullptr;
 };
 
 struct styx_buf {

@@ -84,21 +84,57 @@ __device__ __noinline__ void topk_wave(const float *logits, int n, int k, int re
     }
 }
 
-// Top-k of the router logits computed inside a workgroup (wave 0) into LDS;
-// the workgroup with all-zero block index also publishes the weights and the
-// id row to global memory for the kernels that follow.
-__device__ inline const int32_t *route_in_lds(const Route &r, int32_t *s_ids, float *s_w)
+// Top-k ids of the router logits inside a workgroup, by ranking: the rank of
+// logit e is the number of logits ordered before it (a larger value, or an
+// equal value at a lower index -- the strict '>' of topk_softmax_f32.comp:45),
+// so ranks 0..k-1 are exactly the reference's selection order.  Every thread
+// ranks one logit against a slice of the others; no dependent shuffle chain.
+// Fills the four id rows in s_ids (64 ints); weights are left to the caller.
+// The workgroup with all-zero block index publishes the id row to r.ids_out.
+__device__ inline const int32_t *route_ids_wg(const Route &r, int32_t *s_ids, float *s_lg)
 {
-    if (threadIdx.x < 64) {
-        s_ids[threadIdx.x] = (int32_t)SKIP;
-        topk_wave(r.logits, r.E, r.k, r.renorm, r.remap, r.pmap, r.arena_mode, r.layer, s_w,
-                  s_ids);
+    const int E = r.E, k = r.k;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) s_lg[e] = r.logits[e];
+    if (threadIdx.x < IDS_ROW) s_ids[threadIdx.x] = (int32_t)SKIP;
+    __syncthreads();
+    const int P = E <= 64 ? 4 : E <= 128 ? 2 : 1;  // threads per logit
+    const int per = (int)blockDim.x / P;
+    for (int e0 = 0; e0 < E; e0 += per) {
+        const int e = e0 + (int)threadIdx.x / P, part = (int)threadIdx.x % P;
+        int cnt = 0;
+        if (e < E) {
+            const float v = s_lg[e];
+            const int j1 = (part + 1) * E / P;
+            for (int j = part * E / P; j < j1; j++) {
+                const float u = s_lg[j];
+                cnt += (u > v) || (u == v && j < e);
+            }
+        }
+        if (P >= 2) cnt += __shfl_xor(cnt, 1);
+        if (P >= 4) cnt += __shfl_xor(cnt, 2);
+        if (e < E && part == 0 && cnt < k) s_ids[cnt] = e;
     }
     __syncthreads();
-    if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x < 64) {
-        if (r.ids_out) r.ids_out[threadIdx.x] = s_ids[threadIdx.x];
-        if (r.wts_out && threadIdx.x < r.k) r.wts_out[threadIdx.x] = s_w[threadIdx.x];
+    if ((int)threadIdx.x < k) {
+        const int s = threadIdx.x;
+        const uint32_t e = (uint32_t)s_ids[s];
+        const uint32_t h = r.remap ? r.remap[e] : e;
+        if (h != SKIP) {
+            s_ids[16 + s] = (int32_t)h;
+        } else {
+            uint32_t a = SKIP;
+            if (r.arena_mode)
+                a = (uint32_t)(r.layer * k + s);
+            else if (r.pmap)
+                a = r.pmap[e];
+            s_ids[32 + s] = (int32_t)a;
+            if (a == SKIP) s_ids[48 + s] = (int32_t)e;
+        }
     }
+    __syncthreads();
+    if (r.ids_out && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 &&
+        threadIdx.x < IDS_ROW)
+        r.ids_out[threadIdx.x] = s_ids[threadIdx.x];
     return s_ids;
 }
 

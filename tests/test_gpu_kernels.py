@@ -257,9 +257,9 @@ def test_attention_paged(gpu, nh, nkv, hd, n_steps, page):
     pt = rng.permutation(npages).astype(np.int32)   # logical -> physical, scrambled
     kpool, vpool = gpu.zeros(npages * page * kvd * 4), gpu.zeros(npages * page * kvd * 4)
     base = 1e6
-    ts = np.float64(base) ** (-2.0 / hd)
-    invf = np.array([ts ** i for i in range(hd // 2)], np.float64)
-    invb, ptb = gpu.from_numpy(invf), gpu.from_numpy(pt)
+    rope = np.empty((n_ctx, hd // 2, 2), np.float64)
+    lib().styx_rope_table(C.c_float(base), hd, n_ctx, rope.ctypes.data)
+    invb, ptb = gpu.from_numpy(rope), gpu.from_numpy(pt)
     qn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
     kn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
     qnb, knb = gpu.from_numpy(qn), gpu.from_numpy(kn)

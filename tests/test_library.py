@@ -66,3 +66,30 @@ def test_missing_library_fails_loudly(tmp_path):
         str(ROOT), str(tmp_path / "nope.so"))
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True)
     assert "refused" in out.stdout and "no fallback" in out.stdout
+
+
+def test_rope_table_matches_oracle_rotation():
+    """styx_rope_table (host, no GPU) holds the f64 (cos, sin) the oracle's
+    rope_neox evaluates (ops2.rs:426-442): rotating with the table in f64 and
+    rounding to f32 reproduces the oracle bit for bit."""
+    import numpy as np
+    from oracle import oracle as O
+    from styx_amd._lib import load
+    lib = load
+    hd, n_pos, base = 128, 300, 1e6
+    tab = np.empty((n_pos, hd // 2, 2), np.float64)
+    lib().styx_rope_table(C.c_float(base), hd, n_pos, tab.ctypes.data)
+    assert np.array_equal(tab[0, :, 0], np.ones(hd // 2)) and not tab[0, :, 1].any()
+    assert np.allclose(tab[..., 0] ** 2 + tab[..., 1] ** 2, 1.0, atol=1e-15)
+    rng = np.random.default_rng(4)
+    for pos in (1, 17, 299):
+        x = rng.standard_normal(2 * hd).astype(np.float32)
+        half = hd // 2
+        got = np.empty_like(x)
+        for h in range(2):
+            x0 = x[h * hd:h * hd + half].astype(np.float64)
+            x1 = x[h * hd + half:(h + 1) * hd].astype(np.float64)
+            c, s = tab[pos, :, 0], tab[pos, :, 1]
+            got[h * hd:h * hd + half] = (x0 * c - x1 * s).astype(np.float32)
+            got[h * hd + half:(h + 1) * hd] = (x0 * s + x1 * c).astype(np.float32)
+        assert np.array_equal(got, O.rope_neox(x, hd, 2, pos, base))
