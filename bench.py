@@ -79,6 +79,52 @@ def cpu_baseline(m, prompt, seconds: float, threads: int) -> dict:
                       f"{el:.1f}s, C oracle with {threads} OpenMP threads"}
 
 
+def copy_probe(nbytes: int) -> int:
+    """One plain copy of nbytes between two HBM buffers: its HBM counters
+    should read nbytes fetched and nbytes written."""
+    from styx_amd import Gpu
+    gpu = Gpu(0)
+    src, dst = gpu.zeros(nbytes), gpu.buffer(nbytes)
+    gpu.sync()
+    src.copy_to(dst, 0, 0, nbytes)
+    gpu.sync()
+    log(f"copy probe: {nbytes} bytes")
+    src.free(), dst.free()
+    gpu.close()
+    return 0
+
+
+def stream_read_gbs(gpu, nbytes: int = 2 << 30, reps: int = 10) -> float:
+    """Achievable HBM streaming-read bandwidth: styx_op_read_probe (dwordx4
+    loads, 4 in flight per lane, 2048 x 256 threads) over a 2 GiB buffer,
+    wall clock over `reps` back-to-back launches."""
+    from styx_amd import _lib as L
+    buf, out = gpu.buffer(nbytes), gpu.buffer(2048 * 4 * 4)
+    lib = gpu.lib
+    L.check(lib.styx_op_read_probe(gpu.h, buf.ptr, nbytes, out.ptr, 2048))
+    gpu.sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        L.check(lib.styx_op_read_probe(gpu.h, buf.ptr, nbytes, out.ptr, 2048))
+    gpu.sync()
+    el = time.perf_counter() - t0
+    buf.free(), out.free()
+    return nbytes * reps / el / 1e9
+
+
+def traffic_from_profile() -> dict | None:
+    """HBM bytes per k_gate_up launch measured with rocprofv3 --pmc
+    (FETCH_SIZE, WRITE_SIZE), scaled by the copy-kernel calibration; written
+    by the profiling recipe into profiles/gate_up_traffic.json."""
+    p = ROOT / "profiles" / "gate_up_traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text())
+    except ValueError:
+        return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -91,7 +137,12 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=48, help="(testing only) fewer layers")
     ap.add_argument("--no-graph", action="store_true",
                     help="enqueue kernels one by one instead of replaying a HIP graph per token")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run one device-to-device copy of BYTES (the calibration kernel "
+                         "for rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
     args = ap.parse_args()
+    if args.copy_probe:
+        return copy_probe(args.copy_probe)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -108,6 +159,8 @@ def main() -> int:
     n_ctx = len(prompt) + args.warmup + args.steps + args.timing_steps + 8
 
     gpu = Gpu(0)
+    stream_gbs = stream_read_gbs(gpu)
+    log(f"streaming-read probe: {stream_gbs:.1f} GB/s over 2 GiB")
     t0 = time.perf_counter()
     m = MoeModel.synth(gpu, cfg, n_ctx=max(n_ctx, 512), use_graph=not args.no_graph)
     log(f"built synthetic model in {time.perf_counter() - t0:.1f}s on {gpu.name}: "
@@ -141,8 +194,12 @@ def main() -> int:
     roofline = None
     if gu:
         ach = gu["GB/s"]
+        tr = traffic_from_profile()
         roofline = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                    "frac": round(ach / HBM_PEAK_GBS, 4),
+                    "traffic": tr["bytes_per_launch"] if tr else None,
+                    "stream_read_GBps": round(stream_gbs, 1),
+                    "frac_of_stream_read": round(ach / stream_gbs, 4),
                     "kernel": "k_gate_up (expert gate+up dequant-matvec)",
                     "bytes_per_launch": gu["bytes_per_launch"], "avg_us": gu["avg_us"],
                     "launches": gu["launches"]}

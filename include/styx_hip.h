@@ -191,6 +191,11 @@ int styx_op_gather_slabs(styx_gpu *gpu, const void *const src[3], const int64_t 
  * 64 f32 + 64 u32. */
 int styx_op_argmax(styx_gpu *gpu, const float *v, int n, uint32_t *out, float *scratch_val,
                    uint32_t *scratch_idx);
+/* Measurement helper with no counterpart in the reference: reads every
+ * 16-byte word of [p, p + bytes) once with grid x 256 threads (4 loads in
+ * flight per lane) and writes 4*grid fold words to out, so its duration gives
+ * the achievable HBM streaming-read bandwidth of the device. */
+int styx_op_read_probe(styx_gpu *gpu, const void *p, int64_t bytes, uint32_t *out, int grid);
 /* Seeded synthetic data: N(0, sigma) values quantized to GGUF blocks of
  * `type` (n values), or f32 N(mean, sigma). */
 int styx_op_gen_quant(styx_gpu *gpu, int type, uint64_t seed, float sigma, void *dst, int64_t n);

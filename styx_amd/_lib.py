@@ -118,6 +118,7 @@ _SIGS = {
                                   vp, vp, i32, i32, i32, i32, i32, C.c_float]),
     "styx_op_attn_part_floats": (i64, [i32, i32, i32, i32]),
     "styx_rope_table": (None, [C.c_float, i32, i32, vp]),
+    "styx_op_read_probe": (i32, [vp, vp, i64, vp, i32]),
     "styx_op_gather_slabs": (i32, [vp, vp, vp, vp, vp, vp, i32, i32]),
     "styx_op_argmax": (i32, [vp, vp, i32, vp, vp, vp]),
     "styx_op_gen_quant": (i32, [vp, i32, u64, C.c_float, vp, i64]),

@@ -409,6 +409,14 @@ int styx_op_argmax(styx_gpu *g, const float *v, int n, uint32_t *out, float *sv,
     return STYX_OK;
 }
 
+int styx_op_read_probe(styx_gpu *g, const void *p, int64_t bytes, uint32_t *out, int grid)
+{
+    OP_GPU(g);
+    if (!p || !out) return fail(STYX_E_INVALID, "styx_op_read_probe: NULL pointer");
+    OP_RUN(launch_read_probe(g->stream, p, bytes, out, grid), "styx_op_read_probe");
+    return STYX_OK;
+}
+
 int styx_op_gen_quant(styx_gpu *g, int type, uint64_t seed, float sigma, void *dst, int64_t n)
 {
     OP_GPU(g);

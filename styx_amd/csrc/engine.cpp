@@ -832,7 +832,7 @@ int build_model(styx_moe *m, const styx_moe_synth_cfg &c, const std::vector<Tens
     m->rope_base = c.rope_base;
     m->norm_topk = 1;
     if (m->K < 1 || m->K > MAX_TOPK) return fail(STYX_E_INVALID, "n_expert_used must be in [1, 16] (moe.rs:587)");
-    if (m->E < m->K || m->E > MAX_EXPERTS) return fail(STYX_E_INVALID, "n_expert must be in [k, 512]");
+    if (m->E < m->K || m->E > MAX_EXPERTS || m->E % 16) return fail(STYX_E_INVALID, "n_expert must be a multiple of 16 in [k, 512]");
     if (m->nkv < 1 || m->nh % m->nkv || m->nh / m->nkv > 16) return fail(STYX_E_INVALID, "bad head counts");
     if (m->hd != 64 && m->hd != 128 && m->hd != 256) return fail(STYX_E_INVALID, "head_dim must be 64, 128 or 256");
     {

@@ -166,4 +166,8 @@ hipError_t launch_gen_f32(hipStream_t st, uint64_t seed, float mean, float sigma
 
 hipError_t launch_fill_u32(hipStream_t st, uint32_t *p, uint32_t v, int64_t n);
 
+// Streaming-read probe over bytes (multiple of 16); out gets 4*grid words.
+hipError_t launch_read_probe(hipStream_t st, const void *p, int64_t bytes, uint32_t *out,
+                             int grid);
+
 }  // namespace styx

@@ -220,7 +220,7 @@ struct GatherK {
 __global__ void __launch_bounds__(256) k_gather(GatherK a)
 {
     __shared__ int32_t s_ids[IDS_ROW];
-    __shared__ float s_lg[MAX_EXPERTS];
+    __shared__ __align__(16) float s_lg[MAX_EXPERTS];
     const int s = blockIdx.y, t = blockIdx.z;
     uint32_t e, slot;
     if (a.mode == 0) {
@@ -246,6 +246,8 @@ static hipError_t gather_launch(hipStream_t st, const uint8_t *const src[3],
                                 const int64_t dst_slab[3], const int32_t *ids, const Route *route,
                                 int k, int layer, int mode)
 {
+    if (route && (route->E < k || route->E > MAX_EXPERTS || route->E % 16 || route->k != k))
+        return hipErrorInvalidValue;
     GatherK a{};
     if (route) a.route = *route;
     int64_t mx = 0;
@@ -453,6 +455,36 @@ __global__ void k_fill_u32(uint32_t *p, uint32_t v, int64_t n)
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
         p[i] = v;
+}
+
+// Streaming-read probe: every 16-byte word of [p, p + n16*16) is loaded
+// once (4 loads in flight per lane) and folded into one word per workgroup,
+// so the duration measures achievable HBM read bandwidth.
+__global__ void __launch_bounds__(256) k_read_probe(const uint4 *p, int64_t n16, uint32_t *out)
+{
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    uint32_t acc = 0;
+    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const uint4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^
+               d.z ^ d.w;
+    }
+    for (; i < n16; i += stride) {
+        const uint4 a = p[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
+    if ((threadIdx.x & 63) == 0) out[blockIdx.x * 4 + (threadIdx.x >> 6)] = acc;
+}
+
+hipError_t launch_read_probe(hipStream_t st, const void *p, int64_t bytes, uint32_t *out,
+                             int grid)
+{
+    if (bytes < 16 || bytes % 16 || grid < 1 || grid > 65536) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_read_probe, dim3(grid), dim3(256), 0, st, (const uint4 *)p, bytes / 16,
+                       out);
+    return hipGetLastError();
 }
 
 hipError_t launch_fill_u32(hipStream_t st, uint32_t *p, uint32_t v, int64_t n)

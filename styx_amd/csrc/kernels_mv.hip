@@ -98,54 +98,73 @@ __device__ __forceinline__ LaneMap lane_map(int G)
     return m;
 }
 
-// The activation limbs of one lane's units, loaded once and kept in
-// registers for every row the lane visits.
-template <int T, int UPL> struct LaneX {
-    UX<T> x[UPL];
-    int ub[UPL], us[UPL];
+// Units of one lane: unit gl + u*G of every row it visits.
+template <int UPL> struct LaneU {
+    int ub[UPL], us[UPL];  // block, sub-unit
     bool uv[UPL];
+    int un[UPL];           // unit index in the row
 };
 
 template <int T, int UPL>
-__device__ __forceinline__ void lane_x_load(LaneX<T, UPL> &lx, const Xq &q, int nb, int G)
+__device__ __forceinline__ LaneU<UPL> lane_units(const LaneMap &lm, int nb, int G)
 {
     constexpr int UPB = T == T_Q8_0 ? 1 : 4;
-    const LaneMap lm = lane_map(G);
-    const int units = nb * UPB;
+    LaneU<UPL> lu;
 #pragma unroll
     for (int u = 0; u < UPL; u++) {
-        const int un = lm.gl + u * G;
-        lx.uv[u] = lm.ok && un < units;
-        lx.ub[u] = un / UPB;
-        lx.us[u] = un % UPB;
-        if (lx.uv[u]) ux_load<T>(lx.x[u], q, un);
+        lu.un[u] = lm.gl + u * G;
+        lu.uv[u] = lm.ok && lu.un[u] < nb * UPB;
+        lu.ub[u] = lu.un[u] / UPB;
+        lu.us[u] = lu.un[u] % UPB;
+    }
+    return lu;
+}
+
+template <int T, int UPL>
+__device__ __forceinline__ void issue_rows(UW<T> (&w0)[UPL], UW<T> (&w1)[UPL], const LaneU<UPL> &lu,
+                                           const Mat &mat, int nb, int r, int r2, bool has1,
+                                           bool has2)
+{
+#pragma unroll
+    for (int u = 0; u < UPL; u++) {
+        if (lu.uv[u]) {
+            if (has1) uw_load<T>(w0[u], mat, (int64_t)r * nb + lu.ub[u], lu.us[u]);
+            if (has2) uw_load<T>(w1[u], mat, (int64_t)r2 * nb + lu.ub[u], lu.us[u]);
+        }
     }
 }
 
-template <int T, int UPL, typename Emit>
-__device__ inline void walk_rows_x(const LaneX<T, UPL> &lx, const Mat &mat, int nb, int G,
-                                   int r_begin, int r_end, Emit emit)
+// Row walker: the calling workgroup's lane groups cover rows
+// [r_begin, r_end) two at a time; the result of row r goes to emit(r, v) on
+// the group leader.  The first rows' weight loads are issued before
+// xload(x, lu) fetches (or builds) the lane's activation limbs, so the
+// activation trip overlaps the HBM latency; each next pair of rows is
+// issued as soon as the previous one is consumed.
+template <int T, int UPL, typename XLoad, typename Emit>
+__device__ inline void walk_rows_pf(const Mat &mat, int nb, int G, int r_begin, int r_end,
+                                    XLoad xload, Emit emit)
 {
     const LaneMap lm = lane_map(G);
-    for (int r = r_begin + lm.gid; r < r_end; r += 2 * lm.ngrp) {
+    const LaneU<UPL> lu = lane_units<T, UPL>(lm, nb, G);
+    int r = r_begin + lm.gid;
+    UW<T> w0[UPL], w1[UPL];
+    issue_rows<T, UPL>(w0, w1, lu, mat, nb, r, r + lm.ngrp, r < r_end, r + lm.ngrp < r_end);
+    UX<T> x[UPL];
+    xload(x, lu);
+    for (; r < r_end; r += 2 * lm.ngrp) {
         const int r2 = r + lm.ngrp;
         const bool has2 = r2 < r_end;
-        UW<T> w0[UPL], w1[UPL];
-#pragma unroll
-        for (int u = 0; u < UPL; u++) {
-            if (lx.uv[u]) {
-                uw_load<T>(w0[u], mat, (int64_t)r * nb + lx.ub[u], lx.us[u]);
-                if (has2) uw_load<T>(w1[u], mat, (int64_t)r2 * nb + lx.ub[u], lx.us[u]);
-            }
-        }
         float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
         for (int u = 0; u < UPL; u++) {
-            if (lx.uv[u]) {
-                a0 += udot(w0[u], lx.x[u]);
-                if (has2) a1 += udot(w1[u], lx.x[u]);
+            if (lu.uv[u]) {
+                a0 += udot(w0[u], x[u]);
+                if (has2) a1 += udot(w1[u], x[u]);
             }
         }
+        const int rn = r + 2 * lm.ngrp;
+        issue_rows<T, UPL>(w0, w1, lu, mat, nb, rn, rn + lm.ngrp, rn < r_end,
+                           rn + lm.ngrp < r_end);
         a0 = group_sum(a0, lm.gl, G);
         a1 = group_sum(a1, lm.gl, G);
         if (lm.ok && lm.gl == 0) {
@@ -155,13 +174,22 @@ __device__ inline void walk_rows_x(const LaneX<T, UPL> &lx, const Mat &mat, int 
     }
 }
 
+// Limbs of the lane's units from an Xq vector (global memory or LDS).
+template <int T, int UPL> struct XFrom {
+    Xq q;
+    __device__ __forceinline__ void operator()(UX<T> (&x)[UPL], const LaneU<UPL> &lu) const
+    {
+#pragma unroll
+        for (int u = 0; u < UPL; u++)
+            if (lu.uv[u]) ux_load<T>(x[u], q, lu.un[u]);
+    }
+};
+
 template <int T, int UPL, typename Emit>
 __device__ inline void walk_rows(const Xq &q, const Mat &mat, int nb, int G, int r_begin,
                                  int r_end, Emit emit)
 {
-    LaneX<T, UPL> lx;
-    lane_x_load<T, UPL>(lx, q, nb, G);
-    walk_rows_x<T, UPL>(lx, mat, nb, G, r_begin, r_end, emit);
+    walk_rows_pf<T, UPL>(mat, nb, G, r_begin, r_end, XFrom<T, UPL>{q}, emit);
 }
 
 // Units per lane are a compile-time parameter of every matvec kernel: one
@@ -408,27 +436,25 @@ struct GateUpK {
     int F, k, nb, rpw;
 };
 
-// The lane's activation limbs are loaded before the routing so both
-// memory trips overlap.
+// Routing first (one trip for the logits, then LDS work), then the slot's
+// weight loads, then the activation limbs.
 template <int T, int UPL>
 __device__ inline void gate_up_body(const GateUpK &a, int m, int s, int32_t *s_ids, float *s_lg)
 {
-    LaneX<T, UPL> lx;
-    lane_x_load<T, UPL>(lx, a.xq, a.nb, a.G);
     const int32_t *ids = a.route.logits ? route_ids_wg(a.route, s_ids, s_lg) : a.ids;
     const uint8_t *slab = slab_for(a.src[m], ids, s);
     if (!slab) return;
     const Mat mat = mat_at(slab, T, (int64_t)a.F * a.nb);
     const int r_begin = blockIdx.x * a.rpw, r_end = min(a.F, r_begin + a.rpw);
     float *y = a.gu + ((int64_t)m * a.k + s) * a.F;
-    walk_rows_x<T, UPL>(lx, mat, a.nb, a.G, r_begin, r_end, [=](int r, float v) { y[r] = v; });
+    walk_rows<T, UPL>(a.xq, mat, a.nb, a.G, r_begin, r_end, [=](int r, float v) { y[r] = v; });
 }
 
 template <int TG, int TU, int UPL>
 __global__ void __launch_bounds__(WG) k_gate_up(GateUpK a)
 {
     __shared__ int32_t s_ids[IDS_ROW];
-    __shared__ float s_lg[MAX_EXPERTS];
+    __shared__ __align__(16) float s_lg[MAX_EXPERTS];
     const int s = blockIdx.y, m = blockIdx.z;
     if (m == 0)
         gate_up_body<TG, UPL>(a, 0, s, s_ids, s_lg);
@@ -461,7 +487,7 @@ hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, c
     const Geo gg = pick_geo(tg, H);
     if (!gg.G || blk_elems(tg) != blk_elems(tu) || k < 1 || k > MAX_TOPK || !xq.A)
         return hipErrorInvalidValue;
-    if (route && (route->E < k || route->E > MAX_EXPERTS || route->k != k))
+    if (route && (route->E < k || route->E > MAX_EXPERTS || route->E % 16 || route->k != k))
         return hipErrorInvalidValue;
     if (!route && !ids) return hipErrorInvalidValue;
     GateUpK a{};
@@ -507,25 +533,44 @@ __global__ void __launch_bounds__(WG) k_down(DownK a)
     const int s = blockIdx.y;
     const int r_begin = blockIdx.x * a.rpw, r_end = min(a.H, r_begin + a.rpw);
     // the id row and this slot's gate/up rows are independent loads: issue
-    // both, then swiglu_f32 (ops2.rs:305-309) into LDS
+    // both; the weights go out as soon as the ids are in, and swiglu_f32
+    // (ops2.rs:305-309) with the limbs of its output is built in LDS while
+    // they are in flight
     int32_t idr[3];
 #pragma unroll
     for (int j = 0; j < 3; j++) idr[j] = a.ids[16 * (j + 1) + s];
-    float *hs = (float *)lds;
+    constexpr int PG = 4;  // gate/up values per thread held in registers
     const float *g = a.gu + (int64_t)s * a.F, *u = a.gu + ((int64_t)a.k + s) * a.F;
-    for (int i = threadIdx.x; i < a.F; i += WG) hs[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+    float gv[PG], uv[PG];
+#pragma unroll
+    for (int j = 0; j < PG; j++) {
+        const int i = threadIdx.x + WG * j;
+        gv[j] = i < a.F ? g[i] : 0.0f;
+        uv[j] = i < a.F ? u[i] : 0.0f;
+    }
     const uint8_t *slab = slab_pick(a.src, (uint32_t)idr[0], (uint32_t)idr[1], (uint32_t)idr[2]);
     float *part = a.partial + (int64_t)s * a.H;
     if (!slab) {
         for (int r = r_begin + threadIdx.x; r < r_end; r += WG) part[r] = 0.0f;
         return;
     }
-    __syncthreads();
-    const Xq q = xq_at(lds + (size_t)a.F * 4, a.F);
-    xq_build(hs, nullptr, 0.0f, false, a.F, q, red, nullptr);
-    __syncthreads();
     const Mat mat = mat_at(slab, T, (int64_t)a.H * a.nb);
-    walk_rows<T, UPL>(q, mat, a.nb, a.G, r_begin, r_end, [=](int r, float v) { part[r] = v; });
+    float *hs = (float *)lds;
+    const Xq q = xq_at(lds + (size_t)a.F * 4, a.F);
+    auto build = [&](UX<T> (&x)[UPL], const LaneU<UPL> &lu) {
+#pragma unroll
+        for (int j = 0; j < PG; j++) {
+            const int i = threadIdx.x + WG * j;
+            if (i < a.F) hs[i] = gv[j] / (1.0f + expf(-gv[j])) * uv[j];
+        }
+        for (int i = threadIdx.x + WG * PG; i < a.F; i += WG) hs[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+        __syncthreads();
+        xq_build(hs, nullptr, 0.0f, false, a.F, q, red, nullptr);
+        __syncthreads();
+        XFrom<T, UPL>{q}(x, lu);
+    };
+    walk_rows_pf<T, UPL>(mat, a.nb, a.G, r_begin, r_end, build,
+                         [=](int r, float v) { part[r] = v; });
 }
 
 hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_t *ids,

@@ -93,21 +93,28 @@ __device__ __noinline__ void topk_wave(const float *logits, int n, int k, int re
 // The workgroup with all-zero block index publishes the id row to r.ids_out.
 __device__ inline const int32_t *route_ids_wg(const Route &r, int32_t *s_ids, float *s_lg)
 {
-    const int E = r.E, k = r.k;
-    for (int e = threadIdx.x; e < E; e += blockDim.x) s_lg[e] = r.logits[e];
+    const int E = r.E, k = r.k;  // E % 16 == 0 (checked at launch)
+    for (int e = threadIdx.x; e < E / 4; e += blockDim.x)
+        ((float4 *)s_lg)[e] = ((const float4 *)r.logits)[e];
     if (threadIdx.x < IDS_ROW) s_ids[threadIdx.x] = (int32_t)SKIP;
     __syncthreads();
     const int P = E <= 64 ? 4 : E <= 128 ? 2 : 1;  // threads per logit
-    const int per = (int)blockDim.x / P;
+    const int per = (int)blockDim.x / P, span = E / P;  // span % 4 == 0
     for (int e0 = 0; e0 < E; e0 += per) {
         const int e = e0 + (int)threadIdx.x / P, part = (int)threadIdx.x % P;
         int cnt = 0;
         if (e < E) {
             const float v = s_lg[e];
-            const int j1 = (part + 1) * E / P;
-            for (int j = part * E / P; j < j1; j++) {
-                const float u = s_lg[j];
-                cnt += (u > v) || (u == v && j < e);
+            const int j0 = part * span;
+            const float4 *q = (const float4 *)(s_lg + j0);
+#pragma unroll 8
+            for (int j4 = 0; j4 < span / 4; j4++) {
+                const float4 u = q[j4];
+                const int j = j0 + 4 * j4;
+                cnt += (u.x > v) || (u.x == v && j < e);
+                cnt += (u.y > v) || (u.y == v && j + 1 < e);
+                cnt += (u.z > v) || (u.z == v && j + 2 < e);
+                cnt += (u.w > v) || (u.w == v && j + 3 < e);
             }
         }
         if (P >= 2) cnt += __shfl_xor(cnt, 1);
