@@ -11,6 +11,18 @@ in [0, 151936) (seed 0xC0FFEE) is prefilled, W warmup tokens are decoded,
 then exactly K greedy decode steps are timed (one step = one full forward
 pass of one token, device-side argmax, no host round trip per token).
 
+--config k runs BASELINE.json configs[k-1] instead (SURVEY numbering):
+  1  one qwen3moe layer, q8_0 experts (H 2048, E 128, k 8, F 768): the
+     per-kernel table is the measurement (gate+up, down, reduce)
+  2  the default above
+  3  config 2 with a Zipf(1.1) router bias, experts in pinned host memory
+     and a 6 GiB HBM budget pinned by the bias's expected popularity;
+     reports the hit rate and that tokens equal the all-in-HBM run
+  4  235B-A22B shape (H 4096, 94 layers, 64/4 heads, F 1536, q4_K experts)
+     decoded after synthetic contexts of 512, 4096 and 32768 tokens
+  5  80B-A3B MoE shape (E 512, k 10, F 512, shared expert 512, gate/up
+     q4_K, down q6_K), 48 layers
+
 The JSON line carries:
   value      decode tok/s over the K timed steps
   roofline   the dominant kernel (expert gate/up dequant-matvec, k_gate_up):
@@ -65,18 +77,23 @@ def cpu_baseline(m, prompt, seconds: float, threads: int) -> dict:
     log(f"cpu baseline: exported model to host in {time.perf_counter() - t0:.1f}s")
     O.set_threads(threads)
     n, pos, tok = 0, 0, int(prompt[0])
+    gen = []  # greedy tokens: argmax after the last prompt token, then after each of them
     t0 = time.perf_counter()
     while True:
         logits, *_ = orc.forward(pos, tok)
         n += 1
         pos += 1
-        tok = int(prompt[pos]) if pos < len(prompt) else O.argmax(logits)
+        if pos >= len(prompt):
+            tok = O.argmax(logits)
+            gen.append(tok)
+        else:
+            tok = int(prompt[pos])
         el = time.perf_counter() - t0
         if el >= seconds or pos >= orc.n_ctx:
             break
     return {"value": round(n / el, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} full forward passes (prompt then greedy) of the configs[1] model, "
-                      f"{el:.1f}s, C oracle with {threads} OpenMP threads"}
+            "sample": f"{n} full forward passes (prompt then greedy) of the same model, "
+                      f"{el:.1f}s, C oracle with {threads} OpenMP threads"}, gen
 
 
 def copy_probe(nbytes: int) -> int:
@@ -125,16 +142,91 @@ def traffic_from_profile() -> dict | None:
         return None
 
 
+def config_setup(k: int, layers: int | None):
+    """(synth config, workload text, extra model options) of config k."""
+    from dataclasses import replace
+    from styx_amd import CFG_30B_A3B, CFG_LAYER_Q8, SynthConfig
+    from styx_amd import _lib as L
+    if k == 1:
+        cfg, text = CFG_LAYER_Q8, ("configs[0]: one qwen3moe layer (H 2048, 32/4 heads, E 128, "
+                                   "top-8, F 768), q8_0 experts and attention, vocab 4096")
+    elif k in (2, 3):
+        cfg = CFG_30B_A3B
+        text = ("configs[1]: 48-layer Qwen3-30B-A3B-shaped synthetic qwen3moe, experts mixed "
+                "q4_K/q5_K/q6_K, attention/embedding/head q8_0, all resident in HBM; greedy "
+                "decode after a 16-token prompt")
+        if k == 3:
+            cfg = replace(cfg, router_zipf_s=1.1)
+            text = ("configs[2]: configs[1] with a Zipf(1.1) router bias, experts in pinned host "
+                    "memory, 6 GiB HBM expert budget pinned by expected popularity, cold slabs "
+                    "gathered into the HBM arena in-stream")
+    elif k == 4:
+        cfg = SynthConfig(n_layers=94, n_embd=4096, n_heads=64, n_kv_heads=4, head_dim=128,
+                          n_expert=128, n_expert_used=8, n_ff_exp=1536,
+                          exp_type=(L.Q4_K, L.Q4_K, L.Q4_K))
+        text = ("configs[3]: 94-layer Qwen3-235B-A22B shape (H 4096, 64/4 heads, E 128, top-8, "
+                "F 1536), q4_K experts, q8_0 attention/head; decode after synthetic contexts")
+    elif k == 5:
+        cfg = SynthConfig(n_layers=48, n_embd=2048, n_heads=16, n_kv_heads=2, head_dim=128,
+                          n_expert=512, n_expert_used=10, n_ff_exp=512, n_ff_shexp=512,
+                          exp_type=(L.Q4_K, L.Q4_K, L.Q6_K))
+        text = ("configs[4]: 48-layer 80B-A3B MoE shape (H 2048, E 512, top-10, F 512, shared "
+                "expert 512), gate/up q4_K, down q6_K")
+    else:
+        raise SystemExit(f"bench.py: unknown --config {k}")
+    if layers:
+        cfg = replace(cfg, n_layers=layers)
+    return cfg, text
+
+
+def expected_popularity_csv(m, path: Path) -> None:
+    """Popularity input for config 3: the Zipf bias b_e = -s ln(rank) makes
+    expert e about exp(b_e) times as likely; hits = round(1e6 exp(b_e))."""
+    rows = ["layer,expert,hits"]
+    for l in range(m.hp.n_layers):
+        _, _, data = m.export_tensor(f"blk.{l}.ffn_gate_inp.bias")
+        b = data.view(np.float32)
+        rows += [f"{l},{e},{int(round(1e6 * np.exp(b[e])))}" for e in range(len(b))]
+    path.write_text("\n".join(rows) + "\n")
+
+
+def measure(m, args, prompt):
+    """Prefill, warmup, K timed greedy steps, then per-launch timing steps.
+    Returns (tok/s, seconds, greedy tokens produced after the first)."""
+    gpu = m.gpu
+    t0 = time.perf_counter()
+    for t in prompt:
+        m.forward_token(int(t), want_logits=False)
+    log(f"prefill {len(prompt)} tokens in {time.perf_counter() - t0:.3f}s")
+    toks = [m.decode(args.warmup)] if args.warmup else []
+    gpu.sync()
+    t0 = time.perf_counter()
+    toks.append(m.decode(args.steps))
+    gpu.sync()
+    el = time.perf_counter() - t0
+    log(f"decode {args.steps} steps in {el:.4f}s = {args.steps / el:.1f} tok/s; "
+        f"first tokens {toks[-1][:8].tolist()}")
+    m.set_timing(True)
+    m.kernel_stats_reset()
+    toks.append(m.decode(args.timing_steps))
+    stats = m.kernel_stats()
+    m.set_timing(False)
+    return args.steps / el, el, np.concatenate(toks), stats
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--config", type=int, default=2, help="SURVEY config number, 1-5 (default 2)")
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--timing-steps", type=int, default=16,
                     help="extra decode steps run with per-launch HIP event timing")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--layers", type=int, default=48, help="(testing only) fewer layers")
+    ap.add_argument("--layers", type=int, default=None, help="(testing only) fewer layers")
+    ap.add_argument("--contexts", default="512,4096,32768",
+                    help="config 4: synthetic context lengths to decode after")
     ap.add_argument("--no-graph", action="store_true",
                     help="enqueue kernels one by one instead of replaying a HIP graph per token")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -150,10 +242,9 @@ def main() -> int:
               "single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
         return 2
 
-    from styx_amd import CFG_30B_A3B, Gpu, MoeModel
-    from dataclasses import replace
+    from styx_amd import Gpu, MoeModel
 
-    cfg = replace(CFG_30B_A3B, n_layers=args.layers)
+    cfg, workload = config_setup(args.config, args.layers)
     rng = np.random.default_rng(0xC0FFEE)
     prompt = rng.integers(0, cfg.n_vocab, 16).astype(np.uint32)
     n_ctx = len(prompt) + args.warmup + args.steps + args.timing_steps + 8
@@ -161,40 +252,70 @@ def main() -> int:
     gpu = Gpu(0)
     stream_gbs = stream_read_gbs(gpu)
     log(f"streaming-read probe: {stream_gbs:.1f} GB/s over 2 GiB")
+    extra = {}
     t0 = time.perf_counter()
-    m = MoeModel.synth(gpu, cfg, n_ctx=max(n_ctx, 512), use_graph=not args.no_graph)
+    if args.config == 4:
+        ctxs = [int(c) for c in args.contexts.split(",") if c]
+        m = MoeModel.synth(gpu, cfg, n_ctx=max(ctxs) + n_ctx, use_graph=not args.no_graph)
+    else:
+        m = MoeModel.synth(gpu, cfg, n_ctx=max(n_ctx, 512), use_graph=not args.no_graph)
     log(f"built synthetic model in {time.perf_counter() - t0:.1f}s on {gpu.name}: "
         f"{m.hp.expert_bytes_hbm / 2**30:.2f} GiB experts in HBM, slab {m.slab_bytes} B")
 
-    t0 = time.perf_counter()
-    for t in prompt:
-        m.forward_token(int(t), want_logits=False)
-    log(f"prefill {len(prompt)} tokens in {time.perf_counter() - t0:.3f}s")
-    if args.warmup:
-        m.decode(args.warmup)
+    if args.config == 3:
+        # the all-in-HBM run with the same bias is the reference stream
+        value_hbm, _, toks_hbm, _ = measure(m, args, prompt)
+        hist = Path(os.environ.get("TMPDIR", "/tmp")) / f"styx_zipf_hist_{os.getpid()}.csv"
+        expected_popularity_csv(m, hist)
+        m.close()
+        t0 = time.perf_counter()
+        m = MoeModel.synth(gpu, cfg, n_ctx=max(n_ctx, 512), use_graph=not args.no_graph,
+                           expert_budget_mb=6144, expert_hist=str(hist), arena=True)
+        log(f"host-pinned model in {time.perf_counter() - t0:.1f}s: "
+            f"{m.hp.expert_bytes_hbm / 2**30:.2f} GiB hot in HBM, "
+            f"{m.hp.expert_bytes_host / 2**30:.2f} GiB in host memory")
+        extra["all_in_hbm_tok_s"] = round(value_hbm, 3)
 
-    gpu.sync()
-    t0 = time.perf_counter()
-    toks = m.decode(args.steps)
-    gpu.sync()
-    el = time.perf_counter() - t0
-    value = args.steps / el
-    log(f"decode {args.steps} steps in {el:.4f}s = {value:.1f} tok/s; first tokens {toks[:8].tolist()}")
-
-    # per-launch HIP event timing on the engine's stream
-    m.set_timing(True)
-    m.kernel_stats_reset()
-    m.decode(args.timing_steps)
-    stats = m.kernel_stats()
-    m.set_timing(False)
-    table = kernel_table(stats)
+    if args.config == 4:
+        per_ctx = {}
+        for c in ctxs:
+            m.reset()
+            m.fill_kv(c)
+            args_c = argparse.Namespace(**vars(args))
+            args_c.warmup = min(args.warmup, 4)
+            v, el, toks, stats = measure(m, args_c, prompt[:1])
+            per_ctx[str(c)] = {"tok_s": round(v, 3), "ms_per_step": round(1e3 * el / args.steps, 4),
+                               "kernels": kernel_table(stats)}
+            log(f"context {c}: {v:.1f} tok/s")
+        value, el = per_ctx[str(ctxs[-1])]["tok_s"], None
+        el = args.steps / value
+        table = per_ctx[str(ctxs[-1])]["kernels"]
+        extra["contexts"] = per_ctx
+        toks = None
+    else:
+        value, el, toks, stats = measure(m, args, prompt)
+        table = kernel_table(stats)
     for k, v in table.items():
         log(f"  {k:18s} {v}")
+
+    if args.config == 3:
+        hc = m.last_hot_cold()
+        extra["tokens_equal_all_in_hbm"] = bool(np.array_equal(toks, toks_hbm))
+        # hit rate over a few more tokens (HUD, generate_moe.rs:87-119)
+        hot = cold = 0
+        for _ in range(8):
+            m.decode(1)
+            hc = m.last_hot_cold()
+            hot += int(hc[:, 0].sum())
+            cold += int(hc[:, 1].sum())
+        extra["hit_rate"] = round(hot / max(hot + cold, 1), 4)
+        hist.unlink(missing_ok=True)
+
     gu = table.get("moe_gate_up", {})
     roofline = None
     if gu:
         ach = gu["GB/s"]
-        tr = traffic_from_profile()
+        tr = traffic_from_profile() if args.config == 2 else None
         roofline = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(ach / HBM_PEAK_GBS, 4),
                     "traffic": tr["bytes_per_launch"] if tr else None,
@@ -205,26 +326,32 @@ def main() -> int:
                     "launches": gu["launches"]}
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.config in (1, 2, 5):
+        m.reset()
         threads = min(16, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
-        cpu = cpu_baseline(m, prompt, args.cpu_seconds, threads)
+        cpu, gen = cpu_baseline(m, prompt, args.cpu_seconds, threads)
         log(f"cpu baseline: {cpu}")
+        # the GPU stream starts one token after the oracle's first greedy token
+        n_cmp = min(len(gen) - 1, len(toks))
+        extra["greedy_tokens_verified"] = n_cmp
+        extra["greedy_identical"] = bool(np.array_equal(np.asarray(gen[1:1 + n_cmp], np.uint32),
+                                                        toks[:n_cmp]))
+        log(f"greedy stream vs oracle: {n_cmp} tokens, identical={extra['greedy_identical']}")
 
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * el / args.steps, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "configs[1]: 48-layer Qwen3-30B-A3B-shaped synthetic qwen3moe, "
-                               "experts mixed q4_K/q5_K/q6_K, attention/embedding/head q8_0, "
-                               "all resident in HBM; greedy decode after a 16-token prompt",
-                   "n_layers": cfg.n_layers, "hidden": cfg.n_embd, "experts": cfg.n_expert,
-                   "top_k": cfg.n_expert_used, "expert_ffn": cfg.n_ff_exp, "vocab": cfg.n_vocab,
-                   "batch": 1, "parallelism": "single GPU"},
+        "config": {"workload": workload, "n_layers": cfg.n_layers, "hidden": cfg.n_embd,
+                   "experts": cfg.n_expert, "top_k": cfg.n_expert_used,
+                   "expert_ffn": cfg.n_ff_exp, "vocab": cfg.n_vocab, "batch": 1,
+                   "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": table,
     }
+    line.update(extra)
     print(json.dumps(line), flush=True)
     m.close()
     gpu.close()

@@ -169,7 +169,10 @@ int styx_op_moe_down_reduce(styx_gpu *gpu, int type_down, const styx_expert_src 
  * q [nh*hd], k/v [nkv*hd] raw projections; q_norm/k_norm [hd] or NULL;
  * rope [n_pos][hd/2][2] f64 (cos, sin) from styx_rope_table, n_pos > *pos;
  * kpool/vpool [pages][page_tokens][nkv*hd];
- * page_table [ceil(n_ctx/page_tokens)]; part: styx_op_attn_part_floats(). */
+ * page_table [ceil(n_ctx/page_tokens)]; part: styx_op_attn_part_floats().
+ * The context is split over max_chunks workgroups per kv head, each of at
+ * least `chunk` tokens (a multiple of 16): a context of n_t tokens uses
+ * max(chunk, ceil16(n_t / max_chunks)) tokens per workgroup. */
 int styx_op_attn_decode(styx_gpu *gpu, const float *q, const float *k, const float *v,
                         const float *q_norm, const float *k_norm, float eps,
                         const double *rope, float *kpool, float *vpool,
@@ -249,6 +252,17 @@ typedef struct {
     float router_zipf_s;     /* >0: router bias -s*ln(rank), seeded ranks */
 } styx_moe_synth_cfg;
 
+/* Popularity pinning plan (crates/model/src/moe.rs:774-813), host only:
+ * rank the "layer,expert,hits" rows of hist_csv by hits (descending; ties in
+ * file order) and pin (layer, expert) slabs of slab_bytes[layer] bytes each
+ * until the next does not fit in budget_mb MiB; without a CSV, whole layers
+ * in order.  remap[l*n_expert + e] = hot slot (rank of e among layer l's
+ * pinned experts) or 0xFFFFFFFF.  This is the placement styx_moe_load and
+ * styx_moe_synth use when opts.expert_budget_mb >= 0.  Needs no GPU. */
+int styx_residency_plan(const char *hist_csv, int n_layers, int n_expert,
+                        const uint64_t *slab_bytes, int64_t budget_mb, uint32_t *remap,
+                        uint64_t *pinned_slabs);
+
 /* MoeModel::load (moe.rs:536-1408) from a GGUF file. */
 int styx_moe_load(styx_gpu *gpu, const char *path, const styx_moe_opts *opts, styx_moe **out);
 /* Build a seeded synthetic model directly in HBM (no file). */
@@ -278,6 +292,15 @@ int styx_moe_last_expert_ids(styx_moe *m, uint32_t *out);
 int styx_moe_last_hot_cold(styx_moe *m, uint32_t *out);
 /* MoeModel::reset (moe.rs:1410-1412). */
 int styx_moe_reset(styx_moe *m);
+/* Synthetic context for long-context measurement (no counterpart in the
+ * reference): fill the K and V rows of positions [0, n_t) of every layer
+ * with N(0, sigma) values (seeded, deterministic) and continue as if n_t
+ * tokens had been forwarded; the next styx_moe_forward_token runs at
+ * position n_t. */
+int styx_moe_fill_kv(styx_moe *m, int n_t, uint64_t seed, float sigma);
+/* Copy K and V rows [t0, t0+n) of one layer to the host ([n][n_kv*hd]
+ * each), through the page table. */
+int styx_moe_read_kv(styx_moe *m, int layer, int t0, int n, float *k, float *v);
 /* Total slab swaps done by repinning (MoeModel.repin_swaps). */
 uint64_t styx_moe_repin_swaps(const styx_moe *m);
 /* Residuals of the last token: [n_layers+1][n_embd] (needs record_hidden). */

@@ -119,6 +119,9 @@ _SIGS = {
     "styx_op_attn_part_floats": (i64, [i32, i32, i32, i32]),
     "styx_rope_table": (None, [C.c_float, i32, i32, vp]),
     "styx_op_read_probe": (i32, [vp, vp, i64, vp, i32]),
+    "styx_residency_plan": (i32, [C.c_char_p, i32, i32, vp, i64, vp, vp]),
+    "styx_moe_fill_kv": (i32, [vp, i32, C.c_uint64, C.c_float]),
+    "styx_moe_read_kv": (i32, [vp, i32, i32, i32, vp, vp]),
     "styx_op_gather_slabs": (i32, [vp, vp, vp, vp, vp, vp, i32, i32]),
     "styx_op_argmax": (i32, [vp, vp, i32, vp, vp, vp]),
     "styx_op_gen_quant": (i32, [vp, i32, u64, C.c_float, vp, i64]),

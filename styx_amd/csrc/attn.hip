@@ -30,6 +30,16 @@ constexpr int AT_WG = 256;
 constexpr int AT_WAVES = AT_WG / 64;
 constexpr int TILE = 16;
 
+// Tokens per chunk for a context of n_t tokens: at least a.chunk (a
+// multiple of 16), and enough that n_t fits in a.max_chunks chunks.  Both
+// kernels evaluate it from the device-side position, so the split follows
+// the live context length inside one captured graph.
+__device__ __forceinline__ int attn_chunk(const AttnArgs &a, int n_t)
+{
+    const int need = (n_t + a.max_chunks - 1) / a.max_chunks;
+    return max(a.chunk, (need + 15) / 16 * 16);
+}
+
 __device__ __forceinline__ int64_t kv_off(const AttnArgs &a, int t, int kvh, int kv_dim)
 {
     const int page = a.page_table[t / a.page_tokens];
@@ -111,23 +121,25 @@ __device__ __forceinline__ float sum16(float v)
 // NHG head groups of HPW heads (HPW <= MAXH) and, when fewer than four
 // groups exist, also split the chunk's 16-token tiles NTS = 4 / NHG ways.
 // EPL = hd / 64 output values per lane.  Every global load of a tile (its
-// K quarter-rows and all 16 V rows) is issued before any of it is used; the
-// first tile's loads go out before the q heads are normalised and rotated,
-// and each next tile's page-table entries while the current one is computed.
+// K quarter-rows and all 16 V rows) is issued before any of it is used: the
+// first tile's before the q heads are normalised and rotated, the next
+// tile's K as soon as this tile's scores are formed and its V as soon as this
+// tile's PV is done, with the page-table entries one tile further ahead.
 template <int MAXH, int EPL>
 __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
 {
     constexpr int HD = 64 * EPL, PPL = (HD / 2 + 63) / 64, SEG = HD / 4;
     const int c = blockIdx.x, kvh = blockIdx.y;
-    const int pos = *a.pos, n_t = pos + 1;
-    const int t0 = c * a.chunk;
+    const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
+    const int t0 = c * chunk;
     if (t0 >= n_t) return;
-    const int t1 = min(n_t, t0 + a.chunk);
+    const int t1 = min(n_t, t0 + chunk);
     const int gqa = a.nh / a.nkv, kv_dim = a.nkv * HD;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nts = AT_WAVES / nhg, hg = wave % nhg, ts = wave / nhg;
     const int g0 = hg * hpw;  // first head (within the kv head's group) of this wave
     const int tl = lane & (TILE - 1), qd = lane >> 4;  // token in tile, quarter of hd
+    const int step = nts * TILE;  // this wave's tiles: tb, tb + step, ...
 
     extern __shared__ __align__(16) float sm[];
     // per wave: q [MAXH][HD] | knew [HD] | vnew [HD] | p [MAXH][TILE]
@@ -154,8 +166,50 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
         for (int e = 0; e < EPL; e++) vn[e] = a.v[(int64_t)kvh * HD + lane * EPL + e];
     }
     int tb = t0 + ts * TILE;
-    int64_t row = 0;  // pool offset of token tb + tl's row (this kv head)
-    if (tb + tl < t1) row = kv_off(a, tb + tl, kvh, kv_dim);
+    // K quarter-row of token tb+tl (this lane) and all 16 V rows of the tile
+    // at [tb, tb+16): rows are pool offsets of each lane's token (lane i of
+    // the first 16 holds token tb+i's)
+    float4 kq[SEG / 4];
+    float vv[TILE][EPL];
+    auto load_k = [&](int64_t row, int tbase) {
+        const bool ok = tbase + tl < t1;
+#pragma unroll
+        for (int j = 0; j < SEG / 4; j++)
+            kq[j] = ok ? *(const float4 *)(a.kpool + row + qd * SEG + 4 * j)
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    };
+    auto load_v = [&](int64_t row, int tbase) {
+        const int nt = min(TILE, t1 - tbase);
+#pragma unroll
+        for (int i = 0; i < TILE; i++) {
+            const int64_t ri = __shfl(row, i);
+#pragma unroll
+            for (int e = 0; e < EPL; e++) vv[i][e] = i < nt ? a.vpool[ri + lane * EPL + e] : 0.0f;
+        }
+    };
+    auto row_of = [&](int tbase) -> int64_t {
+        return tbase + tl < t1 ? kv_off(a, tbase + tl, kvh, kv_dim) : 0;
+    };
+    if (tb < t1) {
+        const int64_t row = row_of(tb);
+        load_k(row, tb);
+        load_v(row, tb);
+    }
+    int64_t row_n = row_of(tb + step);  // the next tile's rows, one tile ahead
+
+    // q heads (and the new k head) normalised and rotated into this wave's
+    // LDS while the first tile's loads are in flight
+#pragma unroll
+    for (int i = 0; i < MAXH; i++)
+        if (i < hpw) head_finish<PPL>(hq[i], cs, a.q_norm != nullptr, a.eps, HD, qs + i * HD);
+    if (owns_pos) {
+        head_finish<PPL>(hk, cs, a.k_norm != nullptr, a.eps, HD, knew);
+#pragma unroll
+        for (int e = 0; e < EPL; e++) vnew[lane * EPL + e] = vn[e];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     float m_run[MAXH], l_run[MAXH], o[MAXH][EPL];
 #pragma unroll
@@ -165,45 +219,11 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
 #pragma unroll
         for (int e = 0; e < EPL; e++) o[g][e] = 0.0f;
     }
-    bool first = true;
-    for (; tb < t1; tb += nts * TILE) {
+    for (; tb < t1; tb += step) {
         const int t = tb + tl;
         const bool tv = t < t1;
-        const int nt = min(TILE, t1 - tb);
-        // all of the tile's loads: this lane's K quarter-row, every V row
-        float4 kq[SEG / 4];
-#pragma unroll
-        for (int j = 0; j < SEG / 4; j++)
-            kq[j] = tv ? *(const float4 *)(a.kpool + row + qd * SEG + 4 * j)
-                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float vv[TILE][EPL];
-#pragma unroll
-        for (int i = 0; i < TILE; i++) {
-            const int64_t ri = __shfl(row, i);  // token tb+i's row, held by lane i
-#pragma unroll
-            for (int e = 0; e < EPL; e++)
-                vv[i][e] = i < nt ? a.vpool[ri + lane * EPL + e] : 0.0f;
-        }
-        // next tile's page-table entry while this one is computed
-        const int tn = tb + nts * TILE;
-        if (tn + tl < t1) row = kv_off(a, tn + tl, kvh, kv_dim);
-        if (first) {
-            // q heads (and the new k head) normalised and rotated into this
-            // wave's LDS while the tile's loads are in flight
-#pragma unroll
-            for (int i = 0; i < MAXH; i++)
-                if (i < hpw) head_finish<PPL>(hq[i], cs, a.q_norm != nullptr, a.eps, HD, qs + i * HD);
-            if (owns_pos) {
-                head_finish<PPL>(hk, cs, a.k_norm != nullptr, a.eps, HD, knew);
-#pragma unroll
-                for (int e = 0; e < EPL; e++) vnew[lane * EPL + e] = vn[e];
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            first = false;
-        }
-        // the token at pos comes from LDS (its pool row is written below)
+        const int tn = tb + step;
+        // the token at pos comes from LDS (its pool row is written at the end)
         if (t == pos) {
 #pragma unroll
             for (int j = 0; j < SEG / 4; j++) kq[j] = *(const float4 *)(knew + qd * SEG + 4 * j);
@@ -230,6 +250,8 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
                 }
             }
         }
+        // kq is free: the next tile's K loads overlap this tile's softmax and PV
+        if (tn < t1) load_k(row_n, tn);
 #pragma unroll
         for (int g = 0; g < MAXH; g++) {
             if (g >= hpw) break;
@@ -262,6 +284,10 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
                 }
             }
         }
+        // vv is free: the next tile's V loads, then the page entries of the
+        // tile after it
+        if (tn < t1) load_v(row_n, tn);
+        row_n = row_of(tn + step);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -327,24 +353,25 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     }
 }
 
-// Merge the per-chunk partials (m, l, o) of one query head in chunk order:
+// Merge the per-chunk partials (m, l, o) of one query head:
 // M = max m_c, L = sum l_c e^(m_c-M), out = sum o_c e^(m_c-M) / L; then the
-// limbs of this head's slice of the output.
+// limbs of this head's slice of the output.  256 threads: the chunk factors
+// in parallel, then 4 chunk groups x 64 lanes (each lane hd/64 values)
+// accumulate their share of the chunks and are summed in LDS.
 __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a)
 {
-    extern __shared__ __align__(16) float xs[];  // [hd] output | [max_chunks] factors
+    extern __shared__ __align__(16) float xs[];  // [hd] out | [4][hd] group sums | [max_chunks] factors
     __shared__ float red[16];
-    __shared__ float s_L;
     const int h = blockIdx.x, gqa = a.nh / a.nkv, hd = a.hd, ps = hd + 2;
-    const int n_t = *a.pos + 1;
-    const int n_active = (n_t + a.chunk - 1) / a.chunk;
+    const int n_t = *a.pos + 1, chunk = attn_chunk(a, n_t);
+    const int n_active = (n_t + chunk - 1) / chunk;
     const int kvh = h / gqa, g = h - kvh * gqa;
-    const float *pk = a.part + (int64_t)kvh * a.max_chunks * gqa * ps + (int64_t)g * ps;
-    float *fc = xs + hd;
-    // chunk statistics in parallel: M, then each chunk's factor e^(m_c - M)
+    const int64_t cs = (int64_t)gqa * ps;  // stride between chunks
+    const float *pk = a.part + (int64_t)kvh * a.max_chunks * cs + (int64_t)g * ps;
+    float *gs = xs + hd, *fc = gs + 4 * hd;
     float mloc = -INFINITY;
     for (int cc = threadIdx.x; cc < n_active; cc += blockDim.x) {
-        const float m = pk[(int64_t)cc * gqa * ps + hd];
+        const float m = pk[cc * cs + hd];
         fc[cc] = m;
         mloc = fmaxf(mloc, m);
     }
@@ -357,14 +384,21 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a)
     for (int cc = threadIdx.x; cc < n_active; cc += blockDim.x) {
         const float f = expf(fc[cc] - M);
         fc[cc] = f;
-        lloc += pk[(int64_t)cc * gqa * ps + hd + 1] * f;
+        lloc += pk[cc * cs + hd + 1] * f;
     }
-    const float L = block_sum(lloc, red);
+    const float L = block_sum(lloc, red);  // its barrier also publishes fc
+    const int grp = threadIdx.x >> 6, lane = threadIdx.x & 63, epl = hd / 64;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+    for (int cc = grp; cc < n_active; cc += 4) {
+        const float f = fc[cc];
+        const float *pp = pk + cc * cs + lane * epl;
+        for (int e = 0; e < epl; e++) acc[e] += pp[e] * f;
+    }
+    for (int e = 0; e < epl; e++) gs[grp * hd + lane * epl + e] = acc[e];
+    __syncthreads();
     for (int i = threadIdx.x; i < hd; i += blockDim.x) {
-        float O = 0.0f;
-#pragma unroll 8
-        for (int cc = 0; cc < n_active; cc++) O += pk[(int64_t)cc * gqa * ps + i] * fc[cc];
-        const float v = O / L;
+        const float v = ((gs[i] + gs[hd + i]) + (gs[2 * hd + i] + gs[3 * hd + i])) / L;
         a.out[(int64_t)h * hd + i] = v;
         xs[i] = v;
     }
@@ -405,8 +439,8 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
         return hipErrorInvalidValue;  // gqa of 5, 7, 9.. above 4 heads per wave
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_combine, dim3(a.nh), dim3(std::max(64, std::min(256, a.hd))),
-                       (size_t)(a.hd + a.max_chunks) * 4, st, a);
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.nh), dim3(256), (size_t)(5 * a.hd + a.max_chunks) * 4,
+                       st, a);
     return hipGetLastError();
 }
 

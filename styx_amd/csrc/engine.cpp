@@ -247,8 +247,9 @@ int styx_moe::setup_runtime()
     if (int r = dalloc(&rlog, E)) return r;
     if (int r = dalloc(&wts, (size_t)L * 16)) return r;
     if (int r = dalloc(&ids, (size_t)L * 64)) return r;
-    if (int r = dalloc(&gu, (size_t)2 * K * F)) return r;
-    if (int r = dalloc(&partial, (size_t)K * H)) return r;
+    // one more slot than k: the shared expert when it runs fused
+    if (int r = dalloc(&gu, (size_t)2 * (K + 1) * F)) return r;
+    if (int r = dalloc(&partial, (size_t)(K + 1) * H)) return r;
     if (int r = dalloc(&logits, V)) return r;
     if (int r = dalloc(&hidden, (size_t)(L + 1) * H)) return r;
     if (int r = dalloc(&am_val, 64)) return r;
@@ -284,10 +285,11 @@ int styx_moe::setup_runtime()
     h_pt.assign((size_t)L * pages_per_layer, -1);
     STYX_HIP(hipMemsetAsync(d_pt, 0, sizeof(int32_t) * L * pages_per_layer, gpu->stream));
     next_page = 0;
-    // attention split: at most ~64 chunks over the full context, 16-token
-    // multiples, at least two tiles per chunk
-    chunk = std::max(32, (n_ctx / 64 + 15) / 16 * 16);
-    max_chunks = (n_ctx + chunk - 1) / chunk;
+    // attention split: chunks of at least 32 tokens; at most ~768
+    // workgroups in all (one round of 4-wave workgroups at 3 waves per SIMD
+    // on 256 CUs); the attention kernels size the chunk from the live context
+    chunk = 32;
+    max_chunks = std::min((n_ctx + chunk - 1) / chunk, std::max(16, 768 / nkv));
     const int64_t pf = styx_op_attn_part_floats(nh, nkv, hd, max_chunks);
     if (int r = dalloc(&attn_part, (size_t)pf)) return r;
     // rope factors in f64 for every position of the context (ops2.rs:426-442)
@@ -325,6 +327,45 @@ int styx_moe::ensure_pages(int upto_pos)
     return STYX_OK;
 }
 
+// Which (layer, expert) slabs go to HBM under a byte budget
+// (crates/model/src/moe.rs:774-813).  With a popularity histogram: rank all
+// (layer, expert) entries by hits, descending (ties keep file order; the
+// reference's sort_unstable leaves them unspecified), and take slabs until
+// the next one does not fit.  Without one: whole layers in order.  Each
+// layer's list comes back sorted, so a hot slot index is the rank of the
+// expert id among that layer's hot experts.
+static void plan_hot_experts(const std::vector<std::vector<std::pair<uint32_t, uint64_t>>> *hist,
+                             int L, int E, const std::vector<uint64_t> &slab_cost,
+                             const std::vector<uint64_t> &layer_cost, uint64_t budget,
+                             std::vector<std::vector<uint32_t>> &hot)
+{
+    hot.assign(L, {});
+    uint64_t left = budget;
+    if (hist) {
+        struct Ent { uint64_t hits; int layer; uint32_t e; };
+        std::vector<Ent> ents;
+        for (int l = 0; l < L && l < (int)hist->size(); l++)
+            for (auto &p : (*hist)[l]) ents.push_back({p.second, l, p.first});
+        std::stable_sort(ents.begin(), ents.end(),
+                         [](const Ent &a, const Ent &b) { return a.hits > b.hits; });
+        std::vector<std::vector<char>> seen(L, std::vector<char>(E, 0));
+        for (auto &en : ents) {
+            if (en.e >= (uint32_t)E || seen[en.layer][en.e]) continue;
+            if (left < slab_cost[en.layer]) break;
+            left -= slab_cost[en.layer];
+            seen[en.layer][en.e] = 1;
+            hot[en.layer].push_back(en.e);
+        }
+    } else {
+        for (int l = 0; l < L; l++) {
+            if (left < layer_cost[l]) break;
+            left -= layer_cost[l];
+            for (int e = 0; e < E; e++) hot[l].push_back((uint32_t)e);
+        }
+    }
+    for (auto &v : hot) std::sort(v.begin(), v.end());
+}
+
 // Placement of expert tensors (moe.rs:692-880).  All experts stay in HBM
 // unless opts.expert_budget_mb >= 0; then every expert tensor lives in
 // pinned host memory and the budget buys HBM copies of the hottest
@@ -350,34 +391,14 @@ int styx_moe::place_experts(const std::vector<std::vector<std::pair<uint32_t, ui
         return STYX_OK;
     }
     any_host = true;
-    uint64_t left = (uint64_t)opts.expert_budget_mb << 20;
-    std::vector<std::vector<uint32_t>> hot(L);
-    if (hist) {
-        // global ranking by hits, stable on ties (moe.rs:774-813)
-        struct Ent { uint64_t hits; int layer; uint32_t e; size_t ord; };
-        std::vector<Ent> ents;
-        size_t ord = 0;
-        for (int l = 0; l < L && l < (int)hist->size(); l++)
-            for (auto &p : (*hist)[l]) ents.push_back({p.second, l, p.first, ord++});
-        std::stable_sort(ents.begin(), ents.end(),
-                         [](const Ent &a, const Ent &b) { return a.hits > b.hits; });
-        for (auto &en : ents) {
-            if (en.e >= (uint32_t)E) continue;
-            const auto &ly = layers[en.layer];
-            const uint64_t cost = ly.gate.slab + ly.up.slab + ly.down.slab;
-            if (left < cost) break;
-            left -= cost;
-            hot[en.layer].push_back(en.e);
-        }
-    } else {
-        for (int l = 0; l < L; l++) {
-            const auto &ly = layers[l];
-            const uint64_t cost = ly.gate.bytes() + ly.up.bytes() + ly.down.bytes();
-            if (left < cost) break;
-            left -= cost;
-            for (int e = 0; e < E; e++) hot[l].push_back((uint32_t)e);
-        }
+    std::vector<std::vector<uint32_t>> hot;
+    std::vector<uint64_t> slab_cost(L), layer_cost(L);
+    for (int l = 0; l < L; l++) {
+        const auto &ly = layers[l];
+        slab_cost[l] = ly.gate.slab + ly.up.slab + ly.down.slab;
+        layer_cost[l] = ly.gate.bytes() + ly.up.bytes() + ly.down.bytes();
     }
+    plan_hot_experts(hist, L, E, slab_cost, layer_cost, (uint64_t)opts.expert_budget_mb << 20, hot);
     for (int l = 0; l < L; l++) {
         auto &ly = layers[l];
         auto &ord = hot[l];
@@ -537,15 +558,23 @@ int styx_moe::enqueue_token(bool gen)
             CK(launch_gather(st, src, sslab, arena, arena_slab, nullptr, &rg, K));
             tend(e0, "gather", 0.0);
         }
-        const double slabs_gu = (double)K * (ly.gate.slab + ly.up.slab);
+        // the shared expert runs as slot K of the expert kernels when it has
+        // the routed experts' width and types; otherwise as dense matvecs
+        const bool sh_fused = ly.gsh.dev && Fsh == F && ly.gsh.type == ly.gate.type &&
+                              ly.ush.type == ly.up.type && ly.dsh.type == ly.down.type;
+        const double sh_gu = sh_fused ? (double)(ly.gsh.bytes() + ly.ush.bytes()) : 0.0;
+        const double slabs_gu = (double)K * (ly.gate.slab + ly.up.slab) + sh_gu;
+        const int nsl = K + (sh_fused ? 1 : 0);
         e0 = tstart();
         CK(launch_moe_gate_up(st, ly.gate.type, ly.up.type, sg, su, nullptr, &rt, xq_f, gu, H, F,
-                              K));
-        tend(e0, "moe_gate_up", slabs_gu + xq_bytes(H) + 4.0 * E + 4.0 * 2 * K * F);
+                              K, sh_fused ? ly.gsh.dev : nullptr, sh_fused ? ly.ush.dev : nullptr));
+        tend(e0, "moe_gate_up", slabs_gu + xq_bytes(H) + 4.0 * E + 4.0 * 2 * nsl * F);
         e0 = tstart();
-        CK(launch_moe_down(st, ly.down.type, sd, lid, gu, partial, H, F, K));
-        tend(e0, "moe_down", (double)K * ly.down.slab + 4.0 * 2 * K * F + 4.0 * K * H);
-        if (ly.gsh.dev) {
+        CK(launch_moe_down(st, ly.down.type, sd, lid, gu, partial, H, F, K,
+                           sh_fused ? ly.dsh.dev : nullptr));
+        tend(e0, "moe_down", (double)K * ly.down.slab + (sh_fused ? (double)ly.dsh.bytes() : 0.0) +
+                                 4.0 * 2 * nsl * F + 4.0 * nsl * H);
+        if (ly.gsh.dev && !sh_fused) {
             e0 = tstart();
             DenseSeg s2[2] = {{ly.gsh.dev, sh_g, Fsh}, {ly.ush.dev, sh_u, Fsh}};
             if (ly.gsh.type == ly.ush.type) {
@@ -571,7 +600,7 @@ int styx_moe::enqueue_token(bool gen)
         rd.wts_out = wts + (size_t)l * 16;
         rd.x = x;
         if (ly.gsh.dev) {
-            rd.sh_y = sh_y;
+            rd.sh_y = sh_fused ? partial + (size_t)K * H : sh_y;
             rd.sh_ginp = ly.gate_inp_sh;
             rd.xn = xn;
         }
@@ -943,6 +972,30 @@ int read_hist(const char *path, int L, std::vector<std::vector<std::pair<uint32_
 // ------------------------------------------------------------------ C ABI --
 extern "C" {
 
+int styx_residency_plan(const char *hist_csv, int n_layers, int n_expert,
+                        const uint64_t *slab_bytes, int64_t budget_mb, uint32_t *remap,
+                        uint64_t *pinned_slabs)
+{
+    if (n_layers < 1 || n_expert < 1 || !slab_bytes || !remap || budget_mb < 0)
+        return fail(STYX_E_INVALID, "styx_residency_plan: bad argument");
+    std::vector<std::vector<std::pair<uint32_t, uint64_t>>> hist;
+    if (hist_csv)
+        if (int r = read_hist(hist_csv, n_layers, hist)) return r;
+    std::vector<uint64_t> slab(slab_bytes, slab_bytes + n_layers), layer(n_layers);
+    for (int l = 0; l < n_layers; l++) layer[l] = slab[l] * (uint64_t)n_expert;
+    std::vector<std::vector<uint32_t>> hot;
+    plan_hot_experts(hist_csv ? &hist : nullptr, n_layers, n_expert, slab, layer,
+                     (uint64_t)budget_mb << 20, hot);
+    uint64_t n = 0;
+    for (int l = 0; l < n_layers; l++) {
+        for (int e = 0; e < n_expert; e++) remap[(size_t)l * n_expert + e] = SKIP;
+        for (size_t i = 0; i < hot[l].size(); i++) remap[(size_t)l * n_expert + hot[l][i]] = (uint32_t)i;
+        n += hot[l].size();
+    }
+    if (pinned_slabs) *pinned_slabs = n;
+    return STYX_OK;
+}
+
 static styx_moe_opts default_opts()
 {
     styx_moe_opts o{};
@@ -1215,6 +1268,45 @@ int styx_moe_reset(styx_moe *m)
 {
     if (!m) return fail(STYX_E_INVALID, "styx_moe_reset: NULL model");
     m->n_past = 0;
+    return STYX_OK;
+}
+
+int styx_moe_fill_kv(styx_moe *m, int n_t, uint64_t seed, float sigma)
+{
+    if (!m || n_t < 1 || n_t >= m->n_ctx)
+        return fail(STYX_E_INVALID, "styx_moe_fill_kv: need 1 <= n_t < n_ctx");
+    STYX_HIP(hipSetDevice(m->gpu->device));
+    if (int r = m->ensure_pages(n_t - 1)) return r;
+    const int64_t kvd = (int64_t)m->nkv * m->hd;
+    for (int l = 0; l < m->L; l++)
+        for (int p = 0; p * KV_PAGE_TOKENS < n_t; p++) {
+            const int32_t phys = m->h_pt[(size_t)l * m->pages_per_layer + p];
+            const int rows = std::min(KV_PAGE_TOKENS, n_t - p * KV_PAGE_TOKENS);
+            const size_t off = (size_t)phys * KV_PAGE_TOKENS * kvd;
+            const uint64_t s = seed ^ (((uint64_t)l << 32) | (uint64_t)p << 1);
+            CK(launch_gen_f32(m->gpu->stream, s, 0.0f, sigma, m->kpool + off, rows * kvd));
+            CK(launch_gen_f32(m->gpu->stream, s | 1u, 0.0f, sigma, m->vpool + off, rows * kvd));
+        }
+    STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+    m->n_past = n_t;
+    return STYX_OK;
+}
+
+int styx_moe_read_kv(styx_moe *m, int layer, int t0, int n, float *k, float *v)
+{
+    if (!m || layer < 0 || layer >= m->L || t0 < 0 || n < 0 || t0 + n > m->n_past || !k || !v)
+        return fail(STYX_E_INVALID, "styx_moe_read_kv: bad argument");
+    STYX_HIP(hipSetDevice(m->gpu->device));
+    const int64_t kvd = (int64_t)m->nkv * m->hd;
+    for (int t = t0; t < t0 + n; t++) {
+        const int32_t phys = m->h_pt[(size_t)layer * m->pages_per_layer + t / KV_PAGE_TOKENS];
+        const size_t off = ((size_t)phys * KV_PAGE_TOKENS + t % KV_PAGE_TOKENS) * kvd;
+        STYX_HIP(hipMemcpyAsync(k + (size_t)(t - t0) * kvd, m->kpool + off, sizeof(float) * kvd,
+                                hipMemcpyDeviceToHost, m->gpu->stream));
+        STYX_HIP(hipMemcpyAsync(v + (size_t)(t - t0) * kvd, m->vpool + off, sizeof(float) * kvd,
+                                hipMemcpyDeviceToHost, m->gpu->stream));
+    }
+    STYX_HIP(hipStreamSynchronize(m->gpu->stream));
     return STYX_OK;
 }
 

@@ -74,14 +74,18 @@ hipError_t launch_topk_softmax(hipStream_t st, const float *logits, int n, int k
 
 // gu[0][s] = Wg[e_s] xn, gu[1][s] = Wu[e_s] xn for the k routed slots, xn
 // given by its limbs; routing from `route` (ranked in-kernel) or, if null,
-// the id row `ids`.
+// the id row `ids`.  With sh_gate/sh_up (split-layout matrices of the same
+// types and width F) the shared expert is slot k: gu is [2][k+1][F].
 hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, const ExpSrc &u,
                               const int32_t *ids, const Route *route, const Xq &xq, float *gu,
-                              int H, int F, int k);
+                              int H, int F, int k, const uint8_t *sh_gate = nullptr,
+                              const uint8_t *sh_up = nullptr);
 
-// partial[s] = Wd[e_s] swiglu(gu[0][s], gu[1][s]) for the k routed slots.
+// partial[s] = Wd[e_s] swiglu(gu[0][s], gu[1][s]) for the k routed slots
+// (and the shared expert's down matrix as slot k if sh_down).
 hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_t *ids,
-                           const float *gu, float *partial, int H, int F, int k);
+                           const float *gu, float *partial, int H, int F, int k,
+                           const uint8_t *sh_down = nullptr);
 
 // One workgroup: w_s from the logits and ids (topk_softmax_f32.comp:29-67)
 // or given; x += sum_s w_s partial[s] (moe_reduce_f32.comp:11-13, fixed slot
@@ -117,7 +121,10 @@ struct AttnArgs {
     float *out;                      // [nh*hd]
     Xq xq;                           // optional limbs of out (o-proj input)
     float *part;                     // [nkv][max_chunks][gqa][hd+2]
-    int nh, nkv, hd, chunk, max_chunks;  // chunk: tokens per workgroup, multiple of 16
+    int nh, nkv, hd;
+    int chunk;       // minimum tokens per workgroup (multiple of 16); a context of
+                     // n_t uses max(chunk, ceil16(n_t / max_chunks))
+    int max_chunks;  // workgroups per kv head (grid); partials are sized by it
     float scale;
 };
 hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a);

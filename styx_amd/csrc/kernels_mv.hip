@@ -428,12 +428,13 @@ hipError_t launch_router_topk(hipStream_t st, const RouterArgs &a)
 // ------------------------------------------------------------ gate / up ---
 struct GateUpK {
     ExpSrc src[2];
+    const uint8_t *sh[2];  // shared expert gate/up matrices (slot k) or null
     int G;
     const int32_t *ids;   // id row in memory, used when route.logits is null
     Route route;
     Xq xq;
-    float *gu;  // [2][k][F]
-    int F, k, nb, rpw;
+    float *gu;  // [2][nslots][F]
+    int F, k, nslots, nb, rpw;
 };
 
 // Routing first (one trip for the logits, then LDS work), then the slot's
@@ -441,12 +442,17 @@ struct GateUpK {
 template <int T, int UPL>
 __device__ inline void gate_up_body(const GateUpK &a, int m, int s, int32_t *s_ids, float *s_lg)
 {
-    const int32_t *ids = a.route.logits ? route_ids_wg(a.route, s_ids, s_lg) : a.ids;
-    const uint8_t *slab = slab_for(a.src[m], ids, s);
+    const uint8_t *slab;
+    if (s < a.k) {
+        const int32_t *ids = a.route.logits ? route_ids_wg(a.route, s_ids, s_lg) : a.ids;
+        slab = slab_for(a.src[m], ids, s);
+    } else {
+        slab = a.sh[m];  // the shared expert needs no routing
+    }
     if (!slab) return;
     const Mat mat = mat_at(slab, T, (int64_t)a.F * a.nb);
     const int r_begin = blockIdx.x * a.rpw, r_end = min(a.F, r_begin + a.rpw);
-    float *y = a.gu + ((int64_t)m * a.k + s) * a.F;
+    float *y = a.gu + ((int64_t)m * a.nslots + s) * a.F;
     walk_rows<T, UPL>(a.xq, mat, a.nb, a.G, r_begin, r_end, [=](int r, float v) { y[r] = v; });
 }
 
@@ -482,7 +488,7 @@ static hipError_t launch_gu_tu(hipStream_t st, int tu, int upl, const GateUpK &a
 
 hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, const ExpSrc &u,
                               const int32_t *ids, const Route *route, const Xq &xq, float *gu,
-                              int H, int F, int k)
+                              int H, int F, int k, const uint8_t *sh_gate, const uint8_t *sh_up)
 {
     const Geo gg = pick_geo(tg, H);
     if (!gg.G || blk_elems(tg) != blk_elems(tu) || k < 1 || k > MAX_TOPK || !xq.A)
@@ -493,6 +499,9 @@ hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, c
     GateUpK a{};
     a.src[0] = g;
     a.src[1] = u;
+    a.sh[0] = sh_gate;
+    a.sh[1] = sh_up;
+    a.nslots = k + ((sh_gate && sh_up) ? 1 : 0);
     a.G = gg.G;
     a.ids = ids;
     if (route) a.route = *route;
@@ -502,8 +511,8 @@ hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, c
     a.k = k;
     a.nb = H / blk_elems(tg);
     // ~1024 workgroups in total over the 2*k slot matrices
-    a.rpw = rows_per_wg(2 * k * F, gg.G, 1024);
-    const dim3 grid((F + a.rpw - 1) / a.rpw, k, 2);
+    a.rpw = rows_per_wg(2 * a.nslots * F, gg.G, 1024);
+    const dim3 grid((F + a.rpw - 1) / a.rpw, a.nslots, 2);
     switch (tg) {
     case T_Q8_0: return launch_gu_tu<T_Q8_0>(st, tu, gg.UPL, a, grid);
     case T_Q4_K: return launch_gu_tu<T_Q4_K>(st, tu, gg.UPL, a, grid);
@@ -518,11 +527,12 @@ hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, c
 // weighted combine into the residual is k_reduce_norm.
 struct DownK {
     ExpSrc src;
+    const uint8_t *sh;  // shared expert down matrix (slot k) or null
     int G, UPL;
     const int32_t *ids;
-    const float *gu;
-    float *partial;
-    int H, F, k, nb, rpw;
+    const float *gu;    // [2][nslots][F]
+    float *partial;     // [nslots][H]
+    int H, F, k, nslots, nb, rpw;
 };
 
 template <int T, int UPL>
@@ -536,11 +546,13 @@ __global__ void __launch_bounds__(WG) k_down(DownK a)
     // both; the weights go out as soon as the ids are in, and swiglu_f32
     // (ops2.rs:305-309) with the limbs of its output is built in LDS while
     // they are in flight
-    int32_t idr[3];
+    int32_t idr[3] = {(int32_t)SKIP, (int32_t)SKIP, (int32_t)SKIP};
+    if (s < a.k) {
 #pragma unroll
-    for (int j = 0; j < 3; j++) idr[j] = a.ids[16 * (j + 1) + s];
+        for (int j = 0; j < 3; j++) idr[j] = a.ids[16 * (j + 1) + s];
+    }
     constexpr int PG = 4;  // gate/up values per thread held in registers
-    const float *g = a.gu + (int64_t)s * a.F, *u = a.gu + ((int64_t)a.k + s) * a.F;
+    const float *g = a.gu + (int64_t)s * a.F, *u = a.gu + ((int64_t)a.nslots + s) * a.F;
     float gv[PG], uv[PG];
 #pragma unroll
     for (int j = 0; j < PG; j++) {
@@ -548,7 +560,8 @@ __global__ void __launch_bounds__(WG) k_down(DownK a)
         gv[j] = i < a.F ? g[i] : 0.0f;
         uv[j] = i < a.F ? u[i] : 0.0f;
     }
-    const uint8_t *slab = slab_pick(a.src, (uint32_t)idr[0], (uint32_t)idr[1], (uint32_t)idr[2]);
+    const uint8_t *slab =
+        s < a.k ? slab_pick(a.src, (uint32_t)idr[0], (uint32_t)idr[1], (uint32_t)idr[2]) : a.sh;
     float *part = a.partial + (int64_t)s * a.H;
     if (!slab) {
         for (int r = r_begin + threadIdx.x; r < r_end; r += WG) part[r] = 0.0f;
@@ -574,12 +587,15 @@ __global__ void __launch_bounds__(WG) k_down(DownK a)
 }
 
 hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_t *ids,
-                           const float *gu, float *partial, int H, int F, int k)
+                           const float *gu, float *partial, int H, int F, int k,
+                           const uint8_t *sh_down)
 {
     const Geo g = pick_geo(td, F);
     if (!g.G || k < 1 || k > MAX_TOPK || F > XQ_MAX / 2) return hipErrorInvalidValue;
     DownK a{};
     a.src = d;
+    a.sh = sh_down;
+    a.nslots = k + (sh_down ? 1 : 0);
     a.G = g.G;
     a.UPL = g.UPL;
     a.ids = ids;
@@ -589,8 +605,8 @@ hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_
     a.F = F;
     a.k = k;
     a.nb = F / blk_elems(td);
-    a.rpw = rows_per_wg(k * H, g.G, 1024);
-    const dim3 grid((H + a.rpw - 1) / a.rpw, k, 1);
+    a.rpw = rows_per_wg(a.nslots * H, g.G, 1024);
+    const dim3 grid((H + a.rpw - 1) / a.rpw, a.nslots, 1);
     const size_t lds = (size_t)F * 4 + xq_bytes(F);
     switch (td) {
     case T_Q8_0: upl_dispatch<T_Q8_0>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_down<T_Q8_0, decltype(u)::value>), grid, dim3(WG), lds, st, a); }); break;

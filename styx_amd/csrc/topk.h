@@ -84,27 +84,36 @@ __device__ __noinline__ void topk_wave(const float *logits, int n, int k, int re
     }
 }
 
-// Top-k ids of the router logits inside a workgroup, by ranking: the rank of
-// logit e is the number of logits ordered before it (a larger value, or an
-// equal value at a lower index -- the strict '>' of topk_softmax_f32.comp:45),
-// so ranks 0..k-1 are exactly the reference's selection order.  Every thread
-// ranks one logit against a slice of the others; no dependent shuffle chain.
+// Top-k ids of the router logits inside a workgroup, by ranking.  Order: a
+// larger value first, equal values by lower index -- the strict '>' of
+// topk_softmax_f32.comp:45 -- so ranks 0..k-1 are exactly the reference's
+// selection order.  Up to 128 experts every logit is ranked against all
+// (2 or 4 threads per logit).  Above that, two levels: each wave ranks the
+// logits of its quarter of the experts among that quarter, those of rank < k
+// are candidates (every global top-k logit is in its quarter's top-k), and
+// the <= 4k candidates are ranked among themselves: E^2/4 + 16k^2 compares
+// per workgroup instead of E^2.  No dependent shuffle chain either way.
 // Fills the four id rows in s_ids (64 ints); weights are left to the caller.
 // The workgroup with all-zero block index publishes the id row to r.ids_out.
+// Needs blockDim.x == 256, E % 16 == 0, E <= 512, k <= 16.
 __device__ inline const int32_t *route_ids_wg(const Route &r, int32_t *s_ids, float *s_lg)
 {
-    const int E = r.E, k = r.k;  // E % 16 == 0 (checked at launch)
+    __shared__ __align__(16) float c_val[4 * MAX_TOPK];
+    __shared__ __align__(16) int32_t c_idx[4 * MAX_TOPK];
+    const int E = r.E, k = r.k, Q = E / 4;  // quarter: Q % 4 == 0
     for (int e = threadIdx.x; e < E / 4; e += blockDim.x)
         ((float4 *)s_lg)[e] = ((const float4 *)r.logits)[e];
     if (threadIdx.x < IDS_ROW) s_ids[threadIdx.x] = (int32_t)SKIP;
+    if (threadIdx.x < 4 * MAX_TOPK) c_idx[threadIdx.x] = -1;
     __syncthreads();
-    const int P = E <= 64 ? 4 : E <= 128 ? 2 : 1;  // threads per logit
-    const int per = (int)blockDim.x / P, span = E / P;  // span % 4 == 0
-    for (int e0 = 0; e0 < E; e0 += per) {
-        const int e = e0 + (int)threadIdx.x / P, part = (int)threadIdx.x % P;
+    if (E <= 128) {
+        // direct: P = 256 / E threads rank each logit against a slice of all
+        const int P = E <= 64 ? 4 : 2, span = E / P;
+        const int e = (int)threadIdx.x / P, part = (int)threadIdx.x % P;
         int cnt = 0;
+        float v = 0.0f;
         if (e < E) {
-            const float v = s_lg[e];
+            v = s_lg[e];
             const int j0 = part * span;
             const float4 *q = (const float4 *)(s_lg + j0);
 #pragma unroll 8
@@ -117,9 +126,47 @@ __device__ inline const int32_t *route_ids_wg(const Route &r, int32_t *s_ids, fl
                 cnt += (u.w > v) || (u.w == v && j + 3 < e);
             }
         }
-        if (P >= 2) cnt += __shfl_xor(cnt, 1);
-        if (P >= 4) cnt += __shfl_xor(cnt, 2);
+        cnt += __shfl_xor(cnt, 1);
+        if (P == 4) cnt += __shfl_xor(cnt, 2);
         if (e < E && part == 0 && cnt < k) s_ids[cnt] = e;
+    } else {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const int q0 = wave * Q;
+        for (int e = q0 + lane; e < q0 + Q; e += 64) {
+            const float v = s_lg[e];
+            const float4 *q = (const float4 *)(s_lg + q0);
+            int cnt = 0;
+#pragma unroll 8
+            for (int j4 = 0; j4 < Q / 4; j4++) {
+                const float4 u = q[j4];
+                const int j = q0 + 4 * j4;
+                cnt += (u.x > v) || (u.x == v && j < e);
+                cnt += (u.y > v) || (u.y == v && j + 1 < e);
+                cnt += (u.z > v) || (u.z == v && j + 2 < e);
+                cnt += (u.w > v) || (u.w == v && j + 3 < e);
+            }
+            if (cnt < k) {
+                c_val[wave * k + cnt] = v;
+                c_idx[wave * k + cnt] = e;
+            }
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < 4 * MAX_TOPK) {
+            // every candidate slot (unused ones hold index -1) against all 64
+            const int e = c_idx[threadIdx.x];
+            const float v = c_val[threadIdx.x];
+            int cnt = 0;
+#pragma unroll
+            for (int j = 0; j < 4 * MAX_TOPK; j += 4) {
+                const int4 ej = *(const int4 *)(c_idx + j);
+                const float4 u = *(const float4 *)(c_val + j);
+                cnt += ej.x >= 0 && ((u.x > v) || (u.x == v && ej.x < e));
+                cnt += ej.y >= 0 && ((u.y > v) || (u.y == v && ej.y < e));
+                cnt += ej.z >= 0 && ((u.z > v) || (u.z == v && ej.z < e));
+                cnt += ej.w >= 0 && ((u.w > v) || (u.w == v && ej.w < e));
+            }
+            if (e >= 0 && cnt < k) s_ids[cnt] = e;
+        }
     }
     __syncthreads();
     if ((int)threadIdx.x < k) {

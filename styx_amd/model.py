@@ -144,6 +144,18 @@ class MoeModel:
     def reset(self) -> None:
         L.check(self.lib.styx_moe_reset(self.h))
 
+    def fill_kv(self, n_t: int, seed: int = 0x4B56, sigma: float = 1.0) -> None:
+        """Synthetic context: K/V rows [0, n_t) ~ N(0, sigma); the next token
+        is forwarded at position n_t."""
+        L.check(self.lib.styx_moe_fill_kv(self.h, int(n_t), int(seed), float(sigma)))
+
+    def read_kv(self, layer: int, t0: int, n: int):
+        kvd = self.hp.n_kv_heads * self.hp.head_dim
+        k = np.empty((n, kvd), np.float32)
+        v = np.empty((n, kvd), np.float32)
+        L.check(self.lib.styx_moe_read_kv(self.h, layer, t0, n, k.ctypes.data, v.ctypes.data))
+        return k, v
+
     @property
     def repin_swaps(self) -> int:
         return int(self.lib.styx_moe_repin_swaps(self.h))

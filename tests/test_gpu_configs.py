@@ -1,0 +1,135 @@
+"""GPU tests of the BASELINE configs at their real shapes (reduced layer
+counts where the oracle would be slow), against the CPU oracle:
+
+* configs[4] (80B-A3B MoE shape): 512 experts, top-10, FFN 512, a shared
+  expert of 512, gate/up q4_K and down q6_K;
+* configs[3] (235B-A22B attention shape at long context): 64 q / 4 kv heads
+  (gqa 16), a synthetic context of 4100 tokens across 512-token pages;
+* configs[2] (experts host-pinned, popularity pinning from the reference's
+  own route_hist_30b.csv): bit-identical to all-in-HBM, HUD invariant;
+* configs[1] at full size: greedy tokens identical to the oracle.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from helpers import oracle_from_model, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+HIST = Path(__file__).resolve().parent / "golden" / "route_hist_30b.csv"
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    from styx_amd import Gpu
+    g = Gpu(0)
+    yield g
+    g.close()
+
+
+def check_forward(m, orc, toks, pos0=0):
+    """Per-token logits and per-layer residuals within 1e-4 relative L2."""
+    for i, t in enumerate(toks):
+        lg = m.forward_token(t)
+        hid = m.last_hidden()
+        ol, oh, oids, margins = orc.forward(pos0 + i, t, want_hidden=True)
+        assert rel_l2(lg, ol) < 1e-4, i
+        for l in range(hid.shape[0]):
+            assert rel_l2(hid[l], oh[l]) < 1e-4, (i, l)
+        ids = m.last_expert_ids()
+        for l in range(ids.shape[0]):
+            if margins[l] > 1e-4:
+                assert np.array_equal(ids[l], oids[l].astype(np.uint32)), (i, l)
+
+
+@pytest.mark.parametrize("ff_shexp", [512, 256])
+def test_config5_moe_shape_with_shared_expert(gpu, ff_shexp):
+    """A shared expert of the routed width runs as an extra slot of the
+    expert kernels; another width runs as dense matvecs.  Both match."""
+    from styx_amd import MoeModel, SynthConfig
+    from styx_amd import _lib as L
+    cfg = SynthConfig(n_layers=2, n_embd=2048, n_heads=16, n_kv_heads=2, head_dim=128,
+                      n_expert=512, n_expert_used=10, n_ff_exp=512, n_ff_shexp=ff_shexp,
+                      n_vocab=4096, exp_type=(L.Q4_K, L.Q4_K, L.Q6_K), seed=0x80B)
+    m = MoeModel.synth(gpu, cfg, n_ctx=32, record_hidden=True)
+    orc = oracle_from_model(m, 32)
+    check_forward(m, orc, [1, 4000, 77, 2048])
+    m.close()
+
+
+def test_config4_long_context_attention(gpu):
+    """gqa 16, head_dim 128, context of 4100 synthetic K/V rows (9 pages,
+    ~50 attention chunks) then 3 real tokens."""
+    from styx_amd import MoeModel, SynthConfig
+    cfg = SynthConfig(n_layers=2, n_embd=1024, n_heads=64, n_kv_heads=4, head_dim=128,
+                      n_expert=32, n_expert_used=4, n_ff_exp=256, n_vocab=2048, exp_mix=True,
+                      seed=0x235)
+    n_ctx, n_t = 4160, 4100
+    m = MoeModel.synth(gpu, cfg, n_ctx=n_ctx, record_hidden=True)
+    m.fill_kv(n_t, seed=7, sigma=1.0)
+    orc = oracle_from_model(m, n_ctx)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    kc = orc.kc.reshape(cfg.n_layers, n_ctx, kvd)
+    vc = orc.vc.reshape(cfg.n_layers, n_ctx, kvd)
+    for l in range(cfg.n_layers):
+        k, v = m.read_kv(l, 0, n_t)
+        assert np.isfinite(k).all() and abs(float(k.std()) - 1.0) < 0.05
+        kc[l, :n_t], vc[l, :n_t] = k, v
+    check_forward(m, orc, [17, 1800, 3], pos0=n_t)
+    m.close()
+
+
+def test_config3_hist_pinning_identical(gpu):
+    """48 layers x 128 experts pinned by the reference's popularity CSV under
+    a budget that holds about a third of the slabs; cold experts gathered
+    into the arena: logits bit-identical to all-in-HBM, hot + cold = k per
+    layer, and the pinned set is the one styx_residency_plan computes."""
+    from styx_amd import MoeModel, SynthConfig
+    cfg = SynthConfig(n_layers=48, n_embd=256, n_heads=4, n_kv_heads=2, head_dim=64,
+                      n_expert=128, n_expert_used=8, n_ff_exp=256, n_vocab=1024, exp_mix=True,
+                      seed=0x30B)
+    ref = MoeModel.synth(gpu, cfg, n_ctx=32)
+    budget_mb = int(ref.hp.slab_bytes * 48 * 128 / 3) >> 20
+    m = MoeModel.synth(gpu, cfg, n_ctx=32, expert_budget_mb=budget_mb, expert_hist=str(HIST),
+                       arena=True)
+    assert m.hp.expert_bytes_host > 0 and m.hp.expert_bytes_hbm > 0
+    hot = cold = 0
+    for t in [3, 900, 45, 1000, 2, 512]:
+        la, lb = ref.forward_token(t), m.forward_token(t)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        hc = m.last_hot_cold()
+        assert (hc.sum(1) == cfg.n_expert_used).all()
+        hot += int(hc[:, 0].sum())
+        cold += int(hc[:, 1].sum())
+    assert hot > 0 and cold > 0 and hot + cold == 6 * 48 * 8
+    ref.close()
+    m.close()
+
+
+def test_config2_full_size_greedy_matches_oracle(gpu):
+    """The 48-layer 30B-A3B-shaped model of bench.py: 16-token prompt (seed
+    0xC0FFEE), then greedy tokens identical to the oracle's."""
+    from oracle import oracle as O
+    from styx_amd import CFG_30B_A3B, MoeModel
+    O.set_threads(16)
+    rng = np.random.default_rng(0xC0FFEE)
+    prompt = rng.integers(0, CFG_30B_A3B.n_vocab, 16).astype(np.uint32)
+    n_new = 8
+    m = MoeModel.synth(gpu, CFG_30B_A3B, n_ctx=64)
+    orc = oracle_from_model(m, 64)
+    toks, _, _ = m.generate(prompt, n_new)
+    pos = 0
+    for t in prompt:
+        ol, *_ = orc.forward(pos, int(t))
+        pos += 1
+    ref = [O.argmax(ol)]
+    for _ in range(n_new - 1):
+        ol, *_ = orc.forward(pos, ref[-1])
+        pos += 1
+        ref.append(O.argmax(ol))
+    assert toks.tolist() == ref
+    m.close()

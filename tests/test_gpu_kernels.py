@@ -245,14 +245,18 @@ def _norm_rope_ref(v, w, hd, nh, pos, base, eps=1e-6):
     return O.rope_neox(v, hd, nh, pos, base)
 
 
-@pytest.mark.parametrize("nh,nkv,hd,n_steps,page", [(32, 4, 128, 70, 512), (64, 4, 128, 40, 32),
-                                                  (8, 8, 64, 33, 64)])
-def test_attention_paged(gpu, nh, nkv, hd, n_steps, page):
-    """Fused norm+rope+append+split-context attention over a scrambled page table."""
-    rng = np.random.default_rng(nh + hd)
+@pytest.mark.parametrize("nh,nkv,hd,n_steps,page,max_chunks",
+                         [(32, 4, 128, 70, 512, 4), (64, 4, 128, 40, 32, 4), (8, 8, 64, 33, 64, 4),
+                          (32, 4, 128, 70, 512, 2), (64, 4, 128, 40, 32, 1),
+                          (16, 8, 256, 50, 64, 3)])
+def test_attention_paged(gpu, nh, nkv, hd, n_steps, page, max_chunks):
+    """Fused norm+rope+append+split-context attention over a scrambled page
+    table.  With few chunks the per-chunk span grows past the minimum of 32
+    tokens (max(32, ceil16(n_t / max_chunks))), so waves walk several tiles."""
+    rng = np.random.default_rng(nh + hd + max_chunks)
     kvd = nkv * hd
     n_ctx = 128
-    chunk, max_chunks = 32, n_ctx // 32
+    chunk = 32
     npages = max(1, -(-n_ctx // page))
     pt = rng.permutation(npages).astype(np.int32)   # logical -> physical, scrambled
     kpool, vpool = gpu.zeros(npages * page * kvd * 4), gpu.zeros(npages * page * kvd * 4)

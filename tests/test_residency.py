@@ -1,0 +1,69 @@
+"""Host-side residency planning (crates/model/src/moe.rs:692-880) with the
+reference's own popularity fixture, tests/golden/route_hist_30b.csv (copied
+from the reference's tests/golden/, 48 layers x 128 experts).  No GPU."""
+from __future__ import annotations
+
+import csv
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+from styx_amd._lib import load
+
+HIST = Path(__file__).resolve().parent / "golden" / "route_hist_30b.csv"
+SKIP = 0xFFFFFFFF
+SLAB_30B = 884736 + 1081344 + 1290240  # q4_K + q5_K + q6_K slabs of one (layer, expert)
+
+
+def plan(hist, L, E, slab, budget_mb):
+    remap = np.empty(L * E, np.uint32)
+    n = C.c_uint64()
+    slabs = np.full(L, slab, np.uint64)
+    rc = load().styx_residency_plan(str(hist).encode() if hist else None, L, E, slabs.ctypes.data,
+                                    budget_mb, remap.ctypes.data, C.byref(n))
+    assert rc == 0
+    return remap.reshape(L, E), n.value
+
+
+def read_hits():
+    rows = list(csv.reader(open(HIST)))[1:]
+    hits = np.zeros((48, 128), np.int64)
+    for l, e, h in rows:
+        hits[int(l), int(e)] = int(h)
+    return hits
+
+
+def test_fixture_shape():
+    hits = read_hits()
+    assert hits.shape == (48, 128) and (hits >= 0).all() and hits.sum() > 0
+
+
+def test_6gib_budget_pins_the_hottest_slabs():
+    """config 3: a 6 GiB budget over 3,256,320-byte slabs holds
+    floor(6 GiB / slab) = 1978 slabs (~41 of 128 per layer)."""
+    remap, n = plan(HIST, 48, 128, SLAB_30B, 6144)
+    assert n == (6144 << 20) // SLAB_30B == 1978
+    hot = remap != SKIP
+    assert hot.sum() == n
+    hits = read_hits()
+    # every pinned slab is at least as popular as every unpinned one
+    assert hits[hot].min() >= hits[~hot].max()
+    # hot slots are dense per layer and ordered by expert id
+    for l in range(48):
+        ids = np.nonzero(hot[l])[0]
+        assert np.array_equal(remap[l, ids], np.arange(len(ids)))
+
+
+def test_budget_edges():
+    remap, n = plan(HIST, 48, 128, SLAB_30B, 0)
+    assert n == 0 and (remap == SKIP).all()
+    remap, n = plan(HIST, 48, 128, SLAB_30B, 1 << 30)  # everything fits
+    assert n == 48 * 128 and np.array_equal(remap, np.tile(np.arange(128), (48, 1)))
+
+
+def test_without_histogram_whole_layers_in_order():
+    layer = SLAB_30B * 128
+    remap, n = plan(None, 48, 128, SLAB_30B, (3 * layer + layer // 2) >> 20)
+    assert n == 3 * 128
+    assert (remap[:3] != SKIP).all() and (remap[3:] == SKIP).all()
