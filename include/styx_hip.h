@@ -159,11 +159,11 @@ int styx_op_moe_gate_up(styx_gpu *gpu, int type_gate, int type_up, const styx_ex
                         const styx_expert_src *up, const int32_t *ids, const float *xn, float *gu,
                         int H, int F, int k);
 /* x += sum_s w_s * Wd[e_s] . swiglu(gu[0][s], gu[1][s])  (swiglu_f32 +
- * mul_mat_vec_id ne11=k + moe_reduce_f32, moe.rs:2025-2062).  partial:
- * [k][H] f32 scratch. */
+ * mul_mat_vec_id ne11=k + moe_reduce_f32, moe.rs:2025-2062); gu is
+ * [2][k][F] as written by styx_op_moe_gate_up, x [H] is updated in place. */
 int styx_op_moe_down_reduce(styx_gpu *gpu, int type_down, const styx_expert_src *down,
                             const int32_t *ids, const float *weights, const float *gu, float *x,
-                            float *partial, int H, int F, int k);
+                            int H, int F, int k);
 /* Decode attention over the paged KV cache with fused per-head q/k RMSNorm,
  * NEOX rope and K/V append at *pos (attn_decode_f32.comp, moe.rs:1875-1964).
  * q [nh*hd], k/v [nkv*hd] raw projections; q_norm/k_norm [hd] or NULL;

@@ -113,7 +113,7 @@ _SIGS = {
                                   i32, i32, vp, vp, vp, vp]),
     "styx_op_topk_softmax": (i32, [vp, vp, i32, i32, i32, vp, vp, i32, i32, vp, vp]),
     "styx_op_moe_gate_up": (i32, [vp, i32, i32, vp, vp, vp, vp, vp, i32, i32, i32]),
-    "styx_op_moe_down_reduce": (i32, [vp, i32, vp, vp, vp, vp, vp, vp, i32, i32, i32]),
+    "styx_op_moe_down_reduce": (i32, [vp, i32, vp, vp, vp, vp, vp, i32, i32, i32]),
     "styx_op_attn_decode": (i32, [vp, vp, vp, vp, vp, vp, C.c_float, vp, vp, vp, vp, i32, vp,
                                   vp, vp, i32, i32, i32, i32, i32, C.c_float]),
     "styx_op_attn_part_floats": (i64, [i32, i32, i32, i32]),

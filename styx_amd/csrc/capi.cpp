@@ -32,6 +32,7 @@ static void gpu_destroy(styx_gpu *g)
     hipStreamSynchronize(g->stream);
     hipStreamDestroy(g->stream);
     if (g->xq_scratch) hipFree(g->xq_scratch);
+    if (g->partial_scratch) hipFree(g->partial_scratch);
     delete g;
 }
 
@@ -71,11 +72,14 @@ int styx_gpu_new(int device, styx_gpu **out)
         delete g;
         return hip_fail(e, "hipStreamCreateWithFlags");
     }
+    g->partial_bytes = sizeof(float) * MAX_TOPK * XQ_MAX;
     e = hipMalloc(&g->xq_scratch, xq_bytes(XQ_MAX));
+    if (e == hipSuccess) e = hipMalloc(&g->partial_scratch, g->partial_bytes);
     if (e != hipSuccess) {
+        if (g->xq_scratch) hipFree(g->xq_scratch);
         hipStreamDestroy(g->stream);
         delete g;
-        return hip_fail(e, "hipMalloc(limb scratch)");
+        return hip_fail(e, "hipMalloc(op scratch)");
     }
     *out = g;
     return STYX_OK;
@@ -313,24 +317,28 @@ int styx_op_moe_gate_up(styx_gpu *g, int tg, int tu, const styx_expert_src *gate
 }
 
 int styx_op_moe_down_reduce(styx_gpu *g, int td, const styx_expert_src *down, const int32_t *ids,
-                            const float *weights, const float *gu, float *x, float *partial,
-                            int H, int F, int k)
+                            const float *weights, const float *gu, float *x, int H, int F, int k)
 {
     OP_GPU(g);
-    if (!down || !ids || !weights || !gu || !x || !partial || k < 1 || k > 16)
+    if (!down || !ids || !weights || !gu || !x || k < 1 || k > 16)
         return fail(STYX_E_INVALID, "styx_op_moe_down_reduce: bad argument");
     if (F > XQ_MAX / 2) return fail(STYX_E_INVALID, "styx_op_moe_down_reduce: F > 8192");
     if (H < 32 || H % 32 || H > XQ_MAX)
         return fail(STYX_E_INVALID, "styx_op_moe_down_reduce: bad H");
+    // gu [2][k][F] -> per-slot down rows into a scratch of k x H floats
+    // held by the gpu (serialised with every other op on its stream)
+    if ((size_t)k * H * 4 > g->partial_bytes)
+        return fail(STYX_E_INVALID, "styx_op_moe_down_reduce: k * H too large");
+    float *partial = (float *)g->partial_scratch;
     OP_RUN(launch_moe_down(g->stream, td, to_src(down), ids, gu, partial, H, F, k),
            "styx_op_moe_down_reduce");
-    ReduceArgs r{};
-    r.partial = partial;
-    r.k = k;
-    r.H = H;
-    r.wts = weights;
-    r.x = x;
-    OP_RUN(launch_reduce_norm(g->stream, r), "styx_op_moe_down_reduce");
+    ReduceArgs a{};
+    a.partial = partial;
+    a.k = k;
+    a.H = H;
+    a.wts = weights;
+    a.x = x;
+    OP_RUN(launch_reduce_rows(g->stream, a), "styx_op_moe_down_reduce");
     return STYX_OK;
 }
 

@@ -123,6 +123,7 @@ struct styx_moe {
           *logits = nullptr, *hidden = nullptr, *sh_g = nullptr, *sh_u = nullptr, *sh_y = nullptr,
           *attn_part = nullptr, *am_val = nullptr;
     Xq xq_a{}, xq_o{}, xq_f{}, xq_sh{};  // limbs: layer input, attention out, ffn input, shexp hidden
+    float *ss_a = nullptr;                // partial sums of x^2 behind xq_a (per 256 rows)
     int32_t *ids = nullptr, *d_pos = nullptr;
     uint32_t *d_tok = nullptr, *am_idx = nullptr, *hist = nullptr;
     uint32_t *h_stage = nullptr;  // pinned: tok, pos
@@ -257,6 +258,7 @@ int styx_moe::setup_runtime()
     if (int r = dalloc(&d_pos, 1)) return r;
     if (int r = dalloc(&d_tok, 1)) return r;
     if (int r = dalloc(&hist, (size_t)n_ctx + 1)) return r;
+    if (int r = dalloc(&ss_a, (size_t)H / 32)) return r;
     uint8_t *xqb = nullptr;
     const size_t xa = (xq_bytes(H) + 255) & ~(size_t)255, xo = (xq_bytes(q_dim) + 255) & ~(size_t)255;
     const size_t xs = (xq_bytes(std::max(Fsh, 32)) + 255) & ~(size_t)255;
@@ -285,10 +287,11 @@ int styx_moe::setup_runtime()
     h_pt.assign((size_t)L * pages_per_layer, -1);
     STYX_HIP(hipMemsetAsync(d_pt, 0, sizeof(int32_t) * L * pages_per_layer, gpu->stream));
     next_page = 0;
-    // attention split: chunks of at least 32 tokens; at most ~768
-    // workgroups in all (one round of 4-wave workgroups at 3 waves per SIMD
-    // on 256 CUs); the attention kernels size the chunk from the live context
-    chunk = 32;
+    // attention split: chunks of at least 16 tokens (one tile per wave when
+    // the waves split heads); at most ~768 workgroups in all (one round of
+    // 4-wave workgroups at 3 waves per SIMD on 256 CUs); the attention
+    // kernels size the chunk from the live context
+    chunk = 16;
     max_chunks = std::min((n_ctx + chunk - 1) / chunk, std::max(16, 768 / nkv));
     const int64_t pf = styx_op_attn_part_floats(nh, nkv, hd, max_chunks);
     if (int r = dalloc(&attn_part, (size_t)pf)) return r;
@@ -458,7 +461,9 @@ int styx_moe::enqueue_token(bool gen)
     // the first layer's q/k/v input: limbs of attn_norm_0(x) (or of the LM
     // head's output_norm(x) for a model without layers)
     const float *norm0 = L > 0 ? layers[0].attn_norm : out_norm;
-    CK(launch_embed(st, embd.type, embd.dev, V, H, d_tok, x, norm0, eps, xq_a));
+    CK(launch_embed(st, embd.type, embd.dev, V, H, d_tok, x, norm0, xq_a, ss_a));
+    // every consumer of xq_a applies the RMSNorm scale from the x^2 partials
+    const NormScale ns_a{ss_a, (H + 255) / 256, H, eps};
     if (opts.record_hidden) CK(hipMemcpyAsync(hidden, x, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
     for (int l = 0; l < L; l++) {
         Layer &ly = layers[l];
@@ -466,13 +471,13 @@ int styx_moe::enqueue_token(bool gen)
         if (ly.wq.type == ly.wk.type && ly.wq.type == ly.wv.type) {
             DenseSeg s[3] = {{ly.wq.dev, q, ly.wq.rows}, {ly.wk.dev, kk, ly.wk.rows},
                              {ly.wv.dev, vv, ly.wv.rows}};
-            CK(launch_dense(st, ly.wq.type, H, s, 3, xq_a, 0));
+            CK(launch_dense(st, ly.wq.type, H, s, 3, xq_a, 0, &ns_a));
         } else {
             DenseSeg a{ly.wq.dev, q, ly.wq.rows}, b{ly.wk.dev, kk, ly.wk.rows},
                 c{ly.wv.dev, vv, ly.wv.rows};
-            CK(launch_dense(st, ly.wq.type, H, &a, 1, xq_a, 0));
-            CK(launch_dense(st, ly.wk.type, H, &b, 1, xq_a, 0));
-            CK(launch_dense(st, ly.wv.type, H, &c, 1, xq_a, 0));
+            CK(launch_dense(st, ly.wq.type, H, &a, 1, xq_a, 0, &ns_a));
+            CK(launch_dense(st, ly.wk.type, H, &b, 1, xq_a, 0, &ns_a));
+            CK(launch_dense(st, ly.wv.type, H, &c, 1, xq_a, 0, &ns_a));
         }
         tend(e0, "qkv", (double)(ly.wq.bytes() + ly.wk.bytes() + ly.wv.bytes()) + xq_bytes(H));
         e0 = tstart();
@@ -569,11 +574,6 @@ int styx_moe::enqueue_token(bool gen)
         CK(launch_moe_gate_up(st, ly.gate.type, ly.up.type, sg, su, nullptr, &rt, xq_f, gu, H, F,
                               K, sh_fused ? ly.gsh.dev : nullptr, sh_fused ? ly.ush.dev : nullptr));
         tend(e0, "moe_gate_up", slabs_gu + xq_bytes(H) + 4.0 * E + 4.0 * 2 * nsl * F);
-        e0 = tstart();
-        CK(launch_moe_down(st, ly.down.type, sd, lid, gu, partial, H, F, K,
-                           sh_fused ? ly.dsh.dev : nullptr));
-        tend(e0, "moe_down", (double)K * ly.down.slab + (sh_fused ? (double)ly.dsh.bytes() : 0.0) +
-                                 4.0 * 2 * nsl * F + 4.0 * nsl * H);
         if (ly.gsh.dev && !sh_fused) {
             e0 = tstart();
             DenseSeg s2[2] = {{ly.gsh.dev, sh_g, Fsh}, {ly.ush.dev, sh_u, Fsh}};
@@ -588,6 +588,11 @@ int styx_moe::enqueue_token(bool gen)
             CK(launch_dense(st, ly.dsh.type, Fsh, &sd2, 1, xq_sh, 0));
             tend(e0, "shexp", (double)(ly.gsh.bytes() + ly.ush.bytes() + ly.dsh.bytes()));
         }
+        e0 = tstart();
+        CK(launch_moe_down(st, ly.down.type, sd, lid, gu, partial, H, F, K,
+                           sh_fused ? ly.dsh.dev : nullptr));
+        tend(e0, "moe_down", (double)K * ly.down.slab + (sh_fused ? (double)ly.dsh.bytes() : 0.0) +
+                                 4.0 * 2 * nsl * F + 4.0 * nsl * H);
         e0 = tstart();
         ReduceArgs rd{};
         rd.partial = partial;
@@ -605,17 +610,17 @@ int styx_moe::enqueue_token(bool gen)
             rd.xn = xn;
         }
         rd.norm_w = l + 1 < L ? layers[l + 1].attn_norm : out_norm;
-        rd.eps = eps;
         rd.xq = xq_a;
-        CK(launch_reduce_norm(st, rd));
-        tend(e0, "reduce_norm", 4.0 * K * H + 8.0 * H + 4.0 * E + xq_bytes(H));
+        rd.ss = ss_a;
+        CK(launch_reduce_rows(st, rd));
+        tend(e0, "reduce", 4.0 * nsl * H + 12.0 * H + 4.0 * E + xq_bytes(H));
         if (opts.record_hidden)
             CK(hipMemcpyAsync(hidden + (size_t)(l + 1) * H, x, sizeof(float) * H,
                               hipMemcpyDeviceToDevice, st));
     }
     hipEvent_t e0 = tstart();
     DenseSeg sh{head.dev, logits, V};
-    CK(launch_dense(st, head.type, H, &sh, 1, xq_a, 0));
+    CK(launch_dense(st, head.type, H, &sh, 1, xq_a, 0, &ns_a));
     tend(e0, "lm_head", (double)head.bytes() + xq_bytes(H) + 4.0 * V);
     e0 = tstart();
     CK(launch_argmax(st, logits, V, d_tok, am_val, am_idx, d_pos, gen ? 1 : 0, hist));

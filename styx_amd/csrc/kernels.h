@@ -37,9 +37,11 @@ hipError_t launch_xq(hipStream_t st, const float *x, const float *u, const float
                      float eps, int n, const Xq &q, float *xn_out);
 
 // y_seg = W_seg . x for up to 3 matrices sharing type/ncols, x given by its
-// limbs.  add != 0 accumulates into y.
+// limbs (times the RMSNorm scale of `ns` if given).  add != 0 accumulates
+// into y.
+struct NormScale;
 hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, int nseg,
-                        const Xq &xq, int add);
+                        const Xq &xq, int add, const NormScale *ns = nullptr);
 
 // Router for one layer (fused ffn_norm): writes logits[E] and, from its first
 // workgroup, xn (f32) and its limbs xq (if xq.A).  launch_router_topk also
@@ -58,7 +60,7 @@ hipError_t launch_router_topk(hipStream_t st, const RouterArgs &a);
 
 // Top-k ids ranked inside a consumer kernel from the router logits
 // (topk_softmax_f32 selection order); the first workgroup publishes the id
-// row to ids_out.  The weights are formed by k_reduce_norm.
+// row to ids_out.  The weights are formed by k_down_reduce.
 struct Route {
     const float *logits;
     int E, k;
@@ -82,15 +84,18 @@ hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, c
                               const uint8_t *sh_up = nullptr);
 
 // partial[s] = Wd[e_s] swiglu(gu[0][s], gu[1][s]) for the k routed slots
-// (and the shared expert's down matrix as slot k if sh_down).
+// (and the shared expert's down matrix as slot k if sh_down); gu is
+// [2][nslots][F], partial [nslots][H].
 hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_t *ids,
                            const float *gu, float *partial, int H, int F, int k,
                            const uint8_t *sh_down = nullptr);
 
-// One workgroup: w_s from the logits and ids (topk_softmax_f32.comp:29-67)
-// or given; x += sum_s w_s partial[s] (moe_reduce_f32.comp:11-13, fixed slot
-// order); x += sigmoid(sh_ginp . xn) * sh_y if sh_y (axpy_sig_f32.comp);
-// then, if norm_w, the limbs of rmsnorm(x) * norm_w.
+// H / 256 workgroups: w_s from the router logits and the id row
+// (topk_softmax_f32.comp:29-67) or given in wts;
+//   x += sum_s w_s partial[s]  (s ascending, moe_reduce_f32.comp:11-13)
+//   x += sigmoid(sh_ginp . xn) * sh_y  (axpy_sig_f32.comp)
+// then, if norm_w, the limbs of x ⊙ norm_w and per-256-row partial sums of
+// x^2 into ss ([ceil(H / 256)]) -- the next matvec applies the RMSNorm scale.
 struct ReduceArgs {
     const float *partial;
     int k, H;
@@ -102,10 +107,19 @@ struct ReduceArgs {
     float *x;
     const float *sh_y, *sh_ginp, *xn;
     const float *norm_w;
-    float eps;
     Xq xq;
+    float *ss;
 };
-hipError_t launch_reduce_norm(hipStream_t st, const ReduceArgs &a);
+hipError_t launch_reduce_rows(hipStream_t st, const ReduceArgs &a);
+
+// The scale of an RMSNorm folded into a matvec whose limbs hold x ⊙ w:
+// each dot is multiplied by 1/sqrt(sum(ss[0..n_ss)) / n + eps)
+// (rms_norm_f32, crates/model/src/moe.rs:1746-1766).
+struct NormScale {
+    const float *ss;
+    int n_ss, n;
+    float eps;
+};
 
 // Decode attention over the paged f32 KV cache with fused per-head q/k
 // RMSNorm, NEOX rope and the K/V append at the current position.
@@ -130,10 +144,11 @@ struct AttnArgs {
 hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a);
 
 // x = dequant(token_embd[tok]) for the token held in device memory, and
-// (if q.A) the limbs of rmsnorm(x) * norm_w (or of x if norm_w is null).
+// (if q.A) the limbs of x ⊙ norm_w (of x if norm_w is null) with ss[0] =
+// sum x^2 for the consumer's RMSNorm scale.
 hipError_t launch_embed(hipStream_t st, int t, const uint8_t *w, int64_t nrows, int ncols,
-                        const uint32_t *tok, float *x, const float *norm_w, float eps,
-                        const Xq &q);
+                        const uint32_t *tok, float *x, const float *norm_w, const Xq &q,
+                        float *ss);
 
 // Greedy argmax over logits (ties -> highest index, generate_moe.rs:29),
 // in two kernels through part_val/part_idx (64 entries each).  Writes

@@ -82,11 +82,12 @@ hipError_t launch_dequant_rows(hipStream_t st, int t, const uint8_t *w, int64_t 
 }
 
 // ----------------------------------------------------------- embedding ----
-// x = dequant(token_embd[tok]) and the limbs of rmsnorm(x) * norm_w for the
-// first layer's q/k/v matvec; one workgroup.
+// x = dequant(token_embd[tok]); the limbs of x ⊙ norm_w for the first
+// layer's q/k/v matvec, which applies the RMSNorm scale from ss[0] = sum x^2
+// (ss[1..nss) = 0); one workgroup.
 __global__ void __launch_bounds__(256) k_embed(int t, const uint8_t *w, int64_t nrows, int ncols,
                                                const uint32_t *tok, float *x, const float *nw,
-                                               float eps, Xq q)
+                                               Xq q, float *ss, int nss)
 {
     extern __shared__ __align__(16) float xs[];  // [ncols]
     __shared__ float red[16];
@@ -95,17 +96,32 @@ __global__ void __launch_bounds__(256) k_embed(int t, const uint8_t *w, int64_t 
     const int64_t r = *tok;
     for (int b = threadIdx.x; b < nb; b += blockDim.x) deq_block(t, m, r * nb + b, xs + b * be);
     __syncthreads();
-    for (int i = threadIdx.x; i < ncols; i += blockDim.x) x[i] = xs[i];
-    if (q.A) xq_build(xs, nw, eps, nw != nullptr, ncols, q, red, nullptr);
+    float sq = 0.0f;
+    for (int i = threadIdx.x; i < ncols; i += blockDim.x) {
+        x[i] = xs[i];
+        sq += xs[i] * xs[i];
+    }
+    sq = block_sum(sq, red);
+    if (ss)
+        for (int i = threadIdx.x; i < nss; i += blockDim.x) ss[i] = i == 0 ? sq : 0.0f;
+    if (!q.A) return;
+    for (int g0 = 0; g0 < ncols / 8; g0 += blockDim.x) {
+        const int g = g0 + threadIdx.x;
+        const bool act = g < ncols / 8;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = act ? xs[8 * g + i] * (nw ? nw[8 * g + i] : 1.0f) : 0.0f;
+        xq_group(v, act, g, q);
+    }
 }
 
 hipError_t launch_embed(hipStream_t st, int t, const uint8_t *w, int64_t nrows, int ncols,
-                        const uint32_t *tok, float *x, const float *norm_w, float eps,
-                        const Xq &q)
+                        const uint32_t *tok, float *x, const float *norm_w, const Xq &q,
+                        float *ss)
 {
     if (ncols % 32 || ncols > XQ_MAX || ncols % blk_elems(t)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), (size_t)ncols * 4, st, t, w, nrows, ncols,
-                       tok, x, norm_w, eps, q);
+                       tok, x, norm_w, q, ss, ncols / 32);
     return hipGetLastError();
 }
 

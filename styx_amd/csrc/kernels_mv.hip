@@ -14,10 +14,12 @@
 //                   (mul_mat_vec_id semantics, ne11 = 1), top-k ids ranked
 //                   in-kernel from the router logits.
 //   k_down          expert down matvec, swiglu + limbs of the slot's hidden
-//                   vector built in LDS in front; per-slot rows to partial[s].
-//   k_reduce_norm   topk_softmax weights of the selected ids, moe_reduce
+//                   vector built in LDS in front; per-slot rows to partial[s]
+//                   (the shared expert as one more slot).
+//   k_reduce_rows   topk_softmax weights of the selected ids, moe_reduce
 //                   (x += sum_s w_s y_s, s ascending), the shared-expert
-//                   axpy_sig, then the next RMSNorm and its limbs; one
+//                   axpy_sig, then the limbs of x ⊙ w for the next RMSNorm
+//                   (whose scale the next matvec applies); 256 rows per
 //                   workgroup.
 //
 // No kernel waits on another workgroup: every producer writes what its
@@ -84,7 +86,7 @@ struct LaneMap {
     bool ok;
 };
 
-__device__ __forceinline__ LaneMap lane_map(int G)
+__device__ __forceinline__ LaneMap lane_map(int G, int nwaves = WAVES)
 {
     LaneMap m;
     m.lane = threadIdx.x & 63;
@@ -94,7 +96,7 @@ __device__ __forceinline__ LaneMap lane_map(int G)
     m.gl = m.lane - m.grp * G;
     m.ok = m.grp < m.gpw;
     m.gid = m.wave * m.gpw + m.grp;
-    m.ngrp = WAVES * m.gpw;
+    m.ngrp = nwaves * m.gpw;
     return m;
 }
 
@@ -257,6 +259,7 @@ struct DenseK {
     int rows[3];
     int nseg, total, nb, G, UPL, rpw, add;
     Xq xq;
+    NormScale ns;  // ns.ss == null: no RMSNorm scale
 };
 
 template <int T, int UPL>
@@ -271,15 +274,28 @@ __global__ void __launch_bounds__(WG) k_mv_dense(DenseK a)
             const Mat mat = mat_at(a.w[s], T, (int64_t)a.rows[s] * a.nb);
             float *y = a.y[s];
             const int add = a.add;
-            walk_rows<T, UPL>(a.xq, mat, a.nb, a.G, lo - base, hi - base,
-                              [=](int r, float v) { y[r] = add ? y[r] + v : v; });
+            // the RMSNorm scale is summed while the first weights are in flight
+            float scale = 1.0f;
+            auto xload = [&](UX<T> (&x)[UPL], const LaneU<UPL> &lu) {
+                XFrom<T, UPL>{a.xq}(x, lu);
+                if (a.ns.ss) {
+                    float t = 0.0f;
+                    for (int i = threadIdx.x & 63; i < a.ns.n_ss; i += 64) t += a.ns.ss[i];
+                    t = wave_sum(t);
+                    scale = 1.0f / sqrtf(t / (float)a.ns.n + a.ns.eps);
+                }
+            };
+            walk_rows_pf<T, UPL>(mat, a.nb, a.G, lo - base, hi - base, xload, [&](int r, float v) {
+                v *= scale;
+                y[r] = add ? y[r] + v : v;
+            });
         }
         base += a.rows[s];
     }
 }
 
 hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, int nseg,
-                        const Xq &xq, int add)
+                        const Xq &xq, int add, const NormScale *ns)
 {
     const Geo g = pick_geo(t, ncols);
     if (g.G == 0 || nseg < 1 || nseg > 3 || !xq.A) return hipErrorInvalidValue;
@@ -297,6 +313,7 @@ hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, 
     a.UPL = g.UPL;
     a.add = add;
     a.xq = xq;
+    if (ns) a.ns = *ns;
     a.rpw = rows_per_wg(a.total, g.G, 1024);
     const dim3 grid((a.total + a.rpw - 1) / a.rpw);
     switch (t) {
@@ -524,7 +541,7 @@ hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, c
 
 // ------------------------------------------------------------- down -------
 // partial[s] = Wd[e_s] . swiglu(g_s, u_s) for every routed slot s; the
-// weighted combine into the residual is k_reduce_norm.
+// weighted combine into the residual is k_reduce_rows.
 struct DownK {
     ExpSrc src;
     const uint8_t *sh;  // shared expert down matrix (slot k) or null
@@ -618,105 +635,104 @@ hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_
     return hipGetLastError();
 }
 
-// ------------------------------------------------------- reduce + norm ----
-// One workgroup: weights w_s = softmax(logits)[ids[s]] (renormalised over
-// the k picks if renorm) exactly as topk_softmax_f32.comp:29-67 forms them,
-// or taken from a.wts; then
-//   x[i] += sum_s w_s * partial[s][i]      (moe_reduce_f32.comp:8-13)
-//   x[i] += sigmoid(ginp . xn) * sh_y[i]   (axpy_sig_f32.comp, if sh_y)
-// and, if norm_w, the limbs of rmsnorm(x) * norm_w for the next matvec.
-constexpr int RN_WG = 1024;
+// ------------------------------------------------------------ reduce ----
+// The weighted combine and the next RMSNorm's limbs, over H / RR_ROWS
+// workgroups of RR_ROWS rows each:
+//   w_s = softmax(logits)[e_s], renormalised over the k picks
+//         (topk_softmax_f32.comp:29-67; every workgroup forms them)
+//   x[r] += sum_s w_s partial[s][r]        (moe_reduce_f32.comp:8-13)
+//   x[r] += sigmoid(ginp . xn) * y_sh[r]   (axpy_sig_f32.comp)
+// then the limbs of x ⊙ norm_w for these rows and the partial sum of x^2
+// over them: the next matvec applies the RMSNorm scale 1/sqrt(sum/H + eps).
+constexpr int RR_WG = 256;
+constexpr int RR_ROWS = 256;
 
-__global__ void __launch_bounds__(RN_WG) k_reduce_norm(ReduceArgs a)
+__global__ void __launch_bounds__(RR_WG) k_reduce_rows(ReduceArgs a)
 {
-    extern __shared__ __align__(16) float xs[];  // H floats
     __shared__ float red[16];
     __shared__ float s_w[MAX_TOPK];
     __shared__ float s_wsum, s_sg;
-    // every load that does not depend on the weights is issued first: the
-    // first RN_WG elements of x and of each slot's partial, the routed
-    // logits, the shared-expert operands
-    const int i0 = threadIdx.x;
-    const bool h0 = i0 < a.H;
-    float p0[MAX_TOPK];
+    const int tid = threadIdx.x, r = blockIdx.x * RR_ROWS + tid;  // RR_ROWS == RR_WG
+    const bool hr = r < a.H;
+    // every load that does not depend on the weights first
+    float p[MAX_TOPK];
 #pragma unroll
-    for (int s = 0; s < MAX_TOPK; s++)
-        p0[s] = (s < a.k && h0) ? a.partial[(int64_t)s * a.H + i0] : 0.0f;
-    const float x0 = h0 ? a.x[i0] : 0.0f;
-    const float y0 = (a.sh_y && h0) ? a.sh_y[i0] : 0.0f;
-    float lg_own = -INFINITY, lg_pick = 0.0f;
+    for (int s = 0; s < MAX_TOPK; s++) p[s] = (s < a.k && hr) ? a.partial[(int64_t)s * a.H + r] : 0.0f;
+    const float x0 = hr ? a.x[r] : 0.0f;
+    const float y0 = (a.sh_y && hr) ? a.sh_y[r] : 0.0f;
+    const float nw = (a.norm_w && hr) ? a.norm_w[r] : 1.0f;
+    float lg_pick = 0.0f, mx = -INFINITY;
     if (a.logits) {
-        if (i0 < a.E) lg_own = a.logits[i0];
-        if (i0 < a.k) {
-            const int e = a.ids[i0];
+        for (int e = tid; e < a.E; e += RR_WG) mx = fmaxf(mx, a.logits[e]);
+        if (tid < a.k) {
+            const int e = a.ids[tid];
             lg_pick = (e >= 0 && e < a.E) ? a.logits[e] : -INFINITY;
         }
     }
+    float shd = 0.0f;
+    if (a.sh_y)
+        for (int i = tid; i < a.H; i += RR_WG) shd += a.sh_ginp[i] * a.xn[i];
     if (a.logits) {
-        float mx = lg_own;
-        for (int e = threadIdx.x + RN_WG; e < a.E; e += RN_WG) mx = fmaxf(mx, a.logits[e]);
         mx = wave_max(mx);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+        if ((tid & 63) == 0) red[tid >> 6] = mx;
         __syncthreads();
         mx = red[0];
-        for (int i = 1; i < RN_WG / 64; i++) mx = fmaxf(mx, red[i]);
-        float se = i0 < a.E ? expf(lg_own - mx) : 0.0f;
-        for (int e = threadIdx.x + RN_WG; e < a.E; e += RN_WG) se += expf(a.logits[e] - mx);
+        for (int i = 1; i < RR_WG / 64; i++) mx = fmaxf(mx, red[i]);
+        float se = 0.0f;
+        for (int e = tid; e < a.E; e += RR_WG) se += expf(a.logits[e] - mx);
         se = block_sum(se, red);
-        // each slot's weight in its own thread; the renormalising sum runs in
-        // slot order as in the reference
-        if (i0 < a.k) s_w[i0] = expf(lg_pick - mx) / se;
+        if (tid < a.k) s_w[tid] = expf(lg_pick - mx) / se;
         __syncthreads();
-        if (threadIdx.x == 0 && a.renorm) {
+        if (tid == 0 && a.renorm) {
             float wsum = 0.0f;
             for (int s = 0; s < a.k; s++) wsum += s_w[s];
             s_wsum = wsum;
         }
         __syncthreads();
-        if (i0 < a.k) {
-            const float w = a.renorm ? s_w[i0] / s_wsum : s_w[i0];
-            s_w[i0] = w;  // only this thread touches slot i0 here
-            if (a.wts_out) a.wts_out[i0] = w;
+        if (tid < a.k) {
+            const float w = a.renorm ? s_w[tid] / s_wsum : s_w[tid];
+            s_w[tid] = w;  // only this thread touches slot tid here
+            if (a.wts_out && blockIdx.x == 0) a.wts_out[tid] = w;
         }
-    } else if (i0 < a.k) {
-        s_w[i0] = a.wts[i0];
+    } else if (tid < a.k) {
+        s_w[tid] = a.wts[tid];
     }
     if (a.sh_y) {
-        float d = 0.0f;
-        for (int i = threadIdx.x; i < a.H; i += RN_WG) d += a.sh_ginp[i] * a.xn[i];
-        d = block_sum(d, red);
-        if (threadIdx.x == 0) s_sg = 1.0f / (1.0f + expf(-d));
+        const float d = block_sum(shd, red);
+        if (tid == 0) s_sg = 1.0f / (1.0f + expf(-d));
     }
     __syncthreads();
-    if (h0) {
-        float acc = 0.0f;
+    float acc = 0.0f;
 #pragma unroll
-        for (int s = 0; s < MAX_TOPK; s++)
-            if (s < a.k) acc += s_w[s] * p0[s];
-        float v = x0 + acc;
-        if (a.sh_y) v = v + s_sg * y0;
-        a.x[i0] = v;
-        xs[i0] = v;
-    }
-    for (int i = i0 + RN_WG; i < a.H; i += RN_WG) {
-        float acc = 0.0f;
-        for (int s = 0; s < a.k; s++) acc += s_w[s] * a.partial[(int64_t)s * a.H + i];
-        float v = a.x[i] + acc;
-        if (a.sh_y) v = v + s_sg * a.sh_y[i];
-        a.x[i] = v;
-        xs[i] = v;
-    }
+    for (int s = 0; s < MAX_TOPK; s++)
+        if (s < a.k) acc += s_w[s] * p[s];
+    float xv = x0 + acc;
+    if (a.sh_y) xv = xv + s_sg * y0;
+    if (hr) a.x[r] = xv;
+    if (!a.norm_w) return;
+    // limbs of x ⊙ norm_w: 8 consecutive rows per thread of the first 32
+    float sq = block_sum(hr ? xv * xv : 0.0f, red);
+    if (tid == 0) a.ss[blockIdx.x] = sq;
+    __shared__ __align__(16) float xw[RR_ROWS];
+    xw[tid] = xv * nw;
     __syncthreads();
-    if (a.norm_w) xq_build(xs, a.norm_w, a.eps, true, a.H, a.xq, red, nullptr);
+    const int nrow = min(RR_ROWS, a.H - blockIdx.x * RR_ROWS);
+    if (tid < RR_ROWS / 8) {
+        const bool act = 8 * tid < nrow;
+        float h[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = act ? xw[8 * tid + i] : 0.0f;
+        xq_group(h, act, tid, xq_shift(a.xq, blockIdx.x * RR_ROWS));
+    }
 }
 
-hipError_t launch_reduce_norm(hipStream_t st, const ReduceArgs &a)
+hipError_t launch_reduce_rows(hipStream_t st, const ReduceArgs &a)
 {
-    if (a.k < 1 || a.k > MAX_TOPK || a.H < 32 || a.H % 32 || a.H > XQ_MAX ||
+    if (a.k < 1 || a.k > MAX_TOPK || a.H < 32 || a.H % 32 ||
         (a.logits && (a.E < a.k || a.E > MAX_EXPERTS || !a.ids)) || (!a.logits && !a.wts) ||
-        (a.sh_y && (!a.sh_ginp || !a.xn)) || (a.norm_w && !a.xq.A))
+        (a.sh_y && (!a.sh_ginp || !a.xn)) || (a.norm_w && (!a.xq.A || !a.ss)))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_reduce_norm, dim3(1), dim3(RN_WG), (size_t)a.H * 4, st, a);
+    hipLaunchKernelGGL(k_reduce_rows, dim3((a.H + RR_ROWS - 1) / RR_ROWS), dim3(RR_WG), 0, st, a);
     return hipGetLastError();
 }
 

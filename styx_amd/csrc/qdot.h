@@ -57,10 +57,46 @@ __device__ inline float block_sum(float v, float *red)
     return t;
 }
 
+// Limbs of one group of 8 consecutive values (group g of the vector q).
+// Four consecutive lanes hold the four groups of one 32-value block (groups
+// are 4-aligned); all four must call this together.  Inactive groups pass
+// zeros and write nothing.
+__device__ __forceinline__ void xq_group(const float *v, bool act, int g, Xq q)
+{
+    float am = 0.0f, s8 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        am = fmaxf(am, fabsf(v[i]));
+        s8 += v[i];
+    }
+    am = fmaxf(am, __shfl_xor(am, 1));
+    am = fmaxf(am, __shfl_xor(am, 2));
+    const float s16 = s8 + __shfl_xor(s8, 1);
+    if (!act) return;
+    const float inv = am > 0.0f ? 127.0f / am : 0.0f;
+    uint32_t pa[2] = {0, 0}, pb[2] = {0, 0}, pc[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float y = v[i] * inv;
+        const float a = rintf(y);
+        const float r1 = (y - a) * 254.0f;
+        const float b = rintf(r1);
+        const float c = fminf(fmaxf(rintf((r1 - b) * 254.0f), -127.0f), 127.0f);
+        const int sh = 8 * (i & 3);
+        pa[i >> 2] |= ((uint32_t)(int)a & 0xFFu) << sh;
+        pb[i >> 2] |= ((uint32_t)(int)b & 0xFFu) << sh;
+        pc[i >> 2] |= ((uint32_t)(int)c & 0xFFu) << sh;
+    }
+    *(uint2 *)(q.A + 8 * g) = make_uint2(pa[0], pa[1]);
+    *(uint2 *)(q.B + 8 * g) = make_uint2(pb[0], pb[1]);
+    *(uint2 *)(q.C + 8 * g) = make_uint2(pc[0], pc[1]);
+    if ((g & 3) == 0) q.sx[g >> 2] = am / 127.0f;
+    if ((g & 1) == 0) q.s16[g >> 1] = s16;
+}
+
 // Build the limb form of xn = norm ? x * rsqrt(mean(x^2)+eps) * w : x
 // (n a multiple of 32).  If xn_out is non-null the normalised f32 vector is
-// also written there.
-// Thread t owns 8 consecutive values; four threads share one 32-value block.
+// also written there.  Thread t owns 8 consecutive values per pass.
 __device__ inline void xq_build(const float *__restrict__ x, const float *__restrict__ nw,
                                 float eps, bool norm, int n, Xq q, float *red, float *xn_out)
 {
@@ -97,36 +133,7 @@ __device__ inline void xq_build(const float *__restrict__ x, const float *__rest
 #pragma unroll
             for (int i = 0; i < 8; i++) v[i] = 0.0f;
         }
-        float am = 0.0f, s8 = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            am = fmaxf(am, fabsf(v[i]));
-            s8 += v[i];
-        }
-        // four consecutive lanes share a 32-value block (groups are 4-aligned)
-        am = fmaxf(am, __shfl_xor(am, 1));
-        am = fmaxf(am, __shfl_xor(am, 2));
-        const float s16 = s8 + __shfl_xor(s8, 1);
-        if (!act) continue;
-        const float inv = am > 0.0f ? 127.0f / am : 0.0f;
-        uint32_t pa[2] = {0, 0}, pb[2] = {0, 0}, pc[2] = {0, 0};
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float y = v[i] * inv;
-            const float a = rintf(y);
-            const float r1 = (y - a) * 254.0f;
-            const float b = rintf(r1);
-            const float c = fminf(fmaxf(rintf((r1 - b) * 254.0f), -127.0f), 127.0f);
-            const int sh = 8 * (i & 3);
-            pa[i >> 2] |= ((uint32_t)(int)a & 0xFFu) << sh;
-            pb[i >> 2] |= ((uint32_t)(int)b & 0xFFu) << sh;
-            pc[i >> 2] |= ((uint32_t)(int)c & 0xFFu) << sh;
-        }
-        *(uint2 *)(q.A + 8 * g) = make_uint2(pa[0], pa[1]);
-        *(uint2 *)(q.B + 8 * g) = make_uint2(pb[0], pb[1]);
-        *(uint2 *)(q.C + 8 * g) = make_uint2(pc[0], pc[1]);
-        if ((g & 3) == 0) q.sx[g >> 2] = am / 127.0f;
-        if ((g & 1) == 0) q.s16[g >> 1] = s16;
+        xq_group(v, act, g, q);
     }
 }
 

@@ -19,6 +19,10 @@ struct styx_gpu {
     // the matvec that reads them.  Calls on one styx_gpu are serialised on
     // its stream, so one buffer serves them all.
     void *xq_scratch = nullptr;
+    // Per-slot down rows of styx_op_moe_down_reduce (k x H floats, k <= 16,
+    // H <= 16384), same stream-order rule.
+    void *partial_scratch = nullptr;
+    size_t partial_bytes = 0;
 };
 
 struct styx_buf {
