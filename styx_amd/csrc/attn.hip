@@ -353,14 +353,17 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     }
 }
 
-// Merge the per-chunk partials (m, l, o) of one query head:
-// M = max m_c, L = sum l_c e^(m_c-M), out = sum o_c e^(m_c-M) / L; then the
-// limbs of this head's slice of the output.  256 threads: the chunk factors
-// in parallel, then 4 chunk groups x 64 lanes (each lane hd/64 values)
-// accumulate their share of the chunks and are summed in LDS.
-__global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a)
+// Merge the per-chunk partials (m, l, o) of one query head: M = max m_c,
+// L = sum l_c e^(m_c-M), out = sum o_c e^(m_c-M) / L; then the limbs of this
+// head's slice of the output.  CB_WG threads = CB_GROUPS chunk groups x 64
+// lanes (each lane hd/64 values).  A group takes its chunks in batches of 8
+// whose loads are all issued before any is merged into the group's running
+// (m, l, o); the groups are merged in LDS.
+constexpr int CB_WG = 1024, CB_GROUPS = CB_WG / 64, CB_BATCH = 8;
+
+__global__ void __launch_bounds__(CB_WG) k_attn_combine(AttnArgs a)
 {
-    extern __shared__ __align__(16) float xs[];  // [hd] out | [4][hd] group sums | [max_chunks] factors
+    extern __shared__ __align__(16) float xs[];  // [hd] out | [G][hd] o | [G] m | [G] l
     __shared__ float red[16];
     const int h = blockIdx.x, gqa = a.nh / a.nkv, hd = a.hd, ps = hd + 2;
     const int n_t = *a.pos + 1, chunk = attn_chunk(a, n_t);
@@ -368,37 +371,49 @@ __global__ void __launch_bounds__(256) k_attn_combine(AttnArgs a)
     const int kvh = h / gqa, g = h - kvh * gqa;
     const int64_t cs = (int64_t)gqa * ps;  // stride between chunks
     const float *pk = a.part + (int64_t)kvh * a.max_chunks * cs + (int64_t)g * ps;
-    float *gs = xs + hd, *fc = gs + 4 * hd;
-    float mloc = -INFINITY;
-    for (int cc = threadIdx.x; cc < n_active; cc += blockDim.x) {
-        const float m = pk[cc * cs + hd];
-        fc[cc] = m;
-        mloc = fmaxf(mloc, m);
-    }
-    mloc = wave_max(mloc);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mloc;
-    __syncthreads();
-    float M = red[0];
-    for (int w = 1; w < (int)blockDim.x / 64; w++) M = fmaxf(M, red[w]);
-    float lloc = 0.0f;
-    for (int cc = threadIdx.x; cc < n_active; cc += blockDim.x) {
-        const float f = expf(fc[cc] - M);
-        fc[cc] = f;
-        lloc += pk[cc * cs + hd + 1] * f;
-    }
-    const float L = block_sum(lloc, red);  // its barrier also publishes fc
     const int grp = threadIdx.x >> 6, lane = threadIdx.x & 63, epl = hd / 64;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-    for (int cc = grp; cc < n_active; cc += 4) {
-        const float f = fc[cc];
-        const float *pp = pk + cc * cs + lane * epl;
-        for (int e = 0; e < epl; e++) acc[e] += pp[e] * f;
+    float m = -INFINITY, l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c0 = grp; c0 < n_active; c0 += CB_GROUPS * CB_BATCH) {
+        float mc[CB_BATCH], lc[CB_BATCH], oc[CB_BATCH][4];
+#pragma unroll
+        for (int b = 0; b < CB_BATCH; b++) {
+            const int cc = c0 + CB_GROUPS * b;
+            const bool ok = cc < n_active;
+            const float *pp = pk + (ok ? cc : 0) * cs;
+            mc[b] = ok ? pp[hd] : -INFINITY;
+            lc[b] = ok ? pp[hd + 1] : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) oc[b][e] = (ok && e < epl) ? pp[lane * epl + e] : 0.0f;
+        }
+#pragma unroll
+        for (int b = 0; b < CB_BATCH; b++) {
+            if (mc[b] == -INFINITY) continue;
+            const float mn = fmaxf(m, mc[b]);
+            const float fa = expf(m - mn), fb = expf(mc[b] - mn);
+            l = l * fa + lc[b] * fb;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = o[e] * fa + oc[b][e] * fb;
+            m = mn;
+        }
     }
-    for (int e = 0; e < epl; e++) gs[grp * hd + lane * epl + e] = acc[e];
+    float *go = xs + hd, *gm = go + CB_GROUPS * hd, *gl = gm + CB_GROUPS;
+    for (int e = 0; e < epl; e++) go[grp * hd + lane * epl + e] = o[e];
+    if (lane == 0) {
+        gm[grp] = m;
+        gl[grp] = l;
+    }
     __syncthreads();
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
-        const float v = ((gs[i] + gs[hd + i]) + (gs[2 * hd + i] + gs[3 * hd + i])) / L;
+    if (threadIdx.x < hd) {
+        const int i = threadIdx.x;
+        float M = gm[0];
+        for (int q = 1; q < CB_GROUPS; q++) M = fmaxf(M, gm[q]);
+        float L = 0.0f, O = 0.0f;
+        for (int q = 0; q < CB_GROUPS; q++) {
+            const float f = gm[q] == -INFINITY ? 0.0f : expf(gm[q] - M);
+            L += gl[q] * f;
+            O += go[q * hd + i] * f;
+        }
+        const float v = O / L;
         a.out[(int64_t)h * hd + i] = v;
         xs[i] = v;
     }
@@ -439,8 +454,8 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
         return hipErrorInvalidValue;  // gqa of 5, 7, 9.. above 4 heads per wave
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_combine, dim3(a.nh), dim3(256), (size_t)(5 * a.hd + a.max_chunks) * 4,
-                       st, a);
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.nh), dim3(CB_WG),
+                       (size_t)((CB_GROUPS + 1) * a.hd + 2 * CB_GROUPS) * 4, st, a);
     return hipGetLastError();
 }
 

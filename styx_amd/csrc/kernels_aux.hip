@@ -240,9 +240,16 @@ __global__ void __launch_bounds__(256) k_gather(GatherK a)
     const int s = blockIdx.y, t = blockIdx.z;
     uint32_t e, slot;
     if (a.mode == 0) {
-        const int32_t *ids = a.route.logits ? route_ids_wg(a.route, s_ids, s_lg) : a.ids;
-        slot = (uint32_t)ids[32 + s];
-        e = (uint32_t)ids[s];
+        if (a.route.logits) {
+            const int32_t *ids = route_ids_wg(a.route, s_ids, s_lg);
+            uint32_t r3[3];
+            route_row(a.route, ids[s], s, r3);
+            slot = r3[1];
+            e = (uint32_t)ids[s];
+        } else {
+            slot = (uint32_t)a.ids[32 + s];
+            e = (uint32_t)a.ids[s];
+        }
         if (slot == SKIP) return;
     } else {
         e = (uint32_t)a.ids[s];

@@ -461,8 +461,14 @@ __device__ inline void gate_up_body(const GateUpK &a, int m, int s, int32_t *s_i
 {
     const uint8_t *slab;
     if (s < a.k) {
-        const int32_t *ids = a.route.logits ? route_ids_wg(a.route, s_ids, s_lg) : a.ids;
-        slab = slab_for(a.src[m], ids, s);
+        if (a.route.logits) {
+            const int32_t *ids = route_ids_wg(a.route, s_ids, s_lg);
+            uint32_t r3[3];
+            route_row(a.route, ids[s], s, r3);
+            slab = slab_pick(a.src[m], r3[0], r3[1], r3[2]);
+        } else {
+            slab = slab_for(a.src[m], a.ids, s);
+        }
     } else {
         slab = a.sh[m];  // the shared expert needs no routing
     }

@@ -84,6 +84,25 @@ __device__ __noinline__ void topk_wave(const float *logits, int n, int k, int re
     }
 }
 
+// Hot / arena / host ids of expert e routed to `slot` (topk_softmax_f32.comp
+// id rows 16/32/48): the hot slot from remap (every expert resident at its
+// own index when remap is null), else an arena slot (arena_mode: layer*k +
+// slot, or pmap), else the expert itself read from host memory.
+__device__ __forceinline__ void route_row(const Route &r, int e, int slot, uint32_t ids3[3])
+{
+    const uint32_t h = r.remap ? r.remap[e] : (uint32_t)e;
+    ids3[0] = h;
+    ids3[1] = ids3[2] = SKIP;
+    if (h != SKIP) return;
+    uint32_t a = SKIP;
+    if (r.arena_mode)
+        a = (uint32_t)(r.layer * r.k + slot);
+    else if (r.pmap)
+        a = r.pmap[e];
+    ids3[1] = a;
+    if (a == SKIP) ids3[2] = (uint32_t)e;
+}
+
 // Top-k ids of the router logits inside a workgroup, by ranking.  Order: a
 // larger value first, equal values by lower index -- the strict '>' of
 // topk_softmax_f32.comp:45 -- so ranks 0..k-1 are exactly the reference's
@@ -93,8 +112,9 @@ __device__ __noinline__ void topk_wave(const float *logits, int n, int k, int re
 // are candidates (every global top-k logit is in its quarter's top-k), and
 // the <= 4k candidates are ranked among themselves: E^2/4 + 16k^2 compares
 // per workgroup instead of E^2.  No dependent shuffle chain either way.
-// Fills the four id rows in s_ids (64 ints); weights are left to the caller.
-// The workgroup with all-zero block index publishes the id row to r.ids_out.
+// Fills s_ids[0..k) with the routed experts (route_row gives a slot's other
+// ids); weights are left to the caller.  The workgroup with all-zero block
+// index publishes the whole id row to r.ids_out.
 // Needs blockDim.x == 256, E % 16 == 0, E <= 512, k <= 16.
 __device__ inline const int32_t *route_ids_wg(const Route &r, int32_t *s_ids, float *s_lg)
 {
@@ -169,26 +189,23 @@ __device__ inline const int32_t *route_ids_wg(const Route &r, int32_t *s_ids, fl
         }
     }
     __syncthreads();
-    if ((int)threadIdx.x < k) {
-        const int s = threadIdx.x;
-        const uint32_t e = (uint32_t)s_ids[s];
-        const uint32_t h = r.remap ? r.remap[e] : e;
-        if (h != SKIP) {
-            s_ids[16 + s] = (int32_t)h;
-        } else {
-            uint32_t a = SKIP;
-            if (r.arena_mode)
-                a = (uint32_t)(r.layer * k + s);
-            else if (r.pmap)
-                a = r.pmap[e];
-            s_ids[32 + s] = (int32_t)a;
-            if (a == SKIP) s_ids[48 + s] = (int32_t)e;
-        }
-    }
-    __syncthreads();
+    // the workgroup with all-zero block index publishes the 64-int id row
     if (r.ids_out && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 &&
-        threadIdx.x < IDS_ROW)
-        r.ids_out[threadIdx.x] = s_ids[threadIdx.x];
+        threadIdx.x < IDS_ROW) {
+        const int row = threadIdx.x >> 4, slot = threadIdx.x & 15;
+        int32_t v = (int32_t)SKIP;
+        if (slot < k) {
+            const int e = s_ids[slot];
+            if (row == 0) {
+                v = e;
+            } else {
+                uint32_t ids3[3];
+                route_row(r, e, slot, ids3);
+                v = (int32_t)ids3[row - 1];
+            }
+        }
+        r.ids_out[threadIdx.x] = v;
+    }
     return s_ids;
 }
 
