@@ -353,6 +353,221 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core variant for head_dim 128 and 16 query heads per kv head (the
+// 235B-A22B shape; fewer heads would be padded, which the head-split VALU
+// kernel above does better).  Per 16-token tile a wave forms all heads' scores with
+// v_mfma_f32_16x16x4_f32, S[h][t] = sum_d Q[h][d] K[t][d], 32 k-steps (lane
+// l holds S[4(l/16)+r][l%16]); runs the online softmax with reductions over
+// the 16 lanes of a row; moves P through LDS into the A-operand layout; and
+// accumulates O[h][d] += sum_t P[h][t] V[t][d] with 32 more MFMAs.  The
+// k dimension of Q.K is split as d = 32 (l/16) + m and the output columns
+// as d = 8 (l%16) + b, so every lane's K and V operands are contiguous
+// 32-byte runs.  Arithmetic stays f32 throughout.
+// Lane layout of the builtin (checked on gfx950): lane l supplies
+// A[l%16][l/16] and B[l/16][l%16], and receives D[4(l/16)+r][l%16], r < 4.
+typedef float f4v __attribute__((ext_vector_type(4)));
+constexpr int MH = 16;      // padded heads per kv head
+constexpr int MHD = 128;    // head_dim of this variant
+constexpr int MNB = MHD / 16;
+
+__global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
+{
+    const int c = blockIdx.x, kvh = blockIdx.y;
+    const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
+    const int t0 = c * chunk;
+    if (t0 >= n_t) return;
+    const int t1 = min(n_t, t0 + chunk);
+    const int gqa = a.nh / a.nkv, kv_dim = a.nkv * MHD;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lr = lane & 15, lg = lane >> 4;  // row-lane, k-group
+
+    extern __shared__ __align__(16) float sm[];
+    float *qs = sm;                      // [MH][MHD] normalised, rotated q (zero rows past gqa)
+    float *knew = qs + MH * MHD;         // [MHD]
+    float *vnew = knew + MHD;            // [MHD]
+    float *pt = vnew + MHD;              // [AT_WAVES][MH][16] probabilities
+    float *mo = pt + AT_WAVES * MH * 16; // [AT_WAVES][MH][MHD] merge area
+    float *mm = mo + AT_WAVES * MH * MHD;
+    float *ml = mm + AT_WAVES * MH;
+
+    // prologue: the q heads (one wave per head, round robin) and, in the
+    // chunk holding pos, the new k/v head, normalised and rotated into LDS
+    const bool owns_pos = t1 == n_t;
+    const double2 *csrow = a.rope + (int64_t)pos * (MHD / 2);
+    for (int i = wave; i < MH + (owns_pos ? 1 : 0); i += AT_WAVES) {
+        if (i < gqa) {
+            HeadIn<1> hin;
+            double2 cs[1];
+            cs_load<1>(cs, csrow, MHD);
+            head_load<1>(hin, a.q + (int64_t)(kvh * gqa + i) * MHD, a.q_norm, MHD);
+            head_finish<1>(hin, cs, a.q_norm != nullptr, a.eps, MHD, qs + i * MHD);
+        } else if (i < MH) {
+            for (int e = lane; e < MHD; e += 64) qs[i * MHD + e] = 0.0f;
+        } else {
+            HeadIn<1> hin;
+            double2 cs[1];
+            cs_load<1>(cs, csrow, MHD);
+            head_load<1>(hin, a.k + (int64_t)kvh * MHD, a.k_norm, MHD);
+            head_finish<1>(hin, cs, a.k_norm != nullptr, a.eps, MHD, knew);
+            for (int e = lane; e < MHD; e += 64) vnew[e] = a.v[(int64_t)kvh * MHD + e];
+        }
+    }
+    __syncthreads();
+    if (owns_pos && wave == 0) {
+        const int64_t po = kv_off(a, pos, kvh, kv_dim);
+        for (int e = lane; e < MHD; e += 64) {
+            a.kpool[po + e] = knew[e];
+            a.vpool[po + e] = vnew[e];
+        }
+    }
+    // this lane's Q operand: Q[lr][32 lg + m], m < 32
+    float qv[MHD / 4];
+#pragma unroll
+    for (int m = 0; m < MHD / 4; m += 4) {
+        const float4 v = *(const float4 *)(qs + lr * MHD + 32 * lg + m);
+        qv[m] = v.x; qv[m + 1] = v.y; qv[m + 2] = v.z; qv[m + 3] = v.w;
+    }
+
+    const int step = AT_WAVES * 16;
+    int tb = t0 + wave * 16;
+    float kv[MHD / 4];     // K[tb + lr][32 lg + m]
+    float vvr[4][MNB];     // V[tb + 4q + lg][8 lr + b]
+    auto row_of = [&](int tbase) -> int64_t {
+        return tbase + lr < t1 ? kv_off(a, tbase + lr, kvh, kv_dim) : 0;
+    };
+    auto load_k = [&](int64_t row, int tbase) {
+        const bool ok = tbase + lr < t1;
+#pragma unroll
+        for (int m = 0; m < MHD / 4; m += 4) {
+            const float4 v = ok ? *(const float4 *)(a.kpool + row + 32 * lg + m)
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            kv[m] = v.x; kv[m + 1] = v.y; kv[m + 2] = v.z; kv[m + 3] = v.w;
+        }
+    };
+    auto load_v = [&](int64_t row, int tbase) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int t = 4 * q + lg;  // token in tile of this k-step
+            const int64_t rq = __shfl(row, t);
+            const bool ok = tbase + t < t1;
+#pragma unroll
+            for (int b = 0; b < MNB; b += 4) {
+                const float4 v = ok ? *(const float4 *)(a.vpool + rq + 8 * lr + b)
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                vvr[q][b] = v.x; vvr[q][b + 1] = v.y; vvr[q][b + 2] = v.z; vvr[q][b + 3] = v.w;
+            }
+        }
+    };
+    if (tb < t1) {
+        const int64_t row = row_of(tb);
+        load_k(row, tb);
+        load_v(row, tb);
+    }
+    int64_t row_n = row_of(tb + step);
+
+    float m_run[4], l_run[4];
+    f4v o[MNB];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        m_run[r] = -INFINITY;
+        l_run[r] = 0.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < MNB; b++) o[b] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
+    float *my_p = pt + wave * MH * 16;
+    for (; tb < t1; tb += step) {
+        const int tn = tb + step;
+        const bool tv = tb + lr < t1;
+        // the token at pos comes from LDS (its pool row is written above by
+        // wave 0 of this workgroup, possibly after these loads)
+        if (tb + lr == pos) {
+#pragma unroll
+            for (int m = 0; m < MHD / 4; m++) kv[m] = knew[32 * lg + m];
+        }
+        if (pos >= tb && pos < tb + 16) {
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (tb + 4 * q + lg == pos) {
+#pragma unroll
+                    for (int b = 0; b < MNB; b++) vvr[q][b] = vnew[8 * lr + b];
+                }
+        }
+        // four independent accumulation chains over the k-steps
+        f4v sc4[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) sc4[j] = (f4v){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int m = 0; m < MHD / 4; m++)
+            sc4[m & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[m], kv[m], sc4[m & 3], 0, 0, 0);
+        const f4v sacc = (sc4[0] + sc4[1]) + (sc4[2] + sc4[3]);
+        if (tn < t1) load_k(row_n, tn);  // kv is free
+        // online softmax; lane holds heads 4 lg + r, token lr
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float sv = tv ? sacc[r] * a.scale : -INFINITY;
+            const float m_new = fmaxf(m_run[r], max16(sv));
+            const float p = tv ? expf(sv - m_new) : 0.0f;
+            const float corr = expf(m_run[r] - m_new);
+            l_run[r] = l_run[r] * corr + sum16(p);
+            m_run[r] = m_new;
+#pragma unroll
+            for (int b = 0; b < MNB; b++) o[b][r] *= corr;
+            my_p[(4 * lg + r) * 16 + lr] = p;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // O += P V: A[h = lr][t = 4q + lg] = P, B[t][j = lr] = V[t][8 lr + b]
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float pa = my_p[lr * 16 + 4 * q + lg];
+#pragma unroll
+            for (int b = 0; b < MNB; b++)
+                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vvr[q][b], o[b], 0, 0, 0);
+        }
+        if (tn < t1) load_v(row_n, tn);  // vvr is free
+        row_n = row_of(tn + step);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    // merge the four waves (each covered every head over its own tiles)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int h = 4 * lg + r;
+#pragma unroll
+        for (int b = 0; b < MNB; b++) mo[(wave * MH + h) * MHD + 8 * lr + b] = o[b][r];
+        if (lr == 0) {
+            mm[wave * MH + h] = m_run[r];
+            ml[wave * MH + h] = l_run[r];
+        }
+    }
+    __syncthreads();
+    const int ps = MHD + 2;
+    float *part = a.part + ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
+    for (int idx = threadIdx.x; idx < gqa * MHD; idx += AT_WG) {
+        const int h = idx / MHD, e = idx - h * MHD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < AT_WAVES; w++) M = fmaxf(M, mm[w * MH + h]);
+        float O = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < AT_WAVES; w++) {
+            const float mw = mm[w * MH + h];
+            const float f = mw == -INFINITY ? 0.0f : expf(mw - M);
+            O += mo[(w * MH + h) * MHD + e] * f;
+            L += ml[w * MH + h] * f;
+        }
+        part[h * ps + e] = O;
+        if (e == 0) {
+            part[h * ps + MHD] = M;
+            part[h * ps + MHD + 1] = L;
+        }
+    }
+}
+
 // Merge the per-chunk partials (m, l, o) of one query head: M = max m_c,
 // L = sum l_c e^(m_c-M), out = sum o_c e^(m_c-M) / L; then the limbs of this
 // head's slice of the output.  CB_WG threads = CB_GROUPS chunk groups x 64
@@ -441,6 +656,19 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
     if (gqa < 1 || gqa > 16 || a.nh % a.nkv || (a.hd != 64 && a.hd != 128 && a.hd != 256) ||
         a.chunk < TILE || a.chunk % TILE || a.page_tokens < 1 || a.max_chunks < 1)
         return hipErrorInvalidValue;
+    // the matrix-core variant serves 16 query heads per kv head; its waves
+    // split tokens, so its chunks hold at least one 16-token tile per wave
+    const bool use_mfma = a.hd == MHD && gqa == MH;
+    AttnArgs am = a;
+    if (use_mfma) {
+        am.chunk = std::max(a.chunk, AT_WAVES * TILE);
+        // two of its 4-wave workgroups fit a CU (about 220 registers per
+        // lane): one round of workgroups on 256 CUs
+        am.max_chunks = std::max(1, std::min(a.max_chunks, 512 / a.nkv));
+        const size_t lds = sizeof(float) * ((size_t)MH * MHD + 2 * MHD + AT_WAVES * MH * 16 +
+                                            (size_t)AT_WAVES * MH * MHD + 2 * AT_WAVES * MH);
+        hipLaunchKernelGGL(k_attn_mfma, dim3(am.max_chunks, am.nkv), dim3(AT_WG), lds, st, am);
+    } else {
     // head groups: the largest of 4, 2, 1 dividing gqa
     const int nhg = gqa % 4 == 0 ? 4 : gqa % 2 == 0 ? 2 : 1;
     const int hpw = gqa / nhg;
@@ -452,10 +680,11 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
         launch_k_attn<4>(st, a, nhg, hpw);
     else
         return hipErrorInvalidValue;  // gqa of 5, 7, 9.. above 4 heads per wave
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nh), dim3(CB_WG),
-                       (size_t)((CB_GROUPS + 1) * a.hd + 2 * CB_GROUPS) * 4, st, a);
+                       (size_t)((CB_GROUPS + 1) * a.hd + 2 * CB_GROUPS) * 4, st, am);
     return hipGetLastError();
 }
 
