@@ -38,6 +38,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -129,17 +130,70 @@ def stream_read_gbs(gpu, nbytes: int = 2 << 30, reps: int = 10) -> float:
     return nbytes * reps / el / 1e9
 
 
+TRAFFIC_JSON = ROOT / "profiles" / "gate_up_traffic_30b_a3b.json"
+PMC_COMMANDS = [
+    "rocprofv3 --pmc FETCH_SIZE --kernel-include-regex copyBuffer --output-format csv -d OUT "
+    "-o copy_fetch -- python -u bench.py --copy-probe 268435456",
+    "rocprofv3 --pmc WRITE_SIZE --kernel-include-regex copyBuffer --output-format csv -d OUT "
+    "-o copy_write -- python -u bench.py --copy-probe 268435456",
+    "rocprofv3 --pmc FETCH_SIZE --kernel-include-regex k_gate_up --output-format csv -d OUT "
+    "-o gu_fetch -- python -u bench.py --steps 4 --warmup 1 --timing-steps 1 --no-cpu-baseline "
+    "--no-graph",
+    "rocprofv3 --pmc WRITE_SIZE --kernel-include-regex k_gate_up --output-format csv -d OUT "
+    "-o gu_write -- python -u bench.py --steps 4 --warmup 1 --timing-steps 1 --no-cpu-baseline "
+    "--no-graph",
+]
+
+
 def traffic_from_profile() -> dict | None:
-    """HBM bytes per k_gate_up launch measured with rocprofv3 --pmc
-    (FETCH_SIZE, WRITE_SIZE), scaled by the copy-kernel calibration; written
-    by the profiling recipe into profiles/gate_up_traffic.json."""
-    p = ROOT / "profiles" / "gate_up_traffic.json"
-    if not p.exists():
+    """HBM bytes per k_gate_up launch on config 2, measured with rocprofv3
+    --pmc (FETCH_SIZE, WRITE_SIZE) and scaled by the copy-kernel calibration
+    (``--traffic-from``)."""
+    if not TRAFFIC_JSON.exists():
         return None
     try:
-        return json.loads(p.read_text())
+        return json.loads(TRAFFIC_JSON.read_text())
     except ValueError:
         return None
+
+
+def pmc_values(path: Path, name_re: str) -> list[float]:
+    import csv
+    with open(path) as f:
+        return [float(r["Counter_Value"]) for r in csv.DictReader(f)
+                if re.search(name_re, r["Kernel_Name"])]
+
+
+def traffic_from(out_dir: str) -> int:
+    """Reduce the four PMC_COMMANDS outputs (under out_dir) to HBM bytes per
+    k_gate_up launch.  FETCH_SIZE and WRITE_SIZE read KiB per dispatch; each
+    is scaled by bytes / (counter x 1024) of a plain copy of known size,
+    then the per-dispatch sum is averaged over every k_gate_up dispatch of
+    the run (all three expert type pairs of the configs[1] model)."""
+    d = Path(out_dir)
+    n = 268435456
+    cf = pmc_values(d / "copy_fetch_counter_collection.csv", "copyBuffer")
+    cw = pmc_values(d / "copy_write_counter_collection.csv", "copyBuffer")
+    gf = pmc_values(d / "gu_fetch_counter_collection.csv", "k_gate_up")
+    gw = pmc_values(d / "gu_write_counter_collection.csv", "k_gate_up")
+    if len(cf) != 1 or len(cw) != 1 or not gf or len(gf) != len(gw):
+        raise SystemExit(f"bench.py: unexpected PMC rows in {d}")
+    ff, wf = n / (cf[0] * 1024), n / (cw[0] * 1024)
+    fetch, write = float(np.mean(gf)), float(np.mean(gw))
+    per = fetch * 1024 * ff + write * 1024 * wf
+    algo = 17423616
+    rec = {"kernel": "k_gate_up (expert gate+up dequant-matvec, all three type pairs of the "
+                     "configs[1] model)",
+           "bytes_per_launch": int(round(per)), "algorithmic_bytes_per_launch": algo,
+           "traffic_over_algorithmic": round(per / algo, 4),
+           "fetch_kib_per_dispatch_mean": round(fetch, 2),
+           "write_kib_per_dispatch_mean": round(write, 2), "dispatches": len(gf),
+           "calibration": {"copy_bytes": n, "copy_fetch_kib": cf[0], "copy_write_kib": cw[0],
+                           "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)},
+           "commands": PMC_COMMANDS}
+    TRAFFIC_JSON.write_text(json.dumps(rec, indent=1) + "\n")
+    log(json.dumps(rec))
+    return 0
 
 
 def config_setup(k: int, layers: int | None):
@@ -232,7 +286,12 @@ def main() -> int:
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run one device-to-device copy of BYTES (the calibration kernel "
                          "for rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
+    ap.add_argument("--traffic-from", default=None, metavar="DIR",
+                    help="only reduce the rocprofv3 --pmc outputs in DIR (copy calibration and "
+                         "k_gate_up FETCH_SIZE/WRITE_SIZE) into the HBM-traffic record and exit")
     args = ap.parse_args()
+    if args.traffic_from:
+        return traffic_from(args.traffic_from)
     if args.copy_probe:
         return copy_probe(args.copy_probe)
 
