@@ -26,9 +26,10 @@ pass of one token, device-side argmax, no host round trip per token).
 The JSON line carries:
   value      decode tok/s over the K timed steps
   roofline   the dominant kernel (expert gate/up dequant-matvec, k_gate_up):
-             algorithmic bytes per launch / average launch time measured
-             with HIP events on the engine's stream during extra decode steps
-             run with per-launch timing, against 8 TB/s
+             algorithmic bytes per launch / average launch time, measured
+             with HIP events on the engine's stream around graph replays of
+             the k_gate_up launches of every layer (each reading its own
+             slabs, as a token does), against 8 TB/s
   cpu_baseline  the C oracle (a restatement of the reference's CPU
              dequant-then-dot path, -O2 -ffp-contract=off) decoding the same
              model on the host's cores for a bounded sample
@@ -56,14 +57,56 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def kernel_table(stats: dict) -> dict:
+def kernel_table(m, stats: dict, timing_steps: int, graphs: bool, reps: int = 20) -> dict:
+    """Per-stage table.  `avg_us` is the in-graph duration: the stage's
+    launches for every layer captured as one graph and replayed `reps` times
+    between two HIP events (styx_moe_time_stage), divided by the launches per
+    token.  `event_us` is the eager timing pass, one HIP event pair around
+    each launch (it includes each launch's dispatch, about 2 us more); it is
+    also `avg_us` when graphs are off (rocprofv3 runs)."""
     out = {}
     for name, (n, ms, by) in stats.items():
-        if n:
-            us = ms * 1e3 / n
-            out[name] = {"launches": int(n), "avg_us": round(us, 3),
-                         "bytes_per_launch": round(by / n),
-                         "GB/s": round(by / n / (us * 1e-6) / 1e9, 1) if us > 0 else None}
+        if not n:
+            continue
+        per_tok = max(1, round(n / timing_steps))
+        ev_us = ms * 1e3 / n
+        row = {"launches": int(n), "event_us": round(ev_us, 3), "bytes_per_launch": round(by / n)}
+        us = ev_us
+        if graphs and name != "argmax":
+            rep_us, _ = m.time_stage(name, reps)
+            us = rep_us / per_tok
+        row["avg_us"] = round(us, 3)
+        row["GB/s"] = round(by / n / (us * 1e-6) / 1e9, 1) if us > 0 else None
+        out[name] = row
+    return out
+
+
+MB_PHASES = ["entry", "x_normalised", "limbs", "logits_seen", "ranked", "gate_up_done",
+             "gu_seen", "h_limbs", "down_done", "partials_seen", "end", "gu_issued", "gu_limbs",
+             "gu_dots"]
+
+
+def moe_block_phases(m) -> dict | None:
+    """Timeline of the fused MoE block on the last timed token: for each
+    phase, the median and the latest workgroup (us after the layer's first
+    workgroup entered), averaged over the layers."""
+    tr = m.moe_block_trace()
+    if tr is None:
+        return None
+    st, tpu = tr
+    out = {}
+    per = {p: ([], []) for p in MB_PHASES}
+    for lay in st.astype(np.float64):
+        t0 = lay[:, 0][lay[:, 0] > 0].min()
+        for i, p in enumerate(MB_PHASES):
+            v = lay[:, i][lay[:, i] > 0]
+            if len(v):
+                per[p][0].append(np.median(v - t0) / tpu)
+                per[p][1].append((v.max() - t0) / tpu)
+    for p, (med, mx) in per.items():
+        if med:
+            out[p] = {"median_us": round(float(np.mean(med)), 2),
+                      "last_us": round(float(np.mean(mx)), 2)}
     return out
 
 
@@ -130,29 +173,44 @@ def stream_read_gbs(gpu, nbytes: int = 2 << 30, reps: int = 10) -> float:
     return nbytes * reps / el / 1e9
 
 
-TRAFFIC_JSON = ROOT / "profiles" / "gate_up_traffic_30b_a3b.json"
-PMC_COMMANDS = [
-    "rocprofv3 --pmc FETCH_SIZE --kernel-include-regex copyBuffer --output-format csv -d OUT "
-    "-o copy_fetch -- python -u bench.py --copy-probe 268435456",
-    "rocprofv3 --pmc WRITE_SIZE --kernel-include-regex copyBuffer --output-format csv -d OUT "
-    "-o copy_write -- python -u bench.py --copy-probe 268435456",
-    "rocprofv3 --pmc FETCH_SIZE --kernel-include-regex k_gate_up --output-format csv -d OUT "
-    "-o gu_fetch -- python -u bench.py --steps 4 --warmup 1 --timing-steps 1 --no-cpu-baseline "
-    "--no-graph",
-    "rocprofv3 --pmc WRITE_SIZE --kernel-include-regex k_gate_up --output-format csv -d OUT "
-    "-o gu_write -- python -u bench.py --steps 4 --warmup 1 --timing-steps 1 --no-cpu-baseline "
-    "--no-graph",
-]
+# Kernels whose HBM traffic is measured on config 2, with their algorithmic
+# bytes per launch (means over the 48 layers of configs[1]):
+#   k_moe_block  router E*H*4 + 8 slots x (gate + up + down slab) + 16*H
+#   k_gate_up    8 slots x (gate + up slab) + limbs, logits, outputs
+TRAFFIC_KERNELS = {
+    "k_moe_block": ("moe_block", 128 * 2048 * 4 + 8 * 3256320 + 16 * 2048),
+    "k_gate_up": ("moe_gate_up", 17423616),
+}
 
 
-def traffic_from_profile() -> dict | None:
-    """HBM bytes per k_gate_up launch on config 2, measured with rocprofv3
-    --pmc (FETCH_SIZE, WRITE_SIZE) and scaled by the copy-kernel calibration
-    (``--traffic-from``)."""
-    if not TRAFFIC_JSON.exists():
+def traffic_json(stage: str) -> Path:
+    return ROOT / "profiles" / f"{stage}_traffic_30b_a3b.json"
+
+
+def pmc_commands(kernel: str) -> list[str]:
+    b = ("python -u bench.py --steps 4 --warmup 1 --timing-steps 1 --no-cpu-baseline "
+         "--no-graph")
+    return [
+        "rocprofv3 --pmc FETCH_SIZE --kernel-include-regex copyBuffer --output-format csv "
+        "-d OUT -o copy_fetch -- python -u bench.py --copy-probe 268435456",
+        "rocprofv3 --pmc WRITE_SIZE --kernel-include-regex copyBuffer --output-format csv "
+        "-d OUT -o copy_write -- python -u bench.py --copy-probe 268435456",
+        f"rocprofv3 --pmc FETCH_SIZE --kernel-include-regex {kernel} --output-format csv "
+        f"-d OUT -o k_fetch -- {b}",
+        f"rocprofv3 --pmc WRITE_SIZE --kernel-include-regex {kernel} --output-format csv "
+        f"-d OUT -o k_write -- {b}",
+    ]
+
+
+def traffic_from_profile(stage: str) -> dict | None:
+    """HBM bytes per launch of the stage's kernel on config 2, measured with
+    rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE) and scaled by the copy-kernel
+    calibration (``--traffic-from``)."""
+    p = traffic_json(stage)
+    if not p.exists():
         return None
     try:
-        return json.loads(TRAFFIC_JSON.read_text())
+        return json.loads(p.read_text())
     except ValueError:
         return None
 
@@ -164,34 +222,36 @@ def pmc_values(path: Path, name_re: str) -> list[float]:
                 if re.search(name_re, r["Kernel_Name"])]
 
 
-def traffic_from(out_dir: str) -> int:
-    """Reduce the four PMC_COMMANDS outputs (under out_dir) to HBM bytes per
-    k_gate_up launch.  FETCH_SIZE and WRITE_SIZE read KiB per dispatch; each
-    is scaled by bytes / (counter x 1024) of a plain copy of known size,
-    then the per-dispatch sum is averaged over every k_gate_up dispatch of
-    the run (all three expert type pairs of the configs[1] model)."""
+def traffic_from(out_dir: str, kernel: str) -> int:
+    """Reduce the four pmc_commands(kernel) outputs (under out_dir) to HBM
+    bytes per launch of `kernel`.  FETCH_SIZE and WRITE_SIZE read KiB per
+    dispatch; each is scaled by bytes / (counter x 1024) of a plain copy of
+    known size, then the per-dispatch sum is averaged over every dispatch of
+    the kernel in the run (all layers, so all expert type triples of the
+    configs[1] model)."""
+    if kernel not in TRAFFIC_KERNELS:
+        raise SystemExit(f"bench.py: no algorithmic byte count for {kernel}")
+    stage, algo = TRAFFIC_KERNELS[kernel]
     d = Path(out_dir)
     n = 268435456
     cf = pmc_values(d / "copy_fetch_counter_collection.csv", "copyBuffer")
     cw = pmc_values(d / "copy_write_counter_collection.csv", "copyBuffer")
-    gf = pmc_values(d / "gu_fetch_counter_collection.csv", "k_gate_up")
-    gw = pmc_values(d / "gu_write_counter_collection.csv", "k_gate_up")
+    gf = pmc_values(d / "k_fetch_counter_collection.csv", kernel)
+    gw = pmc_values(d / "k_write_counter_collection.csv", kernel)
     if len(cf) != 1 or len(cw) != 1 or not gf or len(gf) != len(gw):
         raise SystemExit(f"bench.py: unexpected PMC rows in {d}")
     ff, wf = n / (cf[0] * 1024), n / (cw[0] * 1024)
     fetch, write = float(np.mean(gf)), float(np.mean(gw))
     per = fetch * 1024 * ff + write * 1024 * wf
-    algo = 17423616
-    rec = {"kernel": "k_gate_up (expert gate+up dequant-matvec, all three type pairs of the "
-                     "configs[1] model)",
+    rec = {"kernel": f"{kernel} (all layers of the configs[1] model)",
            "bytes_per_launch": int(round(per)), "algorithmic_bytes_per_launch": algo,
            "traffic_over_algorithmic": round(per / algo, 4),
            "fetch_kib_per_dispatch_mean": round(fetch, 2),
            "write_kib_per_dispatch_mean": round(write, 2), "dispatches": len(gf),
            "calibration": {"copy_bytes": n, "copy_fetch_kib": cf[0], "copy_write_kib": cw[0],
                            "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)},
-           "commands": PMC_COMMANDS}
-    TRAFFIC_JSON.write_text(json.dumps(rec, indent=1) + "\n")
+           "commands": pmc_commands(kernel)}
+    traffic_json(stage).write_text(json.dumps(rec, indent=1) + "\n")
     log(json.dumps(rec))
     return 0
 
@@ -265,7 +325,11 @@ def measure(m, args, prompt):
     toks.append(m.decode(args.timing_steps))
     stats = m.kernel_stats()
     m.set_timing(False)
-    return args.steps / el, el, np.concatenate(toks), stats
+    phases = moe_block_phases(m)
+    table = kernel_table(m, stats, args.timing_steps, not args.no_graph)
+    if phases:
+        table["moe_block"]["phases"] = phases
+    return args.steps / el, el, np.concatenate(toks), table
 
 
 def main() -> int:
@@ -281,6 +345,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=None, help="(testing only) fewer layers")
     ap.add_argument("--contexts", default="512,4096,32768",
                     help="config 4: synthetic context lengths to decode after")
+    ap.add_argument("--no-fuse", action="store_true",
+                    help="run the MoE block as four kernels instead of the fused launch")
     ap.add_argument("--no-graph", action="store_true",
                     help="enqueue kernels one by one instead of replaying a HIP graph per token")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -288,10 +354,12 @@ def main() -> int:
                          "for rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
     ap.add_argument("--traffic-from", default=None, metavar="DIR",
                     help="only reduce the rocprofv3 --pmc outputs in DIR (copy calibration and "
-                         "k_gate_up FETCH_SIZE/WRITE_SIZE) into the HBM-traffic record and exit")
+                         "the kernel's FETCH_SIZE/WRITE_SIZE) into the HBM-traffic record and exit")
+    ap.add_argument("--traffic-kernel", default="k_moe_block", choices=sorted(TRAFFIC_KERNELS),
+                    help="kernel of --traffic-from")
     args = ap.parse_args()
     if args.traffic_from:
-        return traffic_from(args.traffic_from)
+        return traffic_from(args.traffic_from, args.traffic_kernel)
     if args.copy_probe:
         return copy_probe(args.copy_probe)
 
@@ -315,9 +383,11 @@ def main() -> int:
     t0 = time.perf_counter()
     if args.config == 4:
         ctxs = [int(c) for c in args.contexts.split(",") if c]
-        m = MoeModel.synth(gpu, cfg, n_ctx=max(ctxs) + n_ctx, use_graph=not args.no_graph)
+        m = MoeModel.synth(gpu, cfg, n_ctx=max(ctxs) + n_ctx, use_graph=not args.no_graph,
+                           fuse=not args.no_fuse)
     else:
-        m = MoeModel.synth(gpu, cfg, n_ctx=max(n_ctx, 512), use_graph=not args.no_graph)
+        m = MoeModel.synth(gpu, cfg, n_ctx=max(n_ctx, 512), use_graph=not args.no_graph,
+                           fuse=not args.no_fuse)
     log(f"built synthetic model in {time.perf_counter() - t0:.1f}s on {gpu.name}: "
         f"{m.hp.expert_bytes_hbm / 2**30:.2f} GiB experts in HBM, slab {m.slab_bytes} B")
 
@@ -329,7 +399,7 @@ def main() -> int:
         m.close()
         t0 = time.perf_counter()
         m = MoeModel.synth(gpu, cfg, n_ctx=max(n_ctx, 512), use_graph=not args.no_graph,
-                           expert_budget_mb=6144, expert_hist=str(hist), arena=True)
+                           fuse=not args.no_fuse, expert_budget_mb=6144, expert_hist=str(hist), arena=True)
         log(f"host-pinned model in {time.perf_counter() - t0:.1f}s: "
             f"{m.hp.expert_bytes_hbm / 2**30:.2f} GiB hot in HBM, "
             f"{m.hp.expert_bytes_host / 2**30:.2f} GiB in host memory")
@@ -342,9 +412,9 @@ def main() -> int:
             m.fill_kv(c)
             args_c = argparse.Namespace(**vars(args))
             args_c.warmup = min(args.warmup, 4)
-            v, el, toks, stats = measure(m, args_c, prompt[:1])
+            v, el, toks, table = measure(m, args_c, prompt[:1])
             per_ctx[str(c)] = {"tok_s": round(v, 3), "ms_per_step": round(1e3 * el / args.steps, 4),
-                               "kernels": kernel_table(stats)}
+                               "kernels": table}
             log(f"context {c}: {v:.1f} tok/s")
         value, el = per_ctx[str(ctxs[-1])]["tok_s"], None
         el = args.steps / value
@@ -352,8 +422,7 @@ def main() -> int:
         extra["contexts"] = per_ctx
         toks = None
     else:
-        value, el, toks, stats = measure(m, args, prompt)
-        table = kernel_table(stats)
+        value, el, toks, table = measure(m, args, prompt)
     for k, v in table.items():
         log(f"  {k:18s} {v}")
 
@@ -370,17 +439,23 @@ def main() -> int:
         extra["hit_rate"] = round(hot / max(hot + cold, 1), 4)
         hist.unlink(missing_ok=True)
 
-    gu = table.get("moe_gate_up", {})
+    # the dominant kernel: the fused MoE block, or gate/up when the block
+    # runs as separate kernels
+    stage = "moe_block" if "moe_block" in table else "moe_gate_up"
+    kname = {"moe_block": "k_moe_block (MoE block: router, expert gate/up/down dequant-matvec, "
+                          "combine)",
+             "moe_gate_up": "k_gate_up (expert gate+up dequant-matvec)"}[stage]
+    gu = table.get(stage, {})
     roofline = None
     if gu:
         ach = gu["GB/s"]
-        tr = traffic_from_profile() if args.config == 2 else None
+        tr = traffic_from_profile(stage) if args.config == 2 else None
         roofline = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(ach / HBM_PEAK_GBS, 4),
                     "traffic": tr["bytes_per_launch"] if tr else None,
                     "stream_read_GBps": round(stream_gbs, 1),
                     "frac_of_stream_read": round(ach / stream_gbs, 4),
-                    "kernel": "k_gate_up (expert gate+up dequant-matvec)",
+                    "kernel": kname,
                     "bytes_per_launch": gu["bytes_per_launch"], "avg_us": gu["avg_us"],
                     "launches": gu["launches"]}
 

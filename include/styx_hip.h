@@ -34,6 +34,7 @@ enum {
     STYX_E_FORMAT = -5,       /* GGUF / tensor layout rejected */
     STYX_E_STATE = -6,        /* call out of order (e.g. KV full) */
     STYX_E_UNSUPPORTED = -7,
+    STYX_E_DEVICE = -8,       /* a device-side wait gave up; model results invalid */
 };
 /* Thread-local message of the last failing call (never NULL). */
 const char *styx_last_error(void);
@@ -229,6 +230,8 @@ typedef struct {
     int repin_max;           /* MOE_REPIN_MAX; 0 = 2 */
     int record_hidden;       /* keep the residual after every layer */
     int time_kernels;        /* HIP events around the expert kernels */
+    int no_fuse;             /* 1: run the MoE block as four kernels instead of
+                                the fused persistent one (same results) */
 } styx_moe_opts;
 
 typedef struct {
@@ -286,6 +289,25 @@ int styx_moe_decode(styx_moe *m, int n_steps, uint32_t *out);
 /* Turn HIP-event timing of every kernel launch on or off (launches are then
  * enqueued one by one instead of replayed as a graph). */
 int styx_moe_set_timing(styx_moe *m, int on);
+/* Phase stamps of the fused MoE block kernel (measurement helper, no
+ * counterpart in the reference) from the last token run with timing on:
+ * [n_layers][*nwg][16] wall-clock ticks per workgroup -- 0 entry, 1 x
+ * normalised, 2 limbs built, 3 logits seen, 4 ranked, 5 gate/up done, 6 g/u
+ * seen, 7 swiglu limbs built, 8 down done, 9 partials seen, 10 end (0: no
+ * such phase).  *nwg = 0 when the model runs the separate kernels; out may
+ * be NULL to query *nwg. */
+int styx_moe_moe_block_trace(styx_moe *m, uint64_t *out, int64_t max_count, int *nwg,
+                             double *ticks_per_us);
+/* Stage timing (measurement helper, no counterpart in the reference): the
+ * launches of one stage ("embed", "qkv", "attn", "o_proj", "router",
+ * "gather", "moe_gate_up", "shexp", "moe_down", "reduce", "lm_head") for
+ * every layer of the last token, captured as one graph (repeated to at
+ * least 32 launches for shallow models) and replayed `reps` times between
+ * two HIP events; *us_per_replay = mean time of one pass over the layers,
+ * *launches = kernels per pass.  Needs one token run first; overwrites
+ * per-token scratch that the next token rewrites before reading. */
+int styx_moe_time_stage(styx_moe *m, const char *stage, int reps, double *us_per_replay,
+                        int *launches);
 /* MoeModel::last_expert_ids (moe.rs:2387-2402): [n_layers][k]. */
 int styx_moe_last_expert_ids(styx_moe *m, uint32_t *out);
 /* MoeModel::last_hot_cold (moe.rs:1512-1521): [n_layers][2] (hot, cold). */

@@ -37,6 +37,7 @@ class MoeOpts(C.Structure):
         ("repin_max", C.c_int),
         ("record_hidden", C.c_int),
         ("time_kernels", C.c_int),
+        ("no_fuse", C.c_int),
     ]
 
 
@@ -135,6 +136,8 @@ _SIGS = {
     "styx_moe_generate": (i32, [vp, vp, i32, i32, vp, vp, vp]),
     "styx_moe_decode": (i32, [vp, i32, vp]),
     "styx_moe_set_timing": (i32, [vp, i32]),
+    "styx_moe_moe_block_trace": (i32, [vp, vp, i64, C.POINTER(i32), C.POINTER(C.c_double)]),
+    "styx_moe_time_stage": (i32, [vp, C.c_char_p, i32, C.POINTER(C.c_double), C.POINTER(i32)]),
     "styx_moe_last_expert_ids": (i32, [vp, vp]),
     "styx_moe_last_hot_cold": (i32, [vp, vp]),
     "styx_moe_reset": (i32, [vp]),

@@ -25,6 +25,7 @@ SOURCES = [
     "kernels_aux.hip",
     "kernels_ref.hip",
     "attn.hip",
+    "moe_block.hip",
     "capi.cpp",
     "dispatch.cpp",
     "engine.cpp",

@@ -13,6 +13,17 @@
 
 namespace styx {
 
+// Global-memory pointers for device code: loads and stores through them are
+// global_* instructions even when the pointer value comes from LDS or a
+// computed struct (a generic pointer would give flat_* instructions, which
+// also count against the LDS wait counter).  The vector types are clang's
+// ext_vector_type so that both compilation passes accept the qualified
+// loads.
+#define STYX_GLOBAL __attribute__((address_space(1)))
+typedef unsigned styx_u4 __attribute__((ext_vector_type(4)));
+typedef unsigned styx_u2 __attribute__((ext_vector_type(2)));
+typedef float styx_f4 __attribute__((ext_vector_type(4)));
+
 enum QType : int { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14 };
 
 constexpr uint32_t SKIP = 0xFFFFFFFFu;

@@ -12,17 +12,17 @@ namespace styx {
 __device__ __forceinline__ void deq_block(int t, const Mat &m, int64_t blk, float *y)
 {
     if (t == T_Q8_0) {
-        const float d = f16f(*(const uint16_t *)(m.r1 + blk * 2));
-        const int8_t *q = (const int8_t *)(m.r0 + blk * 32);
+        const float d = f16f(*(const uint16_t STYX_GLOBAL *)(m.r1 + blk * 2));
+        const int8_t STYX_GLOBAL *q = (const int8_t STYX_GLOBAL *)(m.r0 + blk * 32);
         for (int i = 0; i < 32; i++) y[i] = d * (float)q[i];
         return;
     }
     if (t == T_Q4_K || t == T_Q5_K) {
-        const uint8_t *hd = (t == T_Q4_K ? m.r1 : m.r2) + blk * 16;
-        const uint8_t *qs = m.r0 + blk * 128;
-        const uint8_t *qh = t == T_Q5_K ? m.r1 + blk * 32 : nullptr;
+        const uint8_t STYX_GLOBAL *hd = (t == T_Q4_K ? m.r1 : m.r2) + blk * 16;
+        const uint8_t STYX_GLOBAL *qs = m.r0 + blk * 128;
+        const uint8_t STYX_GLOBAL *qh = t == T_Q5_K ? m.r1 + blk * 32 : nullptr;
         const float d = f16f(hd[0] | (hd[1] << 8)), dmin = f16f(hd[2] | (hd[3] << 8));
-        const uint8_t *sc = hd + 4;
+        const uint8_t STYX_GLOBAL *sc = hd + 4;
         for (int j = 0; j < 4; j++) {
             float s1, m1, s2, m2;
             for (int h = 0; h < 2; h++) {
@@ -51,10 +51,10 @@ __device__ __forceinline__ void deq_block(int t, const Mat &m, int64_t blk, floa
         return;
     }
     if (t == T_Q6_K) {
-        const float d = f16f(*(const uint16_t *)(m.r3 + blk * 2));
+        const float d = f16f(*(const uint16_t STYX_GLOBAL *)(m.r3 + blk * 2));
         for (int n = 0; n < 2; n++) {
-            const uint8_t *ql = m.r0 + blk * 128 + 64 * n, *qh = m.r1 + blk * 64 + 32 * n;
-            const int8_t *sc = (const int8_t *)(m.r2 + blk * 16 + 8 * n);
+            const uint8_t STYX_GLOBAL *ql = m.r0 + blk * 128 + 64 * n, *qh = m.r1 + blk * 64 + 32 * n;
+            const int8_t STYX_GLOBAL *sc = (const int8_t STYX_GLOBAL *)(m.r2 + blk * 16 + 8 * n);
             for (int l = 0; l < 32; l++) {
                 const int is = l / 16;
                 const int q1 = (int)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
@@ -70,17 +70,18 @@ __device__ __forceinline__ void deq_block(int t, const Mat &m, int64_t blk, floa
         return;
     }
     if (t == T_F32) {
-        y[0] = *(const float *)(m.r0 + blk * 4);
+        y[0] = *(const float STYX_GLOBAL *)(m.r0 + blk * 4);
         return;
     }
-    if (t == T_F16) y[0] = f16f(*(const uint16_t *)(m.r0 + blk * 2));
+    if (t == T_F16) y[0] = f16f(*(const uint16_t STYX_GLOBAL *)(m.r0 + blk * 2));
 }
 #pragma clang fp contract(on)
 
 
 // View of one GGUF-layout block as a one-block split matrix.
-__device__ __forceinline__ Mat gguf_blk(const uint8_t *b, int t)
+__device__ __forceinline__ Mat gguf_blk(const uint8_t *bp, int t)
 {
+    const uint8_t STYX_GLOBAL *b = (const uint8_t STYX_GLOBAL *)bp;
     Mat m{b, b, b, b};
     if (t == T_Q8_0) { m.r0 = b + 2; m.r1 = b; }
     else if (t == T_Q4_K) { m.r0 = b + 16; m.r1 = b; }

@@ -133,6 +133,14 @@ struct styx_moe {
     std::vector<int32_t> h_pt;
     int pages_per_layer = 0, next_page = 0, chunk = 64, max_chunks = 1;
     double *rope = nullptr;  // [n_ctx][hd/2] (cos, sin)
+    // fused MoE block (moe_block.hip): tagged exchange buffers, ticket,
+    // abort flag; mb_nwg = its grid (0: the separate kernels run), -1 until
+    // first sized
+    uint64_t *t_lg = nullptr, *t_gu = nullptr, *t_part = nullptr;
+    unsigned long long *mb_ticket = nullptr;
+    int *mb_abort = nullptr;
+    int mb_nwg = -1;
+    uint64_t *mb_trace = nullptr;  // [L][mb_nwg][16] phase stamps of the last timed token
     // arena
     uint8_t *arena[3] = {nullptr, nullptr, nullptr};
     int64_t arena_slab[3] = {0, 0, 0};
@@ -147,6 +155,7 @@ struct styx_moe {
     std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> pending;
     std::vector<hipEvent_t> ev_pool;
     size_t ev_next = 0;
+    std::string stage_only;  // enqueue only this stage's launches (stage timing)
 
     ~styx_moe();
     int alloc(void **p, size_t n);
@@ -156,6 +165,9 @@ struct styx_moe {
         return alloc((void **)p, sizeof(T) * count);
     }
     int setup_runtime();
+    int size_moe_block();
+    int check_abort();
+    void queue_abort_read();
     int place_experts(const std::vector<std::vector<std::pair<uint32_t, uint64_t>>> *hist);
     int enqueue_token(bool gen);
     int run_token(bool gen);
@@ -278,6 +290,7 @@ int styx_moe::setup_runtime()
     void *hs;
     if (int r = alloc_host(&hs, 64)) return r;
     h_stage = (uint32_t *)hs;
+    std::memset(h_stage, 0, 64);
     // paged KV: pool sized for n_ctx on every layer, pages handed out lazily
     pages_per_layer = (n_ctx + KV_PAGE_TOKENS - 1) / KV_PAGE_TOKENS;
     const size_t pool = (size_t)L * pages_per_layer * KV_PAGE_TOKENS * kv_dim;
@@ -295,6 +308,18 @@ int styx_moe::setup_runtime()
     max_chunks = std::min((n_ctx + chunk - 1) / chunk, std::max(16, 768 / nkv));
     const int64_t pf = styx_op_attn_part_floats(nh, nkv, hd, max_chunks);
     if (int r = dalloc(&attn_part, (size_t)pf)) return r;
+    // tagged exchange of the fused MoE block: zero once (tag 0 is never a
+    // launch's), never cleared again
+    if (int r = dalloc(&t_lg, E)) return r;
+    if (int r = dalloc(&t_gu, (size_t)2 * (K + 1) * F)) return r;
+    if (int r = dalloc(&t_part, (size_t)(K + 1) * H)) return r;
+    if (int r = dalloc(&mb_ticket, 64 * 16)) return r;
+    if (int r = dalloc(&mb_abort, 1)) return r;
+    STYX_HIP(hipMemsetAsync(t_lg, 0, sizeof(uint64_t) * E, gpu->stream));
+    STYX_HIP(hipMemsetAsync(t_gu, 0, sizeof(uint64_t) * 2 * (K + 1) * F, gpu->stream));
+    STYX_HIP(hipMemsetAsync(t_part, 0, sizeof(uint64_t) * (K + 1) * H, gpu->stream));
+    STYX_HIP(hipMemsetAsync(mb_ticket, 0, sizeof(unsigned long long) * 64 * 16, gpu->stream));
+    STYX_HIP(hipMemsetAsync(mb_abort, 0, sizeof(int), gpu->stream));
     // rope factors in f64 for every position of the context (ops2.rs:426-442)
     {
         std::vector<double> cs((size_t)n_ctx * hd);
@@ -436,6 +461,50 @@ int styx_moe::place_experts(const std::vector<std::vector<std::pair<uint32_t, ui
     return STYX_OK;
 }
 
+// Grid of the fused MoE block: every workgroup resident at once, at most two
+// per CU, the same for every layer (the launch tag is ticket / grid); 0 when
+// a layer's shapes or placement need the separate kernels, or the model
+// options ask for them.
+int styx_moe::size_moe_block()
+{
+    mb_nwg = 0;
+    if (opts.no_fuse || L == 0) return STYX_OK;
+    int per_cu = 2;
+    for (const Layer &ly : layers) {
+        const bool sh_fused = ly.gsh.dev && Fsh == F && ly.gsh.type == ly.gate.type &&
+                              ly.ush.type == ly.up.type && ly.dsh.type == ly.down.type;
+        if ((ly.gsh.dev && !sh_fused) || (ly.host_experts && opts.arena)) return STYX_OK;
+        per_cu = std::min(per_cu, moe_block_occupancy(ly.gate.type, ly.up.type, ly.down.type, H, F,
+                                                      E, K, sh_fused ? 1 : 0));
+    }
+    if (per_cu < 1) return STYX_OK;
+    int ncu = 0;
+    STYX_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, gpu->device));
+    mb_nwg = per_cu * ncu / 64 * 64;  // the kernel's ticket counters need a multiple of 64
+    if (mb_nwg > 0 && !mb_trace)
+        if (int r = dalloc(&mb_trace, (size_t)L * mb_nwg * 16)) return r;
+    return STYX_OK;
+}
+
+// A fused MoE launch whose wait ran out sets the abort flag; the model's
+// results are then invalid and it stays in error until reloaded.  The flag
+// is copied into the pinned stage (h_stage[4]) ahead of the caller's stream
+// synchronisation (queue_abort_read), then checked here.
+void styx_moe::queue_abort_read()
+{
+    if (mb_abort && mb_nwg > 0)
+        (void)hipMemcpyAsync(&h_stage[4], mb_abort, sizeof(int), hipMemcpyDeviceToHost, gpu->stream);
+}
+
+int styx_moe::check_abort()
+{
+    if (!mb_abort || mb_nwg <= 0) return STYX_OK;
+    if (h_stage[4])
+        return fail(STYX_E_DEVICE, "fused MoE block: a workgroup's wait ran out (not all "
+                                   "workgroups resident?); results of this model are invalid");
+    return STYX_OK;
+}
+
 // ------------------------------------------------------------ forward ----
 int styx_moe::enqueue_token(bool gen)
 {
@@ -458,26 +527,29 @@ int styx_moe::enqueue_token(bool gen)
         stats[id].bytes += bytes;
         pending.push_back({id, {a, e}});
     };
+    auto want = [&](const char *nm) { return stage_only.empty() || stage_only == nm; };
+    if (mb_nwg < 0)
+        if (int r = size_moe_block()) return r;
     // the first layer's q/k/v input: limbs of attn_norm_0(x) (or of the LM
     // head's output_norm(x) for a model without layers)
     const float *norm0 = L > 0 ? layers[0].attn_norm : out_norm;
-    CK(launch_embed(st, embd.type, embd.dev, V, H, d_tok, x, norm0, xq_a, ss_a));
+    if (want("embed")) CK(launch_embed(st, embd.type, embd.dev, V, H, d_tok, x, norm0, xq_a, ss_a));
     // every consumer of xq_a applies the RMSNorm scale from the x^2 partials
     const NormScale ns_a{ss_a, (H + 255) / 256, H, eps};
-    if (opts.record_hidden) CK(hipMemcpyAsync(hidden, x, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
+    if (opts.record_hidden && stage_only.empty()) CK(hipMemcpyAsync(hidden, x, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
     for (int l = 0; l < L; l++) {
         Layer &ly = layers[l];
         hipEvent_t e0 = tstart();
         if (ly.wq.type == ly.wk.type && ly.wq.type == ly.wv.type) {
             DenseSeg s[3] = {{ly.wq.dev, q, ly.wq.rows}, {ly.wk.dev, kk, ly.wk.rows},
                              {ly.wv.dev, vv, ly.wv.rows}};
-            CK(launch_dense(st, ly.wq.type, H, s, 3, xq_a, 0, &ns_a));
+            if (want("qkv")) CK(launch_dense(st, ly.wq.type, H, s, 3, xq_a, 0, &ns_a));
         } else {
             DenseSeg a{ly.wq.dev, q, ly.wq.rows}, b{ly.wk.dev, kk, ly.wk.rows},
                 c{ly.wv.dev, vv, ly.wv.rows};
-            CK(launch_dense(st, ly.wq.type, H, &a, 1, xq_a, 0, &ns_a));
-            CK(launch_dense(st, ly.wk.type, H, &b, 1, xq_a, 0, &ns_a));
-            CK(launch_dense(st, ly.wv.type, H, &c, 1, xq_a, 0, &ns_a));
+            if (want("qkv")) CK(launch_dense(st, ly.wq.type, H, &a, 1, xq_a, 0, &ns_a));
+            if (want("qkv")) CK(launch_dense(st, ly.wk.type, H, &b, 1, xq_a, 0, &ns_a));
+            if (want("qkv")) CK(launch_dense(st, ly.wv.type, H, &c, 1, xq_a, 0, &ns_a));
         }
         tend(e0, "qkv", (double)(ly.wq.bytes() + ly.wk.bytes() + ly.wv.bytes()) + xq_bytes(H));
         e0 = tstart();
@@ -503,12 +575,15 @@ int styx_moe::enqueue_token(bool gen)
         aa.chunk = chunk;
         aa.max_chunks = max_chunks;
         aa.scale = 1.0f / std::sqrt((float)hd);
-        CK(launch_attn_decode(st, aa));
+        if (want("attn")) CK(launch_attn_decode(st, aa));
         tend(e0, "attn", (double)(n_past + 1) * nkv * hd * 8.0);
         e0 = tstart();
         DenseSeg so{ly.wo.dev, x, H};
-        CK(launch_dense(st, ly.wo.type, q_dim, &so, 1, xq_o, 1));
+        if (want("o_proj")) CK(launch_dense(st, ly.wo.type, q_dim, &so, 1, xq_o, 1));
         tend(e0, "o_proj", (double)ly.wo.bytes() + xq_bytes(q_dim) + 8.0 * H);
+        // the MoE block: one fused persistent launch, or router, gate/up,
+        // down and reduce as separate kernels (identical results)
+        const bool fused = mb_nwg > 0;
         e0 = tstart();
         RouterArgs ra{};
         ra.x = x;
@@ -522,8 +597,8 @@ int styx_moe::enqueue_token(bool gen)
         ra.E = E;
         ra.H = H;
         ra.k = K;
-        CK(launch_router(st, ra));
-        tend(e0, "router", (double)E * H * 4 + 8.0 * H + 4.0 * E);
+        if (!fused && want("router")) CK(launch_router(st, ra));
+        if (!fused) tend(e0, "router", (double)E * H * 4 + 8.0 * H + 4.0 * E);
         // top-k ids are ranked by every consumer workgroup from the logits;
         // gate_up's first workgroup publishes the id row, k_reduce_norm the
         // weights
@@ -560,7 +635,7 @@ int styx_moe::enqueue_token(bool gen)
             const int64_t sslab[3] = {ly.gate.slab, ly.up.slab, ly.down.slab};
             Route rg = rt;
             rg.ids_out = nullptr;
-            CK(launch_gather(st, src, sslab, arena, arena_slab, nullptr, &rg, K));
+            if (want("gather")) CK(launch_gather(st, src, sslab, arena, arena_slab, nullptr, &rg, K));
             tend(e0, "gather", 0.0);
         }
         // the shared expert runs as slot K of the expert kernels when it has
@@ -570,11 +645,56 @@ int styx_moe::enqueue_token(bool gen)
         const double sh_gu = sh_fused ? (double)(ly.gsh.bytes() + ly.ush.bytes()) : 0.0;
         const double slabs_gu = (double)K * (ly.gate.slab + ly.up.slab) + sh_gu;
         const int nsl = K + (sh_fused ? 1 : 0);
+        if (fused) {
+            e0 = tstart();
+            MoeBlockArgs mb{};
+            mb.tg = ly.gate.type;
+            mb.tu = ly.up.type;
+            mb.td = ly.down.type;
+            mb.x = x;
+            mb.ffn_norm = ly.ffn_norm;
+            mb.W = ly.router;
+            mb.bias = ly.router_bias;
+            mb.eps = eps;
+            mb.H = H;
+            mb.F = F;
+            mb.E = E;
+            mb.k = K;
+            mb.renorm = norm_topk;
+            mb.src[0] = sg;
+            mb.src[1] = su;
+            mb.src[2] = sd;
+            mb.route = rt;
+            if (sh_fused) {
+                mb.sh[0] = ly.gsh.dev;
+                mb.sh[1] = ly.ush.dev;
+                mb.sh[2] = ly.dsh.dev;
+                mb.sh_ginp = ly.gate_inp_sh;
+            }
+            mb.norm_next = l + 1 < L ? layers[l + 1].attn_norm : out_norm;
+            mb.xq = xq_a;
+            mb.ss = ss_a;
+            mb.wts_out = wts + (size_t)l * 16;
+            mb.t_lg = t_lg;
+            mb.t_gu = t_gu;
+            mb.t_part = t_part;
+            mb.ticket = mb_ticket;
+            mb.abort = mb_abort;
+            mb.nwg = mb_nwg;
+            if (timing) {
+                // phase stamps of every workgroup (eager timed tokens only)
+                mb.trace = mb_trace + (size_t)l * mb_nwg * 16;
+                CK(hipMemsetAsync(mb.trace, 0, sizeof(uint64_t) * mb_nwg * 16, st));
+            }
+            if (want("moe_block")) CK(launch_moe_block(st, mb));
+            tend(e0, "moe_block", (double)E * H * 4 + slabs_gu + (double)K * ly.down.slab +
+                                      (sh_fused ? (double)ly.dsh.bytes() : 0.0) + 16.0 * H);
+        } else {
         e0 = tstart();
-        CK(launch_moe_gate_up(st, ly.gate.type, ly.up.type, sg, su, nullptr, &rt, xq_f, gu, H, F,
+        if (want("moe_gate_up")) CK(launch_moe_gate_up(st, ly.gate.type, ly.up.type, sg, su, nullptr, &rt, xq_f, gu, H, F,
                               K, sh_fused ? ly.gsh.dev : nullptr, sh_fused ? ly.ush.dev : nullptr));
         tend(e0, "moe_gate_up", slabs_gu + xq_bytes(H) + 4.0 * E + 4.0 * 2 * nsl * F);
-        if (ly.gsh.dev && !sh_fused) {
+        if (ly.gsh.dev && !sh_fused && want("shexp")) {
             e0 = tstart();
             DenseSeg s2[2] = {{ly.gsh.dev, sh_g, Fsh}, {ly.ush.dev, sh_u, Fsh}};
             if (ly.gsh.type == ly.ush.type) {
@@ -589,7 +709,7 @@ int styx_moe::enqueue_token(bool gen)
             tend(e0, "shexp", (double)(ly.gsh.bytes() + ly.ush.bytes() + ly.dsh.bytes()));
         }
         e0 = tstart();
-        CK(launch_moe_down(st, ly.down.type, sd, lid, gu, partial, H, F, K,
+        if (want("moe_down")) CK(launch_moe_down(st, ly.down.type, sd, lid, gu, partial, H, F, K,
                            sh_fused ? ly.dsh.dev : nullptr));
         tend(e0, "moe_down", (double)K * ly.down.slab + (sh_fused ? (double)ly.dsh.bytes() : 0.0) +
                                  4.0 * 2 * nsl * F + 4.0 * nsl * H);
@@ -612,18 +732,19 @@ int styx_moe::enqueue_token(bool gen)
         rd.norm_w = l + 1 < L ? layers[l + 1].attn_norm : out_norm;
         rd.xq = xq_a;
         rd.ss = ss_a;
-        CK(launch_reduce_rows(st, rd));
+        if (want("reduce")) CK(launch_reduce_rows(st, rd));
         tend(e0, "reduce", 4.0 * nsl * H + 12.0 * H + 4.0 * E + xq_bytes(H));
-        if (opts.record_hidden)
+        }
+        if (opts.record_hidden && stage_only.empty())
             CK(hipMemcpyAsync(hidden + (size_t)(l + 1) * H, x, sizeof(float) * H,
                               hipMemcpyDeviceToDevice, st));
     }
     hipEvent_t e0 = tstart();
     DenseSeg sh{head.dev, logits, V};
-    CK(launch_dense(st, head.type, H, &sh, 1, xq_a, 0, &ns_a));
+    if (want("lm_head")) CK(launch_dense(st, head.type, H, &sh, 1, xq_a, 0, &ns_a));
     tend(e0, "lm_head", (double)head.bytes() + xq_bytes(H) + 4.0 * V);
     e0 = tstart();
-    CK(launch_argmax(st, logits, V, d_tok, am_val, am_idx, d_pos, gen ? 1 : 0, hist));
+    if (want("argmax")) CK(launch_argmax(st, logits, V, d_tok, am_val, am_idx, d_pos, gen ? 1 : 0, hist));
     tend(e0, "argmax", 4.0 * V);
     return STYX_OK;
 }
@@ -951,6 +1072,7 @@ int build_model(styx_moe *m, const styx_moe_synth_cfg &c, const std::vector<Tens
     m->slab_bytes = l0.gate.slab + l0.up.slab + l0.down.slab;
     if (int r = m->place_experts(hist)) return r;
     if (int r = m->setup_runtime()) return r;
+    if (int r = m->size_moe_block()) return r;
     if (int r = m->build_graphs()) return r;
     return STYX_OK;
 }
@@ -1179,7 +1301,9 @@ int styx_moe_forward_token(styx_moe *m, uint32_t token, float *logits_out)
     if (logits_out)
         STYX_HIP(hipMemcpyAsync(logits_out, m->logits, sizeof(float) * m->V, hipMemcpyDeviceToHost,
                                 m->gpu->stream));
+    m->queue_abort_read();
     STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+    if (int r = m->check_abort()) return r;
     return m->collect_stats();
 }
 
@@ -1207,7 +1331,9 @@ int styx_moe_decode(styx_moe *m, int n_steps, uint32_t *out)
     }
     STYX_HIP(hipMemcpyAsync(out, m->hist + start + 1, sizeof(uint32_t) * n_steps,
                             hipMemcpyDeviceToHost, m->gpu->stream));
+    m->queue_abort_read();
     STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+    if (int r = m->check_abort()) return r;
     return m->collect_stats();
 }
 
@@ -1229,6 +1355,97 @@ int styx_moe_generate(styx_moe *m, const uint32_t *prompt, int n_prompt, int n_p
     const auto t2 = clk::now();
     if (prefill_s) *prefill_s = std::chrono::duration<double>(t1 - t0).count();
     if (decode_s) *decode_s = std::chrono::duration<double>(t2 - t1).count();
+    return STYX_OK;
+}
+
+// Stage timing (measurement, no reference counterpart): the launches of one
+// stage for every layer of the last token, captured as one graph and replayed
+// back to back between two HIP events.  Each layer's launch reads its own
+// weights, so the replays stream as much memory as a token does for that
+// stage.  The replays overwrite per-token scratch (ids rows, partials, the
+// residual and the KV row at the pending position), all of which the next
+// token rewrites before reading; argmax, which advances the decode state, is
+// not a stage here.
+int styx_moe_time_stage(styx_moe *m, const char *stage, int reps, double *us_per_replay,
+                        int *launches)
+{
+    static const char *const ok[] = {"embed",    "qkv",    "attn",        "o_proj",
+                                     "router",   "gather", "moe_gate_up", "shexp",
+                                     "moe_down", "reduce", "moe_block",   "lm_head"};
+    if (!m || !stage || reps < 1 || !us_per_replay)
+        return fail(STYX_E_INVALID, "styx_moe_time_stage: bad argument");
+    if (std::find_if(std::begin(ok), std::end(ok), [&](const char *s) { return !strcmp(s, stage); }) ==
+        std::end(ok))
+        return fail(STYX_E_INVALID, std::string("styx_moe_time_stage: unknown stage ") + stage);
+    if (m->n_past < 1) return fail(STYX_E_STATE, "styx_moe_time_stage: run a token first");
+    STYX_HIP(hipSetDevice(m->gpu->device));
+    if (int r = m->collect_stats()) return r;
+    hipStream_t st = m->gpu->stream;
+    const int saved = m->opts.time_kernels;
+    m->opts.time_kernels = 0;
+    m->stage_only = stage;
+    // at least 32 launches per graph: a shallow model's stage is repeated so
+    // that the graph launch itself does not dominate
+    const int nrep = std::max(1, 32 / std::max(1, m->L));
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+    int r = STYX_OK;
+    for (int i = 0; i < nrep && e == hipSuccess && !r; i++) r = m->enqueue_token(false);
+    hipError_t e2 = e == hipSuccess ? hipStreamEndCapture(st, &g) : e;
+    m->stage_only.clear();
+    m->opts.time_kernels = saved;
+    if (r) {
+        if (g) hipGraphDestroy(g);
+        return r;
+    }
+    if (e2 != hipSuccess) return hip_fail(e2, "styx_moe_time_stage: capture");
+    size_t n = 0;
+    e = hipGraphGetNodes(g, nullptr, &n);
+    hipGraphExec_t ex = nullptr;
+    if (e == hipSuccess) e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "styx_moe_time_stage: instantiate");
+    hipEvent_t a = nullptr, b = nullptr;
+    float ms = 0.0f;
+    e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    for (int i = 0; i < 2 && e == hipSuccess; i++) e = hipGraphLaunch(ex, st);
+    if (e == hipSuccess) e = hipEventRecord(a, st);
+    for (int i = 0; i < reps && e == hipSuccess; i++) e = hipGraphLaunch(ex, st);
+    if (e == hipSuccess) e = hipEventRecord(b, st);
+    if (e == hipSuccess) m->queue_abort_read();
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    if (a) hipEventDestroy(a);
+    if (b) hipEventDestroy(b);
+    hipGraphExecDestroy(ex);
+    if (e != hipSuccess) return hip_fail(e, "styx_moe_time_stage: replay");
+    STYX_HIP(hipStreamSynchronize(st));
+    if (int rr = m->check_abort()) return rr;
+    *us_per_replay = 1000.0 * ms / reps / nrep;
+    if (launches) *launches = (int)(n / nrep);
+    return STYX_OK;
+}
+
+// Phase stamps of the fused MoE block from the last timed token
+// (measurement, no reference counterpart): [n_layers][nwg][16] wall-clock
+// ticks (0 where a workgroup had no such phase).
+int styx_moe_moe_block_trace(styx_moe *m, uint64_t *out, int64_t max_count, int *nwg,
+                             double *ticks_per_us)
+{
+    if (!m || !nwg) return fail(STYX_E_INVALID, "styx_moe_moe_block_trace: bad argument");
+    *nwg = m->mb_nwg > 0 ? m->mb_nwg : 0;
+    if (*nwg == 0 || !out) return STYX_OK;
+    const int64_t n = (int64_t)m->L * m->mb_nwg * 16;
+    if (max_count < n) return fail(STYX_E_INVALID, "styx_moe_moe_block_trace: buffer too small");
+    STYX_HIP(hipSetDevice(m->gpu->device));
+    STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+    STYX_HIP(hipMemcpy(out, m->mb_trace, sizeof(uint64_t) * n, hipMemcpyDeviceToHost));
+    if (ticks_per_us) {
+        int khz = 0;
+        STYX_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, m->gpu->device));
+        *ticks_per_us = khz / 1000.0;
+    }
     return STYX_OK;
 }
 

@@ -90,6 +90,43 @@ hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_
                            const float *gu, float *partial, int H, int F, int k,
                            const uint8_t *sh_down = nullptr);
 
+// The whole MoE block of one layer in one launch of nwg workgroups (all
+// resident at once): ffn RMSNorm + router, top-k, gate/up, swiglu + down,
+// the weighted combine into x and the next RMSNorm's limbs -- the results of
+// launch_router + launch_moe_gate_up + launch_moe_down + launch_reduce_rows,
+// bit for bit.  Workgroups exchange data through the tagged buffers t_lg
+// [E], t_gu [2][k+1][F], t_part [k+1][H] (64-bit words, zeroed once at
+// allocation) and draw a ticket at entry from one of 64 counters (ticket
+// points at 64 x 16 zeroed u64; nwg a multiple of 64); a wait that exceeds
+// max_polls rounds sets *abort.  trace (optional): [nwg][8] wall-clock
+// stamps per workgroup at its phase boundaries.  hipErrorNotSupported: shapes outside the
+// kernel's geometry (use the separate kernels).
+struct MoeBlockArgs {
+    int tg, tu, td;
+    float *x;  // residual [H], updated in place
+    const float *ffn_norm, *W, *bias;
+    float eps;
+    int H, F, E, k, renorm;
+    ExpSrc src[3];
+    Route route;  // remap, pmap, layer, ids_out; arena_mode must be 0
+    const uint8_t *sh[3];
+    const float *sh_ginp;
+    const float *norm_next;  // null: no limbs for a next matvec
+    Xq xq;
+    float *ss;
+    float *wts_out;
+    uint64_t *t_lg, *t_gu, *t_part;
+    unsigned long long *ticket;
+    int *abort;
+    int max_polls;
+    uint64_t *trace;
+    int nwg;
+};
+hipError_t launch_moe_block(hipStream_t st, const MoeBlockArgs &a);
+// Workgroups of the fused MoE kernel that fit on one CU at these shapes
+// (0: shapes not handled by it).
+int moe_block_occupancy(int tg, int tu, int td, int H, int F, int E, int k, int shexp);
+
 // H / 256 workgroups: w_s from the router logits and the id row
 // (topk_softmax_f32.comp:29-67) or given in wts;
 //   x += sum_s w_s partial[s]  (s ascending, moe_reduce_f32.comp:11-13)

@@ -1,0 +1,649 @@
+// moe_block.hip -- the MoE block of one layer as one persistent launch.
+//
+// One kernel runs what k_router, k_gate_up, k_down and k_reduce_rows do
+// (ffn RMSNorm + router logits, top-k ranking, expert gate/up, swiglu +
+// down, the weighted combine and the next RMSNorm's limbs) with the same
+// arithmetic, so its results are bit-identical to theirs.  What changes is
+// the schedule: a workgroup issues the weights of its down rows as soon as
+// the routing is known and keeps them in flight while it computes its
+// gate/up rows, so the down phase waits on the gate/up outputs rather than
+// on a kernel boundary plus an HBM trip.
+//
+// Cross-workgroup data (router logits, gate/up outputs, per-slot down
+// partials) travels as 64-bit words (launch tag << 32 | f32 bits) written
+// and read with relaxed agent-scope atomics: on gfx950 these are plain
+// global stores/loads with device scope (sc1), coherent across the XCDs'
+// L2s, and a word is valid once its tag is the launch's.  No fence and no
+// counter is needed, and no buffer has to be cleared between launches.  The
+// tag is derived from a ticket every workgroup draws at entry
+// (ticket / gridDim + 1), so every launch has its own tag, also when a
+// captured graph replays the same launch.
+//
+// Every wait is bounded: after max_polls rounds, or once another workgroup
+// has given up, a workgroup sets *abort and exits.  The grid is sized to be
+// resident at once (two workgroups per CU), so in normal operation no wait
+// ever approaches the bound; the host checks *abort after each token.
+#include "kernels.h"
+#include "qdot.h"
+#include "topk.h"
+#include "walk.h"
+
+#include <algorithm>
+
+namespace styx {
+
+constexpr int MB_ROUTER_ROWS = 4;  // router rows per workgroup (one per wave), as k_router
+constexpr int MB_RR = 256;         // reduce rows per workgroup, as k_reduce_rows
+constexpr int MB_MAX_F = 2048;     // gate/up width handled here (g and u of a slot in LDS)
+constexpr int MB_TICKETS = 64;     // ticket counters (workgroup w draws from counter w % 64)
+constexpr int MB_GU_ROWS = 4;      // gate/up rows per lane group in flight at once
+constexpr int MB_TRACE = 16;       // trace slots per workgroup (phases 0..10 used)
+
+struct MoeBlockK {
+    const float *x;         // residual [H]: read at entry, updated by the reduce
+    const float *ffn_norm;  // [H]
+    const float *W;         // router [E][H] f32
+    const float *bias;      // [E] or null
+    const float *sh_ginp;   // shared-expert gate input [H] or null
+    const uint8_t *sh[3];   // shared expert gate/up/down as slot k, or null
+    ExpSrc src[3];          // gate, up, down
+    Route route;            // E, k, remap, pmap, ids_out (logits unused)
+    float eps;
+    int H, F, E, k, renorm, nslots;
+    int tg, tu;             // gate / up quant types (the down type is a template parameter)
+    float *x_out;
+    const float *norm_next;
+    Xq xq;
+    float *ss;
+    float *wts_out;
+    uint64_t *t_lg, *t_gu, *t_part;  // tagged [E], [2][nslots][F], [nslots][H]
+    unsigned long long *ticket;  // MB_TICKETS counters, 128 bytes apart
+    int *abort;
+    int max_polls;
+    uint64_t *trace;  // optional: [gridDim][MB_TRACE] wall-clock stamps per workgroup
+    int nR;                                  // router workgroups
+    int G_gu, nb_gu, rpw_gu, bps_gu, n_gu;   // gate/up blocks: [2][nslots][bps_gu]
+    int G_d, nb_d, rpw_d, bps_d, n_d;        // down blocks: [nslots][bps_d]
+    int nRed;                                // reduce workgroups
+    int off_xq, off_lg, off_gu, off_hs, off_xqh;  // dynamic LDS layout (bytes)
+};
+
+// Global loads and stores through pointers read from the LDS copy of the
+// arguments (a generic pointer would become a flat access).
+__device__ __forceinline__ float gld(const float *p) { return *(const float STYX_GLOBAL *)p; }
+__device__ __forceinline__ float4 gld4(const float *p)
+{
+    const styx_f4 v = *(const styx_f4 STYX_GLOBAL *)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+template <typename T> __device__ __forceinline__ void gst(T *p, T v) { *(T STYX_GLOBAL *)p = v; }
+
+__device__ __forceinline__ void tput(uint64_t *p, uint32_t tag, float v)
+{
+    __hip_atomic_store((uint64_t STYX_GLOBAL *)p, ((uint64_t)tag << 32) | __float_as_uint(v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t tget(const uint64_t *p)
+{
+    return __hip_atomic_load((uint64_t STYX_GLOBAL *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Words i = tid + 256 j (i < n) of the workgroup: wait until the word at
+// addr(i) carries `tag` and store its value to dst[i] (addr(i) == null: no
+// word, dst[i] = 0).  Thread 0 decides for the whole workgroup whether to
+// keep waiting.  Returns false when the wait is abandoned (*abort set).
+template <int MAXJ, typename Addr>
+__device__ __forceinline__ bool tpoll(int n, Addr addr, uint32_t tag, float *dst, const MoeBlockK &a)
+{
+    uint32_t pend = 0;
+#pragma unroll
+    for (int j = 0; j < MAXJ; j++) {
+        const int i = (int)threadIdx.x + WG * j;
+        if (i < n) {
+            if (addr(i))
+                pend |= 1u << j;
+            else
+                dst[i] = 0.0f;
+        }
+    }
+    for (int polls = 0;; polls++) {
+        uint64_t v[MAXJ];
+#pragma unroll
+        for (int j = 0; j < MAXJ; j++)
+            v[j] = ((pend >> j) & 1u) ? tget(addr((int)threadIdx.x + WG * j)) : 0ull;
+#pragma unroll
+        for (int j = 0; j < MAXJ; j++) {
+            if (((pend >> j) & 1u) && (uint32_t)(v[j] >> 32) == tag) {
+                dst[threadIdx.x + WG * j] = __uint_as_float((uint32_t)v[j]);
+                pend &= ~(1u << j);
+            }
+        }
+        if (!__syncthreads_or(pend != 0)) return true;
+        // the bound is checked every round, another workgroup's abort every
+        // 32nd (a memory round trip of its own)
+        int stop = 0;
+        if (threadIdx.x == 0)
+            stop = polls >= a.max_polls ||
+                   ((polls & 31) == 31 && __hip_atomic_load((int STYX_GLOBAL *)a.abort, __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT) != 0);
+        if (__syncthreads_or(stop)) {
+            if (threadIdx.x == 0)
+                __hip_atomic_store((int STYX_GLOBAL *)a.abort, 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Bring rows [r0, r1) of a split-layout matrix into this XCD's L2: one
+// dword of every 128-byte line of each region's row range (the rows of a
+// region are contiguous).  The returned word must be consumed later (the
+// loads are then waited for there, not here); the lines stay in L2 for the
+// rest of the kernel unless evicted.
+template <int T>
+__device__ __forceinline__ uint32_t touch_rows(const Mat &m, int nb, int r0, int r1)
+{
+    const Split sp = split_of(T);
+    const uint8_t STYX_GLOBAL *base[4] = {m.r0, m.r1, m.r2, m.r3};
+    uint32_t acc = 0;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        if (g >= sp.nreg) break;
+        const int64_t lo = (int64_t)r0 * nb * sp.sz[g], hi = (int64_t)r1 * nb * sp.sz[g];
+        for (int64_t off = (lo & ~(int64_t)127) + 128 * (int64_t)threadIdx.x; off < hi;
+             off += 128 * WG)
+            acc ^= *(const uint32_t STYX_GLOBAL *)(base[g] + (off < lo ? lo & ~(int64_t)3 : off));
+    }
+    return acc;
+}
+
+// Slab of expert e routed to `slot` (null when e is not a valid expert,
+// which only non-finite logits can cause: the rows then publish zeros).
+__device__ __forceinline__ const uint8_t *routed_slab(const MoeBlockK &a, const ExpSrc &src, int e,
+                                                      int slot)
+{
+    if ((unsigned)e >= (unsigned)a.E) return nullptr;
+    uint32_t r3[3];
+    route_row(a.route, e, slot, r3);
+    return slab_pick(src, r3[0], r3[1], r3[2]);
+}
+
+// Rows [r0, r1) of matrix m (0 gate, 1 up) of slot s against the limbs of
+// xn in LDS, published tagged; a missing slab publishes zeros.
+// `between` runs once the rows' first weights are issued (the caller
+// issues further loads there).
+template <int T, typename Between>
+__device__ __forceinline__ void gu_rows(const MoeBlockK &a, const uint8_t *slab, const Xq &xqx, int m,
+                               int s, int r0, int r1, uint32_t tag, Between between,
+                               uint64_t *tr)
+{
+    uint64_t *y = a.t_gu + ((size_t)m * a.nslots + s) * a.F;
+    if (!slab) {
+        between();
+        for (int r = r0 + (int)threadIdx.x; r < r1; r += WG) tput(y + r, tag, 0.0f);
+        return;
+    }
+    auto stamp = [&](int i) {
+        if (tr && threadIdx.x == 0) tr[i] = wall_clock64();
+    };
+    RowWalkN<T, MB_GU_ROWS> rw;
+    rw.start(mat_at(slab, T, (int64_t)a.F * a.nb_gu), a.nb_gu, a.G_gu, r0, r1);
+    stamp(11);
+    between();
+    UX<T> x[1];
+    XFrom<T, 1>{xqx}(x, rw.lu);
+    stamp(12);
+    rw.run(x, [&](int r, float v) { tput(y + r, tag, v); });
+    stamp(13);
+}
+
+template <typename Between>
+__device__ __forceinline__ void gu_block(const MoeBlockK &a, int b, bool routed_phase,
+                                const int32_t *s_ids, const Xq &xqx, uint32_t tag,
+                                Between between, uint64_t *tr)
+{
+    const int per_m = a.nslots * a.bps_gu;
+    const int m = b / per_m, rem = b - m * per_m, s = rem / a.bps_gu;
+    if ((s < a.k) != routed_phase) return;
+    const int r0 = (rem - s * a.bps_gu) * a.rpw_gu, r1 = min(a.F, r0 + a.rpw_gu);
+    const uint8_t *slab = s < a.k ? routed_slab(a, a.src[m], s_ids[s], s) : a.sh[m];
+    switch (m == 0 ? a.tg : a.tu) {
+    case T_Q8_0: gu_rows<T_Q8_0>(a, slab, xqx, m, s, r0, r1, tag, between, tr); break;
+    case T_Q4_K: gu_rows<T_Q4_K>(a, slab, xqx, m, s, r0, r1, tag, between, tr); break;
+    case T_Q5_K: gu_rows<T_Q5_K>(a, slab, xqx, m, s, r0, r1, tag, between, tr); break;
+    default: gu_rows<T_Q6_K>(a, slab, xqx, m, s, r0, r1, tag, between, tr); break;
+    }
+}
+
+// Gate/up types are switched at run time (one routed row block at a time,
+// nothing held across); the down type and units per lane are template
+// parameters because the down rows' weights stay in registers across the
+// gate/up phase.
+template <int TD, int UD>
+__global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
+{
+    // The arguments are copied to LDS once: this kernel is short of scalar
+    // registers, and the compiler would otherwise re-read argument fields
+    // from the kernarg segment wherever they are used -- chains of dependent
+    // scalar loads on the critical path.
+    static_assert(sizeof(MoeBlockK) % 4 == 0 && sizeof(MoeBlockK) / 4 <= WG, "args copy");
+    __shared__ __align__(16) MoeBlockK s_args;
+    if (threadIdx.x < sizeof(MoeBlockK) / 4)
+        ((uint32_t *)&s_args)[threadIdx.x] = ((const uint32_t *)&args)[threadIdx.x];
+    __syncthreads();
+    const MoeBlockK &a = s_args;
+    extern __shared__ __align__(16) uint8_t lds[];
+    float *xs = (float *)lds;                         // x, then xn = rmsnorm(x) * w
+    const Xq xqx = xq_at(lds + a.off_xq, a.H);        // limbs of xn
+    float *s_lg = (float *)(lds + a.off_lg);          // router logits
+    float *gus = (float *)(lds + a.off_gu);           // g[F] | u[F]; reduce: partials
+    float *hs = (float *)(lds + a.off_hs);            // swiglu(g, u)
+    const Xq xqh = xq_at(lds + a.off_xqh, a.F);       // limbs of hs
+    __shared__ int32_t s_ids[IDS_ROW];
+    __shared__ float red[16];
+    __shared__ uint32_t s_tag;
+    __shared__ float s_w[MAX_TOPK];
+    __shared__ float s_wsum, s_sg;
+
+    const int w = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nwg = gridDim.x;
+    // every workgroup draws its ticket, also one without work: counter
+    // w % 64 is drawn by nwg / 64 workgroups per launch, so
+    // ticket / (nwg / 64) numbers the launch (spreading the draws over 64
+    // counters keeps them from queueing on one address)
+    // phase stamps go to LDS (a global store would hold up the next wait on
+    // the vector memory counter) and are written out when the workgroup ends
+    __shared__ uint64_t s_trace[MB_TRACE];
+    uint64_t *tr = a.trace ? s_trace : nullptr;
+    if (tr && tid < MB_TRACE) s_trace[tid] = 0;
+    auto stamp = [&](int i) {
+        if (tr && tid == 0) tr[i] = wall_clock64();
+    };
+    auto flush = [&] {  // at uniform exits only
+        if (!tr) return;
+        __syncthreads();
+        if (tid < MB_TRACE) gst<uint64_t>(a.trace + (size_t)w * MB_TRACE + tid, tr[tid]);
+    };
+    __syncthreads();
+    stamp(0);
+    // the draw's result is first needed after the entry loads are issued
+    unsigned long long ticket = 0;
+    if (tid == 0)
+        ticket = __hip_atomic_fetch_add(
+            (unsigned long long STYX_GLOBAL *)(a.ticket + (w % MB_TICKETS) * 16), 1ull,
+            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (w >= a.n_gu && w >= a.n_d && w >= a.nRed) {
+        flush();
+        return;
+    }
+
+    // ---- entry (workgroups with gate/up work; the router and reduce
+    // workgroups are among them): router row, x and the ffn norm weight are
+    // independent loads, issued before any reduction (k_router's order)
+    const bool has_x = w < a.n_gu;
+    const bool router = w < a.nR;
+    const int rr = w * MB_ROUTER_ROWS + wave;
+    constexpr int PW = 8, PX = 2;
+    float4 wv[PW];
+    if (has_x) {
+        const float *wr = a.W + (int64_t)min(rr, a.E - 1) * a.H;
+#pragma unroll
+        for (int j = 0; j < PW; j++) {
+            const int c = lane * 4 + 256 * j;
+            wv[j] = (router && c < a.H) ? gld4(wr + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        float4 xv[PX], nv[PX];
+#pragma unroll
+        for (int j = 0; j < PX; j++) {
+            const int i = tid * 4 + WG * 4 * j;
+            xv[j] = i < a.H ? gld4(a.x + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            nv[j] = i < a.H ? gld4(a.ffn_norm + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PX; j++)
+            ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+        for (int i = tid * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {
+            const float4 v = gld4(a.x + i);
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = block_sum(ss, red);
+        const float scale = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+#pragma unroll
+        for (int j = 0; j < PX; j++) {
+            const int i = tid * 4 + WG * 4 * j;
+            if (i < a.H)
+                *(float4 *)(xs + i) = make_float4((xv[j].x * scale) * nv[j].x, (xv[j].y * scale) * nv[j].y,
+                                                  (xv[j].z * scale) * nv[j].z, (xv[j].w * scale) * nv[j].w);
+        }
+        for (int i = tid * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {
+            const float4 v = gld4(a.x + i);
+            const float4 nw = gld4(a.ffn_norm + i);
+            *(float4 *)(xs + i) = make_float4((v.x * scale) * nw.x, (v.y * scale) * nw.y,
+                                              (v.z * scale) * nw.z, (v.w * scale) * nw.w);
+        }
+    }
+    if (tid == 0) s_tag = (uint32_t)(ticket / (unsigned long long)(nwg / MB_TICKETS)) + 1u;
+    __syncthreads();
+    const uint32_t tag = s_tag;
+    stamp(1);
+
+    // ---- router logits (matvec_strided_f32, one row per wave)
+    if (router && rr < a.E) {
+        const float *wr = a.W + (int64_t)rr * a.H;
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PW; j++) {
+            const int c = lane * 4 + 256 * j;
+            if (c < a.H) {
+                const float4 xv4 = *(const float4 *)(xs + c);
+                acc += wv[j].x * xv4.x + wv[j].y * xv4.y + wv[j].z * xv4.z + wv[j].w * xv4.w;
+            }
+        }
+        for (int c = lane * 4 + 256 * PW; c < a.H; c += 256) {
+            const float4 wq = gld4(wr + c);
+            const float4 xv4 = *(const float4 *)(xs + c);
+            acc += wq.x * xv4.x + wq.y * xv4.y + wq.z * xv4.z + wq.w * xv4.w;
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) tput(a.t_lg + rr, tag, a.bias ? acc + gld(a.bias + rr) : acc);
+    }
+
+    // ---- limbs of xn; shared-expert gate/up rows need no routing
+    auto nothing = [] {};
+    if (has_x) {
+        xq_build(xs, nullptr, 0.0f, false, a.H, xqx, red, nullptr);
+        __syncthreads();
+        stamp(2);
+        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b, false, s_ids, xqx, tag, nothing, tr);
+    }
+
+    // ---- routing: every workgroup ranks the logits (topk_softmax_f32 order)
+    if (!tpoll<MAX_EXPERTS / WG>(a.E, [&](int i) { return a.t_lg + i; }, tag, s_lg, a)) return;
+    stamp(3);
+    rank_ids_lds(a.route, s_ids, s_lg, w == 0);
+    stamp(4);
+
+    // ---- this workgroup's down rows: pulled into L2 once its gate/up rows
+    // are done, while it waits for the other workgroups' (HBM is otherwise
+    // idle then); the down phase reads them from there
+    const bool has_d = w < a.n_d;
+    const int ds = has_d ? w / a.bps_d : 0;
+    const int d0 = (w - ds * a.bps_d) * a.rpw_d, d1 = min(a.H, d0 + a.rpw_d);
+    const uint8_t *dslab = nullptr;
+    if (has_d) dslab = ds < a.k ? routed_slab(a, a.src[2], s_ids[ds], ds) : a.sh[2];
+    bool d_started = false;
+    uint32_t touched = 0;
+    auto start_down = [&] {
+        if (d_started) return;
+        d_started = true;
+        if (dslab) touched = touch_rows<TD>(mat_at(dslab, TD, (int64_t)a.H * a.nb_d), a.nb_d, d0, d1);
+    };
+
+    // ---- routed gate/up rows
+    if (has_x)
+        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b, true, s_ids, xqx, tag, nothing, tr);
+    start_down();
+    stamp(5);
+
+    // ---- down: swiglu_f32 (ops2.rs:305-309) of the slot's g and u and its
+    // limbs in LDS, then the rows whose weights are already in flight
+    if (has_d) {
+        const int F = a.F;
+        const uint64_t *g = a.t_gu + (size_t)ds * F, *u = a.t_gu + ((size_t)a.nslots + ds) * F;
+        if (!tpoll<2 * MB_MAX_F / WG>(2 * F, [&](int i) { return i < F ? g + i : u + (i - F); },
+                                       tag, gus, a))
+            return;
+        stamp(6);
+        // the touched lines have long arrived; consuming the word here keeps
+        // the compiler from dropping those loads
+        asm volatile("" ::"v"(touched));
+        RowWalk<TD, UD> dw;
+        if (dslab) dw.start(mat_at(dslab, TD, (int64_t)a.H * a.nb_d), a.nb_d, a.G_d, d0, d1);
+        for (int i = tid; i < F; i += WG) hs[i] = gus[i] / (1.0f + expf(-gus[i])) * gus[F + i];
+        __syncthreads();
+        xq_build(hs, nullptr, 0.0f, false, F, xqh, red, nullptr);
+        __syncthreads();
+        stamp(7);
+        uint64_t *part = a.t_part + (size_t)ds * a.H;
+        if (dslab) {
+            UX<TD> x[UD];
+            XFrom<TD, UD>{xqh}(x, dw.lu);
+            dw.run(x, [&](int r, float v) { tput(part + r, tag, v); });
+        } else {
+            for (int r = d0 + tid; r < d1; r += WG) tput(part + r, tag, 0.0f);
+        }
+        stamp(8);
+    }
+
+    // ---- reduce (k_reduce_rows arithmetic): weights, x += sum_s w_s y_s,
+    // the shared expert's axpy_sig, then the next RMSNorm's limbs.  The
+    // weights and the shared-expert gate need no partials: formed while the
+    // other workgroups' down rows are still being computed.
+    if (w >= a.nRed) {
+        flush();
+        return;
+    }
+    const int r0 = w * MB_RR, nrow = min(MB_RR, a.H - r0);
+    const int r = r0 + tid;
+    const bool hr = tid < nrow;
+    const bool shexp = a.nslots > a.k;
+    const float x0 = hr ? gld(a.x + r) : 0.0f;
+    const float nw = (a.norm_next && hr) ? gld(a.norm_next + r) : 1.0f;
+    float lg_pick = 0.0f, mx = -INFINITY;
+    for (int e = tid; e < a.E; e += WG) mx = fmaxf(mx, s_lg[e]);
+    if (tid < a.k) {
+        const int e = s_ids[tid];
+        lg_pick = (e >= 0 && e < a.E) ? s_lg[e] : -INFINITY;
+    }
+    float shd = 0.0f;
+    if (shexp)
+        for (int i = tid; i < a.H; i += WG) shd += gld(a.sh_ginp + i) * xs[i];
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = red[0];
+    for (int i = 1; i < WAVES; i++) mx = fmaxf(mx, red[i]);
+    float se = 0.0f;
+    for (int e = tid; e < a.E; e += WG) se += expf(s_lg[e] - mx);
+    se = block_sum(se, red);
+    if (tid < a.k) s_w[tid] = expf(lg_pick - mx) / se;
+    __syncthreads();
+    if (tid == 0 && a.renorm) {
+        float wsum = 0.0f;
+        for (int s = 0; s < a.k; s++) wsum += s_w[s];
+        s_wsum = wsum;
+    }
+    __syncthreads();
+    if (tid < a.k) {
+        const float wt = a.renorm ? s_w[tid] / s_wsum : s_w[tid];
+        s_w[tid] = wt;
+        if (a.wts_out && w == 0) gst(a.wts_out + tid, wt);
+    }
+    if (shexp) {
+        const float d = block_sum(shd, red);
+        if (tid == 0) s_sg = 1.0f / (1.0f + expf(-d));
+    }
+    __syncthreads();  // also: gus is reused for the partials
+    float *pl = gus;  // [nslots][MB_RR]
+    if (!tpoll<MAX_TOPK + 1>(a.nslots * MB_RR,
+                             [&](int i) -> const uint64_t * {
+                                 const int s = i / MB_RR, t = i - s * MB_RR;
+                                 return t < nrow ? a.t_part + (size_t)s * a.H + r0 + t : nullptr;
+                             },
+                             tag, pl, a))
+        return;
+    stamp(9);
+    float p[MAX_TOPK];
+#pragma unroll
+    for (int s = 0; s < MAX_TOPK; s++) p[s] = (s < a.k && hr) ? pl[s * MB_RR + tid] : 0.0f;
+    const float y0 = (shexp && hr) ? pl[a.k * MB_RR + tid] : 0.0f;
+    float acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < MAX_TOPK; s++)
+        if (s < a.k) acc += s_w[s] * p[s];
+    float xv = x0 + acc;
+    if (shexp) xv = xv + s_sg * y0;
+    if (hr) gst(a.x_out + r, xv);
+    if (!a.norm_next) {
+        stamp(10);
+        flush();
+        return;
+    }
+    const float sq = block_sum(hr ? xv * xv : 0.0f, red);
+    if (tid == 0) gst(a.ss + w, sq);
+    float *xw = hs;  // MB_RR floats; hs is free once the down rows are done
+    __syncthreads();
+    xw[tid] = xv * nw;
+    __syncthreads();
+    if (tid < MB_RR / 8) {
+        const bool act = 8 * tid < nrow;
+        float h[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = act ? xw[8 * tid + i] : 0.0f;
+        xq_group(h, act, tid, xq_shift(a.xq, r0));
+    }
+    stamp(10);
+    flush();
+}
+
+// ------------------------------------------------------------------ host --
+static int align16(size_t n) { return (int)((n + 15) / 16 * 16); }
+
+using MoeKernel = void (*)(MoeBlockK);
+
+static MoeKernel moe_kernel(int td, int ud)
+{
+    switch (td) {
+    case T_Q8_0:
+        switch (ud) {
+        case 1: return k_moe_block<T_Q8_0, 1>;
+        case 2: return k_moe_block<T_Q8_0, 2>;
+        case 3: return k_moe_block<T_Q8_0, 3>;
+        case 4: return k_moe_block<T_Q8_0, 4>;
+        default: return nullptr;
+        }
+    case T_Q4_K: return ud == 1 ? k_moe_block<T_Q4_K, 1> : ud == 2 ? k_moe_block<T_Q4_K, 2> : nullptr;
+    case T_Q5_K: return ud == 1 ? k_moe_block<T_Q5_K, 1> : ud == 2 ? k_moe_block<T_Q5_K, 2> : nullptr;
+    case T_Q6_K: return ud == 1 ? k_moe_block<T_Q6_K, 1> : ud == 2 ? k_moe_block<T_Q6_K, 2> : nullptr;
+    default: return nullptr;
+    }
+}
+
+// Geometry and LDS of one launch; false if the shapes are outside what the
+// kernel handles (the caller then runs the separate kernels).
+static bool moe_geometry(const MoeBlockArgs &h, int nwg, MoeBlockK &a, size_t &lds)
+{
+    const Geo gg = pick_geo(h.tg, h.H), gd = pick_geo(h.td, h.F), gu = pick_geo(h.tu, h.H);
+    if (!gg.G || !gd.G || gg.UPL != 1 || gu.G != gg.G || gu.UPL != 1 ||
+        blk_elems(h.tg) != blk_elems(h.tu))
+        return false;
+    if (h.F > MB_MAX_F || h.F % 32 || h.H % 32 || h.H > XQ_MAX || h.E % 16 || h.E > MAX_EXPERTS ||
+        h.k < 1 || h.k > MAX_TOPK || h.k > h.E || h.route.arena_mode)
+        return false;
+    a.nslots = h.k + (h.sh[0] ? 1 : 0);
+    a.nR = (h.E + MB_ROUTER_ROWS - 1) / MB_ROUTER_ROWS;
+    a.nRed = (h.H + MB_RR - 1) / MB_RR;
+    // the gate/up walker has MB_GU_ROWS rows per lane group in flight, so a
+    // block of up to MB_GU_ROWS * ngrp rows takes one HBM trip
+    const int ngrp_gu = WAVES * (64 / gg.G), ngrp_d = WAVES * (64 / gd.G);
+    int rpw = (2 * a.nslots * h.F + nwg - 1) / nwg;
+    a.rpw_gu = std::min(MB_GU_ROWS * ngrp_gu, (rpw + ngrp_gu - 1) / ngrp_gu * ngrp_gu);
+    a.bps_gu = (h.F + a.rpw_gu - 1) / a.rpw_gu;
+    a.n_gu = 2 * a.nslots * a.bps_gu;
+    if (nwg % MB_TICKETS) return false;
+    const int per_slot = nwg / a.nslots;
+    if (per_slot < 1) return false;
+    rpw = (h.H + per_slot - 1) / per_slot;
+    a.rpw_d = std::max(ngrp_d, (rpw + ngrp_d - 1) / ngrp_d * ngrp_d);
+    a.bps_d = (h.H + a.rpw_d - 1) / a.rpw_d;
+    a.n_d = a.nslots * a.bps_d;
+    // every workgroup that reads x at entry has gate/up work, whose outputs
+    // the reduce (which rewrites x) waits on
+    if (a.n_d > nwg || a.nR > a.n_gu || a.nRed > a.n_gu) return false;
+    a.G_gu = gg.G;
+    a.nb_gu = h.H / blk_elems(h.tg);
+    a.G_d = gd.G;
+    a.nb_d = h.F / blk_elems(h.td);
+    a.off_xq = align16((size_t)4 * h.H);
+    a.off_lg = a.off_xq + align16(xq_bytes(h.H));
+    a.off_gu = a.off_lg + align16((size_t)4 * h.E);
+    a.off_hs = a.off_gu + align16(std::max((size_t)8 * h.F, (size_t)4 * a.nslots * MB_RR));
+    a.off_xqh = a.off_hs + align16((size_t)4 * std::max(h.F, MB_RR));
+    lds = (size_t)a.off_xqh + align16(xq_bytes(h.F));
+    return true;
+}
+
+int moe_block_occupancy(int tg, int tu, int td, int H, int F, int E, int k, int shexp)
+{
+    MoeKernel kf = moe_kernel(td, pick_geo(td, F).UPL);
+    if (!kf) return 0;
+    MoeBlockArgs h{};
+    h.tg = tg;
+    h.tu = tu;
+    h.td = td;
+    h.H = H;
+    h.F = F;
+    h.E = E;
+    h.k = k;
+    static const uint8_t dummy = 0;
+    if (shexp) h.sh[0] = h.sh[1] = h.sh[2] = &dummy;
+    MoeBlockK a{};
+    size_t lds = 0;
+    if (!moe_geometry(h, 512, a, lds)) return 0;  // the LDS size does not depend on the grid
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)kf, WG, lds) != hipSuccess)
+        return 0;
+    return n;
+}
+
+hipError_t launch_moe_block(hipStream_t st, const MoeBlockArgs &h)
+{
+    MoeKernel kf = moe_kernel(h.td, pick_geo(h.td, h.F).UPL);
+    if (!kf || h.nwg < 1 || !h.x || !h.ffn_norm || !h.W || !h.t_lg || !h.t_gu || !h.t_part ||
+        !h.ticket || !h.abort || (h.sh[0] && (!h.sh[1] || !h.sh[2] || !h.sh_ginp)) ||
+        (h.norm_next && (!h.xq.A || !h.ss)))
+        return hipErrorInvalidValue;
+    MoeBlockK a{};
+    size_t lds = 0;
+    if (!moe_geometry(h, h.nwg, a, lds)) return hipErrorNotSupported;
+    a.x = h.x;
+    a.ffn_norm = h.ffn_norm;
+    a.W = h.W;
+    a.bias = h.bias;
+    a.sh_ginp = h.sh_ginp;
+    for (int i = 0; i < 3; i++) {
+        a.sh[i] = h.sh[i];
+        a.src[i] = h.src[i];
+    }
+    a.route = h.route;
+    a.route.logits = nullptr;
+    a.route.E = h.E;
+    a.route.k = h.k;
+    a.eps = h.eps;
+    a.H = h.H;
+    a.F = h.F;
+    a.E = h.E;
+    a.k = h.k;
+    a.renorm = h.renorm;
+    a.tg = h.tg;
+    a.tu = h.tu;
+    a.x_out = h.x;
+    a.norm_next = h.norm_next;
+    a.xq = h.xq;
+    a.ss = h.ss;
+    a.wts_out = h.wts_out;
+    a.t_lg = h.t_lg;
+    a.t_gu = h.t_gu;
+    a.t_part = h.t_part;
+    a.ticket = h.ticket;
+    a.abort = h.abort;
+    a.max_polls = h.max_polls > 0 ? h.max_polls : 200000;
+    a.trace = h.trace;
+    hipLaunchKernelGGL(kf, dim3(h.nwg), dim3(WG), lds, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace styx

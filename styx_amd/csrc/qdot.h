@@ -240,44 +240,53 @@ template <> struct UW<T_Q6_K> { uint4 p0, p1, qh; uint2 sc; uint32_t d; };
 
 // Region base pointers of one matrix (rows x nb blocks) in split layout.
 struct Mat {
-    const uint8_t *r0, *r1, *r2, *r3;
+    const uint8_t STYX_GLOBAL *r0, *r1, *r2, *r3;
 };
 
 __device__ __forceinline__ Mat mat_at(const uint8_t *base, int t, int64_t nblocks)
 {
     const Split s = split_of(t);
     Mat m;
-    m.r0 = base;
-    m.r1 = base + region_off(s, 1, nblocks);
-    m.r2 = s.nreg > 2 ? base + region_off(s, 2, nblocks) : nullptr;
-    m.r3 = s.nreg > 3 ? base + region_off(s, 3, nblocks) : nullptr;
+    const uint8_t STYX_GLOBAL *g = (const uint8_t STYX_GLOBAL *)base;
+    m.r0 = g;
+    m.r1 = g + region_off(s, 1, nblocks);
+    m.r2 = s.nreg > 2 ? g + region_off(s, 2, nblocks) : nullptr;
+    m.r3 = s.nreg > 3 ? g + region_off(s, 3, nblocks) : nullptr;
     return m;
 }
 
-__device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return *(const uint4 *)p; }
+__device__ __forceinline__ uint4 ldg16(const uint8_t STYX_GLOBAL *p)
+{
+    const styx_u4 v = *(const styx_u4 STYX_GLOBAL *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ldg2(const uint8_t STYX_GLOBAL *p)
+{
+    return *(const uint16_t STYX_GLOBAL *)p;
+}
 
 template <int T> __device__ inline void uw_load(UW<T> &w, const Mat &m, int64_t blk, int sub);
 
 template <> __device__ inline void uw_load<T_Q8_0>(UW<T_Q8_0> &w, const Mat &m, int64_t blk, int)
 {
-    const uint8_t *q = m.r0 + blk * 32;
+    const uint8_t STYX_GLOBAL *q = m.r0 + blk * 32;
     w.q0 = ldg16(q);
     w.q1 = ldg16(q + 16);
-    w.d = *(const uint16_t *)(m.r1 + blk * 2);
+    w.d = ldg2(m.r1 + blk * 2);
 }
 template <> __device__ inline void uw_load<T_Q4_K>(UW<T_Q4_K> &w, const Mat &m, int64_t blk, int c)
 {
-    const uint8_t *q = m.r0 + blk * 128 + 32 * c;
+    const uint8_t STYX_GLOBAL *q = m.r0 + blk * 128 + 32 * c;
     w.q0 = ldg16(q);
     w.q1 = ldg16(q + 16);
     w.hd = ldg16(m.r1 + blk * 16);
 }
 template <> __device__ inline void uw_load<T_Q5_K>(UW<T_Q5_K> &w, const Mat &m, int64_t blk, int c)
 {
-    const uint8_t *q = m.r0 + blk * 128 + 32 * c;
+    const uint8_t STYX_GLOBAL *q = m.r0 + blk * 128 + 32 * c;
     w.q0 = ldg16(q);
     w.q1 = ldg16(q + 16);
-    const uint8_t *h = m.r1 + blk * 32;
+    const uint8_t STYX_GLOBAL *h = m.r1 + blk * 32;
     w.h0 = ldg16(h);
     w.h1 = ldg16(h + 16);
     w.hd = ldg16(m.r2 + blk * 16);
@@ -285,12 +294,13 @@ template <> __device__ inline void uw_load<T_Q5_K>(UW<T_Q5_K> &w, const Mat &m, 
 template <> __device__ inline void uw_load<T_Q6_K>(UW<T_Q6_K> &w, const Mat &m, int64_t blk, int u)
 {
     const int n = (u >> 1) & 1, h = u & 1;
-    const uint8_t *ql = m.r0 + blk * 128 + 64 * n + 16 * h;
+    const uint8_t STYX_GLOBAL *ql = m.r0 + blk * 128 + 64 * n + 16 * h;
     w.p0 = ldg16(ql);
     w.p1 = ldg16(ql + 32);
     w.qh = ldg16(m.r1 + blk * 64 + 32 * n + 16 * h);
-    w.sc = *(const uint2 *)(m.r2 + blk * 16 + 8 * n);
-    w.d = *(const uint16_t *)(m.r3 + blk * 2);
+    const styx_u2 sc = *(const styx_u2 STYX_GLOBAL *)(m.r2 + blk * 16 + 8 * n);
+    w.sc = make_uint2(sc.x, sc.y);
+    w.d = ldg2(m.r3 + blk * 2);
 }
 
 __device__ __forceinline__ void u4_to(const uint4 v, uint32_t *o)

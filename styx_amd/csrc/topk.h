@@ -90,7 +90,7 @@ __device__ __noinline__ void topk_wave(const float *logits, int n, int k, int re
 // slot, or pmap), else the expert itself read from host memory.
 __device__ __forceinline__ void route_row(const Route &r, int e, int slot, uint32_t ids3[3])
 {
-    const uint32_t h = r.remap ? r.remap[e] : (uint32_t)e;
+    const uint32_t h = r.remap ? *(const uint32_t STYX_GLOBAL *)(r.remap + e) : (uint32_t)e;
     ids3[0] = h;
     ids3[1] = ids3[2] = SKIP;
     if (h != SKIP) return;
@@ -98,101 +98,96 @@ __device__ __forceinline__ void route_row(const Route &r, int e, int slot, uint3
     if (r.arena_mode)
         a = (uint32_t)(r.layer * r.k + slot);
     else if (r.pmap)
-        a = r.pmap[e];
+        a = *(const uint32_t STYX_GLOBAL *)(r.pmap + e);
     ids3[1] = a;
     if (a == SKIP) ids3[2] = (uint32_t)e;
 }
 
-// Top-k ids of the router logits inside a workgroup, by ranking.  Order: a
-// larger value first, equal values by lower index -- the strict '>' of
-// topk_softmax_f32.comp:45 -- so ranks 0..k-1 are exactly the reference's
-// selection order.  Up to 128 experts every logit is ranked against all
-// (2 or 4 threads per logit).  Above that, two levels: each wave ranks the
-// logits of its quarter of the experts among that quarter, those of rank < k
-// are candidates (every global top-k logit is in its quarter's top-k), and
-// the <= 4k candidates are ranked among themselves: E^2/4 + 16k^2 compares
-// per workgroup instead of E^2.  No dependent shuffle chain either way.
-// Fills s_ids[0..k) with the routed experts (route_row gives a slot's other
-// ids); weights are left to the caller.  The workgroup with all-zero block
-// index publishes the whole id row to r.ids_out.
-// Needs blockDim.x == 256, E % 16 == 0, E <= 512, k <= 16.
-__device__ inline const int32_t *route_ids_wg(const Route &r, int32_t *s_ids, float *s_lg)
+// Rank key of logit v at index e: larger key = earlier in the reference's
+// selection order (larger value first, equal values by lower index -- the
+// strict '>' of topk_softmax_f32.comp:45).  High word: the f32 bits mapped
+// to an order-preserving unsigned integer (-0 taken as +0, which compares
+// equal to it); low word: ~e.  Every key of a real logit is non-zero.
+__device__ __forceinline__ uint64_t rank_key(float v, int e)
 {
-    __shared__ __align__(16) float c_val[4 * MAX_TOPK];
-    __shared__ __align__(16) int32_t c_idx[4 * MAX_TOPK];
+    uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+}
+
+// Top-k ids of the router logits inside a workgroup, by ranking: the rank
+// of logit e is the number of keys larger than its key, so ranks 0..k-1 are
+// exactly the reference's selection order.  Up to 128 experts every key is
+// ranked against all (2 or 4 threads per logit, one 64-bit compare per
+// pair).  Above that, two levels: each wave ranks the keys of its quarter of
+// the experts among that quarter, those of rank < k are candidates (every
+// global top-k logit is in its quarter's top-k), and the <= 4k candidates
+// are ranked among themselves: E^2/4 + 16k^2 compares per workgroup instead
+// of E^2.  No dependent shuffle chain either way.
+// Fills s_ids[0..k) with the routed experts (route_row gives a slot's other
+// ids); weights are left to the caller.  The logits are in LDS (s_lg,
+// filled by the caller; the ranking synchronises before reading them);
+// the workgroup given `publish` writes the whole id row to r.ids_out.
+// Needs blockDim.x == 256, E % 16 == 0, E <= 512, k <= 16.
+__device__ inline const int32_t *rank_ids_lds(const Route &r, int32_t *s_ids, const float *s_lg,
+                                              bool publish)
+{
+    __shared__ __align__(16) uint64_t s_key[MAX_EXPERTS];
+    __shared__ __align__(16) uint64_t c_key[4 * MAX_TOPK];
     const int E = r.E, k = r.k, Q = E / 4;  // quarter: Q % 4 == 0
-    for (int e = threadIdx.x; e < E / 4; e += blockDim.x)
-        ((float4 *)s_lg)[e] = ((const float4 *)r.logits)[e];
-    if (threadIdx.x < IDS_ROW) s_ids[threadIdx.x] = (int32_t)SKIP;
-    if (threadIdx.x < 4 * MAX_TOPK) c_idx[threadIdx.x] = -1;
+    const int tid = threadIdx.x;
+    if (tid < IDS_ROW) s_ids[tid] = (int32_t)SKIP;
+    if (tid < 4 * MAX_TOPK) c_key[tid] = 0;
+    __syncthreads();
+    for (int e = tid; e < E; e += blockDim.x) s_key[e] = rank_key(s_lg[e], e);
     __syncthreads();
     if (E <= 128) {
-        // direct: P = 256 / E threads rank each logit against a slice of all
+        // direct: P = 256 / E threads rank each key against a slice of all
         const int P = E <= 64 ? 4 : 2, span = E / P;
-        const int e = (int)threadIdx.x / P, part = (int)threadIdx.x % P;
+        const int e = tid / P, part = tid % P;
         int cnt = 0;
-        float v = 0.0f;
         if (e < E) {
-            v = s_lg[e];
-            const int j0 = part * span;
-            const float4 *q = (const float4 *)(s_lg + j0);
+            const uint64_t mk = s_key[e];
+            const ulonglong2 *q = (const ulonglong2 *)(s_key + part * span);
 #pragma unroll 8
-            for (int j4 = 0; j4 < span / 4; j4++) {
-                const float4 u = q[j4];
-                const int j = j0 + 4 * j4;
-                cnt += (u.x > v) || (u.x == v && j < e);
-                cnt += (u.y > v) || (u.y == v && j + 1 < e);
-                cnt += (u.z > v) || (u.z == v && j + 2 < e);
-                cnt += (u.w > v) || (u.w == v && j + 3 < e);
+            for (int j2 = 0; j2 < span / 2; j2++) {
+                const ulonglong2 u = q[j2];
+                cnt += (int)(u.x > mk) + (int)(u.y > mk);
             }
         }
         cnt += __shfl_xor(cnt, 1);
         if (P == 4) cnt += __shfl_xor(cnt, 2);
         if (e < E && part == 0 && cnt < k) s_ids[cnt] = e;
     } else {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const int lane = tid & 63, wave = tid >> 6;
         const int q0 = wave * Q;
+        const ulonglong2 *q = (const ulonglong2 *)(s_key + q0);
         for (int e = q0 + lane; e < q0 + Q; e += 64) {
-            const float v = s_lg[e];
-            const float4 *q = (const float4 *)(s_lg + q0);
+            const uint64_t mk = s_key[e];
             int cnt = 0;
 #pragma unroll 8
-            for (int j4 = 0; j4 < Q / 4; j4++) {
-                const float4 u = q[j4];
-                const int j = q0 + 4 * j4;
-                cnt += (u.x > v) || (u.x == v && j < e);
-                cnt += (u.y > v) || (u.y == v && j + 1 < e);
-                cnt += (u.z > v) || (u.z == v && j + 2 < e);
-                cnt += (u.w > v) || (u.w == v && j + 3 < e);
+            for (int j2 = 0; j2 < Q / 2; j2++) {
+                const ulonglong2 u = q[j2];
+                cnt += (int)(u.x > mk) + (int)(u.y > mk);
             }
-            if (cnt < k) {
-                c_val[wave * k + cnt] = v;
-                c_idx[wave * k + cnt] = e;
-            }
+            if (cnt < k) c_key[wave * k + cnt] = mk;
         }
         __syncthreads();
-        if ((int)threadIdx.x < 4 * MAX_TOPK) {
-            // every candidate slot (unused ones hold index -1) against all 64
-            const int e = c_idx[threadIdx.x];
-            const float v = c_val[threadIdx.x];
+        if (tid < 4 * MAX_TOPK) {
+            // every candidate slot (unused ones hold key 0) against all 64
+            const uint64_t mk = c_key[tid];
             int cnt = 0;
 #pragma unroll
-            for (int j = 0; j < 4 * MAX_TOPK; j += 4) {
-                const int4 ej = *(const int4 *)(c_idx + j);
-                const float4 u = *(const float4 *)(c_val + j);
-                cnt += ej.x >= 0 && ((u.x > v) || (u.x == v && ej.x < e));
-                cnt += ej.y >= 0 && ((u.y > v) || (u.y == v && ej.y < e));
-                cnt += ej.z >= 0 && ((u.z > v) || (u.z == v && ej.z < e));
-                cnt += ej.w >= 0 && ((u.w > v) || (u.w == v && ej.w < e));
+            for (int j2 = 0; j2 < 2 * MAX_TOPK; j2++) {
+                const ulonglong2 u = ((const ulonglong2 *)c_key)[j2];
+                cnt += (int)(u.x > mk) + (int)(u.y > mk);
             }
-            if (e >= 0 && cnt < k) s_ids[cnt] = e;
+            if (mk != 0 && cnt < k) s_ids[cnt] = (int32_t)(0xFFFFFFFFu - (uint32_t)mk);
         }
     }
     __syncthreads();
-    // the workgroup with all-zero block index publishes the 64-int id row
-    if (r.ids_out && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 &&
-        threadIdx.x < IDS_ROW) {
-        const int row = threadIdx.x >> 4, slot = threadIdx.x & 15;
+    if (r.ids_out && publish && tid < IDS_ROW) {
+        const int row = tid >> 4, slot = tid & 15;
         int32_t v = (int32_t)SKIP;
         if (slot < k) {
             const int e = s_ids[slot];
@@ -204,9 +199,18 @@ __device__ inline const int32_t *route_ids_wg(const Route &r, int32_t *s_ids, fl
                 v = (int32_t)ids3[row - 1];
             }
         }
-        r.ids_out[threadIdx.x] = v;
+        *(int32_t STYX_GLOBAL *)(r.ids_out + tid) = v;
     }
     return s_ids;
+}
+
+// Logits from global memory, then rank_ids_lds; the workgroup with all-zero
+// block index publishes the 64-int id row.
+__device__ inline const int32_t *route_ids_wg(const Route &r, int32_t *s_ids, float *s_lg)
+{
+    for (int e = threadIdx.x; e < r.E / 4; e += blockDim.x)
+        ((float4 *)s_lg)[e] = ((const float4 *)r.logits)[e];
+    return rank_ids_lds(r, s_ids, s_lg, blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0);
 }
 
 }  // namespace styx

@@ -56,13 +56,15 @@ CFG_LAYER_Q8 = SynthConfig(n_layers=1, n_vocab=4096)
 
 
 def make_opts(n_ctx=4096, use_graph=True, expert_budget_mb=-1, expert_hist=None, arena=True,
-              repin_interval=0, repin_max=2, record_hidden=False, time_kernels=False):
+              repin_interval=0, repin_max=2, record_hidden=False, time_kernels=False,
+              fuse=True):
     o = L.MoeOpts()
     o.n_ctx, o.use_graph, o.expert_budget_mb = n_ctx, int(use_graph), expert_budget_mb
     o._hist = expert_hist.encode() if expert_hist else None
     o.expert_hist = o._hist
     o.arena, o.repin_interval, o.repin_max = int(arena), repin_interval, repin_max
     o.record_hidden, o.time_kernels = int(record_hidden), int(time_kernels)
+    o.no_fuse = 0 if fuse else 1
     return o
 
 
@@ -123,6 +125,25 @@ class MoeModel:
 
     def set_timing(self, on: bool) -> None:
         L.check(self.lib.styx_moe_set_timing(self.h, int(on)))
+
+    def time_stage(self, stage: str, reps: int = 20) -> tuple[float, int]:
+        """(mean us per graph replay, kernels per replay) of one stage's
+        launches over every layer (styx_moe_time_stage)."""
+        us, n = C.c_double(), C.c_int()
+        L.check(self.lib.styx_moe_time_stage(self.h, stage.encode(), reps, C.byref(us), C.byref(n)))
+        return us.value, n.value
+
+    def moe_block_trace(self) -> tuple[np.ndarray, float] | None:
+        """Phase stamps of the fused MoE block from the last timed token:
+        ([n_layers][nwg][16] ticks, ticks per us), or None without it."""
+        nwg, tpu = C.c_int(), C.c_double()
+        L.check(self.lib.styx_moe_moe_block_trace(self.h, None, 0, C.byref(nwg), None))
+        if nwg.value == 0:
+            return None
+        out = np.zeros((self.hp.n_layers, nwg.value, 16), np.uint64)
+        L.check(self.lib.styx_moe_moe_block_trace(self.h, out.ctypes.data, out.size, C.byref(nwg),
+                                                 C.byref(tpu)))
+        return out, tpu.value
 
     def last_expert_ids(self) -> np.ndarray:
         """moe.rs:2387-2402: [n_layers][k]."""

@@ -92,7 +92,8 @@ def test_config3_hist_pinning_identical(gpu):
     cfg = SynthConfig(n_layers=48, n_embd=256, n_heads=4, n_kv_heads=2, head_dim=64,
                       n_expert=128, n_expert_used=8, n_ff_exp=256, n_vocab=1024, exp_mix=True,
                       seed=0x30B)
-    ref = MoeModel.synth(gpu, cfg, n_ctx=32)
+    # the arena gather runs with the separate MoE kernels: so does the reference
+    ref = MoeModel.synth(gpu, cfg, n_ctx=32, fuse=False)
     budget_mb = int(ref.hp.slab_bytes * 48 * 128 / 3) >> 20
     m = MoeModel.synth(gpu, cfg, n_ctx=32, expert_budget_mb=budget_mb, expert_hist=str(HIST),
                        arena=True)

@@ -87,10 +87,13 @@ def test_host_experts_identical(gpu, budget, arena, tmp_path):
     """Experts in pinned host memory (all cold, or a hot budget from a
     popularity list), gathered into the HBM arena or read in place: logits
     bit-identical to the all-resident model (verify.sh:57-67 placement
-    invariance); hot+cold == k per layer (verify.sh:69-78)."""
+    invariance); hot+cold == k per layer (verify.sh:69-78).  In-place host
+    reads run in the fused MoE kernel, the arena gather with the separate
+    kernels; the reference model runs the same path."""
     from styx_amd import MoeModel
     cfg = small_cfg(seed=17)
-    ref = MoeModel.synth(gpu, cfg, n_ctx=32)
+    # the arena gather runs with the separate MoE kernels: compare like with like
+    ref = MoeModel.synth(gpu, cfg, n_ctx=32, fuse=not arena)
     hist = None
     if budget:
         rng = np.random.default_rng(0)
