@@ -3,11 +3,10 @@
 // One kernel runs what k_router, k_gate_up, k_down and k_reduce_rows do
 // (ffn RMSNorm + router logits, top-k ranking, expert gate/up, swiglu +
 // down, the weighted combine and the next RMSNorm's limbs) with the same
-// arithmetic, so its results are bit-identical to theirs.  What changes is
-// the schedule: a workgroup issues the weights of its down rows as soon as
-// the routing is known and keeps them in flight while it computes its
-// gate/up rows, so the down phase waits on the gate/up outputs rather than
-// on a kernel boundary plus an HBM trip.
+// arithmetic.  What changes is the schedule: no kernel boundary between the
+// phases, the shared expert's gate/up rows before the routing is known, the
+// top-k weights before the partials, and each phase's weights issued as
+// soon as its rows are known.
 //
 // Cross-workgroup data (router logits, gate/up outputs, per-slot down
 // partials) travels as 64-bit words (launch tag << 32 | f32 bits) written
@@ -135,28 +134,6 @@ __device__ __forceinline__ bool tpoll(int n, Addr addr, uint32_t tag, float *dst
         }
         __builtin_amdgcn_s_sleep(1);
     }
-}
-
-// Bring rows [r0, r1) of a split-layout matrix into this XCD's L2: one
-// dword of every 128-byte line of each region's row range (the rows of a
-// region are contiguous).  The returned word must be consumed later (the
-// loads are then waited for there, not here); the lines stay in L2 for the
-// rest of the kernel unless evicted.
-template <int T>
-__device__ __forceinline__ uint32_t touch_rows(const Mat &m, int nb, int r0, int r1)
-{
-    const Split sp = split_of(T);
-    const uint8_t STYX_GLOBAL *base[4] = {m.r0, m.r1, m.r2, m.r3};
-    uint32_t acc = 0;
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-        if (g >= sp.nreg) break;
-        const int64_t lo = (int64_t)r0 * nb * sp.sz[g], hi = (int64_t)r1 * nb * sp.sz[g];
-        for (int64_t off = (lo & ~(int64_t)127) + 128 * (int64_t)threadIdx.x; off < hi;
-             off += 128 * WG)
-            acc ^= *(const uint32_t STYX_GLOBAL *)(base[g] + (off < lo ? lo & ~(int64_t)3 : off));
-    }
-    return acc;
 }
 
 // Slab of expert e routed to `slot` (null when e is not a valid expert,
@@ -366,26 +343,19 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     rank_ids_lds(a.route, s_ids, s_lg, w == 0);
     stamp(4);
 
-    // ---- this workgroup's down rows: pulled into L2 once its gate/up rows
-    // are done, while it waits for the other workgroups' (HBM is otherwise
-    // idle then); the down phase reads them from there
+    // ---- this workgroup's down rows (their weights are loaded once the
+    // slot's gate/up outputs are in: pulling them into L2 earlier, during
+    // the gate/up phase or the wait after it, measured slower -- the extra
+    // requests delay the gate/up stream more than they save later)
     const bool has_d = w < a.n_d;
     const int ds = has_d ? w / a.bps_d : 0;
     const int d0 = (w - ds * a.bps_d) * a.rpw_d, d1 = min(a.H, d0 + a.rpw_d);
     const uint8_t *dslab = nullptr;
     if (has_d) dslab = ds < a.k ? routed_slab(a, a.src[2], s_ids[ds], ds) : a.sh[2];
-    bool d_started = false;
-    uint32_t touched = 0;
-    auto start_down = [&] {
-        if (d_started) return;
-        d_started = true;
-        if (dslab) touched = touch_rows<TD>(mat_at(dslab, TD, (int64_t)a.H * a.nb_d), a.nb_d, d0, d1);
-    };
 
     // ---- routed gate/up rows
     if (has_x)
         for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b, true, s_ids, xqx, tag, nothing, tr);
-    start_down();
     stamp(5);
 
     // ---- down: swiglu_f32 (ops2.rs:305-309) of the slot's g and u and its
@@ -397,9 +367,8 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
                                        tag, gus, a))
             return;
         stamp(6);
-        // the touched lines have long arrived; consuming the word here keeps
-        // the compiler from dropping those loads
-        asm volatile("" ::"v"(touched));
+        // the down weights go out first: the SwiGLU limbs are built while
+        // they are in flight
         RowWalk<TD, UD> dw;
         if (dslab) dw.start(mat_at(dslab, TD, (int64_t)a.H * a.nb_d), a.nb_d, a.G_d, d0, d1);
         for (int i = tid; i < F; i += WG) hs[i] = gus[i] / (1.0f + expf(-gus[i])) * gus[F + i];
