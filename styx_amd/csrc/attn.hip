@@ -21,6 +21,7 @@
 // graph serves every step; chunks past the context exit at once.
 #include "kernels.h"
 #include "qdot.h"
+#include "xchg.h"
 
 #include <algorithm>
 
@@ -117,6 +118,145 @@ __device__ __forceinline__ float sum16(float v)
     return v;
 }
 
+// ------------------------------------------------------ in-kernel combine --
+// With a.t_part the chunk workgroups publish their partials (m, l, o) as
+// tagged words, and query head g of kv head kvh is merged by the workgroup
+// of chunk g mod n_active: its four waves each take every fourth chunk in
+// batches of 8 (all loads of a batch issued together, re-polled until every
+// word carries the launch's tag), merge them online, then the waves merge in
+// LDS and the head's output and its limbs are written.  Only workgroups of
+// chunks below gqa ever wait, and they wait on chunks that never wait, so
+// the launch drains even when not all its workgroups are resident.  A wait
+// is bounded (a.max_polls rounds): a wave that gives up raises a.abort and
+// treats the missing chunks as empty.
+constexpr int CT_BATCH = 8;
+
+__device__ __forceinline__ void part_put(const AttnArgs &a, int64_t idx, uint32_t tag, float v)
+{
+    if (a.t_part)
+        tput(a.t_part + idx, tag, v);
+    else
+        a.part[idx] = v;
+}
+
+// Tag of this workgroup's launch (ticket drawn at entry by thread 0); every
+// thread of the workgroup must call it.
+__device__ __forceinline__ uint32_t attn_tag(const AttnArgs &a, unsigned long long ticket)
+{
+    __shared__ uint32_t s_tag;
+    const int nwg = gridDim.x * gridDim.y;
+    if (threadIdx.x == 0) s_tag = ticket_tag(ticket, nwg, ticket_counters(nwg));
+    __syncthreads();
+    return s_tag;
+}
+
+__device__ __forceinline__ unsigned long long attn_ticket(const AttnArgs &a)
+{
+    if (!a.t_part || threadIdx.x != 0) return 0;
+    const int nwg = gridDim.x * gridDim.y;
+    return draw_ticket(a.tickets, ticket_counters(nwg), blockIdx.x + blockIdx.y * gridDim.x);
+}
+
+template <int EPL>
+__device__ void attn_combine_tail(const AttnArgs &a, int c, int kvh, int n_active, uint32_t tag,
+                                  float *sm)
+{
+    constexpr int HD = 64 * EPL;
+    const int gqa = a.nh / a.nkv, ps = HD + 2;
+    if (c >= gqa) return;
+    __shared__ float red[16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float *go = sm, *gm = go + AT_WAVES * HD, *gl = gm + AT_WAVES, *xo = gl + AT_WAVES;
+    const int64_t cs = (int64_t)gqa * ps;  // stride between chunks
+    for (int g = c; g < gqa; g += n_active) {
+        const uint64_t *pk = a.t_part + (int64_t)kvh * a.max_chunks * cs + (int64_t)g * ps;
+        float m = -INFINITY, l = 0.0f, o[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; e++) o[e] = 0.0f;
+        for (int c0 = wave; c0 < n_active; c0 += AT_WAVES * CT_BATCH) {
+            float mc[CT_BATCH], lc[CT_BATCH], oc[CT_BATCH][EPL];
+            uint32_t pend = 0;
+#pragma unroll
+            for (int b = 0; b < CT_BATCH; b++) {
+                mc[b] = -INFINITY;
+                lc[b] = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) oc[b][e] = 0.0f;
+                if (c0 + AT_WAVES * b < n_active) pend |= 1u << b;
+            }
+            for (int polls = 0; __any(pend != 0); polls++) {
+#pragma unroll
+                for (int b = 0; b < CT_BATCH; b++) {
+                    if (!((pend >> b) & 1u)) continue;
+                    const uint64_t *pp = pk + (int64_t)(c0 + AT_WAVES * b) * cs;
+                    const uint64_t wm = tget(pp + HD), wl = tget(pp + HD + 1);
+                    uint64_t wo[EPL];
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) wo[e] = tget(pp + lane * EPL + e);
+                    bool ok = tvalid(wm, tag) && tvalid(wl, tag);
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) ok = ok && tvalid(wo[e], tag);
+                    if (ok) {
+                        mc[b] = tval(wm);
+                        lc[b] = tval(wl);
+#pragma unroll
+                        for (int e = 0; e < EPL; e++) oc[b][e] = tval(wo[e]);
+                        pend &= ~(1u << b);
+                    }
+                }
+                if (!__any(pend != 0)) break;
+                if (polls >= a.max_polls || ((polls & 31) == 31 && abort_seen(a.abort))) {
+                    if (lane == 0) abort_raise(a.abort);
+                    // missing chunks count as empty: the result is wrong and
+                    // the launch reports it through the abort flag
+#pragma unroll
+                    for (int b = 0; b < CT_BATCH; b++)
+                        if ((pend >> b) & 1u) mc[b] = -INFINITY;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+#pragma unroll
+            for (int b = 0; b < CT_BATCH; b++) {
+                if (mc[b] == -INFINITY) continue;
+                const float mn = fmaxf(m, mc[b]);
+                const float fa = expf(m - mn), fb = expf(mc[b] - mn);
+                l = l * fa + lc[b] * fb;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) o[e] = o[e] * fa + oc[b][e] * fb;
+                m = mn;
+            }
+        }
+        __syncthreads();  // sm is free (the attention phase is over, or the previous head)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) go[wave * HD + lane * EPL + e] = o[e];
+        if (lane == 0) {
+            gm[wave] = m;
+            gl[wave] = l;
+        }
+        __syncthreads();
+        const int h = kvh * gqa + g;
+        if ((int)threadIdx.x < HD) {
+            const int i = threadIdx.x;
+            float M = gm[0];
+            for (int q = 1; q < AT_WAVES; q++) M = fmaxf(M, gm[q]);
+            float L = 0.0f, O = 0.0f;
+            for (int q = 0; q < AT_WAVES; q++) {
+                const float f = gm[q] == -INFINITY ? 0.0f : expf(gm[q] - M);
+                L += gl[q] * f;
+                O += go[q * HD + i] * f;
+            }
+            const float v = O / L;
+            gst(a.out + (int64_t)h * HD + i, v);
+            xo[i] = v;
+        }
+        if (a.xq.A) {
+            __syncthreads();
+            xq_build(xo, nullptr, 0.0f, false, HD, xq_shift(a.xq, h * HD), red, nullptr);
+        }
+    }
+}
+
 // Wave roles: the four waves of a workgroup split the gqa query heads into
 // NHG head groups of HPW heads (HPW <= MAXH) and, when fewer than four
 // groups exist, also split the chunk's 16-token tiles NTS = 4 / NHG ways.
@@ -130,6 +270,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
 {
     constexpr int HD = 64 * EPL, PPL = (HD / 2 + 63) / 64, SEG = HD / 4;
     const int c = blockIdx.x, kvh = blockIdx.y;
+    const unsigned long long ticket = attn_ticket(a);  // also drawn by chunks past the context
     const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
     const int t0 = c * chunk;
     if (t0 >= n_t) return;
@@ -301,20 +442,23 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     }
 
     const int ps = HD + 2;
-    float *part = a.part + ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
+    const int64_t part0 = ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
+    const uint32_t tag = a.t_part ? attn_tag(a, ticket) : 0u;
+    const int n_active = (n_t + chunk - 1) / chunk;
     if (nts == 1) {
         // every wave owns distinct heads: its running state is the partial
 #pragma unroll
         for (int g = 0; g < MAXH; g++) {
             if (g >= hpw) break;
-            float *pg = part + (g0 + g) * ps;
+            const int64_t pg = part0 + (g0 + g) * ps;
 #pragma unroll
-            for (int e = 0; e < EPL; e++) pg[lane * EPL + e] = o[g][e];
+            for (int e = 0; e < EPL; e++) part_put(a, pg + lane * EPL + e, tag, o[g][e]);
             if (lane == 0) {
-                pg[HD] = m_run[g];
-                pg[HD + 1] = l_run[g];
+                part_put(a, pg + HD, tag, m_run[g]);
+                part_put(a, pg + HD + 1, tag, l_run[g]);
             }
         }
+        if (a.t_part) attn_combine_tail<EPL>(a, c, kvh, n_active, tag, sm);
         return;
     }
     // merge the NTS waves of each head group: M = max m_w, L = sum l_w
@@ -345,12 +489,13 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
             O += mo[wi * HD + e] * f;
             L += ml[wi] * f;
         }
-        part[gg * ps + e] = O;
+        part_put(a, part0 + gg * ps + e, tag, O);
         if (e == 0) {
-            part[gg * ps + HD] = M;
-            part[gg * ps + HD + 1] = L;
+            part_put(a, part0 + gg * ps + HD, tag, M);
+            part_put(a, part0 + gg * ps + HD + 1, tag, L);
         }
     }
+    if (a.t_part) attn_combine_tail<EPL>(a, c, kvh, n_active, tag, sm);
 }
 
 // ---------------------------------------------------------------------------
@@ -374,6 +519,7 @@ constexpr int MNB = MHD / 16;
 __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
 {
     const int c = blockIdx.x, kvh = blockIdx.y;
+    const unsigned long long ticket = attn_ticket(a);  // also drawn by chunks past the context
     const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
     const int t0 = c * chunk;
     if (t0 >= n_t) return;
@@ -544,9 +690,10 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
             ml[wave * MH + h] = l_run[r];
         }
     }
+    const uint32_t tag = a.t_part ? attn_tag(a, ticket) : 0u;  // (a barrier)
     __syncthreads();
     const int ps = MHD + 2;
-    float *part = a.part + ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
+    const int64_t part0 = ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
     for (int idx = threadIdx.x; idx < gqa * MHD; idx += AT_WG) {
         const int h = idx / MHD, e = idx - h * MHD;
         float M = -INFINITY;
@@ -560,12 +707,13 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
             O += mo[(w * MH + h) * MHD + e] * f;
             L += ml[w * MH + h] * f;
         }
-        part[h * ps + e] = O;
+        part_put(a, part0 + h * ps + e, tag, O);
         if (e == 0) {
-            part[h * ps + MHD] = M;
-            part[h * ps + MHD + 1] = L;
+            part_put(a, part0 + h * ps + MHD, tag, M);
+            part_put(a, part0 + h * ps + MHD + 1, tag, L);
         }
     }
+    if (a.t_part) attn_combine_tail<MHD / 64>(a, c, kvh, (n_t + chunk - 1) / chunk, tag, sm);
 }
 
 // Merge the per-chunk partials (m, l, o) of one query head: M = max m_c,
@@ -654,7 +802,8 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
 {
     const int gqa = a.nkv > 0 ? a.nh / a.nkv : 0;
     if (gqa < 1 || gqa > 16 || a.nh % a.nkv || (a.hd != 64 && a.hd != 128 && a.hd != 256) ||
-        a.chunk < TILE || a.chunk % TILE || a.page_tokens < 1 || a.max_chunks < 1)
+        a.chunk < TILE || a.chunk % TILE || a.page_tokens < 1 || a.max_chunks < 1 ||
+        (a.t_part && (!a.tickets || !a.abort || a.max_polls < 1)))
         return hipErrorInvalidValue;
     // the matrix-core variant serves 16 query heads per kv head; its waves
     // split tokens, so its chunks hold at least one 16-token tile per wave
@@ -682,7 +831,7 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
         return hipErrorInvalidValue;  // gqa of 5, 7, 9.. above 4 heads per wave
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || a.t_part) return e;  // combined inside the kernel
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nh), dim3(CB_WG),
                        (size_t)((CB_GROUPS + 1) * a.hd + 2 * CB_GROUPS) * 4, st, am);
     return hipGetLastError();

@@ -137,6 +137,10 @@ struct styx_moe {
     // abort flag; mb_nwg = its grid (0: the separate kernels run), -1 until
     // first sized
     uint64_t *t_lg = nullptr, *t_gu = nullptr, *t_part = nullptr;
+    // attention with the chunk partials merged inside its kernel: tagged
+    // partials and the launch's ticket counters
+    uint64_t *at_part = nullptr;
+    unsigned long long *at_tickets = nullptr;
     unsigned long long *mb_ticket = nullptr;
     int *mb_abort = nullptr;
     int mb_nwg = -1;
@@ -146,7 +150,8 @@ struct styx_moe {
     int64_t arena_slab[3] = {0, 0, 0};
     bool any_host = false;
     // graphs
-    hipGraphExec_t g_fwd = nullptr, g_gen = nullptr;
+    // [short context: attention partials merged in-kernel, long: combine kernel]
+    hipGraphExec_t g_fwd[2] = {nullptr, nullptr}, g_gen[2] = {nullptr, nullptr};
     int n_past = 0;
     uint64_t repin_swaps = 0;
     std::vector<void *> dev_allocs, host_allocs;
@@ -169,8 +174,9 @@ struct styx_moe {
     int check_abort();
     void queue_abort_read();
     int place_experts(const std::vector<std::vector<std::pair<uint32_t, uint64_t>>> *hist);
-    int enqueue_token(bool gen);
+    int enqueue_token(bool gen, bool attn_merge_in_kernel);
     int run_token(bool gen);
+    bool attn_merge_in_kernel(int n_t) const;
     int ensure_pages(int upto_pos);
     int build_graphs();
     void maybe_repin();
@@ -185,8 +191,10 @@ styx_moe::~styx_moe()
         hipSetDevice(gpu->device);
         hipStreamSynchronize(gpu->stream);
     }
-    if (g_fwd) hipGraphExecDestroy(g_fwd);
-    if (g_gen) hipGraphExecDestroy(g_gen);
+    for (int i = 0; i < 2; i++) {
+        if (g_fwd[i]) hipGraphExecDestroy(g_fwd[i]);
+        if (g_gen[i]) hipGraphExecDestroy(g_gen[i]);
+    }
     for (auto e : ev_pool) hipEventDestroy(e);
     for (void *p : dev_allocs) hipFree(p);
     for (void *p : host_allocs) hipHostFree(p);
@@ -308,6 +316,10 @@ int styx_moe::setup_runtime()
     max_chunks = std::min((n_ctx + chunk - 1) / chunk, std::max(16, 768 / nkv));
     const int64_t pf = styx_op_attn_part_floats(nh, nkv, hd, max_chunks);
     if (int r = dalloc(&attn_part, (size_t)pf)) return r;
+    if (int r = dalloc(&at_part, (size_t)pf)) return r;
+    if (int r = dalloc(&at_tickets, 64 * 16)) return r;
+    STYX_HIP(hipMemsetAsync(at_part, 0, sizeof(uint64_t) * pf, gpu->stream));
+    STYX_HIP(hipMemsetAsync(at_tickets, 0, sizeof(unsigned long long) * 64 * 16, gpu->stream));
     // tagged exchange of the fused MoE block: zero once (tag 0 is never a
     // launch's), never cleared again
     if (int r = dalloc(&t_lg, E)) return r;
@@ -492,21 +504,39 @@ int styx_moe::size_moe_block()
 // synchronisation (queue_abort_read), then checked here.
 void styx_moe::queue_abort_read()
 {
-    if (mb_abort && mb_nwg > 0)
+    if (mb_abort && !opts.no_fuse)
         (void)hipMemcpyAsync(&h_stage[4], mb_abort, sizeof(int), hipMemcpyDeviceToHost, gpu->stream);
 }
 
 int styx_moe::check_abort()
 {
-    if (!mb_abort || mb_nwg <= 0) return STYX_OK;
+    if (!mb_abort || opts.no_fuse) return STYX_OK;
     if (h_stage[4])
-        return fail(STYX_E_DEVICE, "fused MoE block: a workgroup's wait ran out (not all "
-                                   "workgroups resident?); results of this model are invalid");
+        return fail(STYX_E_DEVICE, "fused MoE block / attention: a workgroup's wait ran out (not "
+                                   "all workgroups resident?); results of this model are invalid");
     return STYX_OK;
 }
 
 // ------------------------------------------------------------ forward ----
-int styx_moe::enqueue_token(bool gen)
+// Whether the attention of a token at context length n_t merges its chunk
+// partials inside the attention kernel: while a head has at most 32 chunks
+// (chunking as the device computes it, attn.hip attn_chunk); beyond that the
+// few merging workgroups are slower than the separate combine kernel.
+bool styx_moe::attn_merge_in_kernel(int n_t) const
+{
+    if (opts.no_fuse) return false;
+    const int gqa = nh / nkv;
+    int ch_min = chunk, mc = max_chunks;
+    if (hd == 128 && gqa == 16) {  // the matrix-core variant's chunking
+        ch_min = std::max(chunk, 64);
+        mc = std::max(1, std::min(max_chunks, 512 / nkv));
+    }
+    const int need = (n_t + mc - 1) / mc;
+    const int ch = std::max(ch_min, (need + 15) / 16 * 16);
+    return (n_t + ch - 1) / ch <= 32;
+}
+
+int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
 {
     hipStream_t st = gpu->stream;
     const int q_dim = nh * hd;
@@ -575,6 +605,12 @@ int styx_moe::enqueue_token(bool gen)
         aa.chunk = chunk;
         aa.max_chunks = max_chunks;
         aa.scale = 1.0f / std::sqrt((float)hd);
+        if (merge_in_kernel) {
+            aa.t_part = at_part;
+            aa.tickets = at_tickets;
+            aa.abort = mb_abort;
+            aa.max_polls = 200000;
+        }
         if (want("attn")) CK(launch_attn_decode(st, aa));
         tend(e0, "attn", (double)(n_past + 1) * nkv * hd * 8.0);
         e0 = tstart();
@@ -752,10 +788,14 @@ int styx_moe::enqueue_token(bool gen)
 int styx_moe::build_graphs()
 {
     if (!opts.use_graph) return STYX_OK;
-    for (int gm = 0; gm < 2; gm++) {
+    // forward / generate x attention merged in the kernel (short contexts)
+    // or by the combine kernel (long ones; the only variant with no_fuse)
+    for (int gm = 0; gm < 4; gm++) {
+        const bool gen = gm / 2 == 1, merge = gm % 2 == 0;
+        if (merge && opts.no_fuse) continue;
         hipGraph_t g;
         STYX_HIP(hipStreamBeginCapture(gpu->stream, hipStreamCaptureModeThreadLocal));
-        int r = enqueue_token(gm == 1);
+        int r = enqueue_token(gen, merge);
         hipError_t e = hipStreamEndCapture(gpu->stream, &g);
         if (r) return r;
         if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
@@ -763,19 +803,21 @@ int styx_moe::build_graphs()
         e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
         hipGraphDestroy(g);
         if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
-        (gm ? g_gen : g_fwd) = ex;
+        (gen ? g_gen : g_fwd)[merge ? 0 : 1] = ex;
     }
     return STYX_OK;
 }
 
+// The token at position n_past (context n_past + 1).
 int styx_moe::run_token(bool gen)
 {
-    hipGraphExec_t g = gen ? g_gen : g_fwd;
+    const bool merge = attn_merge_in_kernel(n_past + 1);
+    hipGraphExec_t g = (gen ? g_gen : g_fwd)[merge ? 0 : 1];
     if (g && !opts.time_kernels) {
         STYX_HIP(hipGraphLaunch(g, gpu->stream));
         return STYX_OK;
     }
-    return enqueue_token(gen);
+    return enqueue_token(gen, merge);
 }
 
 // Online repinning (moe.rs:1450-1508): fold the last token's routing into
@@ -1390,7 +1432,8 @@ int styx_moe_time_stage(styx_moe *m, const char *stage, int reps, double *us_per
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
     int r = STYX_OK;
-    for (int i = 0; i < nrep && e == hipSuccess && !r; i++) r = m->enqueue_token(false);
+    const bool merge = m->attn_merge_in_kernel(m->n_past);  // the last token's context
+    for (int i = 0; i < nrep && e == hipSuccess && !r; i++) r = m->enqueue_token(false, merge);
     hipError_t e2 = e == hipSuccess ? hipStreamEndCapture(st, &g) : e;
     m->stage_only.clear();
     m->opts.time_kernels = saved;

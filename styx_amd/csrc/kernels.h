@@ -177,6 +177,14 @@ struct AttnArgs {
                      // n_t uses max(chunk, ceil16(n_t / max_chunks))
     int max_chunks;  // workgroups per kv head (grid); partials are sized by it
     float scale;
+    // In-kernel combine (optional): partials go out as tagged words to
+    // t_part (same shape as part); for each query head one chunk's
+    // workgroup merges them and writes out + xq, and no combine kernel runs.
+    // tickets: 64 x 16 zeroed u64 (xchg.h); abort: the bounded-wait flag.
+    uint64_t *t_part;
+    unsigned long long *tickets;
+    int *abort;
+    int max_polls;
 };
 hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a);
 

@@ -9,14 +9,8 @@
 // soon as its rows are known.
 //
 // Cross-workgroup data (router logits, gate/up outputs, per-slot down
-// partials) travels as 64-bit words (launch tag << 32 | f32 bits) written
-// and read with relaxed agent-scope atomics: on gfx950 these are plain
-// global stores/loads with device scope (sc1), coherent across the XCDs'
-// L2s, and a word is valid once its tag is the launch's.  No fence and no
-// counter is needed, and no buffer has to be cleared between launches.  The
-// tag is derived from a ticket every workgroup draws at entry
-// (ticket / gridDim + 1), so every launch has its own tag, also when a
-// captured graph replays the same launch.
+// partials) travels as tagged 64-bit words (xchg.h): no fence and no
+// counter is needed, and no buffer has to be cleared between launches.
 //
 // Every wait is bounded: after max_polls rounds, or once another workgroup
 // has given up, a workgroup sets *abort and exits.  The grid is sized to be
@@ -26,6 +20,7 @@
 #include "qdot.h"
 #include "topk.h"
 #include "walk.h"
+#include "xchg.h"
 
 #include <algorithm>
 
@@ -67,27 +62,6 @@ struct MoeBlockK {
     int off_xq, off_lg, off_gu, off_hs, off_xqh;  // dynamic LDS layout (bytes)
 };
 
-// Global loads and stores through pointers read from the LDS copy of the
-// arguments (a generic pointer would become a flat access).
-__device__ __forceinline__ float gld(const float *p) { return *(const float STYX_GLOBAL *)p; }
-__device__ __forceinline__ float4 gld4(const float *p)
-{
-    const styx_f4 v = *(const styx_f4 STYX_GLOBAL *)p;
-    return make_float4(v.x, v.y, v.z, v.w);
-}
-template <typename T> __device__ __forceinline__ void gst(T *p, T v) { *(T STYX_GLOBAL *)p = v; }
-
-__device__ __forceinline__ void tput(uint64_t *p, uint32_t tag, float v)
-{
-    __hip_atomic_store((uint64_t STYX_GLOBAL *)p, ((uint64_t)tag << 32) | __float_as_uint(v),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ uint64_t tget(const uint64_t *p)
-{
-    return __hip_atomic_load((uint64_t STYX_GLOBAL *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Words i = tid + 256 j (i < n) of the workgroup: wait until the word at
 // addr(i) carries `tag` and store its value to dst[i] (addr(i) == null: no
 // word, dst[i] = 0).  Thread 0 decides for the whole workgroup whether to
@@ -123,13 +97,9 @@ __device__ __forceinline__ bool tpoll(int n, Addr addr, uint32_t tag, float *dst
         // 32nd (a memory round trip of its own)
         int stop = 0;
         if (threadIdx.x == 0)
-            stop = polls >= a.max_polls ||
-                   ((polls & 31) == 31 && __hip_atomic_load((int STYX_GLOBAL *)a.abort, __ATOMIC_RELAXED,
-                                                            __HIP_MEMORY_SCOPE_AGENT) != 0);
+            stop = polls >= a.max_polls || ((polls & 31) == 31 && abort_seen(a.abort));
         if (__syncthreads_or(stop)) {
-            if (threadIdx.x == 0)
-                __hip_atomic_store((int STYX_GLOBAL *)a.abort, 1, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+            if (threadIdx.x == 0) abort_raise(a.abort);
             return false;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -247,10 +217,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     stamp(0);
     // the draw's result is first needed after the entry loads are issued
     unsigned long long ticket = 0;
-    if (tid == 0)
-        ticket = __hip_atomic_fetch_add(
-            (unsigned long long STYX_GLOBAL *)(a.ticket + (w % MB_TICKETS) * 16), 1ull,
-            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) ticket = draw_ticket(a.ticket, MB_TICKETS, w);
     if (w >= a.n_gu && w >= a.n_d && w >= a.nRed) {
         flush();
         return;
@@ -302,7 +269,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
                                               (v.z * scale) * nw.z, (v.w * scale) * nw.w);
         }
     }
-    if (tid == 0) s_tag = (uint32_t)(ticket / (unsigned long long)(nwg / MB_TICKETS)) + 1u;
+    if (tid == 0) s_tag = ticket_tag(ticket, nwg, MB_TICKETS);
     __syncthreads();
     const uint32_t tag = s_tag;
     stamp(1);
