@@ -83,7 +83,7 @@ def kernel_table(m, stats: dict, timing_steps: int, graphs: bool, reps: int = 20
 
 MB_PHASES = ["entry", "x_normalised", "limbs", "logits_seen", "ranked", "gate_up_done",
              "gu_seen", "h_limbs", "down_done", "partials_seen", "end", "gu_issued", "gu_limbs",
-             "gu_dots"]
+             "gu_dots", "gu_entered", "gu_slab"]
 
 
 def moe_block_phases(m) -> dict | None:

@@ -243,4 +243,46 @@ template <int T, int NR> struct RowWalkN {
     }
 };
 
+// Rows [r_begin, r_end) in batches of NR rows per lane group: every load of
+// a batch is issued, then (first batch only) xload(x, lu) fetches or builds
+// the limbs, then the batch is consumed.  Nothing is left in flight at the
+// end of an iteration, so the compiler's wait-counter pass never has to
+// guess about pending loads at the loop back-edge (the prefetching walkers
+// above leave the next rows' loads pending there, which in a large kernel
+// made it wait for every earlier load before each row's loads).  Same
+// per-row arithmetic as walk_rows_pf.
+template <int T, int UPL, int NR, typename XLoad, typename Emit>
+__device__ __forceinline__ void walk_rows_batched(const Mat &mat, int nb, int G, int r_begin,
+                                                  int r_end, XLoad xload, Emit emit)
+{
+    const LaneMap lm = lane_map(G);
+    const LaneU<UPL> lu = lane_units<T, UPL>(lm, nb, G);
+    UX<T> x[UPL];
+    bool have_x = false;
+    for (int r = r_begin + lm.gid; r < r_end; r += NR * lm.ngrp) {
+        UW<T> w[NR][UPL];
+#pragma unroll
+        for (int i = 0; i < NR; i++) {
+#pragma unroll
+            for (int u = 0; u < UPL; u++)
+                if (lu.uv[u] && r + i * lm.ngrp < r_end)
+                    uw_load<T>(w[i][u], mat, (int64_t)(r + i * lm.ngrp) * nb + lu.ub[u], lu.us[u]);
+        }
+        if (!have_x) {
+            xload(x, lu);
+            have_x = true;
+        }
+#pragma unroll
+        for (int i = 0; i < NR; i++) {
+            float acc = 0.0f;
+            const bool ok = r + i * lm.ngrp < r_end;
+#pragma unroll
+            for (int u = 0; u < UPL; u++)
+                if (lu.uv[u] && ok) acc += udot(w[i][u], x[u]);
+            acc = group_sum(acc, lm.gl, G);
+            if (lm.ok && lm.gl == 0 && ok) emit(r + i * lm.ngrp, acc);
+        }
+    }
+}
+
 }  // namespace styx
