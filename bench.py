@@ -95,11 +95,18 @@ def moe_block_phases(m) -> dict | None:
         return None
     st, tpu = tr
     out = {}
-    per = {p: ([], []) for p in MB_PHASES}
+    # slots 9 and 10 of the workgroups past the reduce ones time the next
+    # layer's q/k/v folded into the tail: limbs seen, rows stored
+    nred = (int(m.hp.n_embd) + 255) // 256
+    per = {p: ([], []) for p in MB_PHASES + ["qkv_limbs_seen", "qkv_done"]}
     for lay in st.astype(np.float64):
         t0 = lay[:, 0][lay[:, 0] > 0].min()
-        for i, p in enumerate(MB_PHASES):
-            v = lay[:, i][lay[:, i] > 0]
+        cols = [(p, lay[:, i]) for i, p in enumerate(MB_PHASES)]
+        cols[9] = ("partials_seen", lay[:nred, 9])
+        cols[10] = ("end", lay[:nred, 10])
+        cols += [("qkv_limbs_seen", lay[nred:, 9]), ("qkv_done", lay[nred:, 10])]
+        for p, c in cols:
+            v = c[c > 0]
             if len(v):
                 per[p][0].append(np.median(v - t0) / tpu)
                 per[p][1].append((v.max() - t0) / tpu)

@@ -232,6 +232,9 @@ typedef struct {
     int time_kernels;        /* HIP events around the expert kernels */
     int no_fuse;             /* 1: run the MoE block as four kernels instead of
                                 the fused persistent one (same results) */
+    int no_fold_qkv;         /* 1: keep every layer's q/k/v matvec a kernel of
+                                its own instead of the previous fused MoE
+                                block's tail (same results) */
 } styx_moe_opts;
 
 typedef struct {

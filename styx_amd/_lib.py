@@ -38,6 +38,7 @@ class MoeOpts(C.Structure):
         ("record_hidden", C.c_int),
         ("time_kernels", C.c_int),
         ("no_fuse", C.c_int),
+        ("no_fold_qkv", C.c_int),
     ]
 
 

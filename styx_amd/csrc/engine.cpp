@@ -143,6 +143,10 @@ struct styx_moe {
     unsigned long long *at_tickets = nullptr;
     unsigned long long *mb_ticket = nullptr;
     int *mb_abort = nullptr;
+    // qkv_fold[l]: layer l's q/k/v matvec runs in the tail of layer l-1's
+    // fused MoE block, from the tagged limbs in t_xq
+    std::vector<char> qkv_fold;
+    uint64_t *t_xq = nullptr;
     int mb_nwg = -1;
     uint64_t *mb_trace = nullptr;  // [L][mb_nwg][16] phase stamps of the last timed token
     // arena
@@ -495,6 +499,28 @@ int styx_moe::size_moe_block()
     mb_nwg = per_cu * ncu / 64 * 64;  // the kernel's ticket counters need a multiple of 64
     if (mb_nwg > 0 && !mb_trace)
         if (int r = dalloc(&mb_trace, (size_t)L * mb_nwg * 16)) return r;
+    // the next layer's q/k/v folded into the block's tail: q8_0 matrices
+    // whose rows fit the grid beside the reduce workgroups
+    qkv_fold.assign(L, 0);
+    if (mb_nwg > 0 && !opts.no_fold_qkv) {
+        for (int l = 1; l < L; l++) {
+            const Layer &p = layers[l - 1], &ly = layers[l];
+            if (ly.wq.type != T_Q8_0 || ly.wk.type != T_Q8_0 || ly.wv.type != T_Q8_0) continue;
+            const bool sh_fused = p.gsh.dev != nullptr;
+            const int rows[3] = {ly.wq.rows, ly.wk.rows, ly.wv.rows};
+            qkv_fold[l] = moe_block_fold_ok(p.gate.type, p.up.type, p.down.type, H, F, E, K,
+                                            sh_fused ? 1 : 0, rows, mb_nwg)
+                              ? 1
+                              : 0;
+        }
+        bool any = false;
+        for (char c : qkv_fold) any = any || c;
+        if (any && !t_xq) {
+            const size_t n = xq_bytes(H) / 4 + (size_t)(H + 255) / 256;
+            if (int r = dalloc(&t_xq, n)) return r;
+            STYX_HIP(hipMemsetAsync(t_xq, 0, sizeof(uint64_t) * n, gpu->stream));
+        }
+    }
     return STYX_OK;
 }
 
@@ -570,7 +596,9 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
     for (int l = 0; l < L; l++) {
         Layer &ly = layers[l];
         hipEvent_t e0 = tstart();
-        if (ly.wq.type == ly.wk.type && ly.wq.type == ly.wv.type) {
+        const bool folded = !qkv_fold.empty() && qkv_fold[l];  // ran in the previous block
+        if (folded) {
+        } else if (ly.wq.type == ly.wk.type && ly.wq.type == ly.wv.type) {
             DenseSeg s[3] = {{ly.wq.dev, q, ly.wq.rows}, {ly.wk.dev, kk, ly.wk.rows},
                              {ly.wv.dev, vv, ly.wv.rows}};
             if (want("qkv")) CK(launch_dense(st, ly.wq.type, H, s, 3, xq_a, 0, &ns_a));
@@ -581,7 +609,8 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
             if (want("qkv")) CK(launch_dense(st, ly.wk.type, H, &b, 1, xq_a, 0, &ns_a));
             if (want("qkv")) CK(launch_dense(st, ly.wv.type, H, &c, 1, xq_a, 0, &ns_a));
         }
-        tend(e0, "qkv", (double)(ly.wq.bytes() + ly.wk.bytes() + ly.wv.bytes()) + xq_bytes(H));
+        if (!folded)
+            tend(e0, "qkv", (double)(ly.wq.bytes() + ly.wk.bytes() + ly.wv.bytes()) + xq_bytes(H));
         e0 = tstart();
         AttnArgs aa{};
         aa.q = q;
@@ -717,6 +746,22 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
             mb.ticket = mb_ticket;
             mb.abort = mb_abort;
             mb.nwg = mb_nwg;
+            const bool fold_next = l + 1 < L && qkv_fold[l + 1];
+            double qkv_bytes = 0.0;
+            if (fold_next) {
+                const Layer &nx = layers[l + 1];
+                mb.wqkv[0] = nx.wq.dev;
+                mb.wqkv[1] = nx.wk.dev;
+                mb.wqkv[2] = nx.wv.dev;
+                mb.qkv_out[0] = q;
+                mb.qkv_out[1] = kk;
+                mb.qkv_out[2] = vv;
+                mb.qkv_rows[0] = nx.wq.rows;
+                mb.qkv_rows[1] = nx.wk.rows;
+                mb.qkv_rows[2] = nx.wv.rows;
+                mb.t_xq = t_xq;
+                qkv_bytes = (double)(nx.wq.bytes() + nx.wk.bytes() + nx.wv.bytes());
+            }
             if (timing) {
                 // phase stamps of every workgroup (eager timed tokens only)
                 mb.trace = mb_trace + (size_t)l * mb_nwg * 16;
@@ -724,7 +769,8 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
             }
             if (want("moe_block")) CK(launch_moe_block(st, mb));
             tend(e0, "moe_block", (double)E * H * 4 + slabs_gu + (double)K * ly.down.slab +
-                                      (sh_fused ? (double)ly.dsh.bytes() : 0.0) + 16.0 * H);
+                                      (sh_fused ? (double)ly.dsh.bytes() : 0.0) + 16.0 * H +
+                                      qkv_bytes);
         } else {
         e0 = tstart();
         if (want("moe_gate_up")) CK(launch_moe_gate_up(st, ly.gate.type, ly.up.type, sg, su, nullptr, &rt, xq_f, gu, H, F,

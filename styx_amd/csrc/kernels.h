@@ -120,12 +120,24 @@ struct MoeBlockArgs {
     int *abort;
     int max_polls;
     uint64_t *trace;
+    // optional: the next layer's q/k/v matvec folded into the tail (q8_0
+    // split-layout matrices [rows][H]; the RMSNorm of norm_next applied as
+    // by launch_dense with a NormScale); t_xq: tagged [xq_bytes(H)/4 +
+    // H/256] words
+    const uint8_t *wqkv[3];
+    float *qkv_out[3];
+    int qkv_rows[3];
+    uint64_t *t_xq;
     int nwg;
 };
 hipError_t launch_moe_block(hipStream_t st, const MoeBlockArgs &a);
 // Workgroups of the fused MoE kernel that fit on one CU at these shapes
 // (0: shapes not handled by it).
 int moe_block_occupancy(int tg, int tu, int td, int H, int F, int E, int k, int shexp);
+// Whether a block of these shapes on nwg workgroups takes the next layer's
+// q8_0 q/k/v (rows[3] rows of H columns) into its tail.
+bool moe_block_fold_ok(int tg, int tu, int td, int H, int F, int E, int k, int shexp,
+                       const int rows[3], int nwg);
 
 // H / 256 workgroups: w_s from the router logits and the id row
 // (topk_softmax_f32.comp:29-67) or given in wts;

@@ -31,7 +31,9 @@ constexpr int MB_RR = 256;         // reduce rows per workgroup, as k_reduce_row
 constexpr int MB_MAX_F = 2048;     // gate/up width handled here (g and u of a slot in LDS)
 constexpr int MB_TICKETS = 64;     // ticket counters (workgroup w draws from counter w % 64)
 constexpr int MB_GU_ROWS = 4;      // gate/up rows per lane group in flight at once
-constexpr int MB_TRACE = 16;       // trace slots per workgroup (phases 0..10 used)
+constexpr int MB_TRACE = 16;       // trace slots per workgroup
+constexpr int MB_MAX_H = 4096;     // residual width when the next q/k/v is folded in
+constexpr int MB_QJ = 7;           // tagged words per thread and poll round, q/k/v phase
 
 struct MoeBlockK {
     const float *x;         // residual [H]: read at entry, updated by the reduce
@@ -55,6 +57,12 @@ struct MoeBlockK {
     int *abort;
     int max_polls;
     uint64_t *trace;  // optional: [gridDim][MB_TRACE] wall-clock stamps per workgroup
+    // the next layer's q/k/v folded into the tail (wqkv[0] null: not folded)
+    const uint8_t *wqkv[3];  // q8_0 split layout, [rows][H]
+    float *qkv_out[3];
+    int qkv_rows[3];
+    uint64_t *t_xq;          // tagged limbs of x (.) w_next + the x^2 partials
+    int G_q, UPL_q, nb_q, rpw_q, n_q;  // rows per workgroup, workgroups [nRed, nRed + n_q)
     int nR;                                  // router workgroups
     int G_gu, nb_gu, rpw_gu, bps_gu, n_gu;   // gate/up blocks: [2][nslots][bps_gu]
     int G_d, nb_d, rpw_d, bps_d, n_d;        // down blocks: [nslots][bps_d]
@@ -135,14 +143,15 @@ __device__ __forceinline__ void gu_rows(const MoeBlockK &a, const uint8_t *slab,
     auto stamp = [&](int i) {
         if (tr && threadIdx.x == 0) tr[i] = wall_clock64();
     };
-    RowWalkN<T, MB_GU_ROWS> rw;
-    rw.start(mat_at(slab, T, (int64_t)a.F * a.nb_gu), a.nb_gu, a.G_gu, r0, r1);
-    stamp(11);
-    between();
-    UX<T> x[1];
-    XFrom<T, 1>{xqx}(x, rw.lu);
-    stamp(12);
-    rw.run(x, [&](int r, float v) { tput(y + r, tag, v); });
+    walk_rows_batched<T, 1, MB_GU_ROWS>(
+        mat_at(slab, T, (int64_t)a.F * a.nb_gu), a.nb_gu, a.G_gu, r0, r1,
+        [&](UX<T>(&x)[1], const LaneU<1> &lu) {
+            stamp(11);
+            between();
+            XFrom<T, 1>{xqx}(x, lu);
+            stamp(12);
+        },
+        [&](int r, float v) { tput(y + r, tag, v); });
     stamp(13);
 }
 
@@ -155,13 +164,102 @@ __device__ __forceinline__ void gu_block(const MoeBlockK &a, int b, bool routed_
     const int m = b / per_m, rem = b - m * per_m, s = rem / a.bps_gu;
     if ((s < a.k) != routed_phase) return;
     const int r0 = (rem - s * a.bps_gu) * a.rpw_gu, r1 = min(a.F, r0 + a.rpw_gu);
+    if (routed_phase && tr && threadIdx.x == 0) tr[14] = wall_clock64();
     const uint8_t *slab = s < a.k ? routed_slab(a, a.src[m], s_ids[s], s) : a.sh[m];
+    if (routed_phase && tr && threadIdx.x == 0) tr[15] = wall_clock64();
     switch (m == 0 ? a.tg : a.tu) {
     case T_Q8_0: gu_rows<T_Q8_0>(a, slab, xqx, m, s, r0, r1, tag, between, tr); break;
     case T_Q4_K: gu_rows<T_Q4_K>(a, slab, xqx, m, s, r0, r1, tag, between, tr); break;
     case T_Q5_K: gu_rows<T_Q5_K>(a, slab, xqx, m, s, r0, r1, tag, between, tr); break;
     default: gu_rows<T_Q6_K>(a, slab, xqx, m, s, r0, r1, tag, between, tr); break;
     }
+}
+
+// The next layer's q/k/v rows [r0, r1) (of the three matrices stacked):
+// their weights are issued first, then the limbs of x (.) w_next and the
+// x^2 partials are taken from the reduce workgroups' tagged words into LDS,
+// then the rows are formed as k_mv_dense forms them (dot times the RMSNorm
+// scale) in batches of NR rows per lane group, and stored for the next
+// kernel.  Returns false when the wait was abandoned.
+template <int UPL, int NR>
+__device__ __forceinline__ bool qkv_rows(const MoeBlockK &a, int r0, int r1, uint32_t tag, uint8_t *xq_lds,
+                         uint64_t *tr)
+{
+    const int b1 = a.qkv_rows[0], b2 = b1 + a.qkv_rows[1];
+    const Mat m0 = mat_at(a.wqkv[0], T_Q8_0, (int64_t)a.qkv_rows[0] * a.nb_q);
+    const Mat m1 = mat_at(a.wqkv[1], T_Q8_0, (int64_t)a.qkv_rows[1] * a.nb_q);
+    const Mat m2 = mat_at(a.wqkv[2], T_Q8_0, (int64_t)a.qkv_rows[2] * a.nb_q);
+    const LaneMap lm = lane_map(a.G_q);
+    const LaneU<UPL> lu = lane_units<T_Q8_0, UPL>(lm, a.nb_q, a.G_q);
+    UW<T_Q8_0> w[NR][UPL];
+    auto issue = [&](int r) {
+#pragma unroll
+        for (int i = 0; i < NR; i++) {
+            const int gr = r + i * lm.ngrp;
+            if (gr >= r1) continue;
+            const Mat &mm = gr < b1 ? m0 : gr < b2 ? m1 : m2;
+            const int lr = gr < b1 ? gr : gr < b2 ? gr - b1 : gr - b2;
+#pragma unroll
+            for (int u = 0; u < UPL; u++)
+                if (lu.uv[u]) uw_load<T_Q8_0>(w[i][u], mm, (int64_t)lr * a.nb_q + lu.ub[u], lu.us[u]);
+        }
+    };
+    const int rl = r0 + lm.gid;
+    if (rl < r1) issue(rl);
+    // Step 0 runs the row code on the first weights alone (x = 0, nothing
+    // stored) before the limbs are waited for: it fetches that code into the
+    // instruction cache while the wait is still ahead, so the rows formed
+    // after it do not stall on instruction fetches.  Step 1 waits for the
+    // limbs and forms the first rows, each later step issues and forms the
+    // next NR rows of each lane group.  The step count is hidden from the
+    // compiler so that every step runs the same code.
+    const int per_grp = (r1 - r0 + lm.ngrp - 1) / lm.ngrp;
+    const int nstep = 1 + (per_grp + NR - 1) / NR;
+    const int n_ss = (a.H + MB_RR - 1) / MB_RR;
+    UX<T_Q8_0> x[UPL] = {};
+    float scale = 0.0f;
+#pragma clang loop unroll(disable)
+    for (int step = 0; step < nstep; step++) {
+        int p = step;
+        asm volatile("" : "+s"(p));
+        const int r = rl + (p > 1 ? p - 1 : 0) * NR * lm.ngrp;
+        if (p == 1) {
+            // limbs (A | B | C | sx | s16, the layout of xq_at) and the partials
+            const int nw = (int)(xq_bytes(a.H) / 4) + n_ss;
+            for (int c = 0; c < nw; c += MB_QJ * WG)
+                if (!tpoll<MB_QJ>(min(MB_QJ * WG, nw - c), [&](int i) { return a.t_xq + c + i; },
+                                  tag, (float *)xq_lds + c, a))
+                    return false;
+            if (tr && threadIdx.x == 0) tr[9] = wall_clock64();
+            const Xq q = xq_at(xq_lds, a.H);
+            const float *ss = (const float *)(xq_lds + xq_bytes(a.H));
+            float t = 0.0f;
+            for (int i = lm.lane; i < n_ss; i += 64) t += ss[i];
+            t = wave_sum(t);
+            scale = 1.0f / sqrtf(t / (float)a.H + a.eps);
+            // x is rewritten whole: step 0's zeros need no registers across the wait
+#pragma unroll
+            for (int u = 0; u < UPL; u++) x[u] = UX<T_Q8_0>{};
+            XFrom<T_Q8_0, UPL>{q}(x, lu);
+        } else if (p > 1 && r < r1) {
+            issue(r);
+        }
+#pragma unroll
+        for (int i = 0; i < NR; i++) {
+            const int gr = r + i * lm.ngrp;
+            float acc = 0.0f;
+#pragma unroll
+            for (int u = 0; u < UPL; u++)
+                if (lu.uv[u] && gr < r1) acc += udot(w[i][u], x[u]);
+            acc = group_sum(acc, lm.gl, a.G_q);
+            if (p > 0 && lm.ok && lm.gl == 0 && gr < r1) {
+                float *y = gr < b1 ? a.qkv_out[0] + gr : gr < b2 ? a.qkv_out[1] + (gr - b1)
+                                                                 : a.qkv_out[2] + (gr - b2);
+                gst(y, acc * scale);
+            }
+        }
+    }
+    return true;
 }
 
 // Gate/up types are switched at run time (one routed row block at a time,
@@ -218,7 +316,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     // the draw's result is first needed after the entry loads are issued
     unsigned long long ticket = 0;
     if (tid == 0) ticket = draw_ticket(a.ticket, MB_TICKETS, w);
-    if (w >= a.n_gu && w >= a.n_d && w >= a.nRed) {
+    if (w >= a.n_gu && w >= a.n_d && w >= a.nRed && w >= a.nRed + a.n_q) {
         flush();
         return;
     }
@@ -336,8 +434,24 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         stamp(6);
         // the down weights go out first: the SwiGLU limbs are built while
         // they are in flight
-        RowWalk<TD, UD> dw;
-        if (dslab) dw.start(mat_at(dslab, TD, (int64_t)a.H * a.nb_d), a.nb_d, a.G_d, d0, d1);
+        // rows in batches of two per lane group; each batch's loads are
+        // issued together and consumed before the next batch is issued
+        // (nothing pending across iterations: see walk_rows_batched)
+        const Mat dm = dslab ? mat_at(dslab, TD, (int64_t)a.H * a.nb_d) : Mat{};
+        const LaneMap lm = lane_map(a.G_d);
+        const LaneU<UD> lu = lane_units<TD, UD>(lm, a.nb_d, a.G_d);
+        UW<TD> wd[2][UD];
+        auto issue = [&](int r) {
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int u = 0; u < UD; u++)
+                    if (lu.uv[u] && r + i * lm.ngrp < d1)
+                        uw_load<TD>(wd[i][u], dm, (int64_t)(r + i * lm.ngrp) * a.nb_d + lu.ub[u],
+                                    lu.us[u]);
+        };
+        const int rl = d0 + lm.gid;
+        if (dslab && rl < d1) issue(rl);
         for (int i = tid; i < F; i += WG) hs[i] = gus[i] / (1.0f + expf(-gus[i])) * gus[F + i];
         __syncthreads();
         xq_build(hs, nullptr, 0.0f, false, F, xqh, red, nullptr);
@@ -346,12 +460,40 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         uint64_t *part = a.t_part + (size_t)ds * a.H;
         if (dslab) {
             UX<TD> x[UD];
-            XFrom<TD, UD>{xqh}(x, dw.lu);
-            dw.run(x, [&](int r, float v) { tput(part + r, tag, v); });
+            XFrom<TD, UD>{xqh}(x, lu);
+            for (int r = rl; r < d1; r += 2 * lm.ngrp) {
+                if (r != rl) issue(r);
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    float acc = 0.0f;
+                    const bool ok = r + i * lm.ngrp < d1;
+#pragma unroll
+                    for (int u = 0; u < UD; u++)
+                        if (lu.uv[u] && ok) acc += udot(wd[i][u], x[u]);
+                    acc = group_sum(acc, lm.gl, a.G_d);
+                    if (lm.ok && lm.gl == 0 && ok) tput(part + r + i * lm.ngrp, tag, acc);
+                }
+            }
         } else {
             for (int r = d0 + tid; r < d1; r += WG) tput(part + r, tag, 0.0f);
         }
         stamp(8);
+    }
+
+    // ---- the next layer's q/k/v (folded in): workgroups past the reduce
+    // ones, after their down rows
+    if (a.wqkv[0] && w >= a.nRed && w < a.nRed + a.n_q) {
+        const int q0 = (w - a.nRed) * a.rpw_q;
+        const int q1 = min(a.qkv_rows[0] + a.qkv_rows[1] + a.qkv_rows[2], q0 + a.rpw_q);
+        __syncthreads();  // the limbs of xn are no longer read (their LDS is reused)
+        // rows per lane group in flight: all of them at the shapes served
+        // (a single memory round trip), as the registers allow
+        const bool ok = a.UPL_q == 1 ? qkv_rows<1, 4>(a, q0, q1, tag, lds + a.off_xq, tr)
+                                     : qkv_rows<2, 2>(a, q0, q1, tag, lds + a.off_xq, tr);
+        if (!ok) return;
+        stamp(10);
+        flush();
+        return;  // a q/k/v workgroup is past the reduce ones
     }
 
     // ---- reduce (k_reduce_rows arithmetic): weights, x += sum_s w_s y_s,
@@ -434,12 +576,49 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     __syncthreads();
     xw[tid] = xv * nw;
     __syncthreads();
-    if (tid < MB_RR / 8) {
-        const bool act = 8 * tid < nrow;
-        float h[8];
+    if (!a.wqkv[0]) {
+        if (tid < MB_RR / 8) {
+            const bool act = 8 * tid < nrow;
+            float h[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) h[i] = act ? xw[8 * tid + i] : 0.0f;
-        xq_group(h, act, tid, xq_shift(a.xq, r0));
+            for (int i = 0; i < 8; i++) h[i] = act ? xw[8 * tid + i] : 0.0f;
+            xq_group(h, act, tid, xq_shift(a.xq, r0));
+        }
+    } else {
+        // the limbs of these rows built in LDS (gus is free), then written
+        // to the limb buffer and as tagged words for the q/k/v workgroups
+        const Xq ql = xq_at(gus, MB_RR);
+        if (tid < MB_RR / 8) {
+            const bool act = 8 * tid < nrow;
+            float h[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) h[i] = act ? xw[8 * tid + i] : 0.0f;
+            xq_group(h, act, tid, ql);
+        }
+        __syncthreads();
+        const Xq qg = xq_shift(a.xq, r0);
+        const int nv = (nrow + 3) / 4, nsx = (nrow + 31) / 32, n16 = (nrow + 15) / 16;
+        const uint32_t *la = (const uint32_t *)ql.A, *lb = (const uint32_t *)ql.B,
+                       *lc = (const uint32_t *)ql.C;
+        const int H4 = a.H / 4;
+        if (tid < nv) {
+            const int o = r0 / 4 + tid;
+            gst((uint32_t *)qg.A + tid, la[tid]);
+            gst((uint32_t *)qg.B + tid, lb[tid]);
+            gst((uint32_t *)qg.C + tid, lc[tid]);
+            tput(a.t_xq + o, tag, __uint_as_float(la[tid]));
+            tput(a.t_xq + H4 + o, tag, __uint_as_float(lb[tid]));
+            tput(a.t_xq + 2 * H4 + o, tag, __uint_as_float(lc[tid]));
+        }
+        if (tid < nsx) {
+            gst(qg.sx + tid, ql.sx[tid]);
+            tput(a.t_xq + 3 * H4 + r0 / 32 + tid, tag, ql.sx[tid]);
+        }
+        if (tid < n16) {
+            gst(qg.s16 + tid, ql.s16[tid]);
+            tput(a.t_xq + 3 * H4 + a.H / 32 + r0 / 16 + tid, tag, ql.s16[tid]);
+        }
+        if (tid == 0) tput(a.t_xq + xq_bytes(a.H) / 4 + w, tag, sq);
     }
     stamp(10);
     flush();
@@ -499,6 +678,24 @@ static bool moe_geometry(const MoeBlockArgs &h, int nwg, MoeBlockK &a, size_t &l
     // every workgroup that reads x at entry has gate/up work, whose outputs
     // the reduce (which rewrites x) waits on
     if (a.n_d > nwg || a.nR > a.n_gu || a.nRed > a.n_gu) return false;
+    a.n_q = 0;
+    if (h.wqkv[0]) {
+        const Geo gq = pick_geo(T_Q8_0, h.H);
+        if (!gq.G || gq.UPL > 2 || h.H > MB_MAX_H || !h.t_xq || !h.norm_next || !h.wqkv[1] ||
+            !h.wqkv[2] || !h.qkv_out[0] || !h.qkv_out[1] || !h.qkv_out[2])
+            return false;
+        const int rows = h.qkv_rows[0] + h.qkv_rows[1] + h.qkv_rows[2];
+        const int ngrp_q = WAVES * (64 / gq.G), avail = nwg - a.nRed;
+        if (avail < 1) return false;
+        const int r = (rows + avail - 1) / avail;
+        a.G_q = gq.G;
+        a.UPL_q = gq.UPL;
+        a.nb_q = h.H / 32;
+        a.rpw_q = std::max(ngrp_q, (r + ngrp_q - 1) / ngrp_q * ngrp_q);
+        a.n_q = (rows + a.rpw_q - 1) / a.rpw_q;
+        // the partial sums land after the limbs, in the logits' LDS
+        if (a.nRed + a.n_q > nwg || a.nRed > h.E) return false;
+    }
     a.G_gu = gg.G;
     a.nb_gu = h.H / blk_elems(h.tg);
     a.G_d = gd.G;
@@ -510,6 +707,33 @@ static bool moe_geometry(const MoeBlockArgs &h, int nwg, MoeBlockK &a, size_t &l
     a.off_xqh = a.off_hs + align16((size_t)4 * std::max(h.F, MB_RR));
     lds = (size_t)a.off_xqh + align16(xq_bytes(h.F));
     return true;
+}
+
+bool moe_block_fold_ok(int tg, int tu, int td, int H, int F, int E, int k, int shexp,
+                       const int rows[3], int nwg)
+{
+    static const uint8_t dummy = 0;
+    static uint64_t dummy_t = 0;
+    static float dummy_f = 0.0f;
+    MoeBlockArgs h{};
+    h.tg = tg;
+    h.tu = tu;
+    h.td = td;
+    h.H = H;
+    h.F = F;
+    h.E = E;
+    h.k = k;
+    if (shexp) h.sh[0] = h.sh[1] = h.sh[2] = &dummy;
+    h.norm_next = &dummy_f;
+    h.t_xq = &dummy_t;
+    for (int i = 0; i < 3; i++) {
+        h.wqkv[i] = &dummy;
+        h.qkv_out[i] = &dummy_f;
+        h.qkv_rows[i] = rows[i];
+    }
+    MoeBlockK a{};
+    size_t lds = 0;
+    return moe_geometry(h, nwg, a, lds);
 }
 
 int moe_block_occupancy(int tg, int tu, int td, int H, int F, int E, int k, int shexp)
@@ -578,6 +802,12 @@ hipError_t launch_moe_block(hipStream_t st, const MoeBlockArgs &h)
     a.abort = h.abort;
     a.max_polls = h.max_polls > 0 ? h.max_polls : 200000;
     a.trace = h.trace;
+    for (int i = 0; i < 3; i++) {
+        a.wqkv[i] = h.wqkv[i];
+        a.qkv_out[i] = h.qkv_out[i];
+        a.qkv_rows[i] = h.qkv_rows[i];
+    }
+    a.t_xq = h.t_xq;
     hipLaunchKernelGGL(kf, dim3(h.nwg), dim3(WG), lds, st, a);
     return hipGetLastError();
 }

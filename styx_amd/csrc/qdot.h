@@ -33,15 +33,45 @@ __device__ __forceinline__ float limbs_to_f(int A, int B, int C)
     return (float)A + ((float)B + (float)C * R254) * R254;
 }
 
-__device__ __forceinline__ float wave_sum(float v)
+// Butterfly reductions over aligned blocks of G = 2, 4, ..., 64 lanes in
+// VALU operations only (DPP lane permutes, then the gfx950 row swaps), no
+// LDS round trips.  Each step pairs every lane with one partner of the other
+// half of its block and combines the two values; the partner combines the
+// same two values, so after the last step every lane of the block holds the
+// same bits.  Steps: quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror (lane i <-> 7-i of each 8), row_mirror (i <-> 15-i of each
+// 16), v_permlane16_swap (rows 0<->1, 2<->3), v_permlane32_swap (halves).
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v)
 {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int G, typename Op> __device__ __forceinline__ float bfly(float v, Op op)
+{
+    static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "power of two <= 64");
+    if constexpr (G >= 2) v = op(v, dpp_f<0xB1>(v));
+    if constexpr (G >= 4) v = op(v, dpp_f<0x4E>(v));
+    if constexpr (G >= 8) v = op(v, dpp_f<0x141>(v));
+    if constexpr (G >= 16) v = op(v, dpp_f<0x140>(v));
+    if constexpr (G >= 32) {
+        // one of the pair holds row 2j's value in both rows, the other row 2j+1's
+        const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(s[0]), __uint_as_float(s[1]));
+    }
+    if constexpr (G >= 64) {
+        const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(s[0]), __uint_as_float(s[1]));
+    }
     return v;
 }
+template <int G> __device__ __forceinline__ float bfly_sum(float v)
+{
+    return bfly<G>(v, [](float a, float b) { return a + b; });
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return bfly_sum<64>(v); }
 __device__ __forceinline__ float wave_max(float v)
 {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    return bfly<64>(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 // Block-wide sum (blockDim.x multiple of 64, <= 1024).  All threads get it.
@@ -430,9 +460,20 @@ __device__ __forceinline__ float udot(const UW<T_Q6_K> &w, const UX<T_Q6_K> &x)
 }
 
 // Sum over the G lanes of a group; the group leader (gl == 0) gets the total.
-// Groups are consecutive lanes [grp*G, grp*G+G); any 1 <= G <= 64.
+// Groups are consecutive lanes [grp*G, grp*G+G); any 1 <= G <= 64.  A power
+// of two (G is uniform) takes the butterfly, every lane getting the total.
 __device__ __forceinline__ float group_sum(float v, int gl, int G)
 {
+    switch (G) {
+    case 64: return bfly_sum<64>(v);
+    case 32: return bfly_sum<32>(v);
+    case 16: return bfly_sum<16>(v);
+    case 8: return bfly_sum<8>(v);
+    case 4: return bfly_sum<4>(v);
+    case 2: return bfly_sum<2>(v);
+    case 1: return v;
+    default: break;
+    }
     int off = 1;
     while (off * 2 < G) off *= 2;
     for (; off > 0; off >>= 1) {

@@ -57,7 +57,7 @@ CFG_LAYER_Q8 = SynthConfig(n_layers=1, n_vocab=4096)
 
 def make_opts(n_ctx=4096, use_graph=True, expert_budget_mb=-1, expert_hist=None, arena=True,
               repin_interval=0, repin_max=2, record_hidden=False, time_kernels=False,
-              fuse=True):
+              fuse=True, fold_qkv=True):
     o = L.MoeOpts()
     o.n_ctx, o.use_graph, o.expert_budget_mb = n_ctx, int(use_graph), expert_budget_mb
     o._hist = expert_hist.encode() if expert_hist else None
@@ -65,6 +65,7 @@ def make_opts(n_ctx=4096, use_graph=True, expert_budget_mb=-1, expert_hist=None,
     o.arena, o.repin_interval, o.repin_max = int(arena), repin_interval, repin_max
     o.record_hidden, o.time_kernels = int(record_hidden), int(time_kernels)
     o.no_fuse = 0 if fuse else 1
+    o.no_fold_qkv = 0 if fold_qkv else 1
     return o
 
 
