@@ -107,6 +107,19 @@ __host__ __device__ inline int64_t split_index(const Split &s, int64_t nblocks, 
     return -1;
 }
 
+// Greedy-sampling order as one unsigned 64-bit key: f32::total_cmp of the
+// value in the high word (sign-magnitude bits made two's-complement order,
+// then offset to unsigned), the row index in the low word, so the larger key
+// is the larger value and, between equal values, the later row
+// (Iterator::max_by keeps the last maximum, generate_moe.rs:29).  0 is below
+// every key of a real row but the lowest NaN at row 0.
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx)
+{
+    const int32_t b = __float_as_int(v);
+    const uint32_t k = (uint32_t)(b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1)) ^ 0x80000000u;
+    return ((unsigned long long)k << 32) | idx;
+}
+
 // ----------------------------------------------------------------------------
 // Activation limbs ("xq") of an n-value vector (n a multiple of 32): int8
 // planes A, B, C with x ~= sx * (A + (B + C/254)/254), sx = max|x|/127 per 32

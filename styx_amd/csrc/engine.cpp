@@ -121,11 +121,13 @@ struct styx_moe {
     float *x = nullptr, *q = nullptr, *kk = nullptr, *vv = nullptr, *attn = nullptr,
           *xn = nullptr, *rlog = nullptr, *wts = nullptr, *gu = nullptr, *partial = nullptr,
           *logits = nullptr, *hidden = nullptr, *sh_g = nullptr, *sh_u = nullptr, *sh_y = nullptr,
-          *attn_part = nullptr, *am_val = nullptr;
+          *attn_part = nullptr;
     Xq xq_a{}, xq_o{}, xq_f{}, xq_sh{};  // limbs: layer input, attention out, ffn input, shexp hidden
     float *ss_a = nullptr;                // partial sums of x^2 behind xq_a (per 256 rows)
     int32_t *ids = nullptr, *d_pos = nullptr;
-    uint32_t *d_tok = nullptr, *am_idx = nullptr, *hist = nullptr;
+    uint32_t *d_tok = nullptr, *hist = nullptr;
+    // running argmax of the LM head (argmax_key), cleared by its reader
+    unsigned long long *am_word = nullptr;
     uint32_t *h_stage = nullptr;  // pinned: tok, pos
     // KV
     float *kpool = nullptr, *vpool = nullptr;
@@ -277,8 +279,8 @@ int styx_moe::setup_runtime()
     if (int r = dalloc(&partial, (size_t)(K + 1) * H)) return r;
     if (int r = dalloc(&logits, V)) return r;
     if (int r = dalloc(&hidden, (size_t)(L + 1) * H)) return r;
-    if (int r = dalloc(&am_val, 64)) return r;
-    if (int r = dalloc(&am_idx, 64)) return r;
+    if (int r = dalloc(&am_word, 1)) return r;
+    STYX_HIP(hipMemsetAsync(am_word, 0, sizeof(unsigned long long), gpu->stream));
     if (int r = dalloc(&d_pos, 1)) return r;
     if (int r = dalloc(&d_tok, 1)) return r;
     if (int r = dalloc(&hist, (size_t)n_ctx + 1)) return r;
@@ -823,11 +825,13 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
     }
     hipEvent_t e0 = tstart();
     DenseSeg sh{head.dev, logits, V};
-    if (want("lm_head")) CK(launch_dense(st, head.type, H, &sh, 1, xq_a, 0, &ns_a));
+    // the greedy token is reduced inside the LM head (one atomic maximum per
+    // workgroup); a one-thread kernel reads it out
+    if (want("lm_head")) CK(launch_dense(st, head.type, H, &sh, 1, xq_a, 0, &ns_a, am_word));
     tend(e0, "lm_head", (double)head.bytes() + xq_bytes(H) + 4.0 * V);
     e0 = tstart();
-    if (want("argmax")) CK(launch_argmax(st, logits, V, d_tok, am_val, am_idx, d_pos, gen ? 1 : 0, hist));
-    tend(e0, "argmax", 4.0 * V);
+    if (want("argmax")) CK(launch_argmax_word(st, am_word, d_tok, d_pos, gen ? 1 : 0, hist));
+    tend(e0, "argmax", 8.0);
     return STYX_OK;
 }
 
@@ -1509,6 +1513,9 @@ int styx_moe_time_stage(styx_moe *m, const char *stage, int reps, double *us_per
     if (b) hipEventDestroy(b);
     hipGraphExecDestroy(ex);
     if (e != hipSuccess) return hip_fail(e, "styx_moe_time_stage: replay");
+    // LM-head replays leave their maximum in the argmax word: cleared before
+    // the next token's head adds to it
+    STYX_HIP(hipMemsetAsync(m->am_word, 0, sizeof(unsigned long long), st));
     STYX_HIP(hipStreamSynchronize(st));
     if (int rr = m->check_abort()) return rr;
     *us_per_replay = 1000.0 * ms / reps / nrep;

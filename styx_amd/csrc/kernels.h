@@ -41,7 +41,8 @@ hipError_t launch_xq(hipStream_t st, const float *x, const float *u, const float
 // into y.
 struct NormScale;
 hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, int nseg,
-                        const Xq &xq, int add, const NormScale *ns = nullptr);
+                        const Xq &xq, int add, const NormScale *ns = nullptr,
+                        unsigned long long *amax = nullptr);
 
 // Router for one layer (fused ffn_norm): writes logits[E] and, from its first
 // workgroup, xn (f32) and its limbs xq (if xq.A).  launch_router_topk also
@@ -213,6 +214,11 @@ hipError_t launch_embed(hipStream_t st, int t, const uint8_t *w, int64_t nrows, 
 hipError_t launch_argmax(hipStream_t st, const float *v, int n, uint32_t *out_tok,
                          float *part_val, uint32_t *part_idx, int32_t *pos, int advance,
                          uint32_t *hist);
+// The token of a running argmax word that launch_dense(..., amax) filled
+// (argmax_key order): written to out_tok (and hist[pos+1], pos advanced when
+// advance != 0); the word is cleared for the next launch.
+hipError_t launch_argmax_word(hipStream_t st, unsigned long long *amax, uint32_t *out_tok,
+                              int32_t *pos, int advance, uint32_t *hist);
 
 // gather_slabs_f32 semantics: for slot s<k with arena id != SKIP copy expert
 // ids[s]'s slab of each tensor into arena slot ids[32+s].

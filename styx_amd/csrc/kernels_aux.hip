@@ -203,6 +203,28 @@ __global__ void __launch_bounds__(64) k_argmax_final(const float *part_key,
     }
 }
 
+__global__ void __launch_bounds__(64) k_argmax_word(unsigned long long *amax, uint32_t *out_tok,
+                                                    int32_t *pos, int advance, uint32_t *hist)
+{
+    if (threadIdx.x != 0) return;
+    const uint32_t idx = (uint32_t)*amax;
+    *amax = 0ull;
+    *out_tok = idx;
+    if (advance) {
+        const int32_t p = *pos + 1;
+        *pos = p;
+        if (hist) hist[p] = idx;
+    }
+}
+
+hipError_t launch_argmax_word(hipStream_t st, unsigned long long *amax, uint32_t *out_tok,
+                              int32_t *pos, int advance, uint32_t *hist)
+{
+    if (!amax || !out_tok || (advance && !pos)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_argmax_word, dim3(1), dim3(64), 0, st, amax, out_tok, pos, advance, hist);
+    return hipGetLastError();
+}
+
 hipError_t launch_argmax(hipStream_t st, const float *v, int n, uint32_t *out_tok,
                          float *part_val, uint32_t *part_idx, int32_t *pos, int advance,
                          uint32_t *hist)

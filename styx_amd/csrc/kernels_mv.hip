@@ -123,12 +123,14 @@ struct DenseK {
     int nseg, total, nb, G, UPL, rpw, add;
     Xq xq;
     NormScale ns;  // ns.ss == null: no RMSNorm scale
+    unsigned long long *amax;  // optional: running argmax word (argmax_key)
 };
 
 template <int T, int UPL>
 __global__ void __launch_bounds__(WG) k_mv_dense(DenseK a)
 {
     const int r_begin = blockIdx.x * a.rpw, r_end = min(a.total, r_begin + a.rpw);
+    unsigned long long best = 0;  // argmax_key of the best row this lane emitted
     // segments are walked one after another; each starts a fresh row walk
     int base = 0;
     for (int s = 0; s < a.nseg; s++) {
@@ -148,17 +150,33 @@ __global__ void __launch_bounds__(WG) k_mv_dense(DenseK a)
                     scale = 1.0f / sqrtf(t / (float)a.ns.n + a.ns.eps);
                 }
             };
+            const int b0 = base;
             walk_rows_pf<T, UPL>(mat, a.nb, a.G, lo - base, hi - base, xload, [&](int r, float v) {
                 v *= scale;
-                y[r] = add ? y[r] + v : v;
+                v = add ? y[r] + v : v;
+                y[r] = v;
+                if (a.amax) best = max(best, argmax_key(v, (uint32_t)(b0 + r)));
             });
         }
         base += a.rows[s];
     }
+    if (a.amax) {
+        // the workgroup's best row joins the launch's running maximum: one
+        // relaxed device-scope atomic per workgroup (the reading kernel runs
+        // after this one)
+        __shared__ unsigned long long s_best[WAVES];
+        for (int o = 32; o > 0; o >>= 1) best = max(best, (unsigned long long)__shfl_xor(best, o));
+        if ((threadIdx.x & 63) == 0) s_best[threadIdx.x >> 6] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int i = 1; i < WAVES; i++) best = max(best, s_best[i]);
+            __hip_atomic_fetch_max(a.amax, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
 hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, int nseg,
-                        const Xq &xq, int add, const NormScale *ns)
+                        const Xq &xq, int add, const NormScale *ns, unsigned long long *amax)
 {
     const Geo g = pick_geo(t, ncols);
     if (g.G == 0 || nseg < 1 || nseg > 3 || !xq.A) return hipErrorInvalidValue;
@@ -177,6 +195,7 @@ hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, 
     a.add = add;
     a.xq = xq;
     if (ns) a.ns = *ns;
+    a.amax = amax;
     a.rpw = rows_per_wg(a.total, g.G, 1024);
     const dim3 grid((a.total + a.rpw - 1) / a.rpw);
     switch (t) {

@@ -287,12 +287,12 @@ __device__ __forceinline__ Mat mat_at(const uint8_t *base, int t, int64_t nblock
 
 __device__ __forceinline__ uint4 ldg16(const uint8_t STYX_GLOBAL *p)
 {
-    const styx_u4 v = *(const styx_u4 STYX_GLOBAL *)p;
+    const styx_u4 v = __builtin_nontemporal_load((const styx_u4 STYX_GLOBAL *)p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ uint32_t ldg2(const uint8_t STYX_GLOBAL *p)
 {
-    return *(const uint16_t STYX_GLOBAL *)p;
+    return __builtin_nontemporal_load((const uint16_t STYX_GLOBAL *)p);
 }
 
 template <int T> __device__ inline void uw_load(UW<T> &w, const Mat &m, int64_t blk, int sub);
