@@ -77,41 +77,7 @@ struct MoeBlockK {
 template <int MAXJ, typename Addr>
 __device__ __forceinline__ bool tpoll(int n, Addr addr, uint32_t tag, float *dst, const MoeBlockK &a)
 {
-    uint32_t pend = 0;
-#pragma unroll
-    for (int j = 0; j < MAXJ; j++) {
-        const int i = (int)threadIdx.x + WG * j;
-        if (i < n) {
-            if (addr(i))
-                pend |= 1u << j;
-            else
-                dst[i] = 0.0f;
-        }
-    }
-    for (int polls = 0;; polls++) {
-        uint64_t v[MAXJ];
-#pragma unroll
-        for (int j = 0; j < MAXJ; j++)
-            v[j] = ((pend >> j) & 1u) ? tget(addr((int)threadIdx.x + WG * j)) : 0ull;
-#pragma unroll
-        for (int j = 0; j < MAXJ; j++) {
-            if (((pend >> j) & 1u) && (uint32_t)(v[j] >> 32) == tag) {
-                dst[threadIdx.x + WG * j] = __uint_as_float((uint32_t)v[j]);
-                pend &= ~(1u << j);
-            }
-        }
-        if (!__syncthreads_or(pend != 0)) return true;
-        // the bound is checked every round, another workgroup's abort every
-        // 32nd (a memory round trip of its own)
-        int stop = 0;
-        if (threadIdx.x == 0)
-            stop = polls >= a.max_polls || ((polls & 31) == 31 && abort_seen(a.abort));
-        if (__syncthreads_or(stop)) {
-            if (threadIdx.x == 0) abort_raise(a.abort);
-            return false;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
+    return tpoll_wg<MAXJ>(n, addr, tag, dst, a.max_polls, a.abort);
 }
 
 // Slab of expert e routed to `slot` (null when e is not a valid expert,
@@ -596,28 +562,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
             xq_group(h, act, tid, ql);
         }
         __syncthreads();
-        const Xq qg = xq_shift(a.xq, r0);
-        const int nv = (nrow + 3) / 4, nsx = (nrow + 31) / 32, n16 = (nrow + 15) / 16;
-        const uint32_t *la = (const uint32_t *)ql.A, *lb = (const uint32_t *)ql.B,
-                       *lc = (const uint32_t *)ql.C;
-        const int H4 = a.H / 4;
-        if (tid < nv) {
-            const int o = r0 / 4 + tid;
-            gst((uint32_t *)qg.A + tid, la[tid]);
-            gst((uint32_t *)qg.B + tid, lb[tid]);
-            gst((uint32_t *)qg.C + tid, lc[tid]);
-            tput(a.t_xq + o, tag, __uint_as_float(la[tid]));
-            tput(a.t_xq + H4 + o, tag, __uint_as_float(lb[tid]));
-            tput(a.t_xq + 2 * H4 + o, tag, __uint_as_float(lc[tid]));
-        }
-        if (tid < nsx) {
-            gst(qg.sx + tid, ql.sx[tid]);
-            tput(a.t_xq + 3 * H4 + r0 / 32 + tid, tag, ql.sx[tid]);
-        }
-        if (tid < n16) {
-            gst(qg.s16 + tid, ql.s16[tid]);
-            tput(a.t_xq + 3 * H4 + a.H / 32 + r0 / 16 + tid, tag, ql.s16[tid]);
-        }
+        xq_publish(ql, nrow, r0, a.H, a.xq, a.t_xq, tag);
         if (tid == 0) tput(a.t_xq + xq_bytes(a.H) / 4 + w, tag, sq);
     }
     stamp(10);

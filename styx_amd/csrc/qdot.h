@@ -99,9 +99,10 @@ __device__ __forceinline__ void xq_group(const float *v, bool act, int g, Xq q)
         am = fmaxf(am, fabsf(v[i]));
         s8 += v[i];
     }
-    am = fmaxf(am, __shfl_xor(am, 1));
-    am = fmaxf(am, __shfl_xor(am, 2));
-    const float s16 = s8 + __shfl_xor(s8, 1);
+    // groups g^1, g^2 are the neighbouring lanes of a quad (callers run whole quads)
+    am = fmaxf(am, dpp_f<0xB1>(am));
+    am = fmaxf(am, dpp_f<0x4E>(am));
+    const float s16 = s8 + dpp_f<0xB1>(s8);
     if (!act) return;
     const float inv = am > 0.0f ? 127.0f / am : 0.0f;
     uint32_t pa[2] = {0, 0}, pb[2] = {0, 0}, pc[2] = {0, 0};

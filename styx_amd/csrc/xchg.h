@@ -64,6 +64,84 @@ __device__ __forceinline__ void abort_raise(int *abort)
     __hip_atomic_store((int STYX_GLOBAL *)abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Wait (workgroup-uniform) until the n tagged words addr(0..n) carry `tag`
+// and copy their values to dst[0..n) (LDS); addr(i) may return null for a
+// word that is not needed (dst[i] = 0).  Thread t takes words t + WG j,
+// j < MAXJ (n <= MAXJ * blockDim.x).  The wait is bounded: after max_polls
+// rounds, or once another workgroup has raised the abort flag, it raises
+// the flag and returns false.
+template <int MAXJ, typename Addr>
+__device__ __forceinline__ bool tpoll_wg(int n, Addr addr, uint32_t tag, float *dst, int max_polls,
+                                         int *abort)
+{
+    const int nt = blockDim.x;
+    uint32_t pend = 0;
+#pragma unroll
+    for (int j = 0; j < MAXJ; j++) {
+        const int i = (int)threadIdx.x + nt * j;
+        if (i < n) {
+            if (addr(i))
+                pend |= 1u << j;
+            else
+                dst[i] = 0.0f;
+        }
+    }
+    for (int polls = 0;; polls++) {
+        uint64_t v[MAXJ];
+#pragma unroll
+        for (int j = 0; j < MAXJ; j++)
+            v[j] = ((pend >> j) & 1u) ? tget(addr((int)threadIdx.x + nt * j)) : 0ull;
+#pragma unroll
+        for (int j = 0; j < MAXJ; j++) {
+            if (((pend >> j) & 1u) && (uint32_t)(v[j] >> 32) == tag) {
+                dst[threadIdx.x + nt * j] = __uint_as_float((uint32_t)v[j]);
+                pend &= ~(1u << j);
+            }
+        }
+        if (!__syncthreads_or(pend != 0)) return true;
+        // the bound is checked every round, another workgroup's abort every
+        // 32nd (a memory round trip of its own)
+        int stop = 0;
+        if (threadIdx.x == 0) stop = polls >= max_polls || ((polls & 31) == 31 && abort_seen(abort));
+        if (__syncthreads_or(stop)) {
+            if (threadIdx.x == 0) abort_raise(abort);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Limbs of n values (a multiple of 32) built in LDS at ql, elements
+// [e0, e0 + n) of an N-value vector (e0 a multiple of 32): copied into the
+// plain limb buffer qg of the whole vector and published as tagged words in
+// t, laid out as the 32-bit words of xq_at(., N): A | B | C | sx | s16.
+// Threads [0, n / 4) take part.
+__device__ __forceinline__ void xq_publish(const Xq &ql, int n, int e0, int N, const Xq &qg,
+                                           uint64_t *t, uint32_t tag)
+{
+    const int tid = threadIdx.x, N4 = N / 4;
+    const Xq g = xq_shift(qg, e0);
+    if (tid < n / 4) {
+        const uint32_t va = ((const uint32_t *)ql.A)[tid], vb = ((const uint32_t *)ql.B)[tid],
+                       vc = ((const uint32_t *)ql.C)[tid];
+        gst((uint32_t *)g.A + tid, va);
+        gst((uint32_t *)g.B + tid, vb);
+        gst((uint32_t *)g.C + tid, vc);
+        const int o = e0 / 4 + tid;
+        tput(t + o, tag, __uint_as_float(va));
+        tput(t + N4 + o, tag, __uint_as_float(vb));
+        tput(t + 2 * N4 + o, tag, __uint_as_float(vc));
+    }
+    if (tid < n / 32) {
+        gst(g.sx + tid, ql.sx[tid]);
+        tput(t + 3 * N4 + e0 / 32 + tid, tag, ql.sx[tid]);
+    }
+    if (tid < n / 16) {
+        gst(g.s16 + tid, ql.s16[tid]);
+        tput(t + 3 * N4 + N / 32 + e0 / 16 + tid, tag, ql.s16[tid]);
+    }
+}
+
 // Number of ticket counters for a launch of nwg workgroups: the largest
 // power of two dividing nwg, at most 64.
 __host__ __device__ inline int ticket_counters(int nwg)
