@@ -185,7 +185,9 @@ def stream_read_gbs(gpu, nbytes: int = 2 << 30, reps: int = 10) -> float:
 #   k_moe_block  router E*H*4 + 8 slots x (gate + up + down slab) + 16*H
 #   k_gate_up    8 slots x (gate + up slab) + limbs, logits, outputs
 TRAFFIC_KERNELS = {
-    "k_moe_block": ("moe_block", 128 * 2048 * 4 + 8 * 3256320 + 16 * 2048),
+    # router + 8 slots x (gate + up + down) + vectors, and the next layer's
+    # q/k/v (5120 q8_0 rows of 2048: 2176 B each) in 47 of the 48 launches
+    "k_moe_block": ("moe_block", 128 * 2048 * 4 + 8 * 3256320 + 16 * 2048 + 47 * 5120 * 2176 // 48),
     "k_gate_up": ("moe_gate_up", 17423616),
 }
 
