@@ -107,15 +107,21 @@ __device__ __forceinline__ void head_finish(const HeadIn<PPL> &h, const double2 
     }
 }
 
+// Reductions over the 16 lanes of a row (DPP butterflies, every lane of the
+// row gets the result), and the sum over the four rows of a wave at the
+// same row position (the two row swaps: v + (v of lane ^ 16), then + (the
+// same of lane ^ 32), in the same order on both lanes of each pair).
 __device__ __forceinline__ float max16(float v)
 {
-    for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    return bfly<16>(v, [](float a, float b) { return fmaxf(a, b); });
 }
-__device__ __forceinline__ float sum16(float v)
+__device__ __forceinline__ float sum16(float v) { return bfly_sum<16>(v); }
+__device__ __forceinline__ float sum_rows(float v)
 {
-    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(t[0]) + __uint_as_float(t[1]);
 }
 
 // ------------------------------------------------------ in-kernel combine --
@@ -396,8 +402,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
 #pragma unroll
         for (int g = 0; g < MAXH; g++) {
             if (g >= hpw) break;
-            float v = s[g] + __shfl_xor(s[g], 16);
-            v += __shfl_xor(v, 32);
+            float v = sum_rows(s[g]);
             v = tv ? v * a.scale : -INFINITY;
             const float m_new = fmaxf(m_run[g], max16(v));
             const float p = tv ? expf(v - m_new) : 0.0f;
@@ -814,6 +819,12 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
         // two of its 4-wave workgroups fit a CU (about 220 registers per
         // lane): one round of workgroups on 256 CUs
         am.max_chunks = std::max(1, std::min(a.max_chunks, 512 / a.nkv));
+    }
+    // merged in-kernel: the context spans at most ATTN_MERGE_MAX_CHUNKS
+    // chunks of the minimum size, so no chunk workgroup past that count has
+    // work (and the chunk size is the same as with the full grid)
+    if (a.t_part) am.max_chunks = std::min(am.max_chunks, ATTN_MERGE_MAX_CHUNKS);
+    if (use_mfma) {
         const size_t lds = sizeof(float) * ((size_t)MH * MHD + 2 * MHD + AT_WAVES * MH * 16 +
                                             (size_t)AT_WAVES * MH * MHD + 2 * AT_WAVES * MH);
         hipLaunchKernelGGL(k_attn_mfma, dim3(am.max_chunks, am.nkv), dim3(AT_WG), lds, st, am);
@@ -822,11 +833,11 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
     const int nhg = gqa % 4 == 0 ? 4 : gqa % 2 == 0 ? 2 : 1;
     const int hpw = gqa / nhg;
     if (hpw <= 1)
-        launch_k_attn<1>(st, a, nhg, hpw);
+        launch_k_attn<1>(st, am, nhg, hpw);
     else if (hpw <= 2)
-        launch_k_attn<2>(st, a, nhg, hpw);
+        launch_k_attn<2>(st, am, nhg, hpw);
     else if (hpw <= 4)
-        launch_k_attn<4>(st, a, nhg, hpw);
+        launch_k_attn<4>(st, am, nhg, hpw);
     else
         return hipErrorInvalidValue;  // gqa of 5, 7, 9.. above 4 heads per wave
     }

@@ -561,7 +561,7 @@ bool styx_moe::attn_merge_in_kernel(int n_t) const
     }
     const int need = (n_t + mc - 1) / mc;
     const int ch = std::max(ch_min, (need + 15) / 16 * 16);
-    return (n_t + ch - 1) / ch <= 32;
+    return (n_t + ch - 1) / ch <= ATTN_MERGE_MAX_CHUNKS;
 }
 
 int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)

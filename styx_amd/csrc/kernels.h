@@ -200,6 +200,10 @@ struct AttnArgs {
     int max_polls;
 };
 hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a);
+// Chunks per kv head up to which the partials are merged in-kernel (the
+// caller's choice; with t_part the launch has no more chunk workgroups than
+// this, which leaves the chunking of such contexts unchanged).
+constexpr int ATTN_MERGE_MAX_CHUNKS = 32;
 
 // x = dequant(token_embd[tok]) for the token held in device memory, and
 // (if q.A) the limbs of x ⊙ norm_w (of x if norm_w is null) with ss[0] =
