@@ -44,6 +44,9 @@ FLAGS = [
     "-Wno-unused-result",
     "-Wno-unused-value",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # every atomic here is issued by one lane: the optimizer's wave-wide
+    # rewrite would only add a wait for the result right after the atomic
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     f"-I{PKG.parent / 'include'}",
     f"-I{CSRC}",
 ]

@@ -277,16 +277,31 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     constexpr int HD = 64 * EPL, PPL = (HD / 2 + 63) / 64, SEG = HD / 4;
     const int c = blockIdx.x, kvh = blockIdx.y;
     const unsigned long long ticket = attn_ticket(a);  // also drawn by chunks past the context
-    const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
-    const int t0 = c * chunk;
-    if (t0 >= n_t) return;
-    const int t1 = min(n_t, t0 + chunk);
     const int gqa = a.nh / a.nkv, kv_dim = a.nkv * HD;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nts = AT_WAVES / nhg, hg = wave % nhg, ts = wave / nhg;
     const int g0 = hg * hpw;  // first head (within the kv head's group) of this wave
     const int tl = lane & (TILE - 1), qd = lane >> 4;  // token in tile, quarter of hd
     const int step = nts * TILE;  // this wave's tiles: tb, tb + step, ...
+    // loads that do not depend on the position go out with it: this wave's
+    // q heads and norm weights, the new k/v head, and the page-table entry
+    // of this lane's first token for the minimum chunk size (the chunk size
+    // of every short context)
+    HeadIn<PPL> hq[MAXH], hk;
+#pragma unroll
+    for (int i = 0; i < MAXH; i++)
+        if (i < hpw) head_load<PPL>(hq[i], a.q + (int64_t)(kvh * gqa + g0 + i) * HD, a.q_norm, HD);
+    float vn[EPL];
+    head_load<PPL>(hk, a.k + (int64_t)kvh * HD, a.k_norm, HD);
+#pragma unroll
+    for (int e = 0; e < EPL; e++) vn[e] = a.v[(int64_t)kvh * HD + lane * EPL + e];
+    const int t_min = c * a.chunk + ts * TILE + tl, pg_min = t_min / a.page_tokens;
+    const bool spec = pg_min < a.page_table_len;
+    const int32_t pe_min = spec ? a.page_table[pg_min] : 0;
+    const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
+    const int t0 = c * chunk;
+    if (t0 >= n_t) return;
+    const int t1 = min(n_t, t0 + chunk);
 
     extern __shared__ __align__(16) float sm[];
     // per wave: q [MAXH][HD] | knew [HD] | vnew [HD] | p [MAXH][TILE]
@@ -300,18 +315,8 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     // the new k/v head (in the chunk that holds pos), the first tile's
     // page-table entry
     const bool owns_pos = t1 == n_t;
-    HeadIn<PPL> hq[MAXH], hk;
     double2 cs[PPL];
     cs_load<PPL>(cs, a.rope + (int64_t)pos * (HD / 2), HD);
-#pragma unroll
-    for (int i = 0; i < MAXH; i++)
-        if (i < hpw) head_load<PPL>(hq[i], a.q + (int64_t)(kvh * gqa + g0 + i) * HD, a.q_norm, HD);
-    float vn[EPL];
-    if (owns_pos) {
-        head_load<PPL>(hk, a.k + (int64_t)kvh * HD, a.k_norm, HD);
-#pragma unroll
-        for (int e = 0; e < EPL; e++) vn[e] = a.v[(int64_t)kvh * HD + lane * EPL + e];
-    }
     int tb = t0 + ts * TILE;
     // K quarter-row of token tb+tl (this lane) and all 16 V rows of the tile
     // at [tb, tb+16): rows are pool offsets of each lane's token (lane i of
@@ -338,7 +343,14 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
         return tbase + tl < t1 ? kv_off(a, tbase + tl, kvh, kv_dim) : 0;
     };
     if (tb < t1) {
-        const int64_t row = row_of(tb);
+        // the first tile's rows from the early page entry when the chunk
+        // has its minimum size (then tb + tl == t_min)
+        const int64_t row =
+            spec && chunk == a.chunk
+                ? (tb + tl < t1 ? ((int64_t)pe_min * a.page_tokens + t_min % a.page_tokens) * kv_dim +
+                                      (int64_t)kvh * HD
+                                : 0)
+                : row_of(tb);
         load_k(row, tb);
         load_v(row, tb);
     }

@@ -625,6 +625,7 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
         aa.kpool = kpool;
         aa.vpool = vpool;
         aa.page_table = d_pt + (size_t)l * pages_per_layer;
+        aa.page_table_len = pages_per_layer;
         aa.page_tokens = KV_PAGE_TOKENS;
         aa.pos = d_pos;
         aa.out = attn;

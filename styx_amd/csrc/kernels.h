@@ -181,6 +181,7 @@ struct AttnArgs {
     float *kpool, *vpool;            // [pages][page_tokens][kv_dim]
     const int32_t *page_table;       // logical page -> physical page
     int page_tokens;
+    int page_table_len;              // entries of page_table (0: not given)
     const int32_t *pos;              // device scalar
     float *out;                      // [nh*hd]
     Xq xq;                           // optional limbs of out (o-proj input)
