@@ -115,15 +115,44 @@ __device__ __forceinline__ uint64_t rank_key(float v, int e)
     return ((uint64_t)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
 }
 
+// Maximum of a 64-bit key over the wave, every lane getting it: the
+// butterfly of bfly() on both 32-bit halves, the larger key kept at each
+// step.
+template <int CTRL> __device__ __forceinline__ uint32_t dpp_u(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ uint64_t join64(uint32_t hi, uint32_t lo) { return ((uint64_t)hi << 32) | lo; }
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
+{
+    auto mx = [](uint64_t a, uint64_t b) { return a > b ? a : b; };
+    v = mx(v, join64(dpp_u<0xB1>((uint32_t)(v >> 32)), dpp_u<0xB1>((uint32_t)v)));
+    v = mx(v, join64(dpp_u<0x4E>((uint32_t)(v >> 32)), dpp_u<0x4E>((uint32_t)v)));
+    v = mx(v, join64(dpp_u<0x141>((uint32_t)(v >> 32)), dpp_u<0x141>((uint32_t)v)));
+    v = mx(v, join64(dpp_u<0x140>((uint32_t)(v >> 32)), dpp_u<0x140>((uint32_t)v)));
+    {
+        const auto h = __builtin_amdgcn_permlane16_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+        const auto l = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+        v = mx(join64(h[0], l[0]), join64(h[1], l[1]));
+    }
+    {
+        const auto h = __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+        const auto l = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+        v = mx(join64(h[0], l[0]), join64(h[1], l[1]));
+    }
+    return v;
+}
+
 // Top-k ids of the router logits inside a workgroup, by ranking: the rank
-// of logit e is the number of keys larger than its key, so ranks 0..k-1 are
-// exactly the reference's selection order.  Up to 128 experts every key is
-// ranked against all (2 or 4 threads per logit, one 64-bit compare per
-// pair).  Above that, two levels: each wave ranks the keys of its quarter of
-// the experts among that quarter, those of rank < k are candidates (every
-// global top-k logit is in its quarter's top-k), and the <= 4k candidates
-// are ranked among themselves: E^2/4 + 16k^2 compares per workgroup instead
-// of E^2.  No dependent shuffle chain either way.
+// of a key is the number of larger keys, and ranks 0..k-1 are exactly the
+// reference's selection order (keys of rank_key: larger value first, equal
+// values by lower index).  Up to 128 experts every key is ranked against all
+// (2 or 4 threads per logit, one 64-bit compare per pair).  Above that each
+// wave takes a quarter of the experts (at most two keys per lane) and draws
+// its quarter's top min(k, E/4) keys one at a time -- the wave's largest key
+// (wave_max_u64), which its owner then drops -- and, every global top-k key
+// being in its quarter's top k, the <= 4k candidates are ranked among
+// themselves.  Integer compares only.
 // Fills s_ids[0..k) with the routed experts (route_row gives a slot's other
 // ids); weights are left to the caller.  The logits are in LDS (s_lg,
 // filled by the caller; the ranking synchronises before reading them);
@@ -132,17 +161,17 @@ __device__ __forceinline__ uint64_t rank_key(float v, int e)
 __device__ inline const int32_t *rank_ids_lds(const Route &r, int32_t *s_ids, const float *s_lg,
                                               bool publish)
 {
-    __shared__ __align__(16) uint64_t s_key[MAX_EXPERTS];
+    __shared__ __align__(16) uint64_t s_key[128];
     __shared__ __align__(16) uint64_t c_key[4 * MAX_TOPK];
-    const int E = r.E, k = r.k, Q = E / 4;  // quarter: Q % 4 == 0
-    const int tid = threadIdx.x;
+    const int E = r.E, k = r.k, Q = E / 4;  // quarter: Q % 4 == 0, Q <= 128
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q0 = wave * Q;
     if (tid < IDS_ROW) s_ids[tid] = (int32_t)SKIP;
     if (tid < 4 * MAX_TOPK) c_key[tid] = 0;
-    __syncthreads();
-    for (int e = tid; e < E; e += blockDim.x) s_key[e] = rank_key(s_lg[e], e);
-    __syncthreads();
+    __syncthreads();  // also: the caller's logits are in s_lg
     if (E <= 128) {
         // direct: P = 256 / E threads rank each key against a slice of all
+        for (int e = tid; e < E; e += blockDim.x) s_key[e] = rank_key(s_lg[e], e);
+        __syncthreads();
         const int P = E <= 64 ? 4 : 2, span = E / P;
         const int e = tid / P, part = tid % P;
         int cnt = 0;
@@ -159,18 +188,21 @@ __device__ inline const int32_t *rank_ids_lds(const Route &r, int32_t *s_ids, co
         if (P == 4) cnt += __shfl_xor(cnt, 2);
         if (e < E && part == 0 && cnt < k) s_ids[cnt] = e;
     } else {
-        const int lane = tid & 63, wave = tid >> 6;
-        const int q0 = wave * Q;
-        const ulonglong2 *q = (const ulonglong2 *)(s_key + q0);
-        for (int e = q0 + lane; e < q0 + Q; e += 64) {
-            const uint64_t mk = s_key[e];
-            int cnt = 0;
-#pragma unroll 8
-            for (int j2 = 0; j2 < Q / 2; j2++) {
-                const ulonglong2 u = q[j2];
-                cnt += (int)(u.x > mk) + (int)(u.y > mk);
+        uint64_t k0 = lane < Q ? rank_key(s_lg[q0 + lane], q0 + lane) : 0;
+        uint64_t k1 = lane + 64 < Q ? rank_key(s_lg[q0 + lane + 64], q0 + lane + 64) : 0;
+        if (k1 > k0) {
+            const uint64_t t = k0;
+            k0 = k1;
+            k1 = t;
+        }
+        const int kk = min(k, Q);
+        for (int it = 0; it < kk; it++) {
+            const uint64_t m = wave_max_u64(k0);
+            if (lane == 0) c_key[wave * k + it] = m;
+            if (k0 == m) {  // keys are distinct: one lane
+                k0 = k1;
+                k1 = 0;
             }
-            if (cnt < k) c_key[wave * k + cnt] = mk;
         }
         __syncthreads();
         if (tid < 4 * MAX_TOPK) {
