@@ -109,7 +109,7 @@ __device__ __forceinline__ void gu_rows(const MoeBlockK &a, const uint8_t *slab,
     auto stamp = [&](int i) {
         if (tr && threadIdx.x == 0) tr[i] = wall_clock64();
     };
-    walk_rows_batched<T, 1, MB_GU_ROWS>(
+    walk_rows_pipelined<T, 1, MB_GU_ROWS / 2>(
         mat_at(slab, T, (int64_t)a.F * a.nb_gu), a.nb_gu, a.G_gu, r0, r1,
         [&](UX<T>(&x)[1], const LaneU<1> &lu) {
             stamp(11);
@@ -455,7 +455,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         // rows per lane group in flight: all of them at the shapes served
         // (a single memory round trip), as the registers allow
         const bool ok = a.UPL_q == 1 ? qkv_rows<1, 4>(a, q0, q1, tag, lds + a.off_xq, tr)
-                                     : qkv_rows<2, 2>(a, q0, q1, tag, lds + a.off_xq, tr);
+                                     : qkv_rows<2, 3>(a, q0, q1, tag, lds + a.off_xq, tr);
         if (!ok) return;
         stamp(10);
         flush();
@@ -606,11 +606,11 @@ static bool moe_geometry(const MoeBlockArgs &h, int nwg, MoeBlockK &a, size_t &l
     a.nslots = h.k + (h.sh[0] ? 1 : 0);
     a.nR = (h.E + MB_ROUTER_ROWS - 1) / MB_ROUTER_ROWS;
     a.nRed = (h.H + MB_RR - 1) / MB_RR;
-    // the gate/up walker has MB_GU_ROWS rows per lane group in flight, so a
-    // block of up to MB_GU_ROWS * ngrp rows takes one HBM trip
+    // one gate/up block per workgroup: the walker keeps the next
+    // MB_GU_ROWS rows per lane group in flight while a batch is consumed
     const int ngrp_gu = WAVES * (64 / gg.G), ngrp_d = WAVES * (64 / gd.G);
     int rpw = (2 * a.nslots * h.F + nwg - 1) / nwg;
-    a.rpw_gu = std::min(MB_GU_ROWS * ngrp_gu, (rpw + ngrp_gu - 1) / ngrp_gu * ngrp_gu);
+    a.rpw_gu = (rpw + ngrp_gu - 1) / ngrp_gu * ngrp_gu;
     a.bps_gu = (h.F + a.rpw_gu - 1) / a.rpw_gu;
     a.n_gu = 2 * a.nslots * a.bps_gu;
     if (nwg % MB_TICKETS) return false;

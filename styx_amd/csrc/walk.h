@@ -251,6 +251,54 @@ template <int T, int NR> struct RowWalkN {
 // above leave the next rows' loads pending there, which in a large kernel
 // made it wait for every earlier load before each row's loads).  Same
 // per-row arithmetic as walk_rows_pf.
+// As walk_rows_batched, with the next batch's loads issued before the
+// current batch is consumed (two register sets, alternated in a loop
+// unrolled by two), so that a block of several batches streams its weights
+// in one pass instead of one memory round trip per batch.
+template <int T, int UPL, int NR, typename XLoad, typename Emit>
+__device__ __forceinline__ void walk_rows_pipelined(const Mat &mat, int nb, int G, int r_begin,
+                                                    int r_end, XLoad xload, Emit emit)
+{
+    const LaneMap lm = lane_map(G);
+    const LaneU<UPL> lu = lane_units<T, UPL>(lm, nb, G);
+    const int step = NR * lm.ngrp;
+    auto issue = [&](UW<T>(&w)[NR][UPL], int r) {
+#pragma unroll
+        for (int i = 0; i < NR; i++) {
+#pragma unroll
+            for (int u = 0; u < UPL; u++)
+                if (lu.uv[u] && r + i * lm.ngrp < r_end)
+                    uw_load<T>(w[i][u], mat, (int64_t)(r + i * lm.ngrp) * nb + lu.ub[u], lu.us[u]);
+        }
+    };
+    UX<T> x[UPL];
+    auto consume = [&](const UW<T>(&w)[NR][UPL], int r) {
+#pragma unroll
+        for (int i = 0; i < NR; i++) {
+            float acc = 0.0f;
+            const bool ok = r + i * lm.ngrp < r_end;
+#pragma unroll
+            for (int u = 0; u < UPL; u++)
+                if (lu.uv[u] && ok) acc += udot(w[i][u], x[u]);
+            acc = group_sum(acc, lm.gl, G);
+            if (lm.ok && lm.gl == 0 && ok) emit(r + i * lm.ngrp, acc);
+        }
+    };
+    UW<T> wa[NR][UPL], wb[NR][UPL];
+    int r = r_begin + lm.gid;
+    if (r < r_end) issue(wa, r);
+    xload(x, lu);
+    while (r < r_end) {
+        if (r + step < r_end) issue(wb, r + step);
+        consume(wa, r);
+        r += step;
+        if (r >= r_end) break;
+        if (r + step < r_end) issue(wa, r + step);
+        consume(wb, r);
+        r += step;
+    }
+}
+
 template <int T, int UPL, int NR, typename XLoad, typename Emit>
 __device__ __forceinline__ void walk_rows_batched(const Mat &mat, int nb, int G, int r_begin,
                                                   int r_end, XLoad xload, Emit emit)
