@@ -23,6 +23,7 @@
 #include "xchg.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace styx {
 
@@ -293,71 +294,81 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     const bool has_x = w < a.n_gu;
     const bool router = w < a.nR;
     const int rr = w * MB_ROUTER_ROWS + wave;
-    constexpr int PW = 8, PX = 2;
-    float4 wv[PW];
-    if (has_x) {
-        const float *wr = a.W + (int64_t)min(rr, a.E - 1) * a.H;
+    // x and the router row in registers in one trip: PX float4 of x per
+    // thread and PW of the row per lane (H <= 4 * WG * PX); a short row does
+    // not pay for the registers and predicated loads of a long one
+    uint32_t tag = 0;
+    auto entry = [&](auto pw, auto px) {
+        constexpr int PW = decltype(pw)::value, PX = decltype(px)::value;
+        float4 wv[PW];
+        if (has_x) {
+            const float *wr = a.W + (int64_t)min(rr, a.E - 1) * a.H;
 #pragma unroll
-        for (int j = 0; j < PW; j++) {
-            const int c = lane * 4 + 256 * j;
-            wv[j] = (router && c < a.H) ? gld4(wr + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-        float4 xv[PX], nv[PX];
+            for (int j = 0; j < PW; j++) {
+                const int c = lane * 4 + 256 * j;
+                wv[j] = (router && c < a.H) ? gld4(wr + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+            float4 xv[PX], nv[PX];
 #pragma unroll
-        for (int j = 0; j < PX; j++) {
-            const int i = tid * 4 + WG * 4 * j;
-            xv[j] = i < a.H ? gld4(a.x + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            nv[j] = i < a.H ? gld4(a.ffn_norm + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-        float ss = 0.0f;
+            for (int j = 0; j < PX; j++) {
+                const int i = tid * 4 + WG * 4 * j;
+                xv[j] = i < a.H ? gld4(a.x + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                nv[j] = i < a.H ? gld4(a.ffn_norm + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+            float ss = 0.0f;
 #pragma unroll
-        for (int j = 0; j < PX; j++)
-            ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
-        for (int i = tid * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {
-            const float4 v = gld4(a.x + i);
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-        }
-        ss = block_sum(ss, red);
-        const float scale = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+            for (int j = 0; j < PX; j++)
+                ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+            for (int i = tid * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {
+                const float4 v = gld4(a.x + i);
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+            ss = block_sum(ss, red);
+            const float scale = 1.0f / sqrtf(ss / (float)a.H + a.eps);
 #pragma unroll
-        for (int j = 0; j < PX; j++) {
-            const int i = tid * 4 + WG * 4 * j;
-            if (i < a.H)
-                *(float4 *)(xs + i) = make_float4((xv[j].x * scale) * nv[j].x, (xv[j].y * scale) * nv[j].y,
-                                                  (xv[j].z * scale) * nv[j].z, (xv[j].w * scale) * nv[j].w);
-        }
-        for (int i = tid * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {
-            const float4 v = gld4(a.x + i);
-            const float4 nw = gld4(a.ffn_norm + i);
-            *(float4 *)(xs + i) = make_float4((v.x * scale) * nw.x, (v.y * scale) * nw.y,
-                                              (v.z * scale) * nw.z, (v.w * scale) * nw.w);
-        }
-    }
-    if (tid == 0) s_tag = ticket_tag(ticket, nwg, MB_TICKETS);
-    __syncthreads();
-    const uint32_t tag = s_tag;
-    stamp(1);
-
-    // ---- router logits (matvec_strided_f32, one row per wave)
-    if (router && rr < a.E) {
-        const float *wr = a.W + (int64_t)rr * a.H;
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < PW; j++) {
-            const int c = lane * 4 + 256 * j;
-            if (c < a.H) {
-                const float4 xv4 = *(const float4 *)(xs + c);
-                acc += wv[j].x * xv4.x + wv[j].y * xv4.y + wv[j].z * xv4.z + wv[j].w * xv4.w;
+            for (int j = 0; j < PX; j++) {
+                const int i = tid * 4 + WG * 4 * j;
+                if (i < a.H)
+                    *(float4 *)(xs + i) = make_float4((xv[j].x * scale) * nv[j].x, (xv[j].y * scale) * nv[j].y,
+                                                      (xv[j].z * scale) * nv[j].z, (xv[j].w * scale) * nv[j].w);
+            }
+            for (int i = tid * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {
+                const float4 v = gld4(a.x + i);
+                const float4 nw = gld4(a.ffn_norm + i);
+                *(float4 *)(xs + i) = make_float4((v.x * scale) * nw.x, (v.y * scale) * nw.y,
+                                                  (v.z * scale) * nw.z, (v.w * scale) * nw.w);
             }
         }
-        for (int c = lane * 4 + 256 * PW; c < a.H; c += 256) {
-            const float4 wq = gld4(wr + c);
-            const float4 xv4 = *(const float4 *)(xs + c);
-            acc += wq.x * xv4.x + wq.y * xv4.y + wq.z * xv4.z + wq.w * xv4.w;
+        if (tid == 0) s_tag = ticket_tag(ticket, nwg, MB_TICKETS);
+        __syncthreads();
+        tag = s_tag;
+        stamp(1);
+
+        // ---- router logits (matvec_strided_f32, one row per wave)
+        if (router && rr < a.E) {
+            const float *wr = a.W + (int64_t)rr * a.H;
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < PW; j++) {
+                const int c = lane * 4 + 256 * j;
+                if (c < a.H) {
+                    const float4 xv4 = *(const float4 *)(xs + c);
+                    acc += wv[j].x * xv4.x + wv[j].y * xv4.y + wv[j].z * xv4.z + wv[j].w * xv4.w;
+                }
+            }
+            for (int c = lane * 4 + 256 * PW; c < a.H; c += 256) {
+                const float4 wq = gld4(wr + c);
+                const float4 xv4 = *(const float4 *)(xs + c);
+                acc += wq.x * xv4.x + wq.y * xv4.y + wq.z * xv4.z + wq.w * xv4.w;
+            }
+            acc = wave_sum(acc);
+            if (lane == 0) tput(a.t_lg + rr, tag, a.bias ? acc + gld(a.bias + rr) : acc);
         }
-        acc = wave_sum(acc);
-        if (lane == 0) tput(a.t_lg + rr, tag, a.bias ? acc + gld(a.bias + rr) : acc);
-    }
+    };
+    if (a.H <= 2048)
+        entry(std::integral_constant<int, 8>{}, std::integral_constant<int, 2>{});
+    else
+        entry(std::integral_constant<int, MB_MAX_H / 256>{}, std::integral_constant<int, MB_MAX_H / (4 * WG)>{});
 
     // ---- limbs of xn; shared-expert gate/up rows need no routing
     auto nothing = [] {};
