@@ -296,9 +296,12 @@ int styx_moe_set_timing(styx_moe *m, int on);
  * counterpart in the reference) from the last token run with timing on:
  * [n_layers][*nwg][16] wall-clock ticks per workgroup -- 0 entry, 1 x
  * normalised, 2 limbs built, 3 logits seen, 4 ranked, 5 gate/up done, 6 g/u
- * seen, 7 swiglu limbs built, 8 down done, 9 partials seen, 10 end (0: no
- * such phase).  *nwg = 0 when the model runs the separate kernels; out may
- * be NULL to query *nwg. */
+ * seen, 7 swiglu limbs built, 8 down done, 9 partials seen, 10 end (in the
+ * workgroups past the reduce ones that form the next layer's q/k/v: 9 its
+ * limbs seen, 10 its rows stored), 11 gate/up loads issued, 12 gate/up
+ * limbs loaded, 13 gate/up rows done, 14 gate/up block entered, 15 its slab
+ * known (0: no such phase).  *nwg = 0 when the model runs the separate
+ * kernels; out may be NULL to query *nwg. */
 int styx_moe_moe_block_trace(styx_moe *m, uint64_t *out, int64_t max_count, int *nwg,
                              double *ticks_per_us);
 /* Stage timing (measurement helper, no counterpart in the reference): the
