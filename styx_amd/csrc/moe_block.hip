@@ -173,44 +173,24 @@ __device__ __forceinline__ bool qkv_rows(const MoeBlockK &a, int r0, int r1, uin
     };
     const int rl = r0 + lm.gid;
     if (rl < r1) issue(rl);
-    // Step 0 runs the row code on the first weights alone (x = 0, nothing
-    // stored) before the limbs are waited for: it fetches that code into the
-    // instruction cache while the wait is still ahead, so the rows formed
-    // after it do not stall on instruction fetches.  Step 1 waits for the
-    // limbs and forms the first rows, each later step issues and forms the
-    // next NR rows of each lane group.  The step count is hidden from the
-    // compiler so that every step runs the same code.
-    const int per_grp = (r1 - r0 + lm.ngrp - 1) / lm.ngrp;
-    const int nstep = 1 + (per_grp + NR - 1) / NR;
+    // the limbs (A | B | C | sx | s16, the layout of xq_at) and the partials
     const int n_ss = (a.H + MB_RR - 1) / MB_RR;
-    UX<T_Q8_0> x[UPL] = {};
-    float scale = 0.0f;
-#pragma clang loop unroll(disable)
-    for (int step = 0; step < nstep; step++) {
-        int p = step;
-        asm volatile("" : "+s"(p));
-        const int r = rl + (p > 1 ? p - 1 : 0) * NR * lm.ngrp;
-        if (p == 1) {
-            // limbs (A | B | C | sx | s16, the layout of xq_at) and the partials
-            const int nw = (int)(xq_bytes(a.H) / 4) + n_ss;
-            for (int c = 0; c < nw; c += MB_QJ * WG)
-                if (!tpoll<MB_QJ>(min(MB_QJ * WG, nw - c), [&](int i) { return a.t_xq + c + i; },
-                                  tag, (float *)xq_lds + c, a))
-                    return false;
-            if (tr && threadIdx.x == 0) tr[9] = wall_clock64();
-            const Xq q = xq_at(xq_lds, a.H);
-            const float *ss = (const float *)(xq_lds + xq_bytes(a.H));
-            float t = 0.0f;
-            for (int i = lm.lane; i < n_ss; i += 64) t += ss[i];
-            t = wave_sum(t);
-            scale = 1.0f / sqrtf(t / (float)a.H + a.eps);
-            // x is rewritten whole: step 0's zeros need no registers across the wait
-#pragma unroll
-            for (int u = 0; u < UPL; u++) x[u] = UX<T_Q8_0>{};
-            XFrom<T_Q8_0, UPL>{q}(x, lu);
-        } else if (p > 1 && r < r1) {
-            issue(r);
-        }
+    const int nw = (int)(xq_bytes(a.H) / 4) + n_ss;
+    for (int c = 0; c < nw; c += MB_QJ * WG)
+        if (!tpoll<MB_QJ>(min(MB_QJ * WG, nw - c), [&](int i) { return a.t_xq + c + i; }, tag,
+                          (float *)xq_lds + c, a))
+            return false;
+    if (tr && threadIdx.x == 0) tr[9] = wall_clock64();
+    const Xq q = xq_at(xq_lds, a.H);
+    const float *ss = (const float *)(xq_lds + xq_bytes(a.H));
+    float t = 0.0f;
+    for (int i = lm.lane; i < n_ss; i += 64) t += ss[i];
+    t = wave_sum(t);
+    const float scale = 1.0f / sqrtf(t / (float)a.H + a.eps);
+    UX<T_Q8_0> x[UPL];
+    XFrom<T_Q8_0, UPL>{q}(x, lu);
+    for (int r = rl; r < r1; r += NR * lm.ngrp) {
+        if (r != rl) issue(r);
 #pragma unroll
         for (int i = 0; i < NR; i++) {
             const int gr = r + i * lm.ngrp;
@@ -219,7 +199,7 @@ __device__ __forceinline__ bool qkv_rows(const MoeBlockK &a, int r0, int r1, uin
             for (int u = 0; u < UPL; u++)
                 if (lu.uv[u] && gr < r1) acc += udot(w[i][u], x[u]);
             acc = group_sum(acc, lm.gl, a.G_q);
-            if (p > 0 && lm.ok && lm.gl == 0 && gr < r1) {
+            if (lm.ok && lm.gl == 0 && gr < r1) {
                 float *y = gr < b1 ? a.qkv_out[0] + gr : gr < b2 ? a.qkv_out[1] + (gr - b1)
                                                                  : a.qkv_out[2] + (gr - b2);
                 gst(y, acc * scale);
