@@ -282,7 +282,8 @@ def config_setup(k: int, layers: int | None):
             cfg = replace(cfg, router_zipf_s=1.1)
             text = ("configs[2]: configs[1] with a Zipf(1.1) router bias, experts in pinned host "
                     "memory, 6 GiB HBM expert budget pinned by expected popularity, cold slabs "
-                    "gathered into the HBM arena in-stream")
+                    "read in place from host memory by the fused MoE block (--arena: gathered "
+                    "into the HBM arena in-stream)")
     elif k == 4:
         cfg = SynthConfig(n_layers=94, n_embd=4096, n_heads=64, n_kv_heads=4, head_dim=128,
                           n_expert=128, n_expert_used=8, n_ff_exp=1536,
@@ -354,6 +355,10 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=None, help="(testing only) fewer layers")
     ap.add_argument("--contexts", default="512,4096,32768",
                     help="config 4: synthetic context lengths to decode after")
+    ap.add_argument("--arena", action="store_true",
+                    help="configs[2]: gather cold slabs into the HBM arena (the MoE block then "
+                         "runs as separate kernels) instead of reading them in place from host "
+                         "memory inside the fused block")
     ap.add_argument("--no-fuse", action="store_true",
                     help="run the MoE block as four kernels instead of the fused launch")
     ap.add_argument("--no-graph", action="store_true",
@@ -408,7 +413,8 @@ def main() -> int:
         m.close()
         t0 = time.perf_counter()
         m = MoeModel.synth(gpu, cfg, n_ctx=max(n_ctx, 512), use_graph=not args.no_graph,
-                           fuse=not args.no_fuse, expert_budget_mb=6144, expert_hist=str(hist), arena=True)
+                           fuse=not args.no_fuse, expert_budget_mb=6144, expert_hist=str(hist),
+                           arena=args.arena)
         log(f"host-pinned model in {time.perf_counter() - t0:.1f}s: "
             f"{m.hp.expert_bytes_hbm / 2**30:.2f} GiB hot in HBM, "
             f"{m.hp.expert_bytes_host / 2**30:.2f} GiB in host memory")
