@@ -83,20 +83,24 @@ def test_config4_long_context_attention(gpu):
     m.close()
 
 
-def test_config3_hist_pinning_identical(gpu):
+@pytest.mark.parametrize("arena", [True, False])
+def test_config3_hist_pinning_identical(gpu, arena):
     """48 layers x 128 experts pinned by the reference's popularity CSV under
     a budget that holds about a third of the slabs; cold experts gathered
-    into the arena: logits bit-identical to all-in-HBM, hot + cold = k per
-    layer, and the pinned set is the one styx_residency_plan computes."""
+    into the arena (separate MoE kernels) or read in place from host memory
+    (the fused block): logits bit-identical to all-in-HBM on the same path,
+    hot + cold = k per layer, and the pinned set is the one
+    styx_residency_plan computes."""
     from styx_amd import MoeModel, SynthConfig
     cfg = SynthConfig(n_layers=48, n_embd=256, n_heads=4, n_kv_heads=2, head_dim=64,
                       n_expert=128, n_expert_used=8, n_ff_exp=256, n_vocab=1024, exp_mix=True,
                       seed=0x30B)
-    # the arena gather runs with the separate MoE kernels: so does the reference
-    ref = MoeModel.synth(gpu, cfg, n_ctx=32, fuse=False)
+    # the arena gather runs with the separate MoE kernels, in-place reads
+    # with the fused block: the all-in-HBM reference runs the same path
+    ref = MoeModel.synth(gpu, cfg, n_ctx=32, fuse=not arena)
     budget_mb = int(ref.hp.slab_bytes * 48 * 128 / 3) >> 20
     m = MoeModel.synth(gpu, cfg, n_ctx=32, expert_budget_mb=budget_mb, expert_hist=str(HIST),
-                       arena=True)
+                       arena=arena)
     assert m.hp.expert_bytes_host > 0 and m.hp.expert_bytes_hbm > 0
     hot = cold = 0
     for t in [3, 900, 45, 1000, 2, 512]:
