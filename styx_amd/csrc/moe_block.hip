@@ -393,7 +393,6 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         // they are in flight
         // rows in batches of two per lane group; each batch's loads are
         // issued together and consumed before the next batch is issued
-        // (nothing pending across iterations: see walk_rows_batched)
         const Mat dm = dslab ? mat_at(dslab, TD, (int64_t)a.H * a.nb_d) : Mat{};
         const LaneMap lm = lane_map(a.G_d);
         const LaneU<UD> lu = lane_units<TD, UD>(lm, a.nb_d, a.G_d);

@@ -141,120 +141,12 @@ __device__ inline void walk_rows(const Xq &q, const Mat &mat, int nb, int G, int
     walk_rows_pf<T, UPL>(mat, nb, G, r_begin, r_end, XFrom<T, UPL>{q}, emit);
 }
 
-// walk_rows_pf split in two, for UPL units per lane: start() issues the
-// first two rows' weights, run() takes the lane's activation limbs and
-// walks every row, so a caller can keep the first weights in flight across
-// other work (a wait on another workgroup's output).  Same arithmetic as
-// walk_rows_pf.
-template <int T, int UPL> struct RowWalk {
-    LaneMap lm;
-    LaneU<UPL> lu;
-    Mat mat;
-    int nb, G, r, r_end;
-    UW<T> w0[UPL], w1[UPL];
-
-    __device__ __forceinline__ void start(const Mat &m, int nb_, int G_, int r_begin, int r_end_)
-    {
-        mat = m;
-        nb = nb_;
-        G = G_;
-        r_end = r_end_;
-        lm = lane_map(G);
-        lu = lane_units<T, UPL>(lm, nb, G);
-        r = r_begin + lm.gid;
-        issue_rows<T, UPL>(w0, w1, lu, mat, nb, r, r + lm.ngrp, r < r_end, r + lm.ngrp < r_end);
-    }
-
-    template <typename Emit> __device__ __forceinline__ void run(const UX<T> (&x)[UPL], Emit emit)
-    {
-        for (; r < r_end; r += 2 * lm.ngrp) {
-            const int r2 = r + lm.ngrp;
-            const bool has2 = r2 < r_end;
-            float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-            for (int u = 0; u < UPL; u++) {
-                if (lu.uv[u]) {
-                    a0 += udot(w0[u], x[u]);
-                    if (has2) a1 += udot(w1[u], x[u]);
-                }
-            }
-            const int rn = r + 2 * lm.ngrp;
-            issue_rows<T, UPL>(w0, w1, lu, mat, nb, rn, rn + lm.ngrp, rn < r_end,
-                               rn + lm.ngrp < r_end);
-            a0 = group_sum(a0, lm.gl, G);
-            a1 = group_sum(a1, lm.gl, G);
-            if (lm.ok && lm.gl == 0) {
-                emit(r, a0);
-                if (has2) emit(r2, a1);
-            }
-        }
-    }
-};
-
-// One unit per lane, NR rows per lane group in flight at once (rows r,
-// r + ngrp, ..., r + (NR-1) ngrp), then the next NR: a block of up to
-// NR * ngrp rows costs one HBM trip.  Same per-row arithmetic as RowWalk.
-template <int T, int NR> struct RowWalkN {
-    LaneMap lm;
-    LaneU<1> lu;
-    Mat mat;
-    int nb, G, r, r_end;
-    UW<T> w[NR];
-
-    __device__ __forceinline__ void issue()
-    {
-#pragma unroll
-        for (int i = 0; i < NR; i++)
-            if (lu.uv[0] && r + i * lm.ngrp < r_end)
-                uw_load<T>(w[i], mat, (int64_t)(r + i * lm.ngrp) * nb + lu.ub[0], lu.us[0]);
-    }
-
-    __device__ __forceinline__ void start(const Mat &m, int nb_, int G_, int r_begin, int r_end_)
-    {
-        mat = m;
-        nb = nb_;
-        G = G_;
-        r_end = r_end_;
-        lm = lane_map(G);
-        lu = lane_units<T, 1>(lm, nb, G);
-        r = r_begin + lm.gid;
-        issue();
-    }
-
-    template <typename Emit> __device__ __forceinline__ void run(const UX<T> (&x)[1], Emit emit)
-    {
-        for (; r < r_end; r += NR * lm.ngrp) {
-            float acc[NR];
-#pragma unroll
-            for (int i = 0; i < NR; i++) {
-                acc[i] = 0.0f;
-                if (lu.uv[0] && r + i * lm.ngrp < r_end) acc[i] += udot(w[i], x[0]);
-            }
-            const int r_here = r;
-            r += NR * lm.ngrp;
-            issue();
-            r = r_here;
-#pragma unroll
-            for (int i = 0; i < NR; i++) {
-                const float v = group_sum(acc[i], lm.gl, G);
-                if (lm.ok && lm.gl == 0 && r + i * lm.ngrp < r_end) emit(r + i * lm.ngrp, v);
-            }
-        }
-    }
-};
-
-// Rows [r_begin, r_end) in batches of NR rows per lane group: every load of
-// a batch is issued, then (first batch only) xload(x, lu) fetches or builds
-// the limbs, then the batch is consumed.  Nothing is left in flight at the
-// end of an iteration, so the compiler's wait-counter pass never has to
-// guess about pending loads at the loop back-edge (the prefetching walkers
-// above leave the next rows' loads pending there, which in a large kernel
-// made it wait for every earlier load before each row's loads).  Same
-// per-row arithmetic as walk_rows_pf.
-// As walk_rows_batched, with the next batch's loads issued before the
-// current batch is consumed (two register sets, alternated in a loop
-// unrolled by two), so that a block of several batches streams its weights
-// in one pass instead of one memory round trip per batch.
+// Rows [r_begin, r_end) in batches of NR per lane group, the next batch's
+// loads issued before the current batch is consumed (two register sets,
+// alternated in a loop unrolled by two), so that a block of several batches
+// streams its weights in one pass instead of one memory round trip per
+// batch; xload(x, lu) fetches or builds the limbs once the first batch is
+// issued.  Same per-row arithmetic as walk_rows_pf.
 template <int T, int UPL, int NR, typename XLoad, typename Emit>
 __device__ __forceinline__ void walk_rows_pipelined(const Mat &mat, int nb, int G, int r_begin,
                                                     int r_end, XLoad xload, Emit emit)
@@ -296,40 +188,6 @@ __device__ __forceinline__ void walk_rows_pipelined(const Mat &mat, int nb, int 
         if (r + step < r_end) issue(wa, r + step);
         consume(wb, r);
         r += step;
-    }
-}
-
-template <int T, int UPL, int NR, typename XLoad, typename Emit>
-__device__ __forceinline__ void walk_rows_batched(const Mat &mat, int nb, int G, int r_begin,
-                                                  int r_end, XLoad xload, Emit emit)
-{
-    const LaneMap lm = lane_map(G);
-    const LaneU<UPL> lu = lane_units<T, UPL>(lm, nb, G);
-    UX<T> x[UPL];
-    bool have_x = false;
-    for (int r = r_begin + lm.gid; r < r_end; r += NR * lm.ngrp) {
-        UW<T> w[NR][UPL];
-#pragma unroll
-        for (int i = 0; i < NR; i++) {
-#pragma unroll
-            for (int u = 0; u < UPL; u++)
-                if (lu.uv[u] && r + i * lm.ngrp < r_end)
-                    uw_load<T>(w[i][u], mat, (int64_t)(r + i * lm.ngrp) * nb + lu.ub[u], lu.us[u]);
-        }
-        if (!have_x) {
-            xload(x, lu);
-            have_x = true;
-        }
-#pragma unroll
-        for (int i = 0; i < NR; i++) {
-            float acc = 0.0f;
-            const bool ok = r + i * lm.ngrp < r_end;
-#pragma unroll
-            for (int u = 0; u < UPL; u++)
-                if (lu.uv[u] && ok) acc += udot(w[i][u], x[u]);
-            acc = group_sum(acc, lm.gl, G);
-            if (lm.ok && lm.gl == 0 && ok) emit(r + i * lm.ngrp, acc);
-        }
     }
 }
 
