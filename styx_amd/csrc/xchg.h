@@ -64,11 +64,13 @@ __device__ __forceinline__ void abort_raise(int *abort)
     __hip_atomic_store((int STYX_GLOBAL *)abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Wait (workgroup-uniform) until the n tagged words addr(0..n) carry `tag`
-// and copy their values to dst[0..n) (LDS); addr(i) may return null for a
-// word that is not needed (dst[i] = 0).  Thread t takes words t + WG j,
-// j < MAXJ (n <= MAXJ * blockDim.x).  The wait is bounded: after max_polls
-// rounds, or once another workgroup has raised the abort flag, it raises
+// Wait until the n tagged words addr(0..n) carry `tag` and copy their values
+// to dst[0..n) (LDS); addr(i) may return null for a word that is not needed
+// (dst[i] = 0).  Thread t takes words t + blockDim.x j, j < MAXJ
+// (n <= MAXJ * blockDim.x).  Each wave polls its own words until they are
+// all in, with no workgroup barrier between rounds; one barrier at the end
+// (workgroup-uniform call).  The wait is bounded: after max_polls rounds, or
+// once another workgroup has raised the abort flag, the workgroup raises
 // the flag and returns false.
 template <int MAXJ, typename Addr>
 __device__ __forceinline__ bool tpoll_wg(int n, Addr addr, uint32_t tag, float *dst, int max_polls,
@@ -86,7 +88,8 @@ __device__ __forceinline__ bool tpoll_wg(int n, Addr addr, uint32_t tag, float *
                 dst[i] = 0.0f;
         }
     }
-    for (int polls = 0;; polls++) {
+    int failed = 0;
+    for (int polls = 0; __any(pend != 0); polls++) {
         uint64_t v[MAXJ];
 #pragma unroll
         for (int j = 0; j < MAXJ; j++)
@@ -98,17 +101,20 @@ __device__ __forceinline__ bool tpoll_wg(int n, Addr addr, uint32_t tag, float *
                 pend &= ~(1u << j);
             }
         }
-        if (!__syncthreads_or(pend != 0)) return true;
-        // the bound is checked every round, another workgroup's abort every
-        // 32nd (a memory round trip of its own)
-        int stop = 0;
-        if (threadIdx.x == 0) stop = polls >= max_polls || ((polls & 31) == 31 && abort_seen(abort));
-        if (__syncthreads_or(stop)) {
-            if (threadIdx.x == 0) abort_raise(abort);
-            return false;
+        if (!__any(pend != 0)) break;
+        // the bound every round, another workgroup's abort every 32nd (a
+        // memory round trip of its own)
+        if (polls >= max_polls || ((polls & 31) == 31 && __any(abort_seen(abort)))) {
+            failed = 1;
+            break;
         }
         __builtin_amdgcn_s_sleep(1);
     }
+    if (__syncthreads_or(failed)) {
+        if (threadIdx.x == 0) abort_raise(abort);
+        return false;
+    }
+    return true;
 }
 
 // Limbs of n values (a multiple of 32) built in LDS at ql, elements
