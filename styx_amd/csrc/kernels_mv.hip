@@ -126,40 +126,48 @@ struct DenseK {
     unsigned long long *amax;  // optional: running argmax word (argmax_key)
 };
 
+// Rows per lane group and batch of the dense walk: two batches are in
+// flight, of more rows where a lane holds fewer units.
+template <int UPL> constexpr int dense_nr() { return UPL <= 2 ? 2 : 1; }
+
 template <int T, int UPL>
 __global__ void __launch_bounds__(WG) k_mv_dense(DenseK a)
 {
     const int r_begin = blockIdx.x * a.rpw, r_end = min(a.total, r_begin + a.rpw);
     unsigned long long best = 0;  // argmax_key of the best row this lane emitted
-    // segments are walked one after another; each starts a fresh row walk
-    int base = 0;
-    for (int s = 0; s < a.nseg; s++) {
-        const int lo = max(r_begin, base), hi = min(r_end, base + a.rows[s]);
-        if (lo < hi) {
-            const Mat mat = mat_at(a.w[s], T, (int64_t)a.rows[s] * a.nb);
-            float *y = a.y[s];
-            const int add = a.add;
-            // the RMSNorm scale is summed while the first weights are in flight
-            float scale = 1.0f;
-            auto xload = [&](UX<T> (&x)[UPL], const LaneU<UPL> &lu) {
-                XFrom<T, UPL>{a.xq}(x, lu);
-                if (a.ns.ss) {
-                    float t = 0.0f;
-                    for (int i = threadIdx.x & 63; i < a.ns.n_ss; i += 64) t += a.ns.ss[i];
-                    t = wave_sum(t);
-                    scale = 1.0f / sqrtf(t / (float)a.ns.n + a.ns.eps);
-                }
-            };
-            const int b0 = base;
-            walk_rows_pf<T, UPL>(mat, a.nb, a.G, lo - base, hi - base, xload, [&](int r, float v) {
-                v *= scale;
-                v = add ? y[r] + v : v;
-                y[r] = v;
-                if (a.amax) best = max(best, argmax_key(v, (uint32_t)(b0 + r)));
-            });
+    // the segments are walked as one stack of rows, so that a workgroup's
+    // rows that span two segments stream in one pass
+    const int b1 = a.rows[0], b2 = b1 + (a.nseg > 1 ? a.rows[1] : 0);
+    const Mat m0 = mat_at(a.w[0], T, (int64_t)a.rows[0] * a.nb);
+    const Mat m1 = a.nseg > 1 ? mat_at(a.w[1], T, (int64_t)a.rows[1] * a.nb) : m0;
+    const Mat m2 = a.nseg > 2 ? mat_at(a.w[2], T, (int64_t)a.rows[2] * a.nb) : m1;
+    const int add = a.add;
+    // the RMSNorm scale is summed while the first weights are in flight
+    float scale = 1.0f;
+    auto xload = [&](UX<T> (&x)[UPL], const LaneU<UPL> &lu) {
+        XFrom<T, UPL>{a.xq}(x, lu);
+        if (a.ns.ss) {
+            float t = 0.0f;
+            for (int i = threadIdx.x & 63; i < a.ns.n_ss; i += 64) t += a.ns.ss[i];
+            t = wave_sum(t);
+            scale = 1.0f / sqrtf(t / (float)a.ns.n + a.ns.eps);
         }
-        base += a.rows[s];
-    }
+        return true;
+    };
+    auto emit = [&](int r, float v) {
+        const int s = (int)(r >= b1) + (int)(r >= b2);
+        float *y = s == 0 ? a.y[0] + r : s == 1 ? a.y[1] + (r - b1) : a.y[2] + (r - b2);
+        v *= scale;
+        v = add ? *y + v : v;
+        *y = v;
+        if (a.amax) best = max(best, argmax_key(v, (uint32_t)r));
+    };
+    if (a.nseg == 1)
+        walk_rows_pipelined<T, UPL, dense_nr<UPL>()>(OneMat{m0, a.nb}, a.nb, a.G, r_begin, r_end,
+                                                      xload, emit);
+    else
+        walk_rows_pipelined<T, UPL, dense_nr<UPL>()>(Mat3(m0, m1, m2, b1, b2, a.nb), a.nb, a.G,
+                                                      r_begin, r_end, xload, emit);
     if (a.amax) {
         // the workgroup's best row joins the launch's running maximum: one
         // relaxed device-scope atomic per workgroup (the reading kernel runs
@@ -358,7 +366,13 @@ __device__ inline void gate_up_body(const GateUpK &a, int m, int s, int32_t *s_i
     const Mat mat = mat_at(slab, T, (int64_t)a.F * a.nb);
     const int r_begin = blockIdx.x * a.rpw, r_end = min(a.F, r_begin + a.rpw);
     float *y = a.gu + ((int64_t)m * a.nslots + s) * a.F;
-    walk_rows<T, UPL>(a.xq, mat, a.nb, a.G, r_begin, r_end, [=](int r, float v) { y[r] = v; });
+    walk_rows_pipelined<T, UPL, dense_nr<UPL>()>(
+        OneMat{mat, a.nb}, a.nb, a.G, r_begin, r_end,
+        [&](UX<T>(&x)[UPL], const LaneU<UPL> &lu) {
+            XFrom<T, UPL>{a.xq}(x, lu);
+            return true;
+        },
+        [=](int r, float v) { y[r] = v; });
 }
 
 template <int TG, int TU, int UPL>
@@ -486,9 +500,10 @@ __global__ void __launch_bounds__(WG) k_down(DownK a)
         xq_build(hs, nullptr, 0.0f, false, a.F, q, red, nullptr);
         __syncthreads();
         XFrom<T, UPL>{q}(x, lu);
+        return true;
     };
-    walk_rows_pf<T, UPL>(mat, a.nb, a.G, r_begin, r_end, build,
-                         [=](int r, float v) { part[r] = v; });
+    walk_rows_pipelined<T, UPL, dense_nr<UPL>()>(OneMat{mat, a.nb}, a.nb, a.G, r_begin, r_end, build,
+                                                  [=](int r, float v) { part[r] = v; });
 }
 
 hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_t *ids,

@@ -111,12 +111,13 @@ __device__ __forceinline__ void gu_rows(const MoeBlockK &a, const uint8_t *slab,
         if (tr && threadIdx.x == 0) tr[i] = wall_clock64();
     };
     walk_rows_pipelined<T, 1, MB_GU_ROWS / 2>(
-        mat_at(slab, T, (int64_t)a.F * a.nb_gu), a.nb_gu, a.G_gu, r0, r1,
+        OneMat{mat_at(slab, T, (int64_t)a.F * a.nb_gu), a.nb_gu}, a.nb_gu, a.G_gu, r0, r1,
         [&](UX<T>(&x)[1], const LaneU<1> &lu) {
             stamp(11);
             between();
             XFrom<T, 1>{xqx}(x, lu);
             stamp(12);
+            return true;
         },
         [&](int r, float v) { tput(y + r, tag, v); });
     stamp(13);
@@ -143,70 +144,45 @@ __device__ __forceinline__ void gu_block(const MoeBlockK &a, int b, bool routed_
 }
 
 // The next layer's q/k/v rows [r0, r1) (of the three matrices stacked):
-// their weights are issued first, then the limbs of x (.) w_next and the
-// x^2 partials are taken from the reduce workgroups' tagged words into LDS,
-// then the rows are formed as k_mv_dense forms them (dot times the RMSNorm
-// scale) in batches of NR rows per lane group, and stored for the next
-// kernel.  Returns false when the wait was abandoned.
+// their weights are issued first (two batches of NR rows per lane group),
+// then the limbs of x (.) w_next and the x^2 partials are taken from the
+// reduce workgroups' tagged words into LDS, then the rows are formed as
+// k_mv_dense forms them (dot times the RMSNorm scale) and stored for the
+// next kernel.  Returns false when the wait was abandoned.
 template <int UPL, int NR>
 __device__ __forceinline__ bool qkv_rows(const MoeBlockK &a, int r0, int r1, uint32_t tag, uint8_t *xq_lds,
                          uint64_t *tr)
 {
     const int b1 = a.qkv_rows[0], b2 = b1 + a.qkv_rows[1];
-    const Mat m0 = mat_at(a.wqkv[0], T_Q8_0, (int64_t)a.qkv_rows[0] * a.nb_q);
-    const Mat m1 = mat_at(a.wqkv[1], T_Q8_0, (int64_t)a.qkv_rows[1] * a.nb_q);
-    const Mat m2 = mat_at(a.wqkv[2], T_Q8_0, (int64_t)a.qkv_rows[2] * a.nb_q);
-    const LaneMap lm = lane_map(a.G_q);
-    const LaneU<UPL> lu = lane_units<T_Q8_0, UPL>(lm, a.nb_q, a.G_q);
-    UW<T_Q8_0> w[NR][UPL];
-    auto issue = [&](int r) {
-#pragma unroll
-        for (int i = 0; i < NR; i++) {
-            const int gr = r + i * lm.ngrp;
-            if (gr >= r1) continue;
-            const Mat &mm = gr < b1 ? m0 : gr < b2 ? m1 : m2;
-            const int lr = gr < b1 ? gr : gr < b2 ? gr - b1 : gr - b2;
-#pragma unroll
-            for (int u = 0; u < UPL; u++)
-                if (lu.uv[u]) uw_load<T_Q8_0>(w[i][u], mm, (int64_t)lr * a.nb_q + lu.ub[u], lu.us[u]);
-        }
-    };
-    const int rl = r0 + lm.gid;
-    if (rl < r1) issue(rl);
-    // the limbs (A | B | C | sx | s16, the layout of xq_at) and the partials
-    const int n_ss = (a.H + MB_RR - 1) / MB_RR;
-    const int nw = (int)(xq_bytes(a.H) / 4) + n_ss;
-    for (int c = 0; c < nw; c += MB_QJ * WG)
-        if (!tpoll<MB_QJ>(min(MB_QJ * WG, nw - c), [&](int i) { return a.t_xq + c + i; }, tag,
-                          (float *)xq_lds + c, a))
-            return false;
-    if (tr && threadIdx.x == 0) tr[9] = wall_clock64();
-    const Xq q = xq_at(xq_lds, a.H);
-    const float *ss = (const float *)(xq_lds + xq_bytes(a.H));
-    float t = 0.0f;
-    for (int i = lm.lane; i < n_ss; i += 64) t += ss[i];
-    t = wave_sum(t);
-    const float scale = 1.0f / sqrtf(t / (float)a.H + a.eps);
-    UX<T_Q8_0> x[UPL];
-    XFrom<T_Q8_0, UPL>{q}(x, lu);
-    for (int r = rl; r < r1; r += NR * lm.ngrp) {
-        if (r != rl) issue(r);
-#pragma unroll
-        for (int i = 0; i < NR; i++) {
-            const int gr = r + i * lm.ngrp;
-            float acc = 0.0f;
-#pragma unroll
-            for (int u = 0; u < UPL; u++)
-                if (lu.uv[u] && gr < r1) acc += udot(w[i][u], x[u]);
-            acc = group_sum(acc, lm.gl, a.G_q);
-            if (lm.ok && lm.gl == 0 && gr < r1) {
-                float *y = gr < b1 ? a.qkv_out[0] + gr : gr < b2 ? a.qkv_out[1] + (gr - b1)
-                                                                 : a.qkv_out[2] + (gr - b2);
-                gst(y, acc * scale);
-            }
-        }
-    }
-    return true;
+    const Mat3 at(mat_at(a.wqkv[0], T_Q8_0, (int64_t)a.qkv_rows[0] * a.nb_q),
+                  mat_at(a.wqkv[1], T_Q8_0, (int64_t)a.qkv_rows[1] * a.nb_q),
+                  mat_at(a.wqkv[2], T_Q8_0, (int64_t)a.qkv_rows[2] * a.nb_q), b1, b2, a.nb_q);
+    float scale = 0.0f;
+    return walk_rows_pipelined<T_Q8_0, UPL, NR>(
+        at, a.nb_q, a.G_q, r0, r1,
+        [&](UX<T_Q8_0>(&x)[UPL], const LaneU<UPL> &lu) {
+            // the limbs (A | B | C | sx | s16, the layout of xq_at) and the
+            // partials
+            const int n_ss = (a.H + MB_RR - 1) / MB_RR;
+            const int nw = (int)(xq_bytes(a.H) / 4) + n_ss;
+            for (int c = 0; c < nw; c += MB_QJ * WG)
+                if (!tpoll<MB_QJ>(min(MB_QJ * WG, nw - c), [&](int i) { return a.t_xq + c + i; }, tag,
+                                  (float *)xq_lds + c, a))
+                    return false;
+            if (tr && threadIdx.x == 0) tr[9] = wall_clock64();
+            const float *ss = (const float *)(xq_lds + xq_bytes(a.H));
+            float t = 0.0f;
+            for (int i = (int)threadIdx.x & 63; i < n_ss; i += 64) t += ss[i];
+            t = wave_sum(t);
+            scale = 1.0f / sqrtf(t / (float)a.H + a.eps);
+            XFrom<T_Q8_0, UPL>{xq_at(xq_lds, a.H)}(x, lu);
+            return true;
+        },
+        [&](int gr, float acc) {
+            float *y = gr < b1 ? a.qkv_out[0] + gr : gr < b2 ? a.qkv_out[1] + (gr - b1)
+                                                             : a.qkv_out[2] + (gr - b2);
+            gst(y, acc * scale);
+        });
 }
 
 // Gate/up types are switched at run time (one routed row block at a time,
@@ -389,48 +365,29 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
                                        tag, gus, a))
             return;
         stamp(6);
-        // the down weights go out first: the SwiGLU limbs are built while
+        // the down weights go out first (two batches of rows per lane
+        // group: of two rows each with one unit per lane, of one row with
+        // more, as the registers allow): the SwiGLU limbs are built while
         // they are in flight
-        // rows in batches of two per lane group; each batch's loads are
-        // issued together and consumed before the next batch is issued
-        const Mat dm = dslab ? mat_at(dslab, TD, (int64_t)a.H * a.nb_d) : Mat{};
-        const LaneMap lm = lane_map(a.G_d);
-        const LaneU<UD> lu = lane_units<TD, UD>(lm, a.nb_d, a.G_d);
-        UW<TD> wd[2][UD];
-        auto issue = [&](int r) {
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int u = 0; u < UD; u++)
-                    if (lu.uv[u] && r + i * lm.ngrp < d1)
-                        uw_load<TD>(wd[i][u], dm, (int64_t)(r + i * lm.ngrp) * a.nb_d + lu.ub[u],
-                                    lu.us[u]);
-        };
-        const int rl = d0 + lm.gid;
-        if (dslab && rl < d1) issue(rl);
-        for (int i = tid; i < F; i += WG) hs[i] = gus[i] / (1.0f + expf(-gus[i])) * gus[F + i];
-        __syncthreads();
-        xq_build(hs, nullptr, 0.0f, false, F, xqh, red, nullptr);
-        __syncthreads();
-        stamp(7);
         uint64_t *part = a.t_part + (size_t)ds * a.H;
+        auto build = [&] {
+            for (int i = tid; i < F; i += WG) hs[i] = gus[i] / (1.0f + expf(-gus[i])) * gus[F + i];
+            __syncthreads();
+            xq_build(hs, nullptr, 0.0f, false, F, xqh, red, nullptr);
+            __syncthreads();
+            stamp(7);
+        };
         if (dslab) {
-            UX<TD> x[UD];
-            XFrom<TD, UD>{xqh}(x, lu);
-            for (int r = rl; r < d1; r += 2 * lm.ngrp) {
-                if (r != rl) issue(r);
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    float acc = 0.0f;
-                    const bool ok = r + i * lm.ngrp < d1;
-#pragma unroll
-                    for (int u = 0; u < UD; u++)
-                        if (lu.uv[u] && ok) acc += udot(wd[i][u], x[u]);
-                    acc = group_sum(acc, lm.gl, a.G_d);
-                    if (lm.ok && lm.gl == 0 && ok) tput(part + r + i * lm.ngrp, tag, acc);
-                }
-            }
+            walk_rows_pipelined<TD, UD, UD == 1 ? 2 : 1>(
+                OneMat{mat_at(dslab, TD, (int64_t)a.H * a.nb_d), a.nb_d}, a.nb_d, a.G_d, d0, d1,
+                [&](UX<TD>(&x)[UD], const LaneU<UD> &lu) {
+                    build();
+                    XFrom<TD, UD>{xqh}(x, lu);
+                    return true;
+                },
+                [&](int r, float v) { tput(part + r, tag, v); });
         } else {
+            build();
             for (int r = d0 + tid; r < d1; r += WG) tput(part + r, tag, 0.0f);
         }
         stamp(8);
@@ -444,8 +401,8 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         __syncthreads();  // the limbs of xn are no longer read (their LDS is reused)
         // rows per lane group in flight: all of them at the shapes served
         // (a single memory round trip), as the registers allow
-        const bool ok = a.UPL_q == 1 ? qkv_rows<1, 4>(a, q0, q1, tag, lds + a.off_xq, tr)
-                                     : qkv_rows<2, 3>(a, q0, q1, tag, lds + a.off_xq, tr);
+        const bool ok = a.UPL_q == 1 ? qkv_rows<1, 3>(a, q0, q1, tag, lds + a.off_xq, tr)
+                                     : qkv_rows<2, 2>(a, q0, q1, tag, lds + a.off_xq, tr);
         if (!ok) return;
         stamp(10);
         flush();

@@ -1,7 +1,7 @@
 // walk.h -- the row walker shared by the matvec kernels: lane groups of G
-// lanes own rows, each lane owns UPL units of a row, two rows are in flight
-// per lane group, and the first rows' weights are issued before the
-// activation limbs are loaded or built.
+// lanes own rows, each lane owns UPL units of a row, two batches of rows are
+// in flight per lane group, and the first two batches' weights are issued
+// before the activation limbs are loaded or built.
 #pragma once
 
 #include "kernels.h"
@@ -69,60 +69,6 @@ __device__ __forceinline__ LaneU<UPL> lane_units(const LaneMap &lm, int nb, int 
     return lu;
 }
 
-template <int T, int UPL>
-__device__ __forceinline__ void issue_rows(UW<T> (&w0)[UPL], UW<T> (&w1)[UPL], const LaneU<UPL> &lu,
-                                           const Mat &mat, int nb, int r, int r2, bool has1,
-                                           bool has2)
-{
-#pragma unroll
-    for (int u = 0; u < UPL; u++) {
-        if (lu.uv[u]) {
-            if (has1) uw_load<T>(w0[u], mat, (int64_t)r * nb + lu.ub[u], lu.us[u]);
-            if (has2) uw_load<T>(w1[u], mat, (int64_t)r2 * nb + lu.ub[u], lu.us[u]);
-        }
-    }
-}
-
-// Row walker: the calling workgroup's lane groups cover rows
-// [r_begin, r_end) two at a time; the result of row r goes to emit(r, v) on
-// the group leader.  The first rows' weight loads are issued before
-// xload(x, lu) fetches (or builds) the lane's activation limbs, so the
-// activation trip overlaps the HBM latency; each next pair of rows is
-// issued as soon as the previous one is consumed.
-template <int T, int UPL, typename XLoad, typename Emit>
-__device__ inline void walk_rows_pf(const Mat &mat, int nb, int G, int r_begin, int r_end,
-                                    XLoad xload, Emit emit)
-{
-    const LaneMap lm = lane_map(G);
-    const LaneU<UPL> lu = lane_units<T, UPL>(lm, nb, G);
-    int r = r_begin + lm.gid;
-    UW<T> w0[UPL], w1[UPL];
-    issue_rows<T, UPL>(w0, w1, lu, mat, nb, r, r + lm.ngrp, r < r_end, r + lm.ngrp < r_end);
-    UX<T> x[UPL];
-    xload(x, lu);
-    for (; r < r_end; r += 2 * lm.ngrp) {
-        const int r2 = r + lm.ngrp;
-        const bool has2 = r2 < r_end;
-        float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-        for (int u = 0; u < UPL; u++) {
-            if (lu.uv[u]) {
-                a0 += udot(w0[u], x[u]);
-                if (has2) a1 += udot(w1[u], x[u]);
-            }
-        }
-        const int rn = r + 2 * lm.ngrp;
-        issue_rows<T, UPL>(w0, w1, lu, mat, nb, rn, rn + lm.ngrp, rn < r_end,
-                           rn + lm.ngrp < r_end);
-        a0 = group_sum(a0, lm.gl, G);
-        a1 = group_sum(a1, lm.gl, G);
-        if (lm.ok && lm.gl == 0) {
-            emit(r, a0);
-            if (has2) emit(r2, a1);
-        }
-    }
-}
-
 // Limbs of the lane's units from an Xq vector (global memory or LDS).
 template <int T, int UPL> struct XFrom {
     Xq q;
@@ -134,61 +80,139 @@ template <int T, int UPL> struct XFrom {
     }
 };
 
-template <int T, int UPL, typename Emit>
-__device__ inline void walk_rows(const Xq &q, const Mat &mat, int nb, int G, int r_begin,
-                                 int r_end, Emit emit)
-{
-    walk_rows_pf<T, UPL>(mat, nb, G, r_begin, r_end, XFrom<T, UPL>{q}, emit);
-}
+// Where a walked row lives: at(row, mm, b0) gives the matrix and the block
+// index of the row's first unit.  OneMat: rows of one matrix.
+struct OneMat {
+    Mat m;
+    int nb;
+    __device__ __forceinline__ void operator()(int row, Mat &mm, int64_t &b0) const
+    {
+        mm = m;
+        b0 = (int64_t)row * nb;
+    }
+};
 
-// Rows [r_begin, r_end) in batches of NR per lane group, the next batch's
-// loads issued before the current batch is consumed (two register sets,
-// alternated in a loop unrolled by two), so that a block of several batches
-// streams its weights in one pass instead of one memory round trip per
-// batch; xload(x, lu) fetches or builds the limbs once the first batch is
-// issued.  Same per-row arithmetic as walk_rows_pf.
-template <int T, int UPL, int NR, typename XLoad, typename Emit>
-__device__ __forceinline__ void walk_rows_pipelined(const Mat &mat, int nb, int G, int r_begin,
+// Rows of up to three matrices stacked: rows [0, b1) of m0, [b1, b2) of
+// m1, the rest of m2.  The regions of m1 and m2 are kept as byte offsets
+// from the previous matrix's: a select among the matrices compiles to a
+// table in scratch memory, this to adds.
+struct Mat3 {
+    uint64_t base[4], d1[4], d2[4];
+    int b1, b2, nb;
+    __device__ __forceinline__ Mat3(const Mat &m0, const Mat &m1, const Mat &m2, int b1_, int b2_,
+                                    int nb_)
+        : b1(b1_), b2(b2_), nb(nb_)
+    {
+        const Mat *m[3] = {&m0, &m1, &m2};
+        uint64_t r[3][4];
+#pragma unroll
+        for (int i = 0; i < 3; i++) {
+            r[i][0] = (uint64_t)(uintptr_t)m[i]->r0;
+            r[i][1] = (uint64_t)(uintptr_t)m[i]->r1;
+            r[i][2] = (uint64_t)(uintptr_t)m[i]->r2;
+            r[i][3] = (uint64_t)(uintptr_t)m[i]->r3;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            base[j] = r[0][j];
+            d1[j] = r[1][j] - r[0][j];
+            d2[j] = r[2][j] - r[1][j];
+        }
+    }
+    __device__ __forceinline__ void operator()(int row, Mat &mm, int64_t &b0) const
+    {
+        const uint64_t p1 = row >= b1, p2 = row >= b2;
+        uint64_t r[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) r[j] = base[j] + p1 * d1[j] + p2 * d2[j];
+        mm.r0 = (const uint8_t STYX_GLOBAL *)(uintptr_t)r[0];
+        mm.r1 = (const uint8_t STYX_GLOBAL *)(uintptr_t)r[1];
+        mm.r2 = (const uint8_t STYX_GLOBAL *)(uintptr_t)r[2];
+        mm.r3 = (const uint8_t STYX_GLOBAL *)(uintptr_t)r[3];
+        b0 = (int64_t)(row - (int)p1 * b1 - (int)p2 * (b2 - b1)) * nb;
+    }
+};
+
+// Rows [r_begin, r_end) in batches of NR per lane group, with two batches
+// in flight: the first two are issued before xload(x, lu) fetches or builds
+// the limbs (and may wait for them: it returns false to abandon the walk,
+// and the walker then returns false), and each later batch is issued as
+// soon as the one two before it is consumed (two register sets, alternated
+// in a loop unrolled by two).  A block of several batches thus streams its
+// weights in one pass instead of one memory round trip per batch.  A row's
+// result is the group sum of its lanes' unit dots.
+//
+// Every batch issues the same loads on every path: the batch count is the
+// workgroup's (that of the lane group with the most rows), and a row past
+// the block's end, or a lane without a unit, loads the first unit of the
+// block's last row instead and discards it.  The compiler then knows at each consume that
+// exactly the other batch's loads may still be in flight and waits for
+// this batch's alone; with conditional issues it has to wait for all of
+// them, and the walk degrades to one round trip per batch.
+template <int T, int UPL, int NR, typename RowAt, typename XLoad, typename Emit>
+__device__ __forceinline__ bool walk_rows_pipelined(RowAt at, int nb, int G, int r_begin,
                                                     int r_end, XLoad xload, Emit emit)
 {
     const LaneMap lm = lane_map(G);
     const LaneU<UPL> lu = lane_units<T, UPL>(lm, nb, G);
     const int step = NR * lm.ngrp;
-    auto issue = [&](UW<T>(&w)[NR][UPL], int r) {
+    const int nbat = (r_end - r_begin + step - 1) / step;
+    const int r0 = r_begin + lm.gid;
+    auto issue = [&](UW<T>(&w)[NR][UPL], int b) {
 #pragma unroll
         for (int i = 0; i < NR; i++) {
+            const int row = r0 + b * step + i * lm.ngrp;
+            Mat mm;
+            int64_t b0;
+            at(min(row, r_end - 1), mm, b0);
 #pragma unroll
-            for (int u = 0; u < UPL; u++)
-                if (lu.uv[u] && r + i * lm.ngrp < r_end)
-                    uw_load<T>(w[i][u], mat, (int64_t)(r + i * lm.ngrp) * nb + lu.ub[u], lu.us[u]);
+            for (int u = 0; u < UPL; u++) {
+                const bool ok = lu.uv[u] && row < r_end;
+                uw_load<T>(w[i][u], mm, ok ? b0 + lu.ub[u] : b0, ok ? lu.us[u] : 0);
+            }
         }
     };
     UX<T> x[UPL];
-    auto consume = [&](const UW<T>(&w)[NR][UPL], int r) {
+    auto consume = [&](const UW<T>(&w)[NR][UPL], int b) {
 #pragma unroll
         for (int i = 0; i < NR; i++) {
+            const int row = r0 + b * step + i * lm.ngrp;
+            const bool ok = row < r_end;
             float acc = 0.0f;
-            const bool ok = r + i * lm.ngrp < r_end;
 #pragma unroll
             for (int u = 0; u < UPL; u++)
                 if (lu.uv[u] && ok) acc += udot(w[i][u], x[u]);
             acc = group_sum(acc, lm.gl, G);
-            if (lm.ok && lm.gl == 0 && ok) emit(r + i * lm.ngrp, acc);
+            if (lm.ok && lm.gl == 0 && ok) emit(row, acc);
         }
     };
     UW<T> wa[NR][UPL], wb[NR][UPL];
-    int r = r_begin + lm.gid;
-    if (r < r_end) issue(wa, r);
-    xload(x, lu);
-    while (r < r_end) {
-        if (r + step < r_end) issue(wb, r + step);
-        consume(wa, r);
-        r += step;
-        if (r >= r_end) break;
-        if (r + step < r_end) issue(wa, r + step);
-        consume(wb, r);
-        r += step;
+    if (nbat <= 1) {
+        if (nbat == 1) issue(wa, 0);
+        if (!xload(x, lu)) return false;
+        if (nbat == 1) consume(wa, 0);
+        return true;
     }
+    issue(wa, 0);
+    issue(wb, 1);
+    if (!xload(x, lu)) return false;
+    int b = 0;
+    for (; b + 3 < nbat; b += 2) {
+        consume(wa, b);
+        issue(wa, b + 2);
+        consume(wb, b + 1);
+        issue(wb, b + 3);
+    }
+    if (b + 2 < nbat) {
+        consume(wa, b);
+        issue(wa, b + 2);
+        consume(wb, b + 1);
+        consume(wa, b + 2);
+    } else {
+        consume(wa, b);
+        consume(wb, b + 1);
+    }
+    return true;
 }
 
 }  // namespace styx
