@@ -361,6 +361,9 @@ def main() -> int:
                          "memory inside the fused block")
     ap.add_argument("--no-fuse", action="store_true",
                     help="run the MoE block as four kernels instead of the fused launch")
+    ap.add_argument("--no-fold-qkv", action="store_true",
+                    help="launch each layer's q/k/v matvec separately instead of folding it into "
+                         "the previous layer's fused MoE block")
     ap.add_argument("--no-graph", action="store_true",
                     help="enqueue kernels one by one instead of replaying a HIP graph per token")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -398,10 +401,10 @@ def main() -> int:
     if args.config == 4:
         ctxs = [int(c) for c in args.contexts.split(",") if c]
         m = MoeModel.synth(gpu, cfg, n_ctx=max(ctxs) + n_ctx, use_graph=not args.no_graph,
-                           fuse=not args.no_fuse)
+                           fuse=not args.no_fuse, fold_qkv=not args.no_fold_qkv)
     else:
         m = MoeModel.synth(gpu, cfg, n_ctx=max(n_ctx, 512), use_graph=not args.no_graph,
-                           fuse=not args.no_fuse)
+                           fuse=not args.no_fuse, fold_qkv=not args.no_fold_qkv)
     log(f"built synthetic model in {time.perf_counter() - t0:.1f}s on {gpu.name}: "
         f"{m.hp.expert_bytes_hbm / 2**30:.2f} GiB experts in HBM, slab {m.slab_bytes} B")
 
@@ -413,7 +416,8 @@ def main() -> int:
         m.close()
         t0 = time.perf_counter()
         m = MoeModel.synth(gpu, cfg, n_ctx=max(n_ctx, 512), use_graph=not args.no_graph,
-                           fuse=not args.no_fuse, expert_budget_mb=6144, expert_hist=str(hist),
+                           fuse=not args.no_fuse, fold_qkv=not args.no_fold_qkv,
+                           expert_budget_mb=6144, expert_hist=str(hist),
                            arena=args.arena)
         log(f"host-pinned model in {time.perf_counter() - t0:.1f}s: "
             f"{m.hp.expert_bytes_hbm / 2**30:.2f} GiB hot in HBM, "

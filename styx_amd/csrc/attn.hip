@@ -24,6 +24,7 @@
 #include "xchg.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace styx {
 
@@ -169,71 +170,81 @@ __device__ void attn_combine_tail(const AttnArgs &a, int c, int kvh, int n_activ
 {
     constexpr int HD = 64 * EPL;
     const int gqa = a.nh / a.nkv, ps = HD + 2;
-    if (c >= gqa) return;
+    // this workgroup's heads: a contiguous run, so that each round of up to
+    // four heads is one stretch of the output and of its limbs
+    const int hpm = (gqa + n_active - 1) / n_active;
+    const int g_begin = c * hpm, g_end = min(gqa, g_begin + hpm);
+    if (g_begin >= gqa) return;
     __shared__ float red[16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float *go = sm, *gm = go + AT_WAVES * HD, *gl = gm + AT_WAVES, *xo = gl + AT_WAVES;
     const int64_t cs = (int64_t)gqa * ps;  // stride between chunks
-    for (int g = c; g < gqa; g += n_active) {
-        const uint64_t *pk = a.t_part + (int64_t)kvh * a.max_chunks * cs + (int64_t)g * ps;
+    for (int r0 = g_begin; r0 < g_end; r0 += AT_WAVES) {
+        // the round's heads are merged at once: wph waves per head, each
+        // taking every wph-th chunk
+        const int nr = min(AT_WAVES, g_end - r0), wph = AT_WAVES / nr;
+        const int hs = wave / wph, sw = wave - hs * wph;
         float m = -INFINITY, l = 0.0f, o[EPL];
 #pragma unroll
         for (int e = 0; e < EPL; e++) o[e] = 0.0f;
-        for (int c0 = wave; c0 < n_active; c0 += AT_WAVES * CT_BATCH) {
-            float mc[CT_BATCH], lc[CT_BATCH], oc[CT_BATCH][EPL];
-            uint32_t pend = 0;
-#pragma unroll
-            for (int b = 0; b < CT_BATCH; b++) {
-                mc[b] = -INFINITY;
-                lc[b] = 0.0f;
-#pragma unroll
-                for (int e = 0; e < EPL; e++) oc[b][e] = 0.0f;
-                if (c0 + AT_WAVES * b < n_active) pend |= 1u << b;
-            }
-            for (int polls = 0; __any(pend != 0); polls++) {
+        if (hs < nr) {
+            const uint64_t *pk = a.t_part + (int64_t)kvh * a.max_chunks * cs + (int64_t)(r0 + hs) * ps;
+            for (int c0 = sw; c0 < n_active; c0 += wph * CT_BATCH) {
+                float mc[CT_BATCH], lc[CT_BATCH], oc[CT_BATCH][EPL];
+                uint32_t pend = 0;
 #pragma unroll
                 for (int b = 0; b < CT_BATCH; b++) {
-                    if (!((pend >> b) & 1u)) continue;
-                    const uint64_t *pp = pk + (int64_t)(c0 + AT_WAVES * b) * cs;
-                    const uint64_t wm = tget(pp + HD), wl = tget(pp + HD + 1);
-                    uint64_t wo[EPL];
+                    mc[b] = -INFINITY;
+                    lc[b] = 0.0f;
 #pragma unroll
-                    for (int e = 0; e < EPL; e++) wo[e] = tget(pp + lane * EPL + e);
-                    bool ok = tvalid(wm, tag) && tvalid(wl, tag);
+                    for (int e = 0; e < EPL; e++) oc[b][e] = 0.0f;
+                    if (c0 + wph * b < n_active) pend |= 1u << b;
+                }
+                for (int polls = 0; __any(pend != 0); polls++) {
 #pragma unroll
-                    for (int e = 0; e < EPL; e++) ok = ok && tvalid(wo[e], tag);
-                    if (ok) {
-                        mc[b] = tval(wm);
-                        lc[b] = tval(wl);
+                    for (int b = 0; b < CT_BATCH; b++) {
+                        if (!((pend >> b) & 1u)) continue;
+                        const uint64_t *pp = pk + (int64_t)(c0 + wph * b) * cs;
+                        const uint64_t wm = tget(pp + HD), wl = tget(pp + HD + 1);
+                        uint64_t wo[EPL];
 #pragma unroll
-                        for (int e = 0; e < EPL; e++) oc[b][e] = tval(wo[e]);
-                        pend &= ~(1u << b);
+                        for (int e = 0; e < EPL; e++) wo[e] = tget(pp + lane * EPL + e);
+                        bool ok = tvalid(wm, tag) && tvalid(wl, tag);
+#pragma unroll
+                        for (int e = 0; e < EPL; e++) ok = ok && tvalid(wo[e], tag);
+                        if (ok) {
+                            mc[b] = tval(wm);
+                            lc[b] = tval(wl);
+#pragma unroll
+                            for (int e = 0; e < EPL; e++) oc[b][e] = tval(wo[e]);
+                            pend &= ~(1u << b);
+                        }
                     }
+                    if (!__any(pend != 0)) break;
+                    if (polls >= a.max_polls || ((polls & 31) == 31 && abort_seen(a.abort))) {
+                        if (lane == 0) abort_raise(a.abort);
+                        // missing chunks count as empty: the result is wrong
+                        // and the launch reports it through the abort flag
+#pragma unroll
+                        for (int b = 0; b < CT_BATCH; b++)
+                            if ((pend >> b) & 1u) mc[b] = -INFINITY;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
                 }
-                if (!__any(pend != 0)) break;
-                if (polls >= a.max_polls || ((polls & 31) == 31 && abort_seen(a.abort))) {
-                    if (lane == 0) abort_raise(a.abort);
-                    // missing chunks count as empty: the result is wrong and
-                    // the launch reports it through the abort flag
 #pragma unroll
-                    for (int b = 0; b < CT_BATCH; b++)
-                        if ((pend >> b) & 1u) mc[b] = -INFINITY;
-                    break;
+                for (int b = 0; b < CT_BATCH; b++) {
+                    if (mc[b] == -INFINITY) continue;
+                    const float mn = fmaxf(m, mc[b]);
+                    const float fa = expf(m - mn), fb = expf(mc[b] - mn);
+                    l = l * fa + lc[b] * fb;
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) o[e] = o[e] * fa + oc[b][e] * fb;
+                    m = mn;
                 }
-                __builtin_amdgcn_s_sleep(1);
-            }
-#pragma unroll
-            for (int b = 0; b < CT_BATCH; b++) {
-                if (mc[b] == -INFINITY) continue;
-                const float mn = fmaxf(m, mc[b]);
-                const float fa = expf(m - mn), fb = expf(mc[b] - mn);
-                l = l * fa + lc[b] * fb;
-#pragma unroll
-                for (int e = 0; e < EPL; e++) o[e] = o[e] * fa + oc[b][e] * fb;
-                m = mn;
             }
         }
-        __syncthreads();  // sm is free (the attention phase is over, or the previous head)
+        __syncthreads();  // sm is free (the attention phase is over, or the previous round)
 #pragma unroll
         for (int e = 0; e < EPL; e++) go[wave * HD + lane * EPL + e] = o[e];
         if (lane == 0) {
@@ -241,25 +252,39 @@ __device__ void attn_combine_tail(const AttnArgs &a, int c, int kvh, int n_activ
             gl[wave] = l;
         }
         __syncthreads();
-        const int h = kvh * gqa + g;
-        if ((int)threadIdx.x < HD) {
-            const int i = threadIdx.x;
-            float M = gm[0];
-            for (int q = 1; q < AT_WAVES; q++) M = fmaxf(M, gm[q]);
-            float L = 0.0f, O = 0.0f;
-            for (int q = 0; q < AT_WAVES; q++) {
-                const float f = gm[q] == -INFINITY ? 0.0f : expf(gm[q] - M);
-                L += gl[q] * f;
-                O += go[q * HD + i] * f;
+        // the waves of each head merged, the outputs written, their limbs
+        // built (the common one- and two-head rounds with constant bounds)
+        auto finish = [&](auto wph_c, auto nr_c) {
+            constexpr int WPH = decltype(wph_c)::value, NR = decltype(nr_c)::value;
+            const int n = NR ? NR * HD : nr * HD;
+            for (int t = threadIdx.x; t < n; t += AT_WG) {
+                const int hl = t / HD, i = t - hl * HD, w0 = hl * WPH;
+                float M = gm[w0];
+#pragma unroll
+                for (int q = 1; q < WPH; q++) M = fmaxf(M, gm[w0 + q]);
+                float L = 0.0f, O = 0.0f;
+#pragma unroll
+                for (int q = 0; q < WPH; q++) {
+                    const float f = gm[w0 + q] == -INFINITY ? 0.0f : expf(gm[w0 + q] - M);
+                    L += gl[w0 + q] * f;
+                    O += go[(w0 + q) * HD + i] * f;
+                }
+                const float v = O / L;
+                gst(a.out + (int64_t)(kvh * gqa + r0 + hl) * HD + i, v);
+                xo[t] = v;
             }
-            const float v = O / L;
-            gst(a.out + (int64_t)h * HD + i, v);
-            xo[i] = v;
-        }
-        if (a.xq.A) {
-            __syncthreads();
-            xq_build(xo, nullptr, 0.0f, false, HD, xq_shift(a.xq, h * HD), red, nullptr);
-        }
+            if (a.xq.A) {
+                __syncthreads();
+                xq_build(xo, nullptr, 0.0f, false, n, xq_shift(a.xq, (kvh * gqa + r0) * HD), red,
+                         nullptr);
+            }
+        };
+        if (wph == AT_WAVES)
+            finish(std::integral_constant<int, AT_WAVES>{}, std::integral_constant<int, 1>{});
+        else if (wph == AT_WAVES / 2)
+            finish(std::integral_constant<int, AT_WAVES / 2>{}, std::integral_constant<int, 2>{});
+        else
+            finish(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
     }
 }
 
@@ -523,24 +548,25 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
 // l holds S[4(l/16)+r][l%16]); runs the online softmax with reductions over
 // the 16 lanes of a row; moves P through LDS into the A-operand layout; and
 // accumulates O[h][d] += sum_t P[h][t] V[t][d] with 32 more MFMAs.  The
-// k dimension of Q.K is split as d = 32 (l/16) + m and the output columns
-// as d = 8 (l%16) + b, so every lane's K and V operands are contiguous
-// 32-byte runs.  Arithmetic stays f32 throughout.
+// k dimension of Q.K is split as d = kcol(l/16, m) and the output columns
+// as d = vcol(l%16, b) (below), so that each 16-byte load of a wave reads
+// whole 64-byte runs of a K or V row (consecutive lanes, consecutive 16
+// bytes).  Arithmetic stays f32 throughout.
 // Lane layout of the builtin (checked on gfx950): lane l supplies
 // A[l%16][l/16] and B[l/16][l%16], and receives D[4(l/16)+r][l%16], r < 4.
 typedef float f4v __attribute__((ext_vector_type(4)));
 constexpr int MH = 16;      // padded heads per kv head
 constexpr int MHD = 128;    // head_dim of this variant
 constexpr int MNB = MHD / 16;
+// Column of Q and K that lane group g supplies at k-step m (m < 32), and
+// the output column of lane r's accumulator block b (b < 8).
+__device__ __forceinline__ constexpr int kcol(int g, int m) { return 16 * (m >> 2) + 4 * g + (m & 3); }
+__device__ __forceinline__ constexpr int vcol(int r, int b) { return 64 * (b >> 2) + 4 * r + (b & 3); }
 
 __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
 {
     const int c = blockIdx.x, kvh = blockIdx.y;
     const unsigned long long ticket = attn_ticket(a);  // also drawn by chunks past the context
-    const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
-    const int t0 = c * chunk;
-    if (t0 >= n_t) return;
-    const int t1 = min(n_t, t0 + chunk);
     const int gqa = a.nh / a.nkv, kv_dim = a.nkv * MHD;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;  // row-lane, k-group
@@ -554,48 +580,39 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     float *mm = mo + AT_WAVES * MH * MHD;
     float *ml = mm + AT_WAVES * MH;
 
-    // prologue: the q heads (one wave per head, round robin) and, in the
-    // chunk holding pos, the new k/v head, normalised and rotated into LDS
-    const bool owns_pos = t1 == n_t;
-    const double2 *csrow = a.rope + (int64_t)pos * (MHD / 2);
-    for (int i = wave; i < MH + (owns_pos ? 1 : 0); i += AT_WAVES) {
-        if (i < gqa) {
-            HeadIn<1> hin;
-            double2 cs[1];
-            cs_load<1>(cs, csrow, MHD);
-            head_load<1>(hin, a.q + (int64_t)(kvh * gqa + i) * MHD, a.q_norm, MHD);
-            head_finish<1>(hin, cs, a.q_norm != nullptr, a.eps, MHD, qs + i * MHD);
-        } else if (i < MH) {
-            for (int e = lane; e < MHD; e += 64) qs[i * MHD + e] = 0.0f;
-        } else {
-            HeadIn<1> hin;
-            double2 cs[1];
-            cs_load<1>(cs, csrow, MHD);
-            head_load<1>(hin, a.k + (int64_t)kvh * MHD, a.k_norm, MHD);
-            head_finish<1>(hin, cs, a.k_norm != nullptr, a.eps, MHD, knew);
-            for (int e = lane; e < MHD; e += 64) vnew[e] = a.v[(int64_t)kvh * MHD + e];
-        }
-    }
-    __syncthreads();
-    if (owns_pos && wave == 0) {
-        const int64_t po = kv_off(a, pos, kvh, kv_dim);
-        for (int e = lane; e < MHD; e += 64) {
-            a.kpool[po + e] = knew[e];
-            a.vpool[po + e] = vnew[e];
-        }
-    }
-    // this lane's Q operand: Q[lr][32 lg + m], m < 32
-    float qv[MHD / 4];
+    // loads that do not depend on the position go out first: this wave's q
+    // heads (heads wave + 4 j) and norm weights, the new k/v head (wave 0),
+    // and the page-table entry of this lane's first token for the minimum
+    // chunk size (the chunk size of every short context)
+    constexpr int HPW = MH / AT_WAVES;
+    HeadIn<1> hq[HPW], hk;
 #pragma unroll
-    for (int m = 0; m < MHD / 4; m += 4) {
-        const float4 v = *(const float4 *)(qs + lr * MHD + 32 * lg + m);
-        qv[m] = v.x; qv[m + 1] = v.y; qv[m + 2] = v.z; qv[m + 3] = v.w;
+    for (int j = 0; j < HPW; j++) {
+        const int i = wave + AT_WAVES * j;
+        if (i < gqa) head_load<1>(hq[j], a.q + (int64_t)(kvh * gqa + i) * MHD, a.q_norm, MHD);
     }
+    float vn[MHD / 64];
+    if (wave == 0) {
+        head_load<1>(hk, a.k + (int64_t)kvh * MHD, a.k_norm, MHD);
+#pragma unroll
+        for (int e = 0; e < MHD / 64; e++) vn[e] = a.v[(int64_t)kvh * MHD + lane + 64 * e];
+    }
+    const int t_min = c * a.chunk + wave * 16 + lr, pg_min = t_min / a.page_tokens;
+    const bool spec = pg_min < a.page_table_len;
+    const int32_t pe_min = spec ? a.page_table[pg_min] : 0;
+
+    const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
+    const int t0 = c * chunk;
+    if (t0 >= n_t) return;
+    const int t1 = min(n_t, t0 + chunk);
+    const bool owns_pos = t1 == n_t;
+    double2 cs[1];
+    cs_load<1>(cs, a.rope + (int64_t)pos * (MHD / 2), MHD);
 
     const int step = AT_WAVES * 16;
     int tb = t0 + wave * 16;
-    float kv[MHD / 4];     // K[tb + lr][32 lg + m]
-    float vvr[4][MNB];     // V[tb + 4q + lg][8 lr + b]
+    float kv[MHD / 4];     // K[tb + lr][kcol(lg, m)]
+    float vvr[4][MNB];     // V[tb + 4q + lg][vcol(lr, b)]
     auto row_of = [&](int tbase) -> int64_t {
         return tbase + lr < t1 ? kv_off(a, tbase + lr, kvh, kv_dim) : 0;
     };
@@ -603,7 +620,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
         const bool ok = tbase + lr < t1;
 #pragma unroll
         for (int m = 0; m < MHD / 4; m += 4) {
-            const float4 v = ok ? *(const float4 *)(a.kpool + row + 32 * lg + m)
+            const float4 v = ok ? *(const float4 *)(a.kpool + row + kcol(lg, m))
                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             kv[m] = v.x; kv[m + 1] = v.y; kv[m + 2] = v.z; kv[m + 3] = v.w;
         }
@@ -616,18 +633,56 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
             const bool ok = tbase + t < t1;
 #pragma unroll
             for (int b = 0; b < MNB; b += 4) {
-                const float4 v = ok ? *(const float4 *)(a.vpool + rq + 8 * lr + b)
+                const float4 v = ok ? *(const float4 *)(a.vpool + rq + vcol(lr, b))
                                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 vvr[q][b] = v.x; vvr[q][b + 1] = v.y; vvr[q][b + 2] = v.z; vvr[q][b + 3] = v.w;
             }
         }
     };
+    // the first tile's loads, from the early page entry when the chunk has
+    // its minimum size (then tb + lr == t_min)
     if (tb < t1) {
-        const int64_t row = row_of(tb);
+        const int64_t row =
+            spec && chunk == a.chunk
+                ? (tb + lr < t1 ? ((int64_t)pe_min * a.page_tokens + t_min % a.page_tokens) * kv_dim +
+                                      (int64_t)kvh * MHD
+                                : 0)
+                : row_of(tb);
         load_k(row, tb);
         load_v(row, tb);
     }
     int64_t row_n = row_of(tb + step);
+
+    // the q heads and, in the chunk holding pos, the new k/v head,
+    // normalised and rotated into LDS while the first tile is in flight
+#pragma unroll
+    for (int j = 0; j < HPW; j++) {
+        const int i = wave + AT_WAVES * j;
+        if (i < gqa)
+            head_finish<1>(hq[j], cs, a.q_norm != nullptr, a.eps, MHD, qs + i * MHD);
+        else
+            for (int e = lane; e < MHD; e += 64) qs[i * MHD + e] = 0.0f;
+    }
+    if (owns_pos && wave == 0) {
+        head_finish<1>(hk, cs, a.k_norm != nullptr, a.eps, MHD, knew);
+#pragma unroll
+        for (int e = 0; e < MHD / 64; e++) vnew[lane + 64 * e] = vn[e];
+    }
+    __syncthreads();
+    if (owns_pos && wave == 0) {
+        const int64_t po = kv_off(a, pos, kvh, kv_dim);
+        for (int e = lane; e < MHD; e += 64) {
+            a.kpool[po + e] = knew[e];
+            a.vpool[po + e] = vnew[e];
+        }
+    }
+    // this lane's Q operand: Q[lr][kcol(lg, m)], m < 32
+    float qv[MHD / 4];
+#pragma unroll
+    for (int m = 0; m < MHD / 4; m += 4) {
+        const float4 v = *(const float4 *)(qs + lr * MHD + kcol(lg, m));
+        qv[m] = v.x; qv[m + 1] = v.y; qv[m + 2] = v.z; qv[m + 3] = v.w;
+    }
 
     float m_run[4], l_run[4];
     f4v o[MNB];
@@ -646,14 +701,14 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
         // wave 0 of this workgroup, possibly after these loads)
         if (tb + lr == pos) {
 #pragma unroll
-            for (int m = 0; m < MHD / 4; m++) kv[m] = knew[32 * lg + m];
+            for (int m = 0; m < MHD / 4; m++) kv[m] = knew[kcol(lg, m)];
         }
         if (pos >= tb && pos < tb + 16) {
 #pragma unroll
             for (int q = 0; q < 4; q++)
                 if (tb + 4 * q + lg == pos) {
 #pragma unroll
-                    for (int b = 0; b < MNB; b++) vvr[q][b] = vnew[8 * lr + b];
+                    for (int b = 0; b < MNB; b++) vvr[q][b] = vnew[vcol(lr, b)];
                 }
         }
         // four independent accumulation chains over the k-steps
@@ -681,7 +736,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // O += P V: A[h = lr][t = 4q + lg] = P, B[t][j = lr] = V[t][8 lr + b]
+        // O += P V: A[h = lr][t = 4q + lg] = P, B[t][j = lr] = V[t][vcol(lr, b)]
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const float pa = my_p[lr * 16 + 4 * q + lg];
@@ -701,7 +756,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     for (int r = 0; r < 4; r++) {
         const int h = 4 * lg + r;
 #pragma unroll
-        for (int b = 0; b < MNB; b++) mo[(wave * MH + h) * MHD + 8 * lr + b] = o[b][r];
+        for (int b = 0; b < MNB; b++) mo[(wave * MH + h) * MHD + vcol(lr, b)] = o[b][r];
         if (lr == 0) {
             mm[wave * MH + h] = m_run[r];
             ml[wave * MH + h] = l_run[r];
@@ -709,25 +764,39 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     }
     const uint32_t tag = a.t_part ? attn_tag(a, ticket) : 0u;  // (a barrier)
     __syncthreads();
-    const int ps = MHD + 2;
-    const int64_t part0 = ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
-    for (int idx = threadIdx.x; idx < gqa * MHD; idx += AT_WG) {
-        const int h = idx / MHD, e = idx - h * MHD;
+    // per head: M = max_w m_w, the waves' factors f_w = e^(m_w - M) and
+    // L = sum_w l_w f_w, once (in the probabilities' LDS, free now); then
+    // O = sum_w o_w f_w per output value
+    float *mf = pt;              // [AT_WAVES][MH]
+    float *mM = pt + AT_WAVES * MH, *mL = mM + MH;
+    if ((int)threadIdx.x < gqa) {
+        const int h = threadIdx.x;
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < AT_WAVES; w++) M = fmaxf(M, mm[w * MH + h]);
-        float O = 0.0f, L = 0.0f;
+        float L = 0.0f;
 #pragma unroll
         for (int w = 0; w < AT_WAVES; w++) {
             const float mw = mm[w * MH + h];
             const float f = mw == -INFINITY ? 0.0f : expf(mw - M);
-            O += mo[(w * MH + h) * MHD + e] * f;
+            mf[w * MH + h] = f;
             L += ml[w * MH + h] * f;
         }
+        mM[h] = M;
+        mL[h] = L;
+    }
+    __syncthreads();
+    const int ps = MHD + 2;
+    const int64_t part0 = ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
+    for (int idx = threadIdx.x; idx < gqa * MHD; idx += AT_WG) {
+        const int h = idx / MHD, e = idx - h * MHD;
+        float O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < AT_WAVES; w++) O += mo[(w * MH + h) * MHD + e] * mf[w * MH + h];
         part_put(a, part0 + h * ps + e, tag, O);
         if (e == 0) {
-            part_put(a, part0 + h * ps + MHD, tag, M);
-            part_put(a, part0 + h * ps + MHD + 1, tag, L);
+            part_put(a, part0 + h * ps + MHD, tag, mM[h]);
+            part_put(a, part0 + h * ps + MHD + 1, tag, mL[h]);
         }
     }
     if (a.t_part) attn_combine_tail<MHD / 64>(a, c, kvh, (n_t + chunk - 1) / chunk, tag, sm);

@@ -402,7 +402,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         // rows per lane group in flight: all of them at the shapes served
         // (a single memory round trip), as the registers allow
         const bool ok = a.UPL_q == 1 ? qkv_rows<1, 3>(a, q0, q1, tag, lds + a.off_xq, tr)
-                                     : qkv_rows<2, 2>(a, q0, q1, tag, lds + a.off_xq, tr);
+                                     : qkv_rows<2, 3>(a, q0, q1, tag, lds + a.off_xq, tr);
         if (!ok) return;
         stamp(10);
         flush();
