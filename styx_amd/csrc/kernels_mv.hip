@@ -366,7 +366,9 @@ __device__ inline void gate_up_body(const GateUpK &a, int m, int s, int32_t *s_i
     const Mat mat = mat_at(slab, T, (int64_t)a.F * a.nb);
     const int r_begin = blockIdx.x * a.rpw, r_end = min(a.F, r_begin + a.rpw);
     float *y = a.gu + ((int64_t)m * a.nslots + s) * a.F;
-    walk_rows_pipelined<T, UPL, dense_nr<UPL>()>(
+    // one row per batch: these launches give a lane group about two rows,
+    // and a second register set of more would cost occupancy
+    walk_rows_pipelined<T, UPL, 1>(
         OneMat{mat, a.nb}, a.nb, a.G, r_begin, r_end,
         [&](UX<T>(&x)[UPL], const LaneU<UPL> &lu) {
             XFrom<T, UPL>{a.xq}(x, lu);
@@ -502,8 +504,8 @@ __global__ void __launch_bounds__(WG) k_down(DownK a)
         XFrom<T, UPL>{q}(x, lu);
         return true;
     };
-    walk_rows_pipelined<T, UPL, dense_nr<UPL>()>(OneMat{mat, a.nb}, a.nb, a.G, r_begin, r_end, build,
-                                                  [=](int r, float v) { part[r] = v; });
+    walk_rows_pipelined<T, UPL, 1>(OneMat{mat, a.nb}, a.nb, a.G, r_begin, r_end, build,
+                                   [=](int r, float v) { part[r] = v; });  // (as k_gate_up)
 }
 
 hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_t *ids,
