@@ -154,10 +154,25 @@ __global__ void __launch_bounds__(WG) k_mv_dense(DenseK a)
         }
         return true;
     };
-    auto emit = [&](int r, float v) {
+    auto y_of = [&](int r) {
         const int s = (int)(r >= b1) + (int)(r >= b2);
-        float *y = s == 0 ? a.y[0] + r : s == 1 ? a.y[1] + (r - b1) : a.y[2] + (r - b2);
+        return s == 0 ? a.y[0] + r : s == 1 ? a.y[1] + (r - b1) : a.y[2] + (r - b2);
+    };
+    // a residual add with at most one row per thread reads the residual at
+    // entry (it does not depend on the dot products) and adds it after the
+    // walk, instead of a dependent load at the end of each row
+    __shared__ float s_out[WG];
+    const bool early = add && a.rpw <= WG;
+    const int tr = r_begin + (int)threadIdx.x;
+    float res = 0.0f;
+    if (early && tr < r_end) res = *y_of(tr);
+    auto emit = [&](int r, float v) {
         v *= scale;
+        if (early) {
+            s_out[r - r_begin] = v;
+            return;
+        }
+        float *y = y_of(r);
         v = add ? *y + v : v;
         *y = v;
         if (a.amax) best = max(best, argmax_key(v, (uint32_t)r));
@@ -168,6 +183,14 @@ __global__ void __launch_bounds__(WG) k_mv_dense(DenseK a)
     else
         walk_rows_pipelined<T, UPL, dense_nr<UPL>()>(Mat3(m0, m1, m2, b1, b2, a.nb), a.nb, a.G,
                                                       r_begin, r_end, xload, emit);
+    if (early) {
+        __syncthreads();
+        if (tr < r_end) {
+            const float v = res + s_out[threadIdx.x];
+            *y_of(tr) = v;
+            if (a.amax) best = max(best, argmax_key(v, (uint32_t)tr));
+        }
+    }
     if (a.amax) {
         // the workgroup's best row joins the launch's running maximum: one
         // relaxed device-scope atomic per workgroup (the reading kernel runs
