@@ -558,6 +558,7 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 constexpr int MH = 16;      // padded heads per kv head
 constexpr int MHD = 128;    // head_dim of this variant
 constexpr int MNB = MHD / 16;
+constexpr int ATTN_PT_LDS = 256;  // page-table entries kept in LDS (128K tokens of 512)
 // Column of Q and K that lane group g supplies at k-step m (m < 32), and
 // the output column of lane r's accumulator block b (b < 8).
 __device__ __forceinline__ constexpr int kcol(int g, int m) { return 16 * (m >> 2) + 4 * g + (m & 3); }
@@ -600,10 +601,18 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     const int t_min = c * a.chunk + wave * 16 + lr, pg_min = t_min / a.page_tokens;
     const bool spec = pg_min < a.page_table_len;
     const int32_t pe_min = spec ? a.page_table[pg_min] : 0;
+    // the whole page table in LDS when it is short: past the minimum chunk
+    // size (long contexts) the first tile's page entry then needs no memory
+    // trip after the position, nor does any later tile's
+    __shared__ int32_t s_pt[ATTN_PT_LDS];
+    const bool pt_lds = a.page_table_len > 0 && a.page_table_len <= ATTN_PT_LDS;
+    if (pt_lds)
+        for (int i = threadIdx.x; i < a.page_table_len; i += AT_WG) s_pt[i] = a.page_table[i];
 
     const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
     const int t0 = c * chunk;
     if (t0 >= n_t) return;
+    __syncthreads();  // s_pt
     const int t1 = min(n_t, t0 + chunk);
     const bool owns_pos = t1 == n_t;
     double2 cs[1];
@@ -613,9 +622,12 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     int tb = t0 + wave * 16;
     float kv[MHD / 4];     // K[tb + lr][kcol(lg, m)]
     float vvr[4][MNB];     // V[tb + 4q + lg][vcol(lr, b)]
-    auto row_of = [&](int tbase) -> int64_t {
-        return tbase + lr < t1 ? kv_off(a, tbase + lr, kvh, kv_dim) : 0;
+    auto kv_at = [&](int t) -> int64_t {
+        if (!pt_lds) return kv_off(a, t, kvh, kv_dim);
+        return ((int64_t)s_pt[t / a.page_tokens] * a.page_tokens + t % a.page_tokens) * kv_dim +
+               (int64_t)kvh * MHD;
     };
+    auto row_of = [&](int tbase) -> int64_t { return tbase + lr < t1 ? kv_at(tbase + lr) : 0; };
     auto load_k = [&](int64_t row, int tbase) {
         const bool ok = tbase + lr < t1;
 #pragma unroll
@@ -670,7 +682,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     }
     __syncthreads();
     if (owns_pos && wave == 0) {
-        const int64_t po = kv_off(a, pos, kvh, kv_dim);
+        const int64_t po = kv_at(pos);
         for (int e = lane; e < MHD; e += 64) {
             a.kpool[po + e] = knew[e];
             a.vpool[po + e] = vnew[e];
