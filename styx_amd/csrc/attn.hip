@@ -355,13 +355,22 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
             kq[j] = ok ? *(const float4 *)(a.kpool + row + qd * SEG + 4 * j)
                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     };
+    // a lane's EPL values of a V row are contiguous: one load each
     auto load_v = [&](int64_t row, int tbase) {
         const int nt = min(TILE, t1 - tbase);
 #pragma unroll
         for (int i = 0; i < TILE; i++) {
             const int64_t ri = __shfl(row, i);
-#pragma unroll
-            for (int e = 0; e < EPL; e++) vv[i][e] = i < nt ? a.vpool[ri + lane * EPL + e] : 0.0f;
+            const float *src = a.vpool + ri + lane * EPL;
+            if constexpr (EPL == 4) {
+                const float4 v = i < nt ? *(const float4 *)src : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                vv[i][0] = v.x; vv[i][1] = v.y; vv[i][2] = v.z; vv[i][3] = v.w;
+            } else if constexpr (EPL == 2) {
+                const float2 v = i < nt ? *(const float2 *)src : make_float2(0.0f, 0.0f);
+                vv[i][0] = v.x; vv[i][1] = v.y;
+            } else {
+                vv[i][0] = i < nt ? src[0] : 0.0f;
+            }
         }
     };
     auto row_of = [&](int tbase) -> int64_t {
