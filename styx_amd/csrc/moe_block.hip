@@ -123,15 +123,25 @@ __device__ __forceinline__ void gu_rows(const MoeBlockK &a, const uint8_t *slab,
     stamp(13);
 }
 
-template <typename Between>
-__device__ __forceinline__ void gu_block(const MoeBlockK &a, int b, bool routed_phase,
-                                const int32_t *s_ids, const Xq &xqx, uint32_t tag,
-                                Between between, uint64_t *tr)
+// Gate/up block b: matrix m, slot s, rows [r0, r1).
+struct GuPos {
+    int m, s, r0, r1;
+};
+__device__ __forceinline__ GuPos gu_pos(const MoeBlockK &a, int b)
 {
     const int per_m = a.nslots * a.bps_gu;
     const int m = b / per_m, rem = b - m * per_m, s = rem / a.bps_gu;
+    const int r0 = (rem - s * a.bps_gu) * a.rpw_gu;
+    return {m, s, r0, min(a.F, r0 + a.rpw_gu)};
+}
+
+template <typename Between>
+__device__ __forceinline__ void gu_block(const MoeBlockK &a, const GuPos &bp, bool routed_phase,
+                                const int32_t *s_ids, const Xq &xqx, uint32_t tag,
+                                Between between, uint64_t *tr)
+{
+    const int m = bp.m, s = bp.s, r0 = bp.r0, r1 = bp.r1;
     if ((s < a.k) != routed_phase) return;
-    const int r0 = (rem - s * a.bps_gu) * a.rpw_gu, r1 = min(a.F, r0 + a.rpw_gu);
     if (routed_phase && tr && threadIdx.x == 0) tr[14] = wall_clock64();
     const uint8_t *slab = s < a.k ? routed_slab(a, a.src[m], s_ids[s], s) : a.sh[m];
     if (routed_phase && tr && threadIdx.x == 0) tr[15] = wall_clock64();
@@ -236,6 +246,13 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     };
     __syncthreads();
     stamp(0);
+    // this workgroup's first gate/up block and its down rows, decoded once
+    // here: they do not depend on the routing, and the divisions would
+    // otherwise sit between the ranking and the first weight loads
+    const GuPos gp0 = gu_pos(a, w);
+    const bool has_d = w < a.n_d;
+    const int ds = has_d ? w / a.bps_d : 0;
+    const int d0 = (w - ds * a.bps_d) * a.rpw_d, d1 = min(a.H, d0 + a.rpw_d);
     // the draw's result is first needed after the entry loads are issued
     unsigned long long ticket = 0;
     if (tid == 0) ticket = draw_ticket(a.ticket, MB_TICKETS, w);
@@ -332,7 +349,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         xq_build(xs, nullptr, 0.0f, false, a.H, xqx, red, nullptr);
         __syncthreads();
         stamp(2);
-        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b, false, s_ids, xqx, tag, nothing, tr);
+        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), false, s_ids, xqx, tag, nothing, tr);
     }
 
     // ---- routing: every workgroup ranks the logits (topk_softmax_f32 order)
@@ -345,15 +362,12 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     // slot's gate/up outputs are in: pulling them into L2 earlier, during
     // the gate/up phase or the wait after it, measured slower -- the extra
     // requests delay the gate/up stream more than they save later)
-    const bool has_d = w < a.n_d;
-    const int ds = has_d ? w / a.bps_d : 0;
-    const int d0 = (w - ds * a.bps_d) * a.rpw_d, d1 = min(a.H, d0 + a.rpw_d);
     const uint8_t *dslab = nullptr;
     if (has_d) dslab = ds < a.k ? routed_slab(a, a.src[2], s_ids[ds], ds) : a.sh[2];
 
     // ---- routed gate/up rows
     if (has_x)
-        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b, true, s_ids, xqx, tag, nothing, tr);
+        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), true, s_ids, xqx, tag, nothing, tr);
     stamp(5);
 
     // ---- down: swiglu_f32 (ops2.rs:305-309) of the slot's g and u and its
