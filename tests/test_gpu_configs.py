@@ -63,9 +63,11 @@ def test_config5_moe_shape_with_shared_expert(gpu, ff_shexp):
 
 def test_config4_long_context_attention(gpu):
     """gqa 16, head_dim 128, context of 4100 synthetic K/V rows (9 pages,
-    ~50 attention chunks) then 3 real tokens."""
+    ~50 attention chunks) then 3 real tokens.  At the real H of 4096 the
+    layer-0 q/k/v launch gives its workgroups 12 of the 9216 stacked rows,
+    so one workgroup's rows span the q and k matrices."""
     from styx_amd import MoeModel, SynthConfig
-    cfg = SynthConfig(n_layers=2, n_embd=1024, n_heads=64, n_kv_heads=4, head_dim=128,
+    cfg = SynthConfig(n_layers=2, n_embd=4096, n_heads=64, n_kv_heads=4, head_dim=128,
                       n_expert=32, n_expert_used=4, n_ff_exp=256, n_vocab=2048, exp_mix=True,
                       seed=0x235)
     n_ctx, n_t = 4160, 4100
