@@ -269,6 +269,25 @@ int styx_residency_plan(const char *hist_csv, int n_layers, int n_expert,
                         const uint64_t *slab_bytes, int64_t budget_mb, uint32_t *remap,
                         uint64_t *pinned_slabs);
 
+/* Repin choice of one layer (crates/model/src/moe.rs:1465-1497), host only:
+ * the resident experts slot_experts[0..n_slots) ranked coldest first by
+ * hits[], the other experts hottest first (both stable on ties); pair i
+ * swaps while hits[outsider] >= 2 * max(hits[resident], 1), at most
+ * repin_max pairs.  Writes the slot and incoming expert of each swap and
+ * their count.  This is the selection styx_moe_* applies every
+ * opts.repin_interval tokens.  Needs no GPU. */
+int styx_repin_select(const uint64_t *hits, int n_expert, const uint32_t *slot_experts,
+                      int n_slots, int repin_max, uint32_t *swap_slot, uint32_t *swap_expert,
+                      int *n_swaps);
+
+/* The checks MoeModel::load (moe.rs:536-1408) makes before it uploads
+ * anything, without a device: GGUF header, qwen3moe hyperparameters, every
+ * tensor's bytes inside the file, and every tensor the model reads against
+ * the dims and type its hyperparameters imply.  Fills out (may be NULL;
+ * n_ctx and the expert byte counts are 0).  styx_moe_load runs the same
+ * checks first. */
+int styx_moe_check_file(const char *path, styx_moe_hparams *out);
+
 /* MoeModel::load (moe.rs:536-1408) from a GGUF file. */
 int styx_moe_load(styx_gpu *gpu, const char *path, const styx_moe_opts *opts, styx_moe **out);
 /* Build a seeded synthetic model directly in HBM (no file). */

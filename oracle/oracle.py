@@ -70,6 +70,7 @@ def lib() -> C.CDLL:
             "styx_oracle_topk_softmax": (None, [vp, i, i, i, vp, vp, vp, vp]),
             "styx_oracle_swiglu": (None, [vp, vp, i, vp]),
             "styx_oracle_moe_reduce": (None, [vp, vp, i, i, vp]),
+            "styx_oracle_axpy_sig": (None, [vp, f, i, vp]),
             "styx_oracle_rope_neox": (None, [vp, i, i, i, f]),
             "styx_oracle_attn_decode": (None, [vp, vp, vp, i, i, i, i, i, f, vp]),
             "styx_oracle_attn_decode_f64": (None, [vp, vp, vp, i, i, i, i, i, C.c_double, vp]),
@@ -170,6 +171,14 @@ def moe_reduce(d, w, ne, k, x):
     lib().styx_oracle_moe_reduce(_p(np.ascontiguousarray(d, np.float32)),
                                  _p(np.ascontiguousarray(w, np.float32)), ne, k, _p(x))
     return x
+
+
+def axpy_sig(a, g0, d):
+    """d + sigmoid(g0) * a (shaders/axpy_sig_f32.comp:7-11); returns a new array."""
+    d = np.array(d, np.float32, copy=True)
+    a = np.ascontiguousarray(a, np.float32)
+    lib().styx_oracle_axpy_sig(_p(a), C.c_float(g0), len(d), _p(d))
+    return d
 
 
 def rope_neox(x, hd, nh, pos, base):

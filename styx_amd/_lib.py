@@ -122,6 +122,8 @@ _SIGS = {
     "styx_rope_table": (None, [C.c_float, i32, i32, vp]),
     "styx_op_read_probe": (i32, [vp, vp, i64, vp, i32]),
     "styx_residency_plan": (i32, [C.c_char_p, i32, i32, vp, i64, vp, vp]),
+    "styx_repin_select": (i32, [vp, i32, vp, i32, i32, vp, vp, C.POINTER(i32)]),
+    "styx_moe_check_file": (i32, [C.c_char_p, vp]),
     "styx_moe_fill_kv": (i32, [vp, i32, C.c_uint64, C.c_float]),
     "styx_moe_read_kv": (i32, [vp, i32, i32, i32, vp, vp]),
     "styx_op_gather_slabs": (i32, [vp, vp, vp, vp, vp, vp, i32, i32]),

@@ -20,6 +20,7 @@
 #include <cstring>
 #include <fstream>
 #include <functional>
+#include <map>
 #include <memory>
 #include <numeric>
 #include <sstream>
@@ -185,7 +186,8 @@ struct styx_moe {
     bool attn_merge_in_kernel(int n_t) const;
     int ensure_pages(int upto_pos);
     int build_graphs();
-    void maybe_repin();
+    int maybe_repin();
+    std::string broken;  // set when the model's device state can no longer be trusted
     int stat_id(const char *name);
     hipEvent_t ev();
     int collect_stats();
@@ -871,54 +873,88 @@ int styx_moe::run_token(bool gen)
     return enqueue_token(gen, merge);
 }
 
+// Repin choice for one layer (moe.rs:1465-1497): residents ranked coldest
+// first, outsiders hottest first (both stable on ties, where the reference's
+// sort_unstable leaves the order open); the i-th pair swaps while the
+// outsider has at least twice the resident's hits (and at least 2), at most
+// maxsw pairs.  resident[e] says whether expert e holds a hot slot.
+static void repin_select(const uint64_t *hits, int E, const uint32_t *slot_experts, int n_slots,
+                         const std::vector<char> &resident, int maxsw,
+                         std::vector<std::pair<int, uint32_t>> &swaps)
+{
+    swaps.clear();
+    std::vector<int> res(n_slots);
+    std::iota(res.begin(), res.end(), 0);
+    std::stable_sort(res.begin(), res.end(), [&](int a, int b) {
+        return hits[slot_experts[a]] < hits[slot_experts[b]];
+    });
+    std::vector<uint32_t> out;
+    for (int e = 0; e < E; e++)
+        if (!resident[e]) out.push_back((uint32_t)e);
+    std::stable_sort(out.begin(), out.end(),
+                     [&](uint32_t a, uint32_t b) { return hits[a] > hits[b]; });
+    for (int i = 0; i < maxsw && i < n_slots && i < (int)out.size(); i++) {
+        const uint32_t old = slot_experts[res[i]], nw = out[i];
+        if (hits[nw] < 2 * std::max<uint64_t>(hits[old], 1)) break;
+        swaps.push_back({res[i], nw});
+    }
+}
+
 // Online repinning (moe.rs:1450-1508): fold the last token's routing into
 // per-layer hit counters; every repin_interval tokens swap up to repin_max
-// cold slots per layer for outsiders with at least twice the hits.
-void styx_moe::maybe_repin()
+// cold slots per layer for outsiders with at least twice the hits.  The
+// remap (host and device) changes only after the slab copies have landed;
+// a copy that fails leaves a hot slot half-written, so the model is then
+// marked broken and refuses further tokens.
+int styx_moe::maybe_repin()
 {
-    if (opts.repin_interval <= 0 || !any_host) return;
+    if (opts.repin_interval <= 0 || !any_host) return STYX_OK;
     std::vector<int32_t> h((size_t)L * 64);
-    if (hipMemcpy(h.data(), ids, sizeof(int32_t) * h.size(), hipMemcpyDeviceToHost) != hipSuccess)
-        return;
+    STYX_HIP(hipMemcpy(h.data(), ids, sizeof(int32_t) * h.size(), hipMemcpyDeviceToHost));
     for (int l = 0; l < L; l++)
         for (int s = 0; s < K; s++) {
             const uint32_t e = (uint32_t)h[(size_t)l * 64 + s];
             if (e < (uint32_t)E) layers[l].hits[e]++;
         }
-    if (n_past % opts.repin_interval != 0) return;
+    if (n_past % opts.repin_interval != 0) return STYX_OK;
     const int maxsw = opts.repin_max > 0 ? opts.repin_max : 2;
+    std::vector<std::pair<int, uint32_t>> swaps;
+    auto broke = [&](hipError_t e, const char *what) {
+        broken = std::string("repin: ") + what + " failed (" + hipGetErrorString(e) +
+                 "); a hot slot may hold a partial slab, reload the model";
+        return fail(STYX_E_HIP, broken);
+    };
     for (auto &ly : layers) {
         const int n_slots = (int)ly.slot_experts.size();
         if (n_slots == 0 || !ly.host_experts) continue;
-        std::vector<int> res(n_slots);
-        std::iota(res.begin(), res.end(), 0);
-        std::stable_sort(res.begin(), res.end(), [&](int a, int b) {
-            return ly.hits[ly.slot_experts[a]] < ly.hits[ly.slot_experts[b]];
-        });
-        std::vector<uint32_t> out;
-        for (int e = 0; e < E; e++)
-            if (ly.remap[e] == SKIP) out.push_back((uint32_t)e);
-        std::stable_sort(out.begin(), out.end(),
-                         [&](uint32_t a, uint32_t b) { return ly.hits[a] > ly.hits[b]; });
-        bool dirty = false;
-        for (int i = 0; i < maxsw && i < n_slots && i < (int)out.size(); i++) {
-            const int slot = res[i];
-            const uint32_t old = ly.slot_experts[slot], nw = out[i];
-            if (ly.hits[nw] < 2 * std::max<uint64_t>(ly.hits[old], 1)) break;
-            for (Mat *m : {&ly.gate, &ly.up, &ly.down})
-                hipMemcpyAsync(m->hot + (int64_t)slot * m->slab, m->host + (int64_t)nw * m->slab,
-                               m->slab, hipMemcpyHostToDevice, gpu->stream);
+        std::vector<char> resident(E, 0);
+        for (int e = 0; e < E; e++) resident[e] = ly.remap[e] != SKIP;
+        repin_select(ly.hits.data(), E, ly.slot_experts.data(), n_slots, resident, maxsw, swaps);
+        if (swaps.empty()) continue;
+        for (auto &sw : swaps)
+            for (Mat *m : {&ly.gate, &ly.up, &ly.down}) {
+                const hipError_t e = hipMemcpyAsync(m->hot + (int64_t)sw.first * m->slab,
+                                                    m->host + (int64_t)sw.second * m->slab,
+                                                    m->slab, hipMemcpyHostToDevice, gpu->stream);
+                if (e != hipSuccess) return broke(e, "slab copy");
+            }
+        if (hipError_t e = hipStreamSynchronize(gpu->stream); e != hipSuccess)
+            return broke(e, "slab copy");
+        for (auto &sw : swaps) {
+            const uint32_t old = ly.slot_experts[sw.first];
             ly.remap[old] = SKIP;
-            ly.remap[nw] = (uint32_t)slot;
-            ly.slot_experts[slot] = nw;
+            ly.remap[sw.second] = (uint32_t)sw.first;
+            ly.slot_experts[sw.first] = sw.second;
             repin_swaps++;
-            dirty = true;
         }
-        if (dirty)
-            hipMemcpyAsync(ly.remap_dev, ly.remap.data(), sizeof(uint32_t) * E,
-                           hipMemcpyHostToDevice, gpu->stream);
+        if (hipError_t e = hipMemcpyAsync(ly.remap_dev, ly.remap.data(), sizeof(uint32_t) * E,
+                                          hipMemcpyHostToDevice, gpu->stream);
+            e != hipSuccess)
+            return broke(e, "remap upload");
+        if (hipError_t e = hipStreamSynchronize(gpu->stream); e != hipSuccess)
+            return broke(e, "remap upload");
     }
-    hipStreamSynchronize(gpu->stream);
+    return STYX_OK;
 }
 
 // ---------------------------------------------------------- model build --
@@ -1061,8 +1097,88 @@ int64_t spec_bytes(const TensorSpec &t)
     return n_elems(t.dims) / blk_elems(t.type) * blk_bytes(t.type);
 }
 
+// Every tensor the model reads, with the GGUF dims (dims[0] = columns) and
+// type class the hparams imply, checked before anything is allocated or
+// uploaded: a short router, norm or LM-head tensor would otherwise make a
+// kernel read past its allocation.  Names the model does not use are
+// ignored, as the reference's loader ignores them.
+int check_specs(const styx_moe_synth_cfg &c, std::vector<TensorSpec> &specs)
+{
+    const int64_t H = c.n_embd, qd = (int64_t)c.n_heads * c.head_dim,
+                  kvd = (int64_t)c.n_kv_heads * c.head_dim, E = c.n_expert, F = c.n_ff_exp,
+                  Fs = c.n_ff_shexp, V = c.n_vocab, hd = c.head_dim;
+    struct Want { std::vector<int64_t> dims; bool quant; bool required; };
+    std::map<std::string, Want> want;
+    want["token_embd.weight"] = {{H, V}, true, true};
+    want["output.weight"] = {{H, V}, true, true};
+    want["output_norm.weight"] = {{H}, false, true};
+    for (int l = 0; l < c.n_layers; l++) {
+        want[blk(l, "attn_norm")] = {{H}, false, true};
+        want[blk(l, "attn_q_norm")] = {{hd}, false, false};
+        want[blk(l, "attn_k_norm")] = {{hd}, false, false};
+        want[blk(l, "ffn_norm")] = {{H}, false, true};
+        want[blk(l, "attn_q")] = {{H, qd}, true, true};
+        want[blk(l, "attn_k")] = {{H, kvd}, true, true};
+        want[blk(l, "attn_v")] = {{H, kvd}, true, true};
+        want[blk(l, "attn_output")] = {{qd, H}, true, true};
+        want[blk(l, "ffn_gate_inp")] = {{H, E}, false, true};
+        want["blk." + std::to_string(l) + ".ffn_gate_inp.bias"] = {{E}, false, false};
+        want[blk(l, "ffn_gate_exps")] = {{H, F, E}, true, true};
+        want[blk(l, "ffn_up_exps")] = {{H, F, E}, true, true};
+        want[blk(l, "ffn_down_exps")] = {{F, H, E}, true, true};
+        want[blk(l, "ffn_gate_shexp")] = {{H, Fs}, true, Fs > 0};
+        want[blk(l, "ffn_up_shexp")] = {{H, Fs}, true, Fs > 0};
+        want[blk(l, "ffn_down_shexp")] = {{Fs, H}, true, Fs > 0};
+        want[blk(l, "ffn_gate_inp_shexp")] = {{H}, false, Fs > 0};
+    }
+    std::map<std::string, int> seen;
+    std::vector<TensorSpec> used;
+    for (const TensorSpec &t : specs) {
+        auto it = want.find(t.name);
+        if (it == want.end()) continue;
+        used.push_back(t);
+        if (seen[t.name]++) return fail(STYX_E_FORMAT, t.name + ": tensor listed twice");
+        const Want &w = it->second;
+        if (w.quant ? !is_quant(t.type) : t.type != T_F32)
+            return fail(STYX_E_FORMAT, t.name + (w.quant ? ": matrix type must be q8_0/q4_K/q5_K/q6_K"
+                                                         : ": expected f32"));
+        if (t.dims != w.dims) {
+            std::string d, e;
+            for (auto v : t.dims) d += (d.empty() ? "" : ",") + std::to_string(v);
+            for (auto v : w.dims) e += (e.empty() ? "" : ",") + std::to_string(v);
+            return fail(STYX_E_FORMAT, t.name + ": dims [" + d + "] do not match the hparams [" + e + "]");
+        }
+    }
+    for (auto &kv : want)
+        if (kv.second.required && !seen.count(kv.first))
+            return fail(STYX_E_FORMAT, "missing tensor " + kv.first);
+    specs.swap(used);
+    return STYX_OK;
+}
+
+// Hyperparameters the kernels support (the reference's own caps: k <= 16,
+// moe.rs:587; E <= 512, moe.rs:3), checked before anything is allocated.
+int check_cfg(const styx_moe_synth_cfg &c)
+{
+    if (c.n_layers < 1 || c.n_layers > 4096 || c.n_vocab < 1)
+        return fail(STYX_E_INVALID, "n_layers must be in [1, 4096] and n_vocab positive");
+    if (c.n_expert_used < 1 || c.n_expert_used > MAX_TOPK) return fail(STYX_E_INVALID, "n_expert_used must be in [1, 16] (moe.rs:587)");
+    if (c.n_expert < c.n_expert_used || c.n_expert > MAX_EXPERTS || c.n_expert % 16) return fail(STYX_E_INVALID, "n_expert must be a multiple of 16 in [k, 512]");
+    if (c.n_kv_heads < 1 || c.n_heads < 1 || c.n_heads > 1024 || c.n_heads % c.n_kv_heads || c.n_heads / c.n_kv_heads > 16) return fail(STYX_E_INVALID, "bad head counts");
+    if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) return fail(STYX_E_INVALID, "head_dim must be 64, 128 or 256");
+    {
+        const int gqa = c.n_heads / c.n_kv_heads, nhg = gqa % 4 == 0 ? 4 : gqa % 2 == 0 ? 2 : 1;
+        if (gqa / nhg > 4) return fail(STYX_E_INVALID, "gqa must split into <= 4 heads per wave");
+    }
+    if (c.n_embd < 256 || c.n_embd % 256 || c.n_embd > XQ_MAX) return fail(STYX_E_INVALID, "n_embd must be a multiple of 256, <= 16384");
+    if (c.n_heads * c.head_dim > XQ_MAX) return fail(STYX_E_INVALID, "n_head * head_dim must be <= 16384");
+    if (c.n_ff_exp < 32 || c.n_ff_exp % 32 || c.n_ff_exp > 8192) return fail(STYX_E_INVALID, "expert FFN width must be a multiple of 32, <= 8192");
+    if (c.n_ff_shexp < 0 || c.n_ff_shexp % 32 || c.n_ff_shexp > XQ_MAX) return fail(STYX_E_INVALID, "shared expert FFN width must be a multiple of 32, <= 16384");
+    return STYX_OK;
+}
+
 // Common construction from a list of tensors with their sources.
-int build_model(styx_moe *m, const styx_moe_synth_cfg &c, const std::vector<TensorSpec> &specs,
+int build_model(styx_moe *m, const styx_moe_synth_cfg &c, std::vector<TensorSpec> specs,
                 const std::function<Source(const TensorSpec &)> &source,
                 const std::vector<std::vector<std::pair<uint32_t, uint64_t>>> *hist)
 {
@@ -1079,18 +1195,8 @@ int build_model(styx_moe *m, const styx_moe_synth_cfg &c, const std::vector<Tens
     m->eps = c.rms_eps;
     m->rope_base = c.rope_base;
     m->norm_topk = 1;
-    if (m->K < 1 || m->K > MAX_TOPK) return fail(STYX_E_INVALID, "n_expert_used must be in [1, 16] (moe.rs:587)");
-    if (m->E < m->K || m->E > MAX_EXPERTS || m->E % 16) return fail(STYX_E_INVALID, "n_expert must be a multiple of 16 in [k, 512]");
-    if (m->nkv < 1 || m->nh % m->nkv || m->nh / m->nkv > 16) return fail(STYX_E_INVALID, "bad head counts");
-    if (m->hd != 64 && m->hd != 128 && m->hd != 256) return fail(STYX_E_INVALID, "head_dim must be 64, 128 or 256");
-    {
-        const int gqa = m->nh / m->nkv, nhg = gqa % 4 == 0 ? 4 : gqa % 2 == 0 ? 2 : 1;
-        if (gqa / nhg > 4) return fail(STYX_E_INVALID, "gqa must split into <= 4 heads per wave");
-    }
-    if (m->H % 256 || m->H > XQ_MAX) return fail(STYX_E_INVALID, "n_embd must be a multiple of 256, <= 16384");
-    if (m->nh * m->hd > XQ_MAX) return fail(STYX_E_INVALID, "n_head * head_dim must be <= 16384");
-    if (m->F % 32 || m->F > 8192) return fail(STYX_E_INVALID, "expert FFN width must be a multiple of 32, <= 8192");
-    if (m->Fsh % 32 || m->Fsh > XQ_MAX) return fail(STYX_E_INVALID, "shared expert FFN width must be a multiple of 32, <= 16384");
+    if (int r = check_cfg(c)) return r;
+    if (int r = check_specs(c, specs)) return r;
 
     Builder b{m};
     int64_t mx = 0;
@@ -1216,6 +1322,29 @@ int styx_residency_plan(const char *hist_csv, int n_layers, int n_expert,
     return STYX_OK;
 }
 
+int styx_repin_select(const uint64_t *hits, int n_expert, const uint32_t *slot_experts,
+                      int n_slots, int repin_max, uint32_t *swap_slot, uint32_t *swap_expert,
+                      int *n_swaps)
+{
+    if (!hits || n_expert < 1 || n_slots < 0 || n_slots > n_expert || (n_slots && !slot_experts) ||
+        !n_swaps || (repin_max > 0 && (!swap_slot || !swap_expert)))
+        return fail(STYX_E_INVALID, "styx_repin_select: bad argument");
+    std::vector<char> resident(n_expert, 0);
+    for (int i = 0; i < n_slots; i++) {
+        if (slot_experts[i] >= (uint32_t)n_expert || resident[slot_experts[i]])
+            return fail(STYX_E_INVALID, "styx_repin_select: slot experts must be distinct ids < n_expert");
+        resident[slot_experts[i]] = 1;
+    }
+    std::vector<std::pair<int, uint32_t>> swaps;
+    repin_select(hits, n_expert, slot_experts, n_slots, resident, std::max(repin_max, 0), swaps);
+    for (size_t i = 0; i < swaps.size(); i++) {
+        swap_slot[i] = (uint32_t)swaps[i].first;
+        swap_expert[i] = swaps[i].second;
+    }
+    *n_swaps = (int)swaps.size();
+    return STYX_OK;
+}
+
 static styx_moe_opts default_opts()
 {
     styx_moe_opts o{};
@@ -1277,11 +1406,18 @@ int styx_moe_synth(styx_gpu *gpu, const styx_moe_synth_cfg *cfg, const styx_moe_
     return STYX_OK;
 }
 
-int styx_moe_load(styx_gpu *gpu, const char *path, const styx_moe_opts *opts, styx_moe **out)
+}  // extern "C"
+
+namespace {
+
+// Everything MoeModel::load checks before it touches the device: the GGUF
+// header (gguf-rs semantics), the qwen3moe hyperparameters, that every
+// tensor's bytes lie inside the file, and every tensor the model reads
+// against the dims its hyperparameters imply.  On success c holds the
+// hyperparameters and specs the tensors to upload.
+int parse_model_file(const char *path, Gguf &g, styx_moe_synth_cfg &c,
+                     std::vector<TensorSpec> &specs)
 {
-    if (!gpu || !path || !out) return fail(STYX_E_INVALID, "styx_moe_load: NULL argument");
-    STYX_HIP(hipSetDevice(gpu->device));
-    Gguf g;
     std::string err;
     if (!gguf_open(path, g, err)) return fail(STYX_E_FORMAT, std::string("gguf: ") + err);
     std::string arch;
@@ -1289,47 +1425,110 @@ int styx_moe_load(styx_gpu *gpu, const char *path, const styx_moe_opts *opts, st
         return fail(STYX_E_FORMAT, "missing general.architecture");
     if (arch != "qwen3moe")
         return fail(STYX_E_UNSUPPORTED, "unsupported architecture '" + arch + "' (qwen3moe only)");
-    styx_moe_synth_cfg c{};
+    c = styx_moe_synth_cfg{};
     uint32_t u;
     auto need = [&](const std::string &k, int &dst) -> bool {
         if (!g.get_u32(arch + "." + k, u)) return false;
-        dst = (int)u;
+        dst = u > (uint32_t)INT32_MAX ? -1 : (int)u;
         return true;
     };
     if (!need("block_count", c.n_layers) || !need("embedding_length", c.n_embd) ||
         !need("attention.head_count", c.n_heads) || !need("attention.head_count_kv", c.n_kv_heads) ||
         !need("expert_count", c.n_expert) || !need("expert_used_count", c.n_expert_used))
         return fail(STYX_E_FORMAT, "missing qwen3moe hyperparameter metadata");
-    if (!need("attention.key_length", c.head_dim)) c.head_dim = c.n_embd / c.n_heads;
+    if (!need("attention.key_length", c.head_dim)) c.head_dim = c.n_heads > 0 ? c.n_embd / c.n_heads : 0;
+    auto dim_int = [](uint64_t d) { return d > (uint64_t)INT32_MAX ? -1 : (int)d; };
     if (!need("expert_feed_forward_length", c.n_ff_exp)) {
         const GgufTensor *t = g.find("blk.0.ffn_gate_exps.weight");
         if (!t || t->dims.size() < 2) return fail(STYX_E_FORMAT, "no expert_feed_forward_length and no ffn_gate_exps");
-        c.n_ff_exp = (int)t->dims[1];
+        c.n_ff_exp = dim_int(t->dims[1]);
     }
     if (!g.get_f32(arch + ".attention.layer_norm_rms_epsilon", c.rms_eps) ||
         !g.get_f32(arch + ".rope.freq_base", c.rope_base))
         return fail(STYX_E_FORMAT, "missing rms epsilon / rope base");
     const GgufTensor *te = g.find("token_embd.weight");
     if (!te || te->dims.size() != 2) return fail(STYX_E_FORMAT, "missing token_embd.weight");
-    c.n_vocab = (int)te->dims[1];
-    if (const GgufTensor *ts = g.find("blk.0.ffn_gate_shexp.weight")) c.n_ff_shexp = (int)ts->dims[1];
+    c.n_vocab = dim_int(te->dims[1]);
+    if (const GgufTensor *ts = g.find("blk.0.ffn_gate_shexp.weight"))
+        c.n_ff_shexp = ts->dims.size() == 2 ? dim_int(ts->dims[1]) : -1;
+    if (check_cfg(c)) return fail(STYX_E_FORMAT, styx_last_error());
+    struct stat stb;
+    if (stat(path, &stb) != 0) return fail(STYX_E_IO, std::string("stat ") + path);
+    const uint64_t len = (uint64_t)stb.st_size;
+    specs.clear();
+    for (auto &t : g.tensors) {
+        // no sum of the three can wrap: each term is checked against what is left
+        if (g.data_start > len || t.offset > len - g.data_start ||
+            t.size_bytes > len - g.data_start - t.offset)
+            return fail(STYX_E_FORMAT, t.name + ": tensor data past end of file");
+        TensorSpec sp{t.name, (int)t.ggml_type, {}};
+        for (auto d : t.dims) sp.dims.push_back(d > (uint64_t)INT64_MAX ? -1 : (int64_t)d);
+        specs.push_back(sp);
+    }
+    return check_specs(c, specs);
+}
+
+}  // namespace
+
+extern "C" {
+
+int styx_moe_check_file(const char *path, styx_moe_hparams *out)
+{
+    if (!path) return fail(STYX_E_INVALID, "styx_moe_check_file: NULL path");
+    Gguf g;
+    styx_moe_synth_cfg c;
+    std::vector<TensorSpec> specs;
+    if (int r = parse_model_file(path, g, c, specs)) return r;
+    if (out) {
+        *out = styx_moe_hparams{};
+        out->n_layers = c.n_layers;
+        out->n_embd = c.n_embd;
+        out->n_heads = c.n_heads;
+        out->n_kv_heads = c.n_kv_heads;
+        out->head_dim = c.head_dim;
+        out->n_expert = c.n_expert;
+        out->n_expert_used = c.n_expert_used;
+        out->n_ff_exp = c.n_ff_exp;
+        out->n_ff_shexp = c.n_ff_shexp;
+        out->n_vocab = c.n_vocab;
+        out->rms_eps = c.rms_eps;
+        out->rope_base = c.rope_base;
+        out->norm_topk = 1;
+        for (const TensorSpec &t : specs)
+            if (t.name == "blk.0.ffn_gate_exps.weight" || t.name == "blk.0.ffn_up_exps.weight" ||
+                t.name == "blk.0.ffn_down_exps.weight")
+                out->slab_bytes += (uint64_t)(spec_bytes(t) / c.n_expert);
+    }
+    return STYX_OK;
+}
+
+int styx_moe_load(styx_gpu *gpu, const char *path, const styx_moe_opts *opts, styx_moe **out)
+{
+    if (!gpu || !path || !out) return fail(STYX_E_INVALID, "styx_moe_load: NULL argument");
+    Gguf g;
+    styx_moe_synth_cfg c;
+    std::vector<TensorSpec> specs;
+    if (int r = parse_model_file(path, g, c, specs)) return r;
+    STYX_HIP(hipSetDevice(gpu->device));
     // map the file
     int fd = open(path, O_RDONLY);
     if (fd < 0) return fail(STYX_E_IO, std::string("open ") + path);
     struct stat stb;
-    fstat(fd, &stb);
+    if (fstat(fd, &stb) != 0) {
+        close(fd);
+        return fail(STYX_E_IO, std::string("fstat ") + path);
+    }
     const size_t len = (size_t)stb.st_size;
     void *map = mmap(nullptr, len, PROT_READ, MAP_PRIVATE, fd, 0);
     close(fd);
     if (map == MAP_FAILED) return fail(STYX_E_IO, std::string("mmap ") + path);
     struct Unmap { void *p; size_t n; ~Unmap() { munmap(p, n); } } unmap{map, len};
-    std::vector<TensorSpec> specs;
-    for (auto &t : g.tensors) {
-        if (t.offset + t.size_bytes + g.data_start > len)
+    // the file may have changed between the checks and the mapping
+    for (const TensorSpec &t : specs) {
+        const GgufTensor *gt = g.find(t.name);
+        if (g.data_start > len || gt->offset > len - g.data_start ||
+            gt->size_bytes > len - g.data_start - gt->offset)
             return fail(STYX_E_FORMAT, t.name + ": tensor data past end of file");
-        TensorSpec s{t.name, (int)t.ggml_type, {}};
-        for (auto d : t.dims) s.dims.push_back((int64_t)d);
-        specs.push_back(s);
     }
     auto m = std::make_unique<styx_moe>();
     m->gpu = gpu;
@@ -1382,8 +1581,10 @@ int styx_moe_forward_token(styx_moe *m, uint32_t token, float *logits_out)
     if (m->n_past >= m->n_ctx)
         return fail(STYX_E_STATE, "KV arena full (" + std::to_string(m->n_ctx) + ")");
     if (token >= (uint32_t)m->V) return fail(STYX_E_INVALID, "token id out of range");
+    if (!m->broken.empty()) return fail(STYX_E_STATE, m->broken);
     STYX_HIP(hipSetDevice(m->gpu->device));
-    if (m->n_past > 0) m->maybe_repin();
+    if (m->n_past > 0)
+        if (int r = m->maybe_repin()) return r;
     if (int r = m->ensure_pages(m->n_past)) return r;
     m->h_stage[0] = token;
     m->h_stage[1] = (uint32_t)m->n_past;
@@ -1406,6 +1607,7 @@ int styx_moe_decode(styx_moe *m, int n_steps, uint32_t *out)
     if (m->n_past < 1) return fail(STYX_E_STATE, "styx_moe_decode: no token forwarded yet");
     if (m->n_past + n_steps > m->n_ctx) return fail(STYX_E_STATE, "styx_moe_decode: exceeds n_ctx");
     if (n_steps == 0) return STYX_OK;
+    if (!m->broken.empty()) return fail(STYX_E_STATE, m->broken);
     STYX_HIP(hipSetDevice(m->gpu->device));
     const int start = m->n_past;  // position of the pending (argmax) token
     if (int r = m->ensure_pages(start + n_steps - 1)) return r;
@@ -1413,10 +1615,11 @@ int styx_moe_decode(styx_moe *m, int n_steps, uint32_t *out)
     STYX_HIP(hipMemcpyAsync(m->d_pos, &m->h_stage[1], 4, hipMemcpyHostToDevice, m->gpu->stream));
     const bool host_work = (m->opts.repin_interval > 0 && m->any_host) || m->opts.time_kernels;
     for (int i = 0; i < n_steps; i++) {
-        if (host_work && i > 0) {
+        if (host_work) {
             // host bookkeeping between tokens needs the previous token done
+            // (as forward_token, the first step repins for the token before)
             STYX_HIP(hipStreamSynchronize(m->gpu->stream));
-            m->maybe_repin();
+            if (int r = m->maybe_repin()) return r;
             if (int r = m->collect_stats()) return r;
         }
         if (int r = m->run_token(true)) return r;

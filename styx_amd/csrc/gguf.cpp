@@ -201,10 +201,19 @@ bool gguf_open(const std::string &path, Gguf &g, std::string &err)
             err = "Unknown ggml_type: " + std::to_string(t.ggml_type);
             return false;
         }
+        // the reference multiplies unchecked (lib.rs:319-331); a product or
+        // byte size past 2^64 is rejected here instead of wrapping
         uint64_t prod = 1;
-        for (uint64_t d : t.dims) prod *= d;
+        for (uint64_t d : t.dims)
+            if (__builtin_mul_overflow(prod, d, &prod)) {
+                err = "Tensor dimensions overflow: " + t.name;
+                return false;
+            }
         if (prod % el) { err = "First dimension not multiple of block size"; return false; }
-        t.size_bytes = prod / el * by;
+        if (__builtin_mul_overflow(prod / el, by, &t.size_bytes)) {
+            err = "Tensor size overflows: " + t.name;
+            return false;
+        }
         g.tensors.push_back(std::move(t));
     }
     uint64_t align = 32;

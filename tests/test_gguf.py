@@ -136,3 +136,107 @@ def test_writer_roundtrip(tmp_path):
         start = g["data_start"] + t["offset"]
         assert raw[start:start + len(data)] == data.tobytes()
     assert set(g["metadata"]) == {"general.architecture", "x.count", "x.eps"}
+
+
+# ------------------------------------------- model-file checks (no GPU) ----
+
+def tiny_qwen3moe(overrides=None, drop=()):
+    """A 1-layer qwen3moe GGUF's tensor list (q8_0 matrices, f32 norms and
+    router) with the dims its hparams imply; overrides maps a name to
+    (type, dims) to plant a mistake."""
+    hp = dict(n_layers=1, n_embd=256, n_heads=4, n_kv_heads=2, head_dim=64, n_expert=16,
+              n_expert_used=2, n_ff_exp=64, n_vocab=64, rms_eps=1e-6, rope_base=1e6)
+    H, qd, kvd, E, F, V = 256, 256, 128, 16, 64, 64
+    spec = {"token_embd.weight": (8, [H, V]), "output.weight": (8, [H, V]),
+            "output_norm.weight": (0, [H])}
+    p = "blk.0."
+    spec.update({p + "attn_norm.weight": (0, [H]), p + "attn_q_norm.weight": (0, [64]),
+                 p + "attn_k_norm.weight": (0, [64]), p + "ffn_norm.weight": (0, [H]),
+                 p + "attn_q.weight": (8, [H, qd]), p + "attn_k.weight": (8, [H, kvd]),
+                 p + "attn_v.weight": (8, [H, kvd]), p + "attn_output.weight": (8, [qd, H]),
+                 p + "ffn_gate_inp.weight": (0, [H, E]),
+                 p + "ffn_gate_exps.weight": (8, [H, F, E]), p + "ffn_up_exps.weight": (8, [H, F, E]),
+                 p + "ffn_down_exps.weight": (8, [F, H, E])})
+    spec.update(overrides or {})
+    tens = []
+    for name, (typ, dims) in spec.items():
+        if name in drop:
+            continue
+        n = int(np.prod(dims))
+        nbytes = n * 4 if typ == 0 else n // 32 * 34
+        tens.append((name, typ, dims, np.zeros(nbytes, np.uint8)))
+    return hp, tens
+
+
+def check_file(path):
+    from styx_amd import _lib
+    lib = _lib.load()
+    hp = _lib.MoeHparams()
+    rc = lib.styx_moe_check_file(str(path).encode(), C.byref(hp))
+    if rc != 0:
+        raise ValueError(lib.styx_last_error().decode())
+    return hp
+
+
+def write_model(tmp_path, tag, hp, tens):
+    from styx_amd.gguf_io import model_metadata, write
+    p = tmp_path / f"{tag}.gguf"
+    write(p, model_metadata(hp), tens)
+    return p
+
+
+def test_model_file_accepted(tmp_path):
+    hp, tens = tiny_qwen3moe()
+    got = check_file(write_model(tmp_path, "ok", hp, tens))
+    assert (got.n_layers, got.n_embd, got.n_expert, got.n_vocab) == (1, 256, 16, 64)
+    assert got.slab_bytes == 3 * 64 * 256 // 32 * 34
+
+
+@pytest.mark.parametrize("name,typ,dims,needle", [
+    ("blk.0.ffn_gate_inp.weight", 0, [256, 8], "dims"),        # short router
+    ("output.weight", 8, [256, 32], "dims"),                   # short LM head
+    ("output_norm.weight", 0, [128], "dims"),
+    ("blk.0.attn_q_norm.weight", 0, [32], "dims"),
+    ("blk.0.ffn_down_exps.weight", 8, [64, 256, 8], "dims"),
+    ("blk.0.ffn_norm.weight", 8, [256], "expected f32"),
+    ("blk.0.attn_q.weight", 0, [256, 256], "matrix type"),
+    ("blk.0.ffn_gate_inp.bias", 0, [8], "dims"),               # optional tensor, wrong size
+])
+def test_model_file_shape_mismatch_rejected(tmp_path, name, typ, dims, needle):
+    hp, tens = tiny_qwen3moe({name: (typ, dims)})
+    with pytest.raises(ValueError) as e:
+        check_file(write_model(tmp_path, "bad", hp, tens))
+    assert needle in str(e.value) and name in str(e.value)
+
+
+def test_model_file_missing_tensor_rejected(tmp_path):
+    hp, tens = tiny_qwen3moe(drop=("blk.0.ffn_gate_inp.weight",))
+    with pytest.raises(ValueError, match="missing tensor blk.0.ffn_gate_inp.weight"):
+        check_file(write_model(tmp_path, "miss", hp, tens))
+
+
+def test_model_file_offset_near_2_64_rejected(tmp_path):
+    """An offset that makes offset + size + data_start wrap past 2^64 is
+    rejected, not taken as inside the file."""
+    hp, tens = tiny_qwen3moe()
+    p = write_model(tmp_path, "wrap", hp, tens)
+    raw = bytearray(p.read_bytes())
+    name = b"blk.0.ffn_gate_inp.weight"
+    at = raw.index(struct.pack("<Q", len(name)) + name) + 8 + len(name)
+    nd = struct.unpack_from("<I", raw, at)[0]
+    off_at = at + 4 + 8 * nd + 4
+    struct.pack_into("<Q", raw, off_at, (1 << 64) - 64)
+    p.write_bytes(bytes(raw))
+    with pytest.raises(ValueError, match="past end of file"):
+        check_file(p)
+
+
+def test_dims_product_overflow_rejected(tmp_path):
+    """Dims whose product passes 2^64 are rejected (the reference's u64
+    product would wrap in a release build)."""
+    b = header(3, 1, 0)
+    b += gstr(b"big") + u32(3) + u64(1 << 32) + u64(1 << 32) + u64(1 << 8) + u32(0) + u64(0)
+    assert_invalid(tmp_path, "ovf", b, "overflow")
+    b = header(3, 1, 0)
+    b += gstr(b"big") + u32(2) + u64(1 << 62) + u64(2) + u32(0) + u64(0)  # bytes = 2^63 * 4
+    assert_invalid(tmp_path, "ovf2", b, "overflow")

@@ -269,10 +269,14 @@ def quant_q8_0(w: np.ndarray) -> np.ndarray:
     return out.ravel()
 
 
-def tiny_model(seed=0):
+def tiny_model(seed=0, shexp=False, bias=False):
+    """Two-layer q8_0 model; shexp adds a shared expert of width 32 with its
+    sigmoid gate row, bias a per-expert router bias -1.1*ln(rank) over a
+    seeded rank permutation (the config-3 Zipf extension)."""
     rng = np.random.default_rng(seed)
+    Fs = 32 if shexp else 0
     hp = dict(n_layers=2, n_embd=256, n_heads=4, n_kv_heads=2, head_dim=64, n_expert=8,
-              n_expert_used=2, n_ff_exp=64, n_ff_shexp=0, n_vocab=96, rms_eps=1e-6,
+              n_expert_used=2, n_ff_exp=64, n_ff_shexp=Fs, n_vocab=96, rms_eps=1e-6,
               rope_base=1e4, norm_topk=1)
     H, qd, kvd, E, F, V = 256, 256, 128, 8, 64, 96
     T = {}
@@ -301,11 +305,23 @@ def tiny_model(seed=0):
         qmat(p + "ffn_gate_exps.weight", F, H, E)
         qmat(p + "ffn_up_exps.weight", F, H, E)
         qmat(p + "ffn_down_exps.weight", H, F, E)
+        if shexp:
+            qmat(p + "ffn_gate_shexp.weight", Fs, H)
+            qmat(p + "ffn_up_shexp.weight", Fs, H)
+            qmat(p + "ffn_down_shexp.weight", H, Fs)
+            f32(p + "ffn_gate_inp_shexp.weight", 0.1 * rng.standard_normal(H))
+        if bias:
+            f32(p + "ffn_gate_inp.bias", -1.1 * np.log(1 + rng.permutation(E)))
     return hp, T
 
 
-def np_forward(hp, T, toks):
-    """Independent f64 decode of a token sequence (moe.rs:1842-2073 op order)."""
+def np_forward(hp, T, toks, use_bias=True):
+    """Independent f64 decode of a token sequence (moe.rs:1842-2073 op order),
+    plus the two extensions the oracle carries: a router bias added to the
+    logits before top-k, and the shared expert
+    x += sigmoid(ginp . xn) * down_sh(silu(gate_sh xn) * up_sh xn)
+    (shaders/axpy_sig_f32.comp:2, moe.rs:127-151).  Returns per-token logits
+    and the routed ids [token][layer][k]."""
     H, nh, nkv, hd, E, k, F = 256, 4, 2, 64, 8, 2, 64
     eps, base = hp["rms_eps"], hp["rope_base"]
 
@@ -325,12 +341,16 @@ def np_forward(hp, T, toks):
         c, s = np.cos(th), np.sin(th)
         return np.concatenate([v[:, :half] * c - v[:, half:] * s, v[:, :half] * s + v[:, half:] * c], 1)
 
+    def silu(v):
+        return v / (1 + np.exp(-v))
+
     emb = deq("token_embd.weight")
     Kc = [[] for _ in range(2)]
     Vc = [[] for _ in range(2)]
-    out = []
+    out, routed = [], []
     for pos, tok in enumerate(toks):
         x = emb[tok].copy()
+        rids = []
         for l in range(2):
             p = f"blk.{l}."
             xn = rms(x, deq(p + "attn_norm.weight"))
@@ -350,23 +370,71 @@ def np_forward(hp, T, toks):
             x = x + deq(p + "attn_output.weight") @ att.ravel()
             xn = rms(x, deq(p + "ffn_norm.weight"))
             lg = deq(p + "ffn_gate_inp.weight").reshape(E, H) @ xn
+            if use_bias and p + "ffn_gate_inp.bias" in T:
+                lg = lg + deq(p + "ffn_gate_inp.bias")
             order = sorted(range(E), key=lambda i: (-lg[i], i))[:k]
+            rids.append(order)
             pr = np.exp(lg - lg.max())
             pr /= pr.sum()
             w = pr[order] / pr[order].sum()
             G, U, D = deq(p + "ffn_gate_exps.weight"), deq(p + "ffn_up_exps.weight"), deq(p + "ffn_down_exps.weight")
+            moe = np.zeros(H)
             for s_, e in enumerate(order):
                 g, u = G[e] @ xn, U[e] @ xn
-                x = x + w[s_] * (D[e] @ (g / (1 + np.exp(-g)) * u))
+                moe += w[s_] * (D[e] @ (silu(g) * u))
+            if p + "ffn_gate_shexp.weight" in T:
+                hs = silu(deq(p + "ffn_gate_shexp.weight") @ xn) * (deq(p + "ffn_up_shexp.weight") @ xn)
+                gate = 1 / (1 + np.exp(-(deq(p + "ffn_gate_inp_shexp.weight") @ xn)))
+                moe += gate * (deq(p + "ffn_down_shexp.weight") @ hs)
+            x = x + moe
         out.append(deq("output.weight") @ rms(x, deq("output_norm.weight")))
-    return out
+        routed.append(rids)
+    return out, routed
 
 
 def test_oracle_forward_matches_numpy_f64():
     hp, T = tiny_model(0)
     orc = O.OracleModel(hp, T, n_ctx=8)
     toks = [5, 60, 17, 90, 1]
-    ref = np_forward(hp, T, toks)
+    ref, _ = np_forward(hp, T, toks)
     for pos, t in enumerate(toks):
         lg, hid, ids, margins = orc.forward(pos, t, want_hidden=True)
         assert rel_l2(lg, ref[pos]) < 1e-5, pos
+
+
+def test_oracle_forward_shared_expert_and_router_bias_match_numpy_f64():
+    """The oracle's shared-expert branch (axpy_sig merge) and router-bias add
+    (styx_oracle_moe_block) against the independent f64 forward.  The bias is
+    strong enough to change the routed experts on some (token, layer), so a
+    dropped or mis-signed bias fails the id check, and the shared expert
+    moves the logits by far more than the tolerance, so a dropped branch, a
+    wrong gate sign or gate input fails the logits check."""
+    hp, T = tiny_model(3, shexp=True, bias=True)
+    orc = O.OracleModel(hp, T, n_ctx=8)
+    toks = [5, 60, 17, 90, 1, 33]
+    ref, rids = np_forward(hp, T, toks)
+    _, rids_nobias = np_forward(hp, T, toks, use_bias=False)
+    assert rids != rids_nobias, "bias must change the routing somewhere"
+    T_plain = {n: v for n, v in T.items() if "shexp" not in n}
+    ref_plain, _ = np_forward(dict(hp, n_ff_shexp=0), T_plain, toks)
+    assert min(rel_l2(a, b) for a, b in zip(ref, ref_plain)) > 1e-3
+    for pos, t in enumerate(toks):
+        lg, hid, ids, margins = orc.forward(pos, t, want_hidden=True)
+        assert rel_l2(lg, ref[pos]) < 1e-5, pos
+        for l in range(2):
+            if margins[l] > 1e-4:
+                assert ids[l].tolist() == rids[pos][l], (pos, l)
+
+
+def test_axpy_sig_closed_form():
+    """shaders/axpy_sig_f32.comp:7-11, d += sigmoid(g) * a, against f64 for
+    gates across the sigmoid's range (saturated both ways, 0 -> 1/2)."""
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal(300).astype(np.float32)
+    d = rng.standard_normal(300).astype(np.float32)
+    for g in [-100.0, -7.5, -1.0, 0.0, 0.3, 2.0, 15.0, 100.0]:
+        got = O.axpy_sig(a, g, d).astype(np.float64)
+        want = d.astype(np.float64) + a.astype(np.float64) / (1.0 + np.exp(-g))
+        assert np.abs(got - want).max() <= 4e-7 * (np.abs(want) + np.abs(a)).max(), g
+    assert np.array_equal(O.axpy_sig(a, 0.0, np.zeros_like(a)), a * np.float32(0.5))
+    assert np.array_equal(O.axpy_sig(a, 200.0, d), d + a)
