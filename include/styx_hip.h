@@ -255,7 +255,9 @@ typedef struct {
     int exp_mix;             /* 1: type(l, role) = [q4_K,q5_K,q6_K][(l+role)%3] */
     float sigma;             /* weight std, e.g. 0.02 */
     uint64_t seed;
-    float router_zipf_s;     /* >0: router bias -s*ln(rank), seeded ranks */
+    float router_zipf_s;     /* >0: Zipf(s) router bias by a seeded rank
+                                permutation per layer, from
+                                styx_zipf_bias_table(E, k, s, sigma*sqrt(H)) */
 } styx_moe_synth_cfg;
 
 /* Popularity pinning plan (crates/model/src/moe.rs:774-813), host only:
@@ -287,6 +289,15 @@ int styx_repin_select(const uint64_t *hits, int n_expert, const uint32_t *slot_e
  * n_ctx and the expert byte counts are 0).  styx_moe_load runs the same
  * checks first. */
 int styx_moe_check_file(const char *path, styx_moe_hparams *out);
+
+/* Router bias by popularity rank for the synthetic Zipf workload (no
+ * counterpart in the reference, which has no router bias): out[r] is the
+ * bias of the expert of rank r+1 such that, with router logit noise
+ * N(0, sd^2) per expert and token, top-k routing picks it with probability
+ * min(1, lambda * (r+1)^-s) per token (the pi summing to k): Zipf(s)
+ * popularity wherever top-k selection can reach it.  Fitted on a seeded
+ * sample of 4096 tokens; out[0] = 0.  Needs no GPU. */
+int styx_zipf_bias_table(int n_expert, int k, float s, float sd, uint64_t seed, float *out);
 
 /* MoeModel::load (moe.rs:536-1408) from a GGUF file. */
 int styx_moe_load(styx_gpu *gpu, const char *path, const styx_moe_opts *opts, styx_moe **out);

@@ -124,6 +124,7 @@ _SIGS = {
     "styx_residency_plan": (i32, [C.c_char_p, i32, i32, vp, i64, vp, vp]),
     "styx_repin_select": (i32, [vp, i32, vp, i32, i32, vp, vp, C.POINTER(i32)]),
     "styx_moe_check_file": (i32, [C.c_char_p, vp]),
+    "styx_zipf_bias_table": (i32, [i32, i32, C.c_float, C.c_float, u64, vp]),
     "styx_moe_fill_kv": (i32, [vp, i32, C.c_uint64, C.c_float]),
     "styx_moe_read_kv": (i32, [vp, i32, i32, i32, vp, vp]),
     "styx_op_gather_slabs": (i32, [vp, vp, vp, vp, vp, vp, i32, i32]),

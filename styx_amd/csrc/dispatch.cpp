@@ -3,6 +3,7 @@
 // (44-231, 1222-1312) over one HIP stream.  A batch records dispatches
 // (kernel, resolved bindings, push bytes, grid) and runs them in order on
 // submit, then waits -- the reference's submit + fence.
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -27,6 +28,7 @@ struct styx_batch {
     struct Cmd {
         const styx_kernel *k;
         std::vector<void *> ptr;
+        std::vector<uint64_t> size;  // bytes each binding makes visible
         std::vector<uint8_t> push;
         uint32_t gx, gy, gz;
     };
@@ -157,6 +159,8 @@ int styx_batch_dispatch(styx_batch *b, const styx_kernel *k, const styx_binding 
             return fail(STYX_E_INVALID, k->name + ": binding offset must be 64-byte aligned "
                                                   "and inside the buffer (lib.rs:98-100)");
         c.ptr.push_back((char *)bd.buf->ptr + bd.offset);
+        const uint64_t rest = bd.buf->size - bd.offset;
+        c.size.push_back(bd.range == UINT64_MAX ? rest : std::min(bd.range, rest));
     }
     c.push.assign((const uint8_t *)push, (const uint8_t *)push + push_len);
     c.gx = gx;
@@ -174,10 +178,12 @@ int styx_batch_submit(styx_batch *b)
     STYX_HIP(hipSetDevice(b->gpu->device));
     for (auto &c : b->cmds) {
         const uint32_t *spec = c.k->spec.empty() ? nullptr : c.k->spec.data();
-        hipError_t e = refk_launch(b->gpu->stream, c.k->kid, c.ptr.data(), c.push.data(), c.gx,
-                                   c.gy, c.gz, spec, (int)c.k->spec.size() / 2);
+        hipError_t e = refk_launch(b->gpu->stream, c.k->kid, c.ptr.data(), c.size.data(),
+                                   c.push.data(), c.gx, c.gy, c.gz, spec,
+                                   (int)c.k->spec.size() / 2);
         if (e == hipErrorInvalidValue)
-            return fail(STYX_E_INVALID, c.k->name + ": unsupported parameters");
+            return fail(STYX_E_INVALID, c.k->name + ": unsupported parameters, or the push "
+                                                    "constants and grid reach past a binding");
         if (e != hipSuccess) return hip_fail(e, c.k->name.c_str());
     }
     b->cmds.clear();

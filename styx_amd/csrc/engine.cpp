@@ -1276,6 +1276,66 @@ int build_model(styx_moe *m, const styx_moe_synth_cfg &c, std::vector<TensorSpec
     return STYX_OK;
 }
 
+// Router bias by popularity rank for a Zipf(s) skew under top-k routing.
+// Zipf popularity cannot be met exactly by top-k selection (for s = 1.1,
+// k = 8, E = 128 the top expert would need 1.8 picks per token), so the
+// target is the closest feasible one: the expert of rank r is picked with
+// probability pi_r = min(1, lambda * r^-s) per token, lambda such that the
+// pi sum to k (the top expert is then picked on every token, the rest
+// follow r^-s).  The biases are fitted on a seeded sample of 4096 tokens of
+// router logit noise, N(0, sd^2) per expert and token (the synthetic
+// router: weights N(0, sigma), unit-RMS normalised input, so
+// sd = sigma * sqrt(H)): each round counts the top-k picks of bias + noise
+// and moves log-popularity toward log pi.  Deterministic in the seed;
+// entry 0 (rank 1) is 0.
+std::vector<float> zipf_bias_table(int E, int k, double s, double sd, uint64_t seed)
+{
+    std::vector<double> z(E), pi(E), b(E);
+    for (int r = 0; r < E; r++) z[r] = std::pow(r + 1.0, -s);
+    double lo = 0.0, hi = 1e9;
+    for (int it = 0; it < 200; it++) {
+        const double mid = 0.5 * (lo + hi);
+        double sum = 0.0;
+        for (double v : z) sum += std::min(1.0, mid * v);
+        (sum < k ? lo : hi) = mid;
+    }
+    for (int r = 0; r < E; r++) pi[r] = std::min(1.0, hi * z[r]);
+    const int T = 4096;
+    std::vector<float> noise((size_t)T * E);
+    uint64_t st = seed;
+    for (size_t i = 0; i < noise.size(); i += 2) {
+        const double u1 = ((double)(splitmix(st) >> 11) + 1.0) * 0x1p-53;
+        const double u2 = (double)(splitmix(st) >> 11) * 0x1p-53;
+        const double rr = std::sqrt(-2.0 * std::log(u1));
+        noise[i] = (float)(sd * rr * std::cos(6.283185307179586 * u2));
+        if (i + 1 < noise.size()) noise[i + 1] = (float)(sd * rr * std::sin(6.283185307179586 * u2));
+    }
+    for (int r = 0; r < E; r++) b[r] = sd * std::log(pi[r]);
+    std::vector<int> cnt(E);
+    std::vector<std::pair<float, int>> row(E);
+    for (int it = 0; it < 300; it++) {
+        std::fill(cnt.begin(), cnt.end(), 0);
+        for (int t = 0; t < T; t++) {
+            for (int e = 0; e < E; e++) row[e] = {(float)b[e] + noise[(size_t)t * E + e], e};
+            std::nth_element(row.begin(), row.begin() + (k - 1), row.end(),
+                             [](const std::pair<float, int> &x, const std::pair<float, int> &y) {
+                                 return x.first > y.first || (x.first == y.first && x.second < y.second);
+                             });
+            for (int i = 0; i < k; i++) cnt[row[i].second]++;
+        }
+        for (int r = 0; r < E; r++) {
+            const double p = std::max((double)cnt[r], 0.5) / T;
+            b[r] += 0.3 * sd * (std::log(pi[r]) - std::log(p));
+        }
+    }
+    // popularity falls with rank: the tail's few picks per round leave
+    // sampling noise, which a running minimum removes
+    for (int r = 1; r < E; r++) b[r] = std::min(b[r], b[r - 1]);
+    std::vector<float> out(E);
+    for (int r = 0; r < E; r++) out[r] = (float)(b[r] - b[0]);
+    return out;
+}
+
 int read_hist(const char *path, int L, std::vector<std::vector<std::pair<uint32_t, uint64_t>>> &h)
 {
     std::ifstream f(path);
@@ -1319,6 +1379,15 @@ int styx_residency_plan(const char *hist_csv, int n_layers, int n_expert,
         n += hot[l].size();
     }
     if (pinned_slabs) *pinned_slabs = n;
+    return STYX_OK;
+}
+
+int styx_zipf_bias_table(int n_expert, int k, float s, float sd, uint64_t seed, float *out)
+{
+    if (n_expert < 1 || k < 1 || k > n_expert || !(s > 0) || !(sd > 0) || !out)
+        return fail(STYX_E_INVALID, "styx_zipf_bias_table: bad argument");
+    const std::vector<float> t = zipf_bias_table(n_expert, k, s, sd, seed);
+    std::copy(t.begin(), t.end(), out);
     return STYX_OK;
 }
 
@@ -1368,19 +1437,23 @@ int styx_moe_synth(styx_gpu *gpu, const styx_moe_synth_cfg *cfg, const styx_moe_
     m->n_ctx = m->opts.n_ctx > 0 ? m->opts.n_ctx : 4096;
     const styx_moe_synth_cfg c = *cfg;
     auto specs = model_specs(c);
-    // router bias for Zipf-skewed routing: b_e = -s * ln(rank_e), ranks a
-    // seeded permutation per layer
+    // router bias for Zipf-skewed routing: the bias of rank r from a table
+    // calibrated to the synthetic router's logit spread, ranks a seeded
+    // permutation per layer
     std::vector<std::vector<float>> biases(c.n_layers);
-    if (c.router_zipf_s > 0)
+    if (c.router_zipf_s > 0) {
+        const std::vector<float> tab =
+            zipf_bias_table(c.n_expert, c.n_expert_used, c.router_zipf_s,
+                            (double)c.sigma * std::sqrt((double)c.n_embd), c.seed ^ 0x5A1Full);
         for (int l = 0; l < c.n_layers; l++) {
             std::vector<int> rank(c.n_expert);
             std::iota(rank.begin(), rank.end(), 1);
             uint64_t s = c.seed ^ fnv1a64("zipf." + std::to_string(l));
             for (int i = c.n_expert - 1; i > 0; i--) std::swap(rank[i], rank[splitmix(s) % (i + 1)]);
             biases[l].resize(c.n_expert);
-            for (int e = 0; e < c.n_expert; e++)
-                biases[l][e] = (float)(-(double)c.router_zipf_s * std::log((double)rank[e]));
+            for (int e = 0; e < c.n_expert; e++) biases[l][e] = tab[rank[e] - 1];
         }
+    }
     auto source = [&](const TensorSpec &t) {
         Source s;
         s.seed = c.seed ^ fnv1a64(t.name);

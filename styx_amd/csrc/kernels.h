@@ -231,10 +231,12 @@ hipError_t launch_gather(hipStream_t st, const uint8_t *const src[3], const int6
                          uint8_t *const dst[3], const int64_t dst_slab[3],
                          const int32_t *ids, const Route *route, int k);
 // Plain gather with explicit expert list (reference binding: ids = expert
-// per slot, arena slot layer*k+s).
+// per slot, arena slot layer*k+s).  src_count (or null): slabs readable in
+// each source; an id at or past it is skipped like SKIP.
 hipError_t launch_gather_list(hipStream_t st, const uint8_t *const src[3],
                               const int64_t src_slab[3], uint8_t *const dst[3],
-                              const int64_t dst_slab[3], const int32_t *ids, int k, int layer);
+                              const int64_t dst_slab[3], const int32_t *ids, int k, int layer,
+                              const int64_t *src_count = nullptr);
 
 // GGUF block layout <-> split layout, for nmat matrices of nblocks blocks.
 hipError_t launch_to_split(hipStream_t st, int t, const uint8_t *src, uint8_t *dst,

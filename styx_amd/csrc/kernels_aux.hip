@@ -253,6 +253,7 @@ struct GatherK {
     const int32_t *ids;
     Route route;  // mode 0 with route.logits: the id row is computed in-kernel
     int k, layer, mode;  // mode 0: arena row of an id row; 1: expert list
+    int64_t src_count[3];  // mode 1: slabs readable per source (0: unbounded)
 };
 
 __global__ void __launch_bounds__(256) k_gather(GatherK a)
@@ -275,7 +276,7 @@ __global__ void __launch_bounds__(256) k_gather(GatherK a)
         if (slot == SKIP) return;
     } else {
         e = (uint32_t)a.ids[s];
-        if (e == SKIP) return;
+        if (e == SKIP || (a.src_count[t] > 0 && (int64_t)e >= a.src_count[t])) return;
         slot = (uint32_t)(a.layer * a.k + s);
     }
     const int64_t n16 = a.src_slab[t] / 16;
@@ -289,7 +290,7 @@ __global__ void __launch_bounds__(256) k_gather(GatherK a)
 static hipError_t gather_launch(hipStream_t st, const uint8_t *const src[3],
                                 const int64_t src_slab[3], uint8_t *const dst[3],
                                 const int64_t dst_slab[3], const int32_t *ids, const Route *route,
-                                int k, int layer, int mode)
+                                int k, int layer, int mode, const int64_t *src_count = nullptr)
 {
     if (route && (route->E < k || route->E > MAX_EXPERTS || route->E % 16 || route->k != k))
         return hipErrorInvalidValue;
@@ -303,6 +304,7 @@ static hipError_t gather_launch(hipStream_t st, const uint8_t *const src[3],
         a.src_slab[t] = src_slab[t];
         a.dst[t] = dst[t];
         a.dst_slab[t] = dst_slab[t];
+        a.src_count[t] = src_count ? src_count[t] : 0;
         mx = std::max(mx, src_slab[t]);
     }
     a.ids = ids;
@@ -323,9 +325,10 @@ hipError_t launch_gather(hipStream_t st, const uint8_t *const src[3], const int6
 
 hipError_t launch_gather_list(hipStream_t st, const uint8_t *const src[3],
                               const int64_t src_slab[3], uint8_t *const dst[3],
-                              const int64_t dst_slab[3], const int32_t *ids, int k, int layer)
+                              const int64_t dst_slab[3], const int32_t *ids, int k, int layer,
+                              const int64_t *src_count)
 {
-    return gather_launch(st, src, src_slab, dst, dst_slab, ids, nullptr, k, layer, 1);
+    return gather_launch(st, src, src_slab, dst, dst_slab, ids, nullptr, k, layer, 1, src_count);
 }
 
 // ---------------------------------------------------------- generator ----

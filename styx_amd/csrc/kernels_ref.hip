@@ -9,6 +9,7 @@
 #include "refk.h"
 #include "topk.h"
 
+#include <algorithm>
 #include <cstring>
 
 namespace styx {
@@ -141,6 +142,7 @@ struct MmvRef {
     int type;
     uint32_t ncols, stride_a, stride_b, stride_d, batch_stride_a, batch_stride_b, batch_stride_d;
     uint32_t ne11, expert_i1, nbi1, nrows, num_rows;
+    int64_t n_mat;  // matrices readable from A (ids at or past it are skipped)
 };
 
 __global__ void __launch_bounds__(64) kr_mmv(MmvRef p)
@@ -151,7 +153,7 @@ __global__ void __launch_bounds__(64) kr_mmv(MmvRef p)
     if (p.ids) {
         // get_offsets() of mul_mat_vec_base (crates/vk-backend/tests/kernels.rs:124-131)
         const uint32_t e = (uint32_t)p.ids[slot + p.expert_i1 * p.nbi1];
-        if (e == SKIP) return;
+        if (e == SKIP || (int64_t)e >= p.n_mat) return;
         a_blk = (int64_t)e * (p.batch_stride_a / be);
         b_off = (int64_t)(slot % p.ne11) * p.stride_b + (int64_t)p.expert_i1 * p.batch_stride_b;
         d_off = (int64_t)slot * p.stride_d + (int64_t)p.expert_i1 * p.batch_stride_d;
@@ -181,31 +183,58 @@ __global__ void __launch_bounds__(64) kr_topk(const float *logits, float *w, int
     topk_wave(logits, (int)n, (int)k, (int)renorm, remap, pmap, 0, 0, w, ids);
 }
 
-hipError_t refk_launch(hipStream_t st, int kid, void *const *ptr, const void *push, uint32_t gx,
-                       uint32_t gy, uint32_t gz, const uint32_t *spec, int n_spec)
+// Whether n elements of `bytes_each` bytes fit in a binding of `size` bytes
+// (n may be 0).
+static bool fits(uint64_t size, uint64_t n, uint64_t bytes_each)
+{
+    return n == 0 || (bytes_each != 0 && n <= size / bytes_each);
+}
+
+hipError_t refk_launch(hipStream_t st, int kid, void *const *ptr, const uint64_t *size,
+                       const void *push, uint32_t gx, uint32_t gy, uint32_t gz,
+                       const uint32_t *spec, int n_spec)
 {
     const uint32_t *pc = (const uint32_t *)push;
+    const hipError_t bad = hipErrorInvalidValue;
     switch (kid) {
-    case RK_MOE_REDUCE:
+    case RK_MOE_REDUCE: {
+        // push: ne, k
+        const uint64_t ne = pc[0], k = pc[1];
+        if (!fits(size[0], k * ne, 4) || !fits(size[1], k, 4) || !fits(size[2], ne, 4)) return bad;
         hipLaunchKernelGGL(kr_moe_reduce, dim3(gx), dim3(256), 0, st, (const float *)ptr[0],
                            (const float *)ptr[1], (float *)ptr[2], pc[0], pc[1]);
         break;
+    }
     case RK_ADD:
+        if (!fits(size[0], pc[0], 4) || !fits(size[1], pc[0], 4) || !fits(size[2], pc[0], 4)) return bad;
         hipLaunchKernelGGL(kr_add, dim3(gx), dim3(256), 0, st, (const float *)ptr[0],
                            (const float *)ptr[1], (float *)ptr[2], pc[0]);
         break;
     case RK_AXPY_SIG:
+        if (!fits(size[0], pc[0], 4) || !fits(size[1], 1, 4) || !fits(size[2], pc[0], 4)) return bad;
         hipLaunchKernelGGL(kr_axpy_sig, dim3(gx), dim3(256), 0, st, (const float *)ptr[0],
                            (const float *)ptr[1], (float *)ptr[2], pc[0]);
         break;
-    case RK_MATVEC_STRIDED:
+    case RK_MATVEC_STRIDED: {
+        // push: ncols, stride; one row per workgroup
+        const uint64_t nc = pc[0], stride = pc[1];
+        if (!fits(size[0], (uint64_t)(gx - 1) * stride + nc, 4) || !fits(size[1], nc, 4) ||
+            !fits(size[2], gx, 4))
+            return bad;
         hipLaunchKernelGGL(kr_matvec_strided, dim3(gx), dim3(32), 0, st, (const float *)ptr[0],
                            (const float *)ptr[1], (float *)ptr[2], pc[0], pc[1]);
         break;
+    }
     case RK_ATTN: {
+        // push: n_t, hd, kv_dim, gqa, scale; one query head per workgroup
         float scale;
         std::memcpy(&scale, pc + 4, 4);
-        if (pc[1] > 256 || pc[3] == 0) return hipErrorInvalidValue;
+        const uint64_t n_t = pc[0], hd = pc[1], kvd = pc[2], gqa = pc[3];
+        if (hd == 0 || hd > 256 || gqa == 0) return bad;
+        const uint64_t kv_need = n_t ? (n_t - 1) * kvd + ((gx - 1) / gqa) * hd + hd : 0;
+        if (!fits(size[0], (uint64_t)gx * hd, 4) || !fits(size[1], kv_need, 4) ||
+            !fits(size[2], kv_need, 4) || !fits(size[3], (uint64_t)gx * hd, 4))
+            return bad;
         hipLaunchKernelGGL(kr_attn_decode, dim3(gx), dim3(128), 0, st, (const float *)ptr[0],
                            (const float *)ptr[1], (const float *)ptr[2], (float *)ptr[3], pc[0],
                            pc[1], pc[2], pc[3], scale);
@@ -213,6 +242,7 @@ hipError_t refk_launch(hipStream_t st, int kid, void *const *ptr, const void *pu
     }
     case RK_SWIGLU:
         // GluPush: n is the first field
+        if (!fits(size[0], pc[0], 4) || !fits(size[1], pc[0], 4) || !fits(size[2], pc[0], 4)) return bad;
         hipLaunchKernelGGL(kr_swiglu, dim3((pc[0] + 255) / 256), dim3(256), 0, st,
                            (const float *)ptr[0], (const float *)ptr[1], (float *)ptr[2], pc[0]);
         break;
@@ -223,30 +253,45 @@ hipError_t refk_launch(hipStream_t st, int kid, void *const *ptr, const void *pu
         int mul = 1;
         for (int i = 0; i + 1 < 2 * n_spec; i += 2)
             if (spec[i] == 1) mul = spec[i + 1] != 0;
+        const uint64_t nc = pc[1], arow = pc[6], drow = pc[22];
+        if (!fits(size[0], (uint64_t)(gx - 1) * arow + nc, 4) || (mul && !fits(size[1], nc, 4)) ||
+            !fits(size[2], (uint64_t)(gx - 1) * drow + nc, 4))
+            return bad;
         hipLaunchKernelGGL(kr_rms_norm, dim3(gx), dim3(256), 0, st, (const float *)ptr[0],
                            (const float *)ptr[1], (float *)ptr[2], pc[1], pc[6], pc[22], eps, mul);
         break;
     }
     case RK_TOPK:
+        // push: n, k, renorm; writes the 64-entry id row
         if (pc[0] < 1 || pc[0] > MAX_EXPERTS || pc[1] < 1 || pc[1] > MAX_TOPK)
-            return hipErrorInvalidValue;
+            return bad;
+        if (!fits(size[0], pc[0], 4) || !fits(size[1], pc[1], 4) || !fits(size[2], IDS_ROW, 4) ||
+            !fits(size[3], pc[0], 4) || !fits(size[4], pc[0], 4))
+            return bad;
         hipLaunchKernelGGL(kr_topk, dim3(1), dim3(64), 0, st, (const float *)ptr[0],
                            (float *)ptr[1], (int32_t *)ptr[2], (const uint32_t *)ptr[3],
                            (const uint32_t *)ptr[4], pc[0], pc[1], pc[2]);
         break;
     case RK_GATHER: {
         // push: dst_vg, dst_vu, dst_vd, src_vg, src_vu, src_vd, layer, k, canary
-        if (pc[8] != 0) return hipErrorInvalidValue;
+        if (pc[8] != 0) return bad;
         const uint8_t *src[3] = {(const uint8_t *)ptr[0], (const uint8_t *)ptr[1],
                                  (const uint8_t *)ptr[2]};
         uint8_t *dst[3] = {(uint8_t *)ptr[3], (uint8_t *)ptr[4], (uint8_t *)ptr[5]};
         const int64_t ss[3] = {16ll * pc[3], 16ll * pc[4], 16ll * pc[5]};
         const int64_t ds[3] = {16ll * pc[0], 16ll * pc[1], 16ll * pc[2]};
+        const uint64_t k = pc[7], slots = ((uint64_t)pc[6] + 1) * k;
+        if (k < 1 || k > MAX_TOPK || !fits(size[6], k, 4)) return bad;
+        int64_t cnt[3];
+        for (int t = 0; t < 3; t++) {
+            if (ss[t] == 0 || !fits(size[3 + t], slots, (uint64_t)ds[t])) return bad;
+            cnt[t] = (int64_t)(size[t] / (uint64_t)ss[t]);
+        }
         return launch_gather_list(st, src, ss, dst, ds, (const int32_t *)ptr[6], (int)pc[7],
-                                  (int)pc[6]);
+                                  (int)pc[6], cnt);
     }
     default: {
-        if (kid < RK_MMV_BASE || kid >= RK_MMV_BASE + 8) return hipErrorInvalidValue;
+        if (kid < RK_MMV_BASE || kid >= RK_MMV_BASE + 8) return bad;
         const int ti = (kid - RK_MMV_BASE) % 4;
         const bool with_id = kid >= RK_MMV_BASE + 4;
         static const int types[4] = {T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K};
@@ -262,7 +307,8 @@ hipError_t refk_launch(hipStream_t st, int kid, void *const *ptr, const void *pu
         p.batch_stride_a = pc[4];
         p.batch_stride_b = pc[5];
         p.batch_stride_d = pc[6];
-        if (p.ncols % blk_elems(p.type)) return hipErrorInvalidValue;
+        const uint64_t be = blk_elems(p.type), bb = blk_bytes(p.type), nb = p.ncols / be;
+        if (p.ncols == 0 || p.ncols % be || p.stride_a < nb) return bad;
         if (with_id) {
             // MatVecIdPush: ..., fusion_flags, nei0, ne11, expert_i1, nbi1
             p.ids = (const int32_t *)ptr[5];
@@ -271,12 +317,30 @@ hipError_t refk_launch(hipStream_t st, int kid, void *const *ptr, const void *pu
             p.nbi1 = pc[11];
             p.nrows = gx;
             p.num_rows = 1;
+            if (p.batch_stride_a % be) return bad;
+            // one matrix: nrows rows of stride_a blocks, within the expert stride
+            const uint64_t mat_blocks = (uint64_t)p.batch_stride_a / be;
+            const uint64_t used_blocks = (uint64_t)(p.nrows - 1) * p.stride_a + nb;
+            if (mat_blocks == 0 || used_blocks > mat_blocks) return bad;
+            p.n_mat = (int64_t)(size[0] / (mat_blocks * bb));
+            const uint64_t nsl = gy, ne11 = p.ne11;
+            const uint64_t b_need = (std::min<uint64_t>(nsl, ne11) - 1) * p.stride_b +
+                                    (uint64_t)p.expert_i1 * p.batch_stride_b + p.ncols;
+            const uint64_t d_need = (nsl - 1) * p.stride_d +
+                                    (uint64_t)p.expert_i1 * p.batch_stride_d + p.nrows;
+            const uint64_t id_need = (nsl - 1) + (uint64_t)p.expert_i1 * p.nbi1 + 1;
+            if (!fits(size[1], b_need, 4) || !fits(size[2], d_need, 4) || !fits(size[5], id_need, 4))
+                return bad;
         } else {
             // MatVecPush: stride_d = nrows (MatVecPush::simple); NUM_ROWS spec id 1
             p.num_rows = 1;
             for (int i = 0; i + 1 < 2 * n_spec; i += 2)
                 if (spec[i] == 1) p.num_rows = spec[i + 1] ? spec[i + 1] : 1;
             p.nrows = p.stride_d;
+            p.n_mat = 1;
+            if (p.nrows == 0 || !fits(size[0], (uint64_t)(p.nrows - 1) * p.stride_a + nb, bb) ||
+                !fits(size[1], p.ncols, 4) || !fits(size[2], p.nrows, 4))
+                return bad;
         }
         hipLaunchKernelGGL(kr_mmv, dim3(gx, with_id ? gy : 1, 1), dim3(64), 0, st, p);
         break;

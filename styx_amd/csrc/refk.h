@@ -19,9 +19,14 @@ enum RefKernel {
     RK_MMV_BASE = 32,  // +0..3 mul_mat_vec_{q8_0,q4_k,q5_k,q6_k}, +4..7 the _id forms
 };
 
-// Launch reference kernel `kid` with resolved binding pointers, the raw
-// push-constant block, the reference grid and spec constants (id, value pairs).
-hipError_t refk_launch(hipStream_t st, int kid, void *const *ptr, const void *push, uint32_t gx,
-                       uint32_t gy, uint32_t gz, const uint32_t *spec, int n_spec);
+// Launch reference kernel `kid` with resolved binding pointers and the bytes
+// each binding makes visible, the raw push-constant block, the reference
+// grid and spec constants (id, value pairs).  Returns hipErrorInvalidValue,
+// launching nothing, when the push constants and grid would reach past a
+// binding; ids read from device memory that name a matrix or slab past its
+// binding are treated as SKIP by the kernels.
+hipError_t refk_launch(hipStream_t st, int kid, void *const *ptr, const uint64_t *size,
+                       const void *push, uint32_t gx, uint32_t gy, uint32_t gz,
+                       const uint32_t *spec, int n_spec);
 
 }  // namespace styx

@@ -1,0 +1,329 @@
+"""GPU tests of the drop-in dispatch level of the boundary: the reference's
+pipeline names, binding order and push-constant bytes through
+styx_kernel_get + styx_batch_dispatch + styx_batch_submit (the
+Gpu::create_pipeline / Batch surface of crates/vk-backend/src/lib.rs), with
+the reference tests' own seeds, shapes and tolerances where a reference test
+exists (crates/vk-backend/tests/{kernels,ops2}.rs), checked against the CPU
+oracle.  Quant weights are in GGUF block layout, as the reference uploads
+them."""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+import pytest
+
+from helpers import Lcg, clamp_f16_exponents, rel_l2
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SKIP = 0xFFFFFFFF
+BLK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+F16_AT = {8: (0,), 12: (0, 2), 13: (0, 2), 14: (208,)}
+NAME = {8: "q8_0", 12: "q4_k", 13: "q5_k", 14: "q6_k"}
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    from styx_amd import Gpu
+    g = Gpu(0)
+    yield g
+    g.close()
+
+
+def run(gpu, name, binds, push: bytes, grid, spec=()):
+    from styx_amd.runtime import Batch, Kernel
+    k = Kernel(gpu, name, list(spec))
+    b = Batch(gpu)
+    b.begin()
+    b.dispatch(k, binds, push, grid)
+    b.submit()
+    b.free()
+    k.free()
+
+
+def f32buf(gpu, a):
+    return gpu.from_numpy(np.ascontiguousarray(a, np.float32))
+
+
+def sum_bound(t, a, rows, cols, x):
+    """|y - y_exact| <= cols * 2^-24 * sum |w x| for any f32 summation order
+    of the dot product (Higham, Accuracy and Stability, eq. 3.5)."""
+    w = O.dequant(t, a, rows * cols).reshape(rows, cols).astype(np.float64)
+    return cols * 2.0 ** -24 * (np.abs(w) @ np.abs(x.astype(np.float64)))
+
+
+def mmv_id_push(ncols, nrows, be, k, ne11=1, batch_stride_a=None):
+    # MatVecIdPush (ops.rs:123-136), as moe.rs:1576-1589 fills it
+    return struct.pack("<12I", ncols, ncols // be, ncols, nrows,
+                       batch_stride_a if batch_stride_a is not None else nrows * ncols,
+                       ncols, k * nrows, 0, k, ne11, 0, 1)
+
+
+def test_mul_mat_vec_id_q4_k_routing(gpu):
+    """kernels.rs:150-285: 8 q4_K experts of 32 x 512 (LCG 0xcafef00d, f16
+    exponents clamped), ids [6,1,3,0], grid (32, 4); each slot within the
+    reference's 2e-2 relative and the f32 forward-error bound of its
+    expert's f64 matvec; routing [0,6,1,3] permutes the slots exactly."""
+    r = Lcg(0xCAFEF00D)
+    a = r.bytes(8 * 32 * 2 * 144)
+    clamp_f16_exponents(a, 144, (0, 2))
+    x = r.f32s(512)
+    ebytes = 32 * 2 * 144
+    ba, bx, bd = gpu.from_numpy(a), f32buf(gpu, x), gpu.zeros(4 * 32 * 4)
+    f0, f1 = gpu.zeros(16), gpu.zeros(16)
+    ids = gpu.from_numpy(np.array([6, 1, 3, 0], np.int32))
+    push = mmv_id_push(512, 32, 256, 4)
+    run(gpu, "mul_mat_vec_id_q4_k_f32_f32", [ba, bx, bd, f0, f1, ids], push, (32, 4, 1),
+        [(0, 32), (1, 1), (2, 1)])
+    got = bd.download(np.float32)
+    for s, e in enumerate([6, 1, 3, 0]):
+        w = a[e * ebytes:(e + 1) * ebytes]
+        y64 = O.matvec_f64(12, w, 32, 512, x)
+        g = got[32 * s:32 * s + 32].astype(np.float64)
+        assert (np.abs(g - y64) <= sum_bound(12, w, 32, 512, x)).all(), s
+        assert np.max(np.abs(g - y64) / np.maximum(np.abs(y64), 1e-3)) < 2e-2
+    ids.upload(np.array([0, 6, 1, 3], np.int32))
+    run(gpu, "mul_mat_vec_id_q4_k_f32_f32", [ba, bx, bd, f0, f1, ids], push, (32, 4, 1),
+        [(0, 32), (1, 1), (2, 1)])
+    got2 = bd.download(np.float32)
+    assert np.array_equal(got2[:32], got[96:128]) and np.array_equal(got2[32:64], got[:32])
+
+
+@pytest.mark.parametrize("t", [8, 13, 14])
+def test_mul_mat_vec_id_other_types_skip_and_ne11(gpu, t):
+    """The q8_0 / q5_K / q6_K expert pipelines (no reference test covers q5_K
+    and q6_K: parity against the oracle's public-format decoders), with a
+    SKIP slot left untouched and ne11 = k (slot s reads x[s], the down
+    projection's binding, moe.rs:2039-2048)."""
+    be, bb = BLK[t]
+    E, rows, cols, k = 6, 48, 512, 3
+    rng = np.random.default_rng(40 + t)
+    a = rng.integers(0, 256, E * rows * (cols // be) * bb).astype(np.uint8)
+    clamp_f16_exponents(a, bb, F16_AT[t])
+    x = rng.standard_normal(k * cols).astype(np.float32)
+    sentinel = np.full(k * rows, 7.0, np.float32)
+    ba, bx, bd = gpu.from_numpy(a), f32buf(gpu, x), f32buf(gpu, sentinel)
+    f0, f1 = gpu.zeros(16), gpu.zeros(16)
+    idl = [4, SKIP, 1]
+    ids = gpu.from_numpy(np.array(idl, np.uint32))
+    run(gpu, f"mul_mat_vec_id_{NAME[t]}_f32_f32", [ba, bx, bd, f0, f1, ids],
+        mmv_id_push(cols, rows, be, k, ne11=k), (rows, k, 1))
+    got = bd.download(np.float32)
+    ebytes = rows * (cols // be) * bb
+    assert (got[rows:2 * rows] == 7.0).all()
+    for s, e in enumerate(idl):
+        if e == SKIP:
+            continue
+        w = a[e * ebytes:(e + 1) * ebytes]
+        xs = x[s * cols:(s + 1) * cols]
+        y64 = O.matvec_f64(t, w, rows, cols, xs)
+        assert (np.abs(got[s * rows:(s + 1) * rows] - y64) <= sum_bound(t, w, rows, cols, xs)).all()
+
+
+def test_mul_mat_vec_id_out_of_range_expert_is_skipped(gpu):
+    """An id naming a matrix past the weight binding is skipped like SKIP
+    (the slot keeps its contents) instead of reading past the buffer."""
+    t, rows, cols = 8, 16, 64
+    a = np.random.default_rng(3).integers(0, 256, 2 * rows * 2 * 34).astype(np.uint8)
+    clamp_f16_exponents(a, 34, (0,))
+    x = np.ones(cols, np.float32)
+    bd = f32buf(gpu, np.full(2 * rows, 5.0, np.float32))
+    ids = gpu.from_numpy(np.array([1, 9], np.int32))
+    run(gpu, "mul_mat_vec_id_q8_0_f32_f32",
+        [gpu.from_numpy(a), f32buf(gpu, x), bd, gpu.zeros(16), gpu.zeros(16), ids],
+        mmv_id_push(cols, rows, 32, 2), (rows, 2, 1))
+    got = bd.download(np.float32)
+    assert (got[rows:] == 5.0).all()
+    assert np.allclose(got[:rows], O.matvec_f64(8, a[rows * 68:], rows, cols, x), rtol=1e-5, atol=1e-5)
+
+
+def test_mul_mat_vec_q8_0(gpu):
+    """ops2.rs:225-292: LCG 0x51ce, 128 x 1024 q8_0, MatVecPush::simple with
+    block stride, grid (128, 1, 1); reference tolerance 1e-3 relative, and
+    the f32 forward-error bound."""
+    r = Lcg(0x51CE)
+    a = r.bytes(128 * 32 * 34)
+    clamp_f16_exponents(a, 34, (0,))
+    x = r.f32s(1024)
+    bd = gpu.zeros(128 * 4)
+    push = struct.pack("<13I", 1024, 32, 1024, 128, 128 * 1024, 1024, 128, 0, 0, 1, 1, 1, 1)
+    run(gpu, "mul_mat_vec_q8_0_f32_f32", [gpu.from_numpy(a), f32buf(gpu, x), bd, gpu.zeros(16),
+                                          gpu.zeros(16)], push, (128, 1, 1),
+        [(0, 32), (1, 1), (2, 1)])
+    got = bd.download(np.float32).astype(np.float64)
+    y64 = O.matvec_f64(8, a, 128, 1024, x)
+    assert (np.abs(got - y64) <= sum_bound(8, a, 128, 1024, x)).all()
+    assert np.max(np.abs(got - y64) / np.maximum(np.abs(y64), 1e-3)) < 1e-3
+
+
+def test_rms_norm(gpu):
+    """kernels.rs:41-122: LCG 0x12345678, 4 rows of 2048, eps 1e-6,
+    do_multiply = 0 (spec (1, 0)); reference tolerance 1e-5 absolute."""
+    x = Lcg(0x12345678).f32s(2048 * 4)
+    dims = lambda n0, n1: [n0, n1, 1, 1, 1, n0, n0 * n1, n0 * n1]
+    push = struct.pack("<25I", 2048 * 4, *dims(2048, 4), *dims(2048, 1), *dims(2048, 4)) + \
+        struct.pack("<I2fi", 0, 1e-6, 0.0, 0)
+    bd = gpu.zeros(2048 * 4 * 4)
+    run(gpu, "rms_norm_f32", [f32buf(gpu, x), f32buf(gpu, np.ones(2048)), bd], push, (4, 1, 1),
+        [(1, 0)])
+    got = bd.download(np.float32).reshape(4, 2048)
+    xr = x.reshape(4, 2048).astype(np.float64)
+    ref = xr / np.sqrt((xr ** 2).mean(1, keepdims=True) + 1e-6)
+    assert np.max(np.abs(got - ref)) < 1e-5
+    assert np.max(np.abs(got - O.rms_norm(x, None, 2048, 4, 1e-6).reshape(4, 2048))) < 1e-6
+
+
+def test_swiglu(gpu):
+    """ops2.rs:296-348: LCG 0x5119, gate = 4 * lcg, up = lcg, n = 3072 x 2,
+    GluPush::split, grid ceil(n / 512); reference tolerance 1e-5."""
+    r = Lcg(0x5119)
+    n = 3072 * 2
+    g = (r.f32s(n) * np.float32(4.0)).astype(np.float32)
+    u = r.f32s(n)
+    push = struct.pack("<27I", n, *([0] * 26))  # n first; the other fields are strides
+    bd = gpu.zeros(n * 4)
+    run(gpu, "swiglu_f32", [f32buf(gpu, g), f32buf(gpu, u), bd], push, ((n + 511) // 512, 1, 1))
+    got = bd.download(np.float32)
+    gd = g.astype(np.float64)
+    assert np.max(np.abs(got - gd / (1 + np.exp(-gd)) * u)) < 1e-5
+    assert np.max(np.abs(got - O.swiglu(g, u))) < 1e-6
+
+
+def test_topk_softmax(gpu):
+    """topk_softmax_f32 (shaders/topk_softmax_f32.comp) with its five
+    bindings: ids bit-exact against the oracle including the hot / arena /
+    host rows, weights within 1e-6 relative; tied logits keep the lower
+    index."""
+    rng = np.random.default_rng(5)
+    E, k = 128, 8
+    lg = rng.standard_normal(E).astype(np.float32)
+    lg[17] = lg[90] = np.float32(lg.max() + 0.5)          # a tie at the top
+    remap = np.full(E, SKIP, np.uint32)
+    remap[::3] = np.arange(len(remap[::3]))
+    pmap = np.full(E, SKIP, np.uint32)
+    pmap[1::3] = 40 + np.arange(len(pmap[1::3]))
+    bw, bi = gpu.zeros(64), gpu.from_numpy(np.full(64, -7, np.int32))
+    run(gpu, "topk_softmax_f32", [f32buf(gpu, lg), bw, bi, gpu.from_numpy(remap),
+                                  gpu.from_numpy(pmap)], struct.pack("<3I", E, k, 1), (1, 1, 1))
+    w_ref, ids_ref = O.topk_softmax(lg, k, True, remap, pmap)
+    ids = bi.download(np.int32)
+    for row in (0, 16, 32, 48):
+        assert np.array_equal(ids[row:row + k], ids_ref[row:row + k]), row
+    assert ids[0] == 17 and ids[1] == 90
+    assert rel_l2(bw.download(np.float32, k), w_ref) < 1e-6
+
+
+def test_moe_reduce_add_axpy_sig(gpu):
+    """moe_reduce_f32 (x += sum_s w_s d_s, s ascending), add_flat_f32 and
+    axpy_sig_f32 (shaders/*.comp) against the oracle: the reduce bit for
+    bit (same order, no contraction), the sigmoid merge within 2 ulp."""
+    rng = np.random.default_rng(6)
+    ne, k = 2048, 8
+    d = rng.standard_normal(k * ne).astype(np.float32)
+    w = rng.random(k).astype(np.float32)
+    x = rng.standard_normal(ne).astype(np.float32)
+    bx = f32buf(gpu, x)
+    run(gpu, "moe_reduce_f32", [f32buf(gpu, d), f32buf(gpu, w), bx], struct.pack("<2I", ne, k),
+        ((ne + 255) // 256, 1, 1))
+    assert np.array_equal(bx.download(np.float32), O.moe_reduce(d, w, ne, k, x))
+    a, b = d[:ne], d[ne:2 * ne]
+    bo = gpu.zeros(ne * 4)
+    run(gpu, "add_flat_f32", [f32buf(gpu, a), f32buf(gpu, b), bo], struct.pack("<I", ne),
+        ((ne + 255) // 256, 1, 1))
+    assert np.array_equal(bo.download(np.float32), a + b)
+    for g0 in (-3.0, 0.0, 1.7):
+        bd = f32buf(gpu, x)
+        run(gpu, "axpy_sig_f32", [f32buf(gpu, a), f32buf(gpu, np.array([g0])), bd],
+            struct.pack("<I", ne), ((ne + 255) // 256, 1, 1))
+        ref = O.axpy_sig(a, g0, x)
+        assert np.max(np.abs(bd.download(np.float32) - ref)) <= 2 * np.spacing(np.abs(ref).max())
+
+
+def test_matvec_strided(gpu):
+    """matvec_strided_f32 (the router, shaders/matvec_strided_f32.comp): the
+    shader's 32 lane-strided partials and halving tree, as the oracle
+    restates them; against the oracle within 1 ulp-scale and f64 within
+    the forward-error bound."""
+    rng = np.random.default_rng(7)
+    E, H = 128, 2048
+    W = (0.02 * rng.standard_normal(E * H)).astype(np.float32)
+    x = rng.standard_normal(H).astype(np.float32)
+    bd = gpu.zeros(E * 4)
+    run(gpu, "matvec_strided_f32", [f32buf(gpu, W), f32buf(gpu, x), bd], struct.pack("<2I", H, H),
+        (E, 1, 1))
+    got = bd.download(np.float32)
+    ref = O.router_strided(W, x, E, H)
+    assert np.max(np.abs(got - ref)) <= 4 * np.spacing(np.abs(ref).max())
+    Wd = W.reshape(E, H).astype(np.float64)
+    bound = H * 2.0 ** -24 * (np.abs(Wd) @ np.abs(x.astype(np.float64)))
+    assert (np.abs(got - Wd @ x.astype(np.float64)) <= bound).all()
+
+
+@pytest.mark.parametrize("n_t,gqa", [(1, 8), (37, 8), (300, 16)])
+def test_attn_decode(gpu, n_t, gqa):
+    """attn_decode_f32 (shaders/attn_decode_f32.comp:31-79), one workgroup
+    per query head over contiguous f32 K/V rows: against the oracle's f32
+    restatement and the f64 two-pass softmax within 1e-5 relative; n_t = 1
+    returns the V row."""
+    rng = np.random.default_rng(n_t)
+    hd, nkv = 128, 4
+    nh, kvd = nkv * gqa, nkv * 128
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    K = rng.standard_normal(n_t * kvd).astype(np.float32)
+    V = rng.standard_normal(n_t * kvd).astype(np.float32)
+    scale = np.float32(1 / np.sqrt(hd))
+    bo = gpu.zeros(nh * hd * 4)
+    run(gpu, "attn_decode_f32", [f32buf(gpu, q), f32buf(gpu, K), f32buf(gpu, V), bo],
+        struct.pack("<4If", n_t, hd, kvd, gqa, scale), (nh, 1, 1))
+    got = bo.download(np.float32)
+    assert rel_l2(got, O.attn_decode(q, K, V, n_t, hd, kvd, gqa, nh, scale)) < 1e-6
+    assert rel_l2(got, O.attn_decode_f64(q, K, V, n_t, hd, kvd, gqa, nh, float(scale))) < 1e-5
+    if n_t == 1:
+        for h in range(nh):
+            kv = (h // gqa) * hd
+            assert np.allclose(got[h * hd:(h + 1) * hd], V[kv:kv + hd], rtol=1e-6)
+
+
+def test_gather_slabs(gpu):
+    """gather_slabs_f32 (shaders/gather_slabs_f32.comp:40-86): slab e of each
+    tensor to arena slot layer*k+s, byte-exact against the oracle; SKIP
+    slots and every other arena slot untouched."""
+    rng = np.random.default_rng(8)
+    E, k, layer = 12, 4, 2
+    slabs = [4096, 4608, 6144]
+    dst_slab = 6144
+    src = [rng.integers(0, 256, E * s, dtype=np.uint8) for s in slabs]
+    arena0 = [rng.integers(0, 256, (layer + 1) * k * dst_slab, dtype=np.uint8) for _ in range(3)]
+    ids = np.array([7, SKIP, 0, 11], np.uint32)
+    bsrc = [gpu.from_numpy(a) for a in src]
+    bdst = [gpu.from_numpy(a) for a in arena0]
+    push = struct.pack("<9I", *[dst_slab // 16] * 3, *[s // 16 for s in slabs], layer, k, 0)
+    run(gpu, "gather_slabs_f32", bsrc + bdst + [gpu.from_numpy(ids)], push, (k, 1, 1))
+    import ctypes as C
+    want = [a.copy() for a in arena0]
+    O.lib().styx_oracle_gather_slabs((C.c_void_p * 3)(*[a.ctypes.data for a in src]),
+                                     (C.c_int64 * 3)(*slabs),
+                                     (C.c_void_p * 3)(*[a.ctypes.data for a in want]),
+                                     (C.c_int64 * 3)(dst_slab, dst_slab, dst_slab),
+                                     ids.ctypes.data, k, layer)
+    for t in range(3):
+        got = bdst[t].download()
+        assert np.array_equal(got, want[t]), t
+        assert not np.array_equal(got, arena0[t])
+
+
+def test_dispatch_rejects_reach_past_binding(gpu):
+    """Push constants or a grid that would read or write past a binding are
+    refused on the host (nothing is launched): a matvec whose rows exceed
+    the weight buffer, a reduce longer than its output."""
+    from styx_amd import _lib as L
+    a = np.zeros(16 * 2 * 34, np.uint8)
+    push = struct.pack("<13I", 64, 2, 64, 32, 32 * 64, 64, 32, 0, 0, 1, 1, 1, 1)  # 32 rows, 16 stored
+    with pytest.raises(L.StyxError, match="reach past"):
+        run(gpu, "mul_mat_vec_q8_0_f32_f32", [gpu.from_numpy(a), gpu.zeros(256), gpu.zeros(128),
+                                              gpu.zeros(16), gpu.zeros(16)], push, (32, 1, 1))
+    with pytest.raises(L.StyxError, match="reach past"):
+        run(gpu, "moe_reduce_f32", [gpu.zeros(8 * 1024 * 4), gpu.zeros(32), gpu.zeros(512 * 4)],
+            struct.pack("<2I", 1024, 8), (4, 1, 1))

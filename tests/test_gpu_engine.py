@@ -150,3 +150,41 @@ def test_kv_full_and_reset(gpu):
     again = m.forward_token(3)
     assert np.array_equal(first.view(np.uint32), again.view(np.uint32))
     m.close()
+
+
+@pytest.mark.parametrize("arena", [False, True])
+def test_repin_swaps_keep_logits_identical(gpu, arena):
+    """Online repinning (moe.rs:1450-1508) on host-pinned experts: the hot
+    set comes from the reference's route_hist_30b.csv, which knows nothing
+    of this synthetic model's routing, so routed experts soon have twice the
+    hits of pinned ones and slabs are swapped in every 2 tokens.  Logits stay
+    bit-identical to the all-in-HBM model across the swaps (forward_token,
+    then graph decode with repinning between steps), hot + cold = k per
+    layer, and more routed slots hit the hot set after the swaps."""
+    from pathlib import Path
+    from styx_amd import MoeModel, SynthConfig
+    hist = Path(__file__).resolve().parent / "golden" / "route_hist_30b.csv"
+    cfg = SynthConfig(n_layers=4, n_embd=256, n_heads=4, n_kv_heads=2, head_dim=64, n_expert=128,
+                      n_expert_used=8, n_ff_exp=256, n_vocab=1024, exp_mix=True, seed=0x4E9)
+    ref = MoeModel.synth(gpu, cfg, n_ctx=64, fuse=not arena)
+    budget_mb = int(ref.hp.slab_bytes * 4 * 128 / 4) >> 20
+    m = MoeModel.synth(gpu, cfg, n_ctx=64, fuse=not arena, expert_budget_mb=budget_mb,
+                       expert_hist=str(hist), arena=arena, repin_interval=2, repin_max=4)
+    hot_first = hot_last = 0
+    toks = [3, 900, 45, 1000, 2, 512, 77, 640, 5, 6, 7, 8, 9, 10, 11, 12]
+    for i, t in enumerate(toks):
+        la, lb = ref.forward_token(t), m.forward_token(t)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), i
+        hc = m.last_hot_cold()
+        assert (hc.sum(1) == cfg.n_expert_used).all()
+        if i < 4:
+            hot_first += int(hc[:, 0].sum())
+        if i >= len(toks) - 4:
+            hot_last += int(hc[:, 0].sum())
+    assert m.repin_swaps > 0
+    swaps = m.repin_swaps
+    assert np.array_equal(ref.decode(12), m.decode(12))
+    assert m.repin_swaps >= swaps
+    assert hot_last > hot_first
+    ref.close()
+    m.close()

@@ -67,3 +67,30 @@ def test_without_histogram_whole_layers_in_order():
     remap, n = plan(None, 48, 128, SLAB_30B, (3 * layer + layer // 2) >> 20)
     assert n == 3 * 128
     assert (remap[:3] != SKIP).all() and (remap[3:] == SKIP).all()
+
+
+def test_zipf_bias_table_gives_zipf_popularity():
+    """The configs[2] router bias (styx_zipf_bias_table): on an independent
+    sample of router logit noise N(0, (0.02 sqrt(2048))^2), top-8 routing
+    over 128 experts picks rank r with a frequency that falls as r^-1.1
+    (least-squares exponent over the ranks picked on fewer than half the
+    tokens), rank 1 on every token, and the 41 most popular experts (a
+    6 GiB budget at the 30B shape) take 0.81 of the picks, the capped-Zipf
+    value; biases fall with rank, and the table is deterministic."""
+    E, k, s, sd = 128, 8, 1.1, 0.02 * 2048 ** 0.5
+    t = np.empty(E, np.float32)
+    assert load().styx_zipf_bias_table(E, k, C.c_float(s), C.c_float(sd), 77, t.ctypes.data) == 0
+    t2 = np.empty(E, np.float32)
+    load().styx_zipf_bias_table(E, k, C.c_float(s), C.c_float(sd), 77, t2.ctypes.data)
+    assert np.array_equal(t, t2) and t[0] == 0 and (np.diff(t) <= 0).all()
+    rng = np.random.default_rng(2024)
+    n = 20000
+    lg = t + (sd * rng.standard_normal((n, E))).astype(np.float32)
+    top = np.argpartition(-lg, k, axis=1)[:, :k]
+    freq = np.bincount(top.ravel(), minlength=E) / n
+    r = np.arange(1, E + 1)
+    m = freq < 0.5
+    slope = np.polyfit(np.log(r[m]), np.log(freq[m]), 1)[0]
+    assert abs(slope + 1.1) < 0.1, slope
+    assert freq[0] > 0.98
+    assert abs(freq[:41].sum() / k - 0.812) < 0.02
