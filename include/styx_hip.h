@@ -181,6 +181,22 @@ int styx_op_attn_decode(styx_gpu *gpu, const float *q, const float *k, const flo
                         float *out, float *part, int nh, int nkv, int hd, int chunk,
                         int max_chunks, float scale);
 int64_t styx_op_attn_part_floats(int nh, int nkv, int hd, int max_chunks);
+/* No counterpart in the reference.  styx_op_attn_decode without the `part`
+ * workspace, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * chunk partials live in a static device array of the library,
+ * STYX_NOALLOC_ATTN_PART_FLOATS floats (8 MiB) per GPU, held until the
+ * process ends; a call needing more (styx_op_attn_part_floats(nh, nkv, hd,
+ * max_chunks) above it) is rejected with STYX_E_INVALID.  Allocates
+ * nothing.  Every call on one GPU shares that array: calls that overlap on
+ * one GPU (other streams or threads) race. */
+#define STYX_NOALLOC_ATTN_PART_FLOATS (2u * 1024u * 1024u)
+int styx_op_attn_decode_noalloc(styx_gpu *gpu, const float *q, const float *k, const float *v,
+                                const float *q_norm, const float *k_norm, float eps,
+                                const double *rope, float *kpool, float *vpool,
+                                const int32_t *page_table, int page_tokens, const int32_t *pos,
+                                float *out, int nh, int nkv, int hd, int chunk, int max_chunks,
+                                float scale);
 /* Host-side NEOX rope table: out[p][i] = (cos, sin)(p * base^(-2i/hd)) in
  * f64 for p < n_pos, i < hd/2 (crates/vk-backend/tests/ops2.rs:426-442).
  * out holds n_pos * hd doubles.  Needs no GPU. */

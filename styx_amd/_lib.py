@@ -118,6 +118,8 @@ _SIGS = {
     "styx_op_moe_down_reduce": (i32, [vp, i32, vp, vp, vp, vp, vp, i32, i32, i32]),
     "styx_op_attn_decode": (i32, [vp, vp, vp, vp, vp, vp, C.c_float, vp, vp, vp, vp, i32, vp,
                                   vp, vp, i32, i32, i32, i32, i32, C.c_float]),
+    "styx_op_attn_decode_noalloc": (i32, [vp, vp, vp, vp, vp, vp, C.c_float, vp, vp, vp, vp, i32,
+                                          vp, vp, i32, i32, i32, i32, i32, C.c_float]),
     "styx_op_attn_part_floats": (i64, [i32, i32, i32, i32]),
     "styx_rope_table": (None, [C.c_float, i32, i32, vp]),
     "styx_op_read_probe": (i32, [vp, vp, i64, vp, i32]),

@@ -2,6 +2,7 @@
 // (crates/vk-backend/src/lib.rs replacement; see include/styx_hip.h)
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <vector>
 #include <string>
 
@@ -25,6 +26,30 @@ int hip_fail(hipError_t e, const char *what)
 }
 
 void clear_error() { t_err.clear(); }
+
+// Chunk partials of styx_op_attn_decode_noalloc: a static device array, so
+// that entry point allocates nothing.  Each GPU holds its own copy for the
+// life of the process.  In host code `scratch` only names the symbol; its
+// device address on each GPU comes from hipGetSymbolAddress (noalloc_scratch).
+static __device__ __align__(256) float scratch[STYX_NOALLOC_ATTN_PART_FLOATS];
+
+// Device address of this GPU's copy of `scratch`, looked up once per device
+// with that device current (the caller has set it).
+static int noalloc_scratch(int device, float **out)
+{
+    static std::mutex mu;
+    static std::vector<float *> addr;
+    std::lock_guard<std::mutex> lock(mu);
+    if ((int)addr.size() <= device) addr.resize(device + 1, nullptr);
+    if (!addr[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        addr[device] = (float *)p;
+    }
+    *out = addr[device];
+    return STYX_OK;
+}
 
 static void gpu_destroy(styx_gpu *g)
 {
@@ -71,6 +96,11 @@ int styx_gpu_new(int device, styx_gpu **out)
     if (e != hipSuccess) {
         delete g;
         return hip_fail(e, "hipStreamCreateWithFlags");
+    }
+    if (int r = noalloc_scratch(device, &g->noalloc_part)) {
+        hipStreamDestroy(g->stream);
+        delete g;
+        return r;
     }
     g->partial_bytes = sizeof(float) * MAX_TOPK * XQ_MAX;
     e = hipMalloc(&g->xq_scratch, xq_bytes(XQ_MAX));
@@ -373,6 +403,30 @@ int styx_op_attn_decode(styx_gpu *g, const float *q, const float *k, const float
     a.scale = scale;
     OP_RUN(launch_attn_decode(g->stream, a), "styx_op_attn_decode");
     return STYX_OK;
+}
+
+int styx_op_attn_decode_noalloc(styx_gpu *g, const float *q, const float *k, const float *v,
+                                const float *q_norm, const float *k_norm, float eps,
+                                const double *rope, float *kpool, float *vpool,
+                                const int32_t *page_table, int page_tokens, const int32_t *pos,
+                                float *out, int nh, int nkv, int hd, int chunk, int max_chunks,
+                                float scale)
+{
+    OP_GPU(g);
+    const int64_t need = styx_op_attn_part_floats(nh, nkv, hd, max_chunks);
+    if (need <= 0 || max_chunks < 1)
+        return fail(STYX_E_INVALID, "styx_op_attn_decode_noalloc: bad head counts or max_chunks");
+    if (need > (int64_t)STYX_NOALLOC_ATTN_PART_FLOATS)
+        return fail(STYX_E_INVALID,
+                    "styx_op_attn_decode_noalloc: partials of " + std::to_string(need) +
+                        " floats (nh, nkv, hd, max_chunks) exceed the static scratch of " +
+                        std::to_string((long long)STYX_NOALLOC_ATTN_PART_FLOATS) +
+                        " floats; lower max_chunks or use styx_op_attn_decode");
+    // every chunk the combine reads is written by the same launch first, so
+    // the shared array needs no clearing between calls
+    return styx_op_attn_decode(g, q, k, v, q_norm, k_norm, eps, rope, kpool, vpool, page_table,
+                               page_tokens, pos, out, g->noalloc_part, nh, nkv, hd, chunk,
+                               max_chunks, scale);
 }
 
 void styx_rope_table(float base, int hd, int n_pos, double *out)

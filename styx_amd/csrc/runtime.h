@@ -23,6 +23,10 @@ struct styx_gpu {
     // H <= 16384), same stream-order rule.
     void *partial_scratch = nullptr;
     size_t partial_bytes = 0;
+    // Device address of this device's copy of the static attention-partials
+    // array of styx_op_attn_decode_noalloc (capi.cpp), looked up at
+    // styx_gpu_new with the device current.
+    float *noalloc_part = nullptr;
 };
 
 struct styx_buf {
