@@ -144,7 +144,30 @@ def cpu_baseline(m, prompt, seconds: float, threads: int) -> dict:
             break
     return {"value": round(n / el, 4), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{n} full forward passes (prompt then greedy) of the same model, "
-                      f"{el:.1f}s, C oracle with {threads} OpenMP threads"}, gen
+                      f"{el:.1f}s, C oracle with {threads} OpenMP threads",
+            "host": host_info(threads)}, gen
+
+
+def host_info(threads: int) -> dict:
+    """The host the CPU baseline ran on: logical CPUs the process may use
+    and in all, the CPU model and socket count from lscpu, the OpenMP
+    threads used."""
+    import subprocess
+    info = {"omp_threads": threads, "nproc": len(os.sched_getaffinity(0)),
+            "logical_cpus": os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() == "Model name":
+                info["model_name"] = v.strip()
+            elif k.strip() == "Socket(s)":
+                info["sockets"] = int(v.strip()) if v.strip().isdigit() else v.strip()
+            elif k.strip() == "Core(s) per socket":
+                info["cores_per_socket"] = int(v.strip()) if v.strip().isdigit() else v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return info
 
 
 def copy_probe(nbytes: int) -> int:
@@ -162,22 +185,27 @@ def copy_probe(nbytes: int) -> int:
     return 0
 
 
-def stream_read_gbs(gpu, nbytes: int = 2 << 30, reps: int = 10) -> float:
-    """Achievable HBM streaming-read bandwidth: styx_op_read_probe (dwordx4
-    loads, 4 in flight per lane, 2048 x 256 threads) over a 2 GiB buffer,
-    wall clock over `reps` back-to-back launches."""
+def stream_read_gbs(gpu, nbytes: int = 2 << 30, reps: int = 10) -> tuple[float, int]:
+    """Achievable HBM streaming-read bandwidth: styx_op_read_probe (each
+    workgroup a contiguous chunk, 8 non-temporal dwordx4 loads in flight per
+    lane) over a 2 GiB buffer, wall clock over `reps` back-to-back launches,
+    at 1024 to 16384 workgroups of 256; the best rate and its grid."""
     from styx_amd import _lib as L
-    buf, out = gpu.buffer(nbytes), gpu.buffer(2048 * 4 * 4)
+    grids = (1024, 2048, 4096, 8192, 16384)
+    buf, out = gpu.buffer(nbytes), gpu.buffer(max(grids) * 4 * 4)
     lib = gpu.lib
-    L.check(lib.styx_op_read_probe(gpu.h, buf.ptr, nbytes, out.ptr, 2048))
-    gpu.sync()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        L.check(lib.styx_op_read_probe(gpu.h, buf.ptr, nbytes, out.ptr, 2048))
-    gpu.sync()
-    el = time.perf_counter() - t0
+    best = (0.0, 0)
+    for g in grids:
+        L.check(lib.styx_op_read_probe(gpu.h, buf.ptr, nbytes, out.ptr, g))
+        gpu.sync()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            L.check(lib.styx_op_read_probe(gpu.h, buf.ptr, nbytes, out.ptr, g))
+        gpu.sync()
+        el = time.perf_counter() - t0
+        best = max(best, (nbytes * reps / el / 1e9, g))
     buf.free(), out.free()
-    return nbytes * reps / el / 1e9
+    return best
 
 
 # Kernels whose HBM traffic is measured on config 2, with their algorithmic
@@ -314,6 +342,39 @@ def expected_popularity_csv(m, path: Path) -> None:
     path.write_text("\n".join(rows) + "\n")
 
 
+def zipf_report(m, n_tok: int) -> dict:
+    """Routing statistics of n_tok more greedy tokens (HUD,
+    generate_moe.rs:87-119): the hit rate against the HBM hot set, and the
+    popularity the router bias produced: each layer's experts ranked by
+    their bias, picks per token of each rank over all layers, the
+    least-squares exponent of picks vs rank over the ranks picked on fewer
+    than half the tokens, and the share of picks among the 41 top ranks
+    (the hot slots a 6 GiB budget holds per layer at this shape)."""
+    L, E, k = m.hp.n_layers, m.hp.n_expert, m.hp.n_expert_used
+    rank_of = np.empty((L, E), np.int64)
+    for l in range(L):
+        b = m.export_tensor(f"blk.{l}.ffn_gate_inp.bias")[2].view(np.float32)
+        rank_of[l, np.argsort(-b, kind="stable")] = np.arange(E)
+    picks = np.zeros(E, np.int64)
+    hot = cold = 0
+    for _ in range(n_tok):
+        m.decode(1)
+        ids = m.last_expert_ids().astype(np.int64)
+        for l in range(L):
+            picks[rank_of[l, ids[l]]] += 1
+        hc = m.last_hot_cold()
+        hot += int(hc[:, 0].sum())
+        cold += int(hc[:, 1].sum())
+    per_tok = picks / (n_tok * L)
+    r = np.arange(1, E + 1)
+    sel = (per_tok < 0.5) & (per_tok > 0)
+    slope = float(np.polyfit(np.log(r[sel]), np.log(per_tok[sel]), 1)[0]) if sel.sum() > 2 else None
+    return {"hit_rate": round(hot / max(hot + cold, 1), 4), "routing_tokens": n_tok,
+            "zipf_fitted_exponent": None if slope is None else round(-slope, 3),
+            "top41_pick_share": round(float(picks[:41].sum() / picks.sum()), 4),
+            "rank1_picks_per_token": round(float(per_tok[0]), 4)}
+
+
 def measure(m, args, prompt):
     """Prefill, warmup, K timed greedy steps, then per-launch timing steps.
     Returns (tok/s, seconds, greedy tokens produced after the first)."""
@@ -394,8 +455,8 @@ def main() -> int:
     n_ctx = len(prompt) + args.warmup + args.steps + args.timing_steps + 8
 
     gpu = Gpu(0)
-    stream_gbs = stream_read_gbs(gpu)
-    log(f"streaming-read probe: {stream_gbs:.1f} GB/s over 2 GiB")
+    stream_gbs, stream_grid = stream_read_gbs(gpu)
+    log(f"streaming-read probe: {stream_gbs:.1f} GB/s over 2 GiB ({stream_grid} workgroups)")
     extra = {}
     t0 = time.perf_counter()
     if args.config == 4:
@@ -446,16 +507,8 @@ def main() -> int:
         log(f"  {k:18s} {v}")
 
     if args.config == 3:
-        hc = m.last_hot_cold()
         extra["tokens_equal_all_in_hbm"] = bool(np.array_equal(toks, toks_hbm))
-        # hit rate over a few more tokens (HUD, generate_moe.rs:87-119)
-        hot = cold = 0
-        for _ in range(8):
-            m.decode(1)
-            hc = m.last_hot_cold()
-            hot += int(hc[:, 0].sum())
-            cold += int(hc[:, 1].sum())
-        extra["hit_rate"] = round(hot / max(hot + cold, 1), 4)
+        extra.update(zipf_report(m, 128))
         hist.unlink(missing_ok=True)
 
     # the dominant kernel: the fused MoE block, or gate/up when the block

@@ -212,9 +212,10 @@ int styx_op_gather_slabs(styx_gpu *gpu, const void *const src[3], const int64_t 
 int styx_op_argmax(styx_gpu *gpu, const float *v, int n, uint32_t *out, float *scratch_val,
                    uint32_t *scratch_idx);
 /* Measurement helper with no counterpart in the reference: reads every
- * 16-byte word of [p, p + bytes) once with grid x 256 threads (4 loads in
- * flight per lane) and writes 4*grid fold words to out, so its duration gives
- * the achievable HBM streaming-read bandwidth of the device. */
+ * 16-byte word of [p, p + bytes) once with grid x 256 threads (each
+ * workgroup a contiguous chunk, 8 non-temporal 16-byte loads in flight per
+ * lane) and writes 4*grid fold words to out, so its duration gives the
+ * achievable HBM streaming-read bandwidth of the device. */
 int styx_op_read_probe(styx_gpu *gpu, const void *p, int64_t bytes, uint32_t *out, int grid);
 /* Seeded synthetic data: N(0, sigma) values quantized to GGUF blocks of
  * `type` (n values), or f32 N(mean, sigma). */
@@ -273,7 +274,8 @@ typedef struct {
     uint64_t seed;
     float router_zipf_s;     /* >0: Zipf(s) router bias by a seeded rank
                                 permutation per layer, from
-                                styx_zipf_bias_table(E, k, s, sigma*sqrt(H)) */
+                                styx_zipf_bias_table(E, k, s,
+                                1.05 * sigma * sqrt(H)) */
 } styx_moe_synth_cfg;
 
 /* Popularity pinning plan (crates/model/src/moe.rs:774-813), host only:

@@ -508,19 +508,28 @@ __global__ void k_fill_u32(uint32_t *p, uint32_t v, int64_t n)
 // Streaming-read probe: every 16-byte word of [p, p + n16*16) is loaded
 // once (4 loads in flight per lane) and folded into one word per workgroup,
 // so the duration measures achievable HBM read bandwidth.
+// Streaming-read probe: workgroup b reads the contiguous chunk
+// [b * n16 / grid, (b + 1) * n16 / grid) of 16-byte words, each lane with
+// 8 non-temporal dwordx4 loads in flight per trip (a wave covers 8 KB of
+// consecutive lines per trip), and folds them into one word per wave so the
+// loads cannot be dropped.
 __global__ void __launch_bounds__(256) k_read_probe(const uint4 *p, int64_t n16, uint32_t *out)
 {
-    const int64_t stride = (int64_t)gridDim.x * 256;
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+    const u4v STYX_GLOBAL *q = (const u4v STYX_GLOBAL *)p;
+    const int64_t c0 = n16 * blockIdx.x / gridDim.x, c1 = n16 * (blockIdx.x + 1) / gridDim.x;
     uint32_t acc = 0;
-    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    for (; i + 3 * stride < n16; i += 4 * stride) {
-        const uint4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
-        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^
-               d.z ^ d.w;
+    int64_t i = c0 + threadIdx.x;
+    for (; i + 7 * 256 < c1; i += 8 * 256) {
+        u4v v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = __builtin_nontemporal_load(q + i + 256 * j);
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
     }
-    for (; i < n16; i += stride) {
-        const uint4 a = p[i];
-        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    for (; i < c1; i += 256) {
+        const u4v v = __builtin_nontemporal_load(q + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
     }
     for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
     if ((threadIdx.x & 63) == 0) out[blockIdx.x * 4 + (threadIdx.x >> 6)] = acc;

@@ -220,6 +220,64 @@ class MoeModel:
         self.close()
 
 
+class Hud:
+    """The residency HUD of generate_moe.rs:87-119: per-token (hot, cold)
+    routed-slot counts folded into totals and a per-layer cold count, then
+    the reference's summary lines (hot/cold shares, cold PCIe bytes, the
+    per-layer cold heatmap, repin swaps)."""
+
+    def __init__(self, n_layers: int, k: int, slab_bytes: int):
+        self.k, self.slab_bytes = k, slab_bytes
+        self.hot = self.cold = 0
+        self.cold_by_layer = np.zeros(n_layers, np.int64)
+
+    def tick(self, hot_cold: np.ndarray) -> None:
+        """hud_tick: fold one token's MoeModel.last_hot_cold() ([L][2])."""
+        hc = np.asarray(hot_cold, np.int64)
+        self.hot += int(hc[:, 0].sum())
+        self.cold += int(hc[:, 1].sum())
+        self.cold_by_layer += hc[:, 1]
+
+    def lines(self, n_tok: int, repin_swaps: int = 0) -> list[str]:
+        """The summary after n_tok forwarded tokens (prompt + generated - 1)."""
+        total = max(self.hot + self.cold, 1)
+        streamed = self.cold * self.slab_bytes
+        out = [f"hud: hot {100.0 * self.hot / total:.1f}% ({self.hot}) | "
+               f"cold {100.0 * self.cold / total:.1f}% ({self.cold}) | "
+               f"cold PCIe ~{streamed / 2**30:.2f} GiB total, "
+               f"~{streamed / max(n_tok, 1) / 2**20:.1f} MiB/tok"]
+        glyphs = ""
+        for c in self.cold_by_layer:
+            f = c / max(n_tok * self.k, 1)
+            glyphs += "." if f == 0 else str(min(int(f * 10.0), 9))
+        out.append(f"hud: cold/layer [{glyphs}] (.=0%, 9=90%+ of k={self.k} slots)")
+        if repin_swaps > 0:
+            out.append(f"hud: repin {repin_swaps} slab swaps "
+                       f"(~{repin_swaps * self.slab_bytes / 2**30:.2f} GiB copied)")
+        return out
+
+
+def generate_hud(m: MoeModel, prompt, n_predict: int) -> tuple[list[int], list[str]]:
+    """generate_moe.rs:44-119 with MOE_HUD: token-at-a-time prefill, greedy
+    argmax on the host (ties to the last index), a HUD tick after every
+    forward_token call (prompt and generated tokens alike; the last
+    generated token is not forwarded).  Returns (tokens, HUD lines)."""
+    hud = Hud(m.hp.n_layers, m.hp.n_expert_used, m.slab_bytes)
+    logits = None
+    for t in prompt:
+        logits = m.forward_token(int(t))
+        hud.tick(m.last_hot_cold())
+    nxt = argmax_last(logits)
+    out = [nxt]
+    for _ in range(1, n_predict):
+        logits = m.forward_token(nxt)
+        hud.tick(m.last_hot_cold())
+        nxt = argmax_last(logits)
+        out.append(nxt)
+    n_tok = len(prompt) + len(out) - 1
+    return out, hud.lines(n_tok, m.repin_swaps)
+
+
 def argmax_last(v: np.ndarray) -> int:
     """generate_moe.rs:29: max_by(total_cmp) -> the LAST maximal index."""
     b = v.astype(np.float32).view(np.int32).astype(np.int64)

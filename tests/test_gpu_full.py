@@ -156,6 +156,15 @@ def test_config3_host_pinned_6gib_identical(gpu, tmp_path, arena):
     print(f"\nconfigs[2] arena={arena}: {steps} tokens bit-identical to all-in-HBM; "
           f"hit rate {hot / (hot + cold):.3f}")
     assert 0.5 < hot / (hot + cold) < 1.0
+    # the HUD of generate_moe.rs:87-119 over scripts/verify.sh:69-78's run:
+    # 2 prompt + 32 generated tokens, 33 forwarded, 48 layers, k 8
+    import re
+    from styx_amd import generate_hud
+    m.reset()
+    _, hud = generate_hud(m, prompt[:2], 32)
+    print("\n".join(hud))
+    assert sum(int(v) for v in re.findall(r"\((\d+)\)", hud[0])) == 12672
+    assert re.match(r"^hud: cold/layer \[[.0-9]{48}\]", hud[1])
     m.close()
 
 

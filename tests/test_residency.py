@@ -94,3 +94,23 @@ def test_zipf_bias_table_gives_zipf_popularity():
     assert abs(slope + 1.1) < 0.1, slope
     assert freq[0] > 0.98
     assert abs(freq[:41].sum() / k - 0.812) < 0.02
+
+
+def test_hud_lines_match_reference_format():
+    """generate_moe.rs:87-119: totals, shares, cold PCIe bytes, the
+    per-layer heatmap (. = no cold slot, digit = tenths of k slots cold,
+    capped at 9) and the repin line."""
+    from styx_amd import Hud
+    slab = 3256320
+    h = Hud(4, 8, slab)
+    h.tick(np.array([[8, 0], [4, 4], [0, 8], [7, 1]]))
+    h.tick(np.array([[8, 0], [6, 2], [0, 8], [8, 0]]))
+    lines = h.lines(2, repin_swaps=3)
+    # hot 8+4+0+7 + 8+6+0+8 = 41, cold 0+4+8+1 + 0+2+8+0 = 23 of 64 slots;
+    # 23 cold slabs of 3256320 B = 0.07 GiB, 35.7 MiB per token
+    assert lines[0] == ("hud: hot 64.1% (41) | cold 35.9% (23) | cold PCIe ~0.07 GiB total, "
+                        "~35.7 MiB/tok")
+    # layer cold shares over 2 tokens x 8 slots: 0, 6/16, 16/16, 1/16
+    assert lines[1] == "hud: cold/layer [.390] (.=0%, 9=90%+ of k=8 slots)"
+    assert lines[2] == f"hud: repin 3 slab swaps (~{3 * slab / 2**30:.2f} GiB copied)"
+    assert len(Hud(48, 8, slab).lines(1)) == 2  # no repin line without swaps
