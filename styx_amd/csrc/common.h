@@ -3,8 +3,10 @@
 // Block formats are GGUF's (crates/gguf-rs/src/lib.rs:242-332).  In HBM the
 // engine keeps every quant matrix in a "split" layout: the same bytes as the
 // GGUF blocks, regrouped per matrix into aligned regions (quants, high bits,
-// scales, f16 factors) so that every lane issues 16-byte loads.  The regrouping
-// is a byte permutation: dequantized values are bit-identical.
+// scales, f16 factors) so that every lane issues 16-byte loads, and inside
+// the quant regions interleaved (ilv_off) so that the 16-byte loads of
+// neighbouring lanes cover whole 128-byte lines.  The regrouping is a byte
+// permutation: dequantized values are bit-identical.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -95,13 +97,46 @@ __host__ __device__ inline int64_t region_off(const Split &s, int r, int64_t nbl
     return o;
 }
 
+// Place of byte i (0 <= i < sz[r]) of block b inside region r.  A unit
+// load reads 16 bytes of one block's quant region, and a wave's neighbouring
+// lanes read the same 16-byte position of neighbouring units, so those
+// halves are stored side by side:
+//   - 32-byte regions (q8_0 quants, q5_K high bits), groups of 8 blocks: the
+//     first 16 bytes of the 8 blocks, then their last 16 bytes;
+//   - 128-byte regions (q4_K / q5_K quants, q6_K low bits), pairs of blocks:
+//     each block is four units, unit v reading bytes [16 v', +16) and
+//     [16 v' + 32, +16) of its 64-byte half (q6_K: v = 2n + h, runs
+//     64n + 16h and +32) or [32 v, +16) and [32 v + 16, +16) (q4_K / q5_K
+//     quarter v): per pair, the first load of all 8 units, then the second.
+// Every other region keeps the blocks' bytes in order.  A matrix's block
+// count must be a multiple of ilv_group(t).
+__host__ __device__ inline int64_t ilv_off(int t, int r, int64_t b, int i)
+{
+    if (r == 0 && (t == T_Q4_K || t == T_Q5_K))
+        return (b >> 1) * 256 + ((i >> 4) & 1) * 128 + (b & 1) * 64 + (i >> 5) * 16 + (i & 15);
+    if (r == 0 && t == T_Q6_K)
+        return (b >> 1) * 256 + ((i >> 5) & 1) * 128 + (b & 1) * 64 +
+               (2 * (i >> 6) + ((i >> 4) & 1)) * 16 + (i & 15);
+    if ((r == 0 && t == T_Q8_0) || (r == 1 && t == T_Q5_K))
+        return (b >> 3) * 256 + (i >> 4) * 128 + (b & 7) * 16 + (i & 15);
+    return b * split_of(t).sz[r] + i;
+}
+
+// Blocks per interleave group of type t (ilv_off): a matrix's block count
+// must be a multiple of it.
+__host__ __device__ inline int ilv_group(int t)
+{
+    return t == T_Q8_0 || t == T_Q5_K ? 8 : t == T_Q4_K || t == T_Q6_K ? 2 : 1;
+}
+
 // Map GGUF byte index (block b, byte i) of a matrix with nblocks blocks to its
 // split-layout byte index.
-__host__ __device__ inline int64_t split_index(const Split &s, int64_t nblocks, int64_t b, int i)
+__host__ __device__ inline int64_t split_index(int t, const Split &s, int64_t nblocks, int64_t b,
+                                               int i)
 {
     for (int r = 0; r < s.nreg; r++) {
         if (i >= s.src[r] && i < s.src[r] + s.sz[r]) {
-            return region_off(s, r, nblocks) + b * s.sz[r] + (i - s.src[r]);
+            return region_off(s, r, nblocks) + ilv_off(t, r, b, i - s.src[r]);
         }
     }
     return -1;

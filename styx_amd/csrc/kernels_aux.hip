@@ -26,11 +26,11 @@ __global__ void k_to_split(int t, const uint8_t *src, uint8_t *dst, int64_t nblo
         const int64_t mbase = m * nblocks * bb;
         for (int r = 0; r < s.nreg; r++) {
             const int64_t so = mbase + b * bb + s.src[r];
-            const int64_t po = mbase + region_off(s, r, nblocks) + b * s.sz[r];
+            const int64_t po = mbase + region_off(s, r, nblocks);
             if (dir == 0)
-                for (int j = 0; j < s.sz[r]; j++) dst[po + j] = src[so + j];
+                for (int j = 0; j < s.sz[r]; j++) dst[po + ilv_off(t, r, b, j)] = src[so + j];
             else
-                for (int j = 0; j < s.sz[r]; j++) dst[so + j] = src[po + j];
+                for (int j = 0; j < s.sz[r]; j++) dst[so + j] = src[po + ilv_off(t, r, b, j)];
         }
     }
 }
@@ -38,7 +38,8 @@ __global__ void k_to_split(int t, const uint8_t *src, uint8_t *dst, int64_t nblo
 static hipError_t split_launch(hipStream_t st, int t, const uint8_t *src, uint8_t *dst,
                                int64_t nblocks, int64_t nmat, int dir)
 {
-    if (blk_bytes(t) == 0) return hipErrorInvalidValue;
+    if (blk_bytes(t) == 0 || nblocks < 1 || nmat < 1 || nblocks % ilv_group(t))
+        return hipErrorInvalidValue;
     const int64_t total = nblocks * nmat;
     const int64_t nwg = std::min<int64_t>((total + 255) / 256, 65536);
     hipLaunchKernelGGL(k_to_split, dim3((unsigned)std::max<int64_t>(nwg, 1)), dim3(256), 0, st, t,

@@ -166,7 +166,7 @@ __global__ void __launch_bounds__(64) kr_mmv(MmvRef p)
         for (uint32_t b = threadIdx.x; b < nb; b += 64) {
             const uint8_t *blk = p.A + (a_blk + (int64_t)r * p.stride_a + b) * bb;
             float y[256];
-            deq_block(t, gguf_blk(blk, t), 0, y);
+            deq_block(t, gguf_blk(blk, t), 0, y, false);
             const float *x = p.B + b_off + (int64_t)b * be;
             for (int i = 0; i < be; i++) acc += y[i] * x[i];
         }

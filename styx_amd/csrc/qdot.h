@@ -298,36 +298,43 @@ __device__ __forceinline__ uint32_t ldg2(const uint8_t STYX_GLOBAL *p)
 
 template <int T> __device__ inline void uw_load(UW<T> &w, const Mat &m, int64_t blk, int sub);
 
+// The quant regions are interleaved (ilv_off): the first 16 bytes of a
+// 32-byte region sit at ilv8(blk), its last 16 bytes 128 bytes later; the
+// two loads of unit v of a 128-byte region at ilv2(blk) + 16 v and 128
+// bytes later.
+__device__ __forceinline__ int64_t ilv8(int64_t blk) { return (blk >> 3) * 256 + (blk & 7) * 16; }
+__device__ __forceinline__ int64_t ilv2(int64_t blk) { return (blk >> 1) * 256 + (blk & 1) * 64; }
+
 template <> __device__ inline void uw_load<T_Q8_0>(UW<T_Q8_0> &w, const Mat &m, int64_t blk, int)
 {
-    const uint8_t STYX_GLOBAL *q = m.r0 + blk * 32;
+    const uint8_t STYX_GLOBAL *q = m.r0 + ilv8(blk);
     w.q0 = ldg16(q);
-    w.q1 = ldg16(q + 16);
+    w.q1 = ldg16(q + 128);
     w.d = ldg2(m.r1 + blk * 2);
 }
 template <> __device__ inline void uw_load<T_Q4_K>(UW<T_Q4_K> &w, const Mat &m, int64_t blk, int c)
 {
-    const uint8_t STYX_GLOBAL *q = m.r0 + blk * 128 + 32 * c;
+    const uint8_t STYX_GLOBAL *q = m.r0 + ilv2(blk) + 16 * c;
     w.q0 = ldg16(q);
-    w.q1 = ldg16(q + 16);
+    w.q1 = ldg16(q + 128);
     w.hd = ldg16(m.r1 + blk * 16);
 }
 template <> __device__ inline void uw_load<T_Q5_K>(UW<T_Q5_K> &w, const Mat &m, int64_t blk, int c)
 {
-    const uint8_t STYX_GLOBAL *q = m.r0 + blk * 128 + 32 * c;
+    const uint8_t STYX_GLOBAL *q = m.r0 + ilv2(blk) + 16 * c;
     w.q0 = ldg16(q);
-    w.q1 = ldg16(q + 16);
-    const uint8_t STYX_GLOBAL *h = m.r1 + blk * 32;
+    w.q1 = ldg16(q + 128);
+    const uint8_t STYX_GLOBAL *h = m.r1 + ilv8(blk);
     w.h0 = ldg16(h);
-    w.h1 = ldg16(h + 16);
+    w.h1 = ldg16(h + 128);
     w.hd = ldg16(m.r2 + blk * 16);
 }
 template <> __device__ inline void uw_load<T_Q6_K>(UW<T_Q6_K> &w, const Mat &m, int64_t blk, int u)
 {
     const int n = (u >> 1) & 1, h = u & 1;
-    const uint8_t STYX_GLOBAL *ql = m.r0 + blk * 128 + 64 * n + 16 * h;
+    const uint8_t STYX_GLOBAL *ql = m.r0 + ilv2(blk) + 16 * u;
     w.p0 = ldg16(ql);
-    w.p1 = ldg16(ql + 32);
+    w.p1 = ldg16(ql + 128);
     w.qh = ldg16(m.r1 + blk * 64 + 32 * n + 16 * h);
     const styx_u2 sc = *(const styx_u2 STYX_GLOBAL *)(m.r2 + blk * 16 + 8 * n);
     w.sc = make_uint2(sc.x, sc.y);
