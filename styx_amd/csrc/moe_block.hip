@@ -358,10 +358,9 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     rank_ids_lds(a.route, s_ids, s_lg, w == 0);
     stamp(4);
 
-    // ---- this workgroup's down rows (their weights are loaded once the
-    // slot's gate/up outputs are in: pulling them into L2 earlier, during
-    // the gate/up phase or the wait after it, measured slower -- the extra
-    // requests delay the gate/up stream more than they save later)
+    // ---- this workgroup's down rows (their weights are issued after the
+    // workgroup's own gate/up rows and before the wait for the slot's
+    // outputs; issuing them during the gate/up phase delays that stream)
     const uint8_t *dslab = nullptr;
     if (has_d) dslab = ds < a.k ? routed_slab(a, a.src[2], s_ids[ds], ds) : a.sh[2];
 
@@ -375,14 +374,17 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     if (has_d) {
         const int F = a.F;
         const uint64_t *g = a.t_gu + (size_t)ds * F, *u = a.t_gu + ((size_t)a.nslots + ds) * F;
-        if (!tpoll<2 * MB_MAX_F / WG>(2 * F, [&](int i) { return i < F ? g + i : u + (i - F); },
-                                       tag, gus, a))
-            return;
-        stamp(6);
+        auto wait_gu = [&] {
+            const bool ok = tpoll<2 * MB_MAX_F / WG>(
+                2 * F, [&](int i) { return i < F ? g + i : u + (i - F); }, tag, gus, a);
+            stamp(6);
+            return ok;
+        };
         // the down weights go out first (two batches of rows per lane
         // group: of two rows each with one unit per lane, of one row with
-        // more, as the registers allow): the SwiGLU limbs are built while
-        // they are in flight
+        // more, as the registers allow), before the wait for the slot's g
+        // and u: they stream while the slowest gate/up rows are finished,
+        // and the SwiGLU limbs are built once g and u are in
         uint64_t *part = a.t_part + (size_t)ds * a.H;
         auto build = [&] {
             for (int i = tid; i < F; i += WG) hs[i] = gus[i] / (1.0f + expf(-gus[i])) * gus[F + i];
@@ -392,15 +394,18 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
             stamp(7);
         };
         if (dslab) {
-            walk_rows_pipelined<TD, UD, UD == 1 ? 2 : 1>(
-                OneMat{mat_at(dslab, TD, (int64_t)a.H * a.nb_d), a.nb_d}, a.nb_d, a.G_d, d0, d1,
-                [&](UX<TD>(&x)[UD], const LaneU<UD> &lu) {
-                    build();
-                    XFrom<TD, UD>{xqh}(x, lu);
-                    return true;
-                },
-                [&](int r, float v) { tput(part + r, tag, v); });
+            if (!walk_rows_pipelined<TD, UD, UD == 1 ? 2 : 1>(
+                    OneMat{mat_at(dslab, TD, (int64_t)a.H * a.nb_d), a.nb_d}, a.nb_d, a.G_d, d0, d1,
+                    [&](UX<TD>(&x)[UD], const LaneU<UD> &lu) {
+                        if (!wait_gu()) return false;
+                        build();
+                        XFrom<TD, UD>{xqh}(x, lu);
+                        return true;
+                    },
+                    [&](int r, float v) { tput(part + r, tag, v); }))
+                return;
         } else {
+            if (!wait_gu()) return;
             build();
             for (int r = d0 + tid; r < d1; r += WG) tput(part + r, tag, 0.0f);
         }
