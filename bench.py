@@ -343,36 +343,99 @@ def expected_popularity_csv(m, path: Path) -> None:
 
 
 def zipf_report(m, n_tok: int) -> dict:
-    """Routing statistics of n_tok more greedy tokens (HUD,
-    generate_moe.rs:87-119): the hit rate against the HBM hot set, and the
-    popularity the router bias produced: each layer's experts ranked by
-    their bias, picks per token of each rank over all layers, the
-    least-squares exponent of picks vs rank over the ranks picked on fewer
-    than half the tokens, and the share of picks among the 41 top ranks
-    (the hot slots a 6 GiB budget holds per layer at this shape)."""
+    """Routing statistics (the HUD of generate_moe.rs:87-119) of n_tok
+    tokens drawn uniformly from the vocabulary and forwarded one by one (a
+    random model's greedy stream soon cycles through a few tokens, so it
+    would measure its own cycle, not the router's popularity), then of as
+    many greedy decode steps: the hit rate against the HBM hot set on each,
+    and the popularity the router bias produced on the random tokens --
+    each layer's experts ranked by their bias, picks per token of each rank
+    over all layers, the least-squares exponent of picks vs rank over the
+    ranks picked on fewer than half the tokens, the share of picks among
+    the 41 top ranks (the hot slots a 6 GiB budget holds per layer at this
+    shape)."""
     L, E, k = m.hp.n_layers, m.hp.n_expert, m.hp.n_expert_used
     rank_of = np.empty((L, E), np.int64)
     for l in range(L):
         b = m.export_tensor(f"blk.{l}.ffn_gate_inp.bias")[2].view(np.float32)
         rank_of[l, np.argsort(-b, kind="stable")] = np.arange(E)
     picks = np.zeros(E, np.int64)
+    rng = np.random.default_rng(0x21FF)
     hot = cold = 0
-    for _ in range(n_tok):
-        m.decode(1)
+    for t in rng.integers(0, m.hp.n_vocab, n_tok):
+        m.forward_token(int(t), want_logits=False)
         ids = m.last_expert_ids().astype(np.int64)
         for l in range(L):
             picks[rank_of[l, ids[l]]] += 1
         hc = m.last_hot_cold()
         hot += int(hc[:, 0].sum())
         cold += int(hc[:, 1].sum())
+    ghot = gcold = 0
+    for _ in range(n_tok):
+        m.decode(1)
+        hc = m.last_hot_cold()
+        ghot += int(hc[:, 0].sum())
+        gcold += int(hc[:, 1].sum())
     per_tok = picks / (n_tok * L)
     r = np.arange(1, E + 1)
     sel = (per_tok < 0.5) & (per_tok > 0)
     slope = float(np.polyfit(np.log(r[sel]), np.log(per_tok[sel]), 1)[0]) if sel.sum() > 2 else None
-    return {"hit_rate": round(hot / max(hot + cold, 1), 4), "routing_tokens": n_tok,
+    return {"hit_rate": round(ghot / max(ghot + gcold, 1), 4),
+            "hit_rate_random_tokens": round(hot / max(hot + cold, 1), 4),
+            "routing_tokens": n_tok,
             "zipf_fitted_exponent": None if slope is None else round(-slope, 3),
             "top41_pick_share": round(float(picks[:41].sum() / picks.sum()), 4),
-            "rank1_picks_per_token": round(float(per_tok[0]), 4)}
+            "rank1_picks_per_token": round(float(per_tok[0]), 4),
+            "picks_by_rank": picks.tolist()}
+
+
+def gather_report(m, table: dict, extra: dict) -> dict:
+    """Cold-slab traffic of the arena placement: the cold slabs per layer at
+    the measured hit rate, the gather launch's event time in the timed
+    tokens (on the copy stream, overlapping the hot slots' expert kernels),
+    and host-pinned -> HBM rates of the gather kernel alone over k slabs of
+    each tensor and of the copy engine (SDMA, hipMemcpyAsync) moving as many
+    bytes."""
+    from styx_amd import _lib as L
+    k, slab = m.hp.n_expert_used, m.slab_bytes
+    cold = k * (1.0 - extra["hit_rate"])
+    out = {"cold_slabs_per_layer": round(cold, 3)}
+    g = table.get("gather")
+    if g:
+        out["in_token_gather_us_per_layer"] = g["event_us"]
+    gpu = m.gpu
+    import ctypes as C
+    # the gather kernel alone (styx_op_gather_slabs) on k slabs of each of the
+    # three tensors' sizes, host-pinned -> HBM, against the copy engine
+    sizes = [slab // 3 // 16 * 16] * 3
+    srcs = [gpu.buffer(k * sz, L.BUF_HOST_PINNED) for sz in sizes]
+    dsts = [gpu.buffer(k * sz) for sz in sizes]
+    ids = gpu.from_numpy(np.arange(k, dtype=np.int32))
+    sp = (C.c_void_p * 3)(*[b.ptr for b in srcs])
+    dp = (C.c_void_p * 3)(*[b.ptr for b in dsts])
+    sl = (C.c_int64 * 3)(*sizes)
+
+    def gather():
+        L.check(gpu.lib.styx_op_gather_slabs(gpu.h, sp, sl, dp, sl, ids.ptr, k, 0))
+    gather()
+    gpu.sync()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        gather()
+    gpu.sync()
+    el = (time.perf_counter() - t0) / 5
+    out["kernel_gather_h2d_GBps"] = round(k * sum(sizes) / el / 1e9, 2)
+    n = k * sum(sizes)
+    src, dst = gpu.buffer(n, L.BUF_HOST_PINNED), gpu.buffer(n)
+    src.copy_to(dst, 0, 0, n)
+    t0 = time.perf_counter()
+    for _ in range(5):
+        src.copy_to(dst, 0, 0, n)
+    el = (time.perf_counter() - t0) / 5
+    out["sdma_h2d_GBps"] = round(n / el / 1e9, 2)
+    for b in srcs + dsts + [src, dst, ids]:
+        b.free()
+    return out
 
 
 def measure(m, args, prompt):
@@ -420,6 +483,9 @@ def main() -> int:
                     help="configs[2]: gather cold slabs into the HBM arena (the MoE block then "
                          "runs as separate kernels) instead of reading them in place from host "
                          "memory inside the fused block")
+    ap.add_argument("--routing-tokens", type=int, default=128,
+                    help="configs[2]: greedy tokens whose routing gives the hit rate and the "
+                         "fitted popularity exponent")
     ap.add_argument("--no-fuse", action="store_true",
                     help="run the MoE block as four kernels instead of the fused launch")
     ap.add_argument("--no-fold-qkv", action="store_true",
@@ -453,6 +519,8 @@ def main() -> int:
     rng = np.random.default_rng(0xC0FFEE)
     prompt = rng.integers(0, cfg.n_vocab, 16).astype(np.uint32)
     n_ctx = len(prompt) + args.warmup + args.steps + args.timing_steps + 8
+    if args.config == 3:
+        n_ctx += 2 * args.routing_tokens
 
     gpu = Gpu(0)
     stream_gbs, stream_grid = stream_read_gbs(gpu)
@@ -508,8 +576,10 @@ def main() -> int:
 
     if args.config == 3:
         extra["tokens_equal_all_in_hbm"] = bool(np.array_equal(toks, toks_hbm))
-        extra.update(zipf_report(m, 128))
+        extra.update(zipf_report(m, args.routing_tokens))
         hist.unlink(missing_ok=True)
+        if args.arena:
+            extra["gather"] = gather_report(m, table, extra)
 
     # the dominant kernel: the fused MoE block, or gate/up when the block
     # runs as separate kernels

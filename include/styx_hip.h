@@ -275,7 +275,7 @@ typedef struct {
     float router_zipf_s;     /* >0: Zipf(s) router bias by a seeded rank
                                 permutation per layer, from
                                 styx_zipf_bias_table(E, k, s,
-                                1.05 * sigma * sqrt(H)) */
+                                0.9 * sigma * sqrt(H)) */
 } styx_moe_synth_cfg;
 
 /* Popularity pinning plan (crates/model/src/moe.rs:774-813), host only:

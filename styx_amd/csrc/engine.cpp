@@ -159,6 +159,11 @@ struct styx_moe {
     // graphs
     // [short context: attention partials merged in-kernel, long: combine kernel]
     hipGraphExec_t g_fwd[2] = {nullptr, nullptr}, g_gen[2] = {nullptr, nullptr};
+    // arena placement: the cold-slab gather runs on a second stream (same
+    // priority), forked after the router and joined before the cold slots'
+    // expert kernels, so that it overlaps the hot slots' gate/up and down
+    hipStream_t st_copy = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     int n_past = 0;
     uint64_t repin_swaps = 0;
     std::vector<void *> dev_allocs, host_allocs;
@@ -204,6 +209,12 @@ styx_moe::~styx_moe()
         if (g_gen[i]) hipGraphExecDestroy(g_gen[i]);
     }
     for (auto e : ev_pool) hipEventDestroy(e);
+    if (ev_fork) hipEventDestroy(ev_fork);
+    if (ev_join) hipEventDestroy(ev_join);
+    if (st_copy) {
+        hipStreamSynchronize(st_copy);
+        hipStreamDestroy(st_copy);
+    }
     for (void *p : dev_allocs) hipFree(p);
     for (void *p : host_allocs) hipHostFree(p);
     if (gpu) gpu_release(gpu);
@@ -467,8 +478,14 @@ int styx_moe::place_experts(const std::vector<std::vector<std::pair<uint32_t, ui
         STYX_HIP(hipMemcpyAsync(ly.remap_dev, ly.remap.data(), sizeof(uint32_t) * E,
                                 hipMemcpyHostToDevice, gpu->stream));
     }
-    // in-stream arena: k slots per tensor, each the largest slab of its kind
+    // arena: k slots per tensor, each the largest slab of its kind, filled
+    // by the gather on the copy stream
     if (opts.arena) {
+        if (!st_copy) {
+            STYX_HIP(hipStreamCreateWithFlags(&st_copy, hipStreamNonBlocking));
+            STYX_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
+            STYX_HIP(hipEventCreateWithFlags(&ev_join, hipEventDisableTiming));
+        }
         for (int t = 0; t < 3; t++) {
             int64_t mx = 0;
             for (auto &ly : layers) mx = std::max(mx, (t == 0 ? ly.gate : t == 1 ? ly.up : ly.down).slab);
@@ -573,16 +590,16 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     hipStreamIsCapturing(st, &cs);
     const bool timing = opts.time_kernels != 0 && cs == hipStreamCaptureStatusNone;
-    auto tstart = [&]() -> hipEvent_t {
+    auto tstart = [&](hipStream_t on = nullptr) -> hipEvent_t {
         if (!timing) return nullptr;
         hipEvent_t e = ev();
-        hipEventRecord(e, st);
+        hipEventRecord(e, on ? on : st);
         return e;
     };
-    auto tend = [&](hipEvent_t a, const char *nm, double bytes) {
+    auto tend = [&](hipEvent_t a, const char *nm, double bytes, hipStream_t on = nullptr) {
         if (!timing) return;
         hipEvent_t e = ev();
-        hipEventRecord(e, st);
+        hipEventRecord(e, on ? on : st);
         const int id = stat_id(nm);
         stats[id].bytes += bytes;
         pending.push_back({id, {a, e}});
@@ -699,14 +716,21 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
                 s.gtt_slab = m.slab;
             }
         }
-        if (ly.host_experts && opts.arena) {
-            e0 = tstart();
+        // the cold slabs are gathered on the copy stream while the hot
+        // slots' expert kernels run on this one
+        const bool overlap = ly.host_experts && opts.arena && st_copy;
+        if (overlap) {
+            CK(hipEventRecord(ev_fork, st));
+            CK(hipStreamWaitEvent(st_copy, ev_fork, 0));
+            e0 = tstart(st_copy);
             const uint8_t *src[3] = {ly.gate.host_dev, ly.up.host_dev, ly.down.host_dev};
             const int64_t sslab[3] = {ly.gate.slab, ly.up.slab, ly.down.slab};
             Route rg = rt;
             rg.ids_out = nullptr;
-            if (want("gather")) CK(launch_gather(st, src, sslab, arena, arena_slab, nullptr, &rg, K));
-            tend(e0, "gather", 0.0);
+            if (want("gather"))
+                CK(launch_gather(st_copy, src, sslab, arena, arena_slab, nullptr, &rg, K));
+            tend(e0, "gather", 0.0, st_copy);
+            CK(hipEventRecord(ev_join, st_copy));
         }
         // the shared expert runs as slot K of the expert kernels when it has
         // the routed experts' width and types; otherwise as dense matvecs
@@ -777,11 +801,17 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
                                       (sh_fused ? (double)ly.dsh.bytes() : 0.0) + 16.0 * H +
                                       qkv_bytes);
         } else {
+        // two passes with the copy stream (hot slots, then -- once the
+        // gather has landed -- the arena slots), one without
+        const int passes = overlap ? 2 : 1;
+        for (int pass = 0; pass < passes; pass++) {
+        const int filter = overlap ? (pass == 0 ? SLOTS_HOT : SLOTS_COLD) : SLOTS_ALL;
+        if (pass == 1) CK(hipStreamWaitEvent(st, ev_join, 0));
         e0 = tstart();
         if (want("moe_gate_up")) CK(launch_moe_gate_up(st, ly.gate.type, ly.up.type, sg, su, nullptr, &rt, xq_f, gu, H, F,
-                              K, sh_fused ? ly.gsh.dev : nullptr, sh_fused ? ly.ush.dev : nullptr));
-        tend(e0, "moe_gate_up", slabs_gu + xq_bytes(H) + 4.0 * E + 4.0 * 2 * nsl * F);
-        if (ly.gsh.dev && !sh_fused && want("shexp")) {
+                              K, sh_fused ? ly.gsh.dev : nullptr, sh_fused ? ly.ush.dev : nullptr, filter));
+        tend(e0, "moe_gate_up", pass == 1 ? 0.0 : slabs_gu + xq_bytes(H) + 4.0 * E + 4.0 * 2 * nsl * F);
+        if (pass == 0 && ly.gsh.dev && !sh_fused && want("shexp")) {
             e0 = tstart();
             DenseSeg s2[2] = {{ly.gsh.dev, sh_g, Fsh}, {ly.ush.dev, sh_u, Fsh}};
             if (ly.gsh.type == ly.ush.type) {
@@ -797,9 +827,10 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
         }
         e0 = tstart();
         if (want("moe_down")) CK(launch_moe_down(st, ly.down.type, sd, lid, gu, partial, H, F, K,
-                           sh_fused ? ly.dsh.dev : nullptr));
-        tend(e0, "moe_down", (double)K * ly.down.slab + (sh_fused ? (double)ly.dsh.bytes() : 0.0) +
+                           sh_fused ? ly.dsh.dev : nullptr, filter));
+        tend(e0, "moe_down", pass == 1 ? 0.0 : (double)K * ly.down.slab + (sh_fused ? (double)ly.dsh.bytes() : 0.0) +
                                  4.0 * 2 * nsl * F + 4.0 * nsl * H);
+        }
         e0 = tstart();
         ReduceArgs rd{};
         rd.partial = partial;
@@ -1440,11 +1471,12 @@ int styx_moe_synth(styx_gpu *gpu, const styx_moe_synth_cfg *cfg, const styx_moe_
     // router bias for Zipf-skewed routing: the bias of rank r from a table
     // calibrated to the synthetic router's logit spread, ranks a seeded
     // permutation per layer.  The spread is sigma * sqrt(H) (unit-RMS
-    // input) times ZIPF_SPREAD: measured on the 30B-A3B shape, the decoded
-    // tokens' router logits act as noise about 5% wider than that (a table
-    // for 1.0x gave a fitted popularity exponent of 0.97, for 1.25x 1.56;
-    // 1.05x gives the 1.1 asked for)
-    constexpr double ZIPF_SPREAD = 1.05;
+    // input) times ZIPF_SPREAD, set on the 30B-A3B shape from the routing
+    // of tokens drawn at random: the router logits there are not i.i.d.
+    // across tokens (each expert has a persistent offset), and a table for
+    // 0.9x the i.i.d. spread gives a fitted popularity exponent of 1.17
+    // over the unsaturated ranks (1.0x: 1.45, 1.05x: 1.54)
+    constexpr double ZIPF_SPREAD = 0.9;
     std::vector<std::vector<float>> biases(c.n_layers);
     if (c.router_zipf_s > 0) {
         const std::vector<float> tab =

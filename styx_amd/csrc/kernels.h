@@ -79,17 +79,23 @@ hipError_t launch_topk_softmax(hipStream_t st, const float *logits, int n, int k
 // given by its limbs; routing from `route` (ranked in-kernel) or, if null,
 // the id row `ids`.  With sh_gate/sh_up (split-layout matrices of the same
 // types and width F) the shared expert is slot k: gu is [2][k+1][F].
+// Slot filter of the expert kernels: every routed slot, only the slots whose
+// expert is hot (in HBM; the shared expert counts as hot), or only the
+// others (arena / host).  A filtered-out slot's outputs are left untouched,
+// so a hot launch and a cold launch together write what one launch does.
+enum SlotFilter { SLOTS_ALL = 0, SLOTS_HOT = 1, SLOTS_COLD = 2 };
+
 hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, const ExpSrc &u,
                               const int32_t *ids, const Route *route, const Xq &xq, float *gu,
                               int H, int F, int k, const uint8_t *sh_gate = nullptr,
-                              const uint8_t *sh_up = nullptr);
+                              const uint8_t *sh_up = nullptr, int filter = SLOTS_ALL);
 
 // partial[s] = Wd[e_s] swiglu(gu[0][s], gu[1][s]) for the k routed slots
 // (and the shared expert's down matrix as slot k if sh_down); gu is
 // [2][nslots][F], partial [nslots][H].
 hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_t *ids,
                            const float *gu, float *partial, int H, int F, int k,
-                           const uint8_t *sh_down = nullptr);
+                           const uint8_t *sh_down = nullptr, int filter = SLOTS_ALL);
 
 // The whole MoE block of one layer in one launch of nwg workgroups (all
 // resident at once): ffn RMSNorm + router, top-k, gate/up, swiglu + down,

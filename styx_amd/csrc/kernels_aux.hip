@@ -285,7 +285,17 @@ __global__ void __launch_bounds__(256) k_gather(GatherK a)
     const int64_t c1 = min(n16, c0 + GATHER_CHUNK / 16);
     const uint4 *src = (const uint4 *)(a.src[t] + (int64_t)e * a.src_slab[t]);
     uint4 *dst = (uint4 *)(a.dst[t] + (int64_t)slot * a.dst_slab[t]);
-    for (int64_t i = c0 + threadIdx.x; i < c1; i += 256) dst[i] = src[i];
+    // four loads in flight per thread: the source is host memory across
+    // PCIe, with a round trip of microseconds
+    int64_t i = c0 + threadIdx.x;
+    for (; i + 3 * 256 < c1; i += 4 * 256) {
+        const uint4 v0 = src[i], v1 = src[i + 256], v2 = src[i + 512], v3 = src[i + 768];
+        dst[i] = v0;
+        dst[i + 256] = v1;
+        dst[i + 512] = v2;
+        dst[i + 768] = v3;
+    }
+    for (; i < c1; i += 256) dst[i] = src[i];
 }
 
 static hipError_t gather_launch(hipStream_t st, const uint8_t *const src[3],

@@ -364,8 +364,15 @@ struct GateUpK {
     Route route;
     Xq xq;
     float *gu;  // [2][nslots][F]
-    int F, k, nslots, nb, rpw;
+    int F, k, nslots, nb, rpw, filter;
 };
+
+// Whether a slot with hot id h (SKIP: not hot) passes the launch's filter
+// (SlotFilter); the shared expert slot counts as hot.
+__device__ __forceinline__ bool slot_passes(int filter, bool hot)
+{
+    return filter == SLOTS_ALL || (filter == SLOTS_HOT) == hot;
+}
 
 // Routing first (one trip for the logits, then LDS work), then the slot's
 // weight loads, then the activation limbs.
@@ -374,15 +381,17 @@ __device__ inline void gate_up_body(const GateUpK &a, int m, int s, int32_t *s_i
 {
     const uint8_t *slab;
     if (s < a.k) {
+        uint32_t r3[3];
         if (a.route.logits) {
             const int32_t *ids = route_ids_wg(a.route, s_ids, s_lg);
-            uint32_t r3[3];
             route_row(a.route, ids[s], s, r3);
-            slab = slab_pick(a.src[m], r3[0], r3[1], r3[2]);
         } else {
-            slab = slab_for(a.src[m], a.ids, s);
+            for (int j = 0; j < 3; j++) r3[j] = (uint32_t)a.ids[16 * (j + 1) + s];
         }
+        if (!slot_passes(a.filter, r3[0] != SKIP)) return;
+        slab = slab_pick(a.src[m], r3[0], r3[1], r3[2]);
     } else {
+        if (!slot_passes(a.filter, true)) return;
         slab = a.sh[m];  // the shared expert needs no routing
     }
     if (!slab) return;
@@ -432,7 +441,8 @@ static hipError_t launch_gu_tu(hipStream_t st, int tu, int upl, const GateUpK &a
 
 hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, const ExpSrc &u,
                               const int32_t *ids, const Route *route, const Xq &xq, float *gu,
-                              int H, int F, int k, const uint8_t *sh_gate, const uint8_t *sh_up)
+                              int H, int F, int k, const uint8_t *sh_gate, const uint8_t *sh_up,
+                              int filter)
 {
     const Geo gg = pick_geo(tg, H);
     if (!gg.G || blk_elems(tg) != blk_elems(tu) || k < 1 || k > MAX_TOPK || !xq.A)
@@ -453,6 +463,7 @@ hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, c
     a.gu = gu;
     a.F = F;
     a.k = k;
+    a.filter = filter;
     a.nb = H / blk_elems(tg);
     // ~1024 workgroups in total over the 2*k slot matrices
     a.rpw = rows_per_wg(2 * a.nslots * F, gg.G, 1024);
@@ -476,7 +487,7 @@ struct DownK {
     const int32_t *ids;
     const float *gu;    // [2][nslots][F]
     float *partial;     // [nslots][H]
-    int H, F, k, nslots, nb, rpw;
+    int H, F, k, nslots, nb, rpw, filter;
 };
 
 template <int T, int UPL>
@@ -495,6 +506,7 @@ __global__ void __launch_bounds__(WG) k_down(DownK a)
 #pragma unroll
         for (int j = 0; j < 3; j++) idr[j] = a.ids[16 * (j + 1) + s];
     }
+    if (!slot_passes(a.filter, s >= a.k || (uint32_t)idr[0] != SKIP)) return;
     constexpr int PG = 4;  // gate/up values per thread held in registers
     const float *g = a.gu + (int64_t)s * a.F, *u = a.gu + ((int64_t)a.nslots + s) * a.F;
     float gv[PG], uv[PG];
@@ -533,7 +545,7 @@ __global__ void __launch_bounds__(WG) k_down(DownK a)
 
 hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_t *ids,
                            const float *gu, float *partial, int H, int F, int k,
-                           const uint8_t *sh_down)
+                           const uint8_t *sh_down, int filter)
 {
     const Geo g = pick_geo(td, F);
     if (!g.G || k < 1 || k > MAX_TOPK || F > XQ_MAX / 2) return hipErrorInvalidValue;
@@ -549,6 +561,7 @@ hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_
     a.H = H;
     a.F = F;
     a.k = k;
+    a.filter = filter;
     a.nb = F / blk_elems(td);
     a.rpw = rows_per_wg(a.nslots * H, g.G, 1024);
     const dim3 grid((H + a.rpw - 1) / a.rpw, a.nslots, 1);
