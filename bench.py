@@ -117,6 +117,40 @@ def moe_block_phases(m) -> dict | None:
     return out
 
 
+AT_PHASES = ["entry", "q_rotated", "tiles_done", "partials_stored", "partials_seen", "end"]
+
+
+def attn_phases(m) -> dict | None:
+    """Timeline of the attention launch on the last timed token: for each
+    phase, the median and the latest workgroup (us after the layer's first
+    workgroup entered), averaged over the layers; and the active chunks."""
+    tr = m.attn_trace()
+    if tr is None:
+        return None
+    st, tpu = tr
+    per = {p: ([], []) for p in AT_PHASES}
+    chunks = []
+    for lay in st.astype(np.float64):
+        live = lay[lay[:, 7] > 0]
+        if not len(live):
+            continue
+        t0 = live[:, 0].min()
+        chunks.append(int(live[0, 6]))
+        for i, p in enumerate(AT_PHASES):
+            v = live[:, i][live[:, i] > 0]
+            if len(v):
+                per[p][0].append(np.median(v - t0) / tpu)
+                per[p][1].append((v.max() - t0) / tpu)
+    if not chunks:
+        return None
+    out = {"active_chunks": chunks[-1], "workgroups": int((st[-1][:, 7] > 0).sum())}
+    for p, (med, mx) in per.items():
+        if med:
+            out[p] = {"median_us": round(float(np.mean(med)), 2),
+                      "last_us": round(float(np.mean(mx)), 2)}
+    return out
+
+
 def cpu_baseline(m, prompt, seconds: float, threads: int) -> dict:
     """Oracle decode of the same model on host cores (bounded sample)."""
     from oracle import oracle as O
@@ -460,9 +494,12 @@ def measure(m, args, prompt):
     stats = m.kernel_stats()
     m.set_timing(False)
     phases = moe_block_phases(m)
+    aph = attn_phases(m)
     table = kernel_table(m, stats, args.timing_steps, not args.no_graph)
     if phases:
         table["moe_block"]["phases"] = phases
+    if aph and "attn" in table:
+        table["attn"]["phases"] = aph
     return args.steps / el, el, np.concatenate(toks), table
 
 

@@ -352,6 +352,15 @@ int styx_moe_set_timing(styx_moe *m, int on);
  * kernels; out may be NULL to query *nwg. */
 int styx_moe_moe_block_trace(styx_moe *m, uint64_t *out, int64_t max_count, int *nwg,
                              double *ticks_per_us);
+/* Phase stamps of the attention launches from the last timed token
+ * (measurement helper, no counterpart in the reference):
+ * [n_layers][*nwg][8] wall-clock ticks per workgroup -- 0 entry, 1 q heads
+ * normalised and rotated, 2 the chunk's tiles done, 3 partials stored, 4
+ * partials of the first merged head seen (in-kernel combine), 5 end, 6 the
+ * active chunks, 7 (kv head << 16 | chunk) + 1; all 0 for a workgroup past
+ * the context.  out may be NULL to query *nwg. */
+int styx_moe_attn_trace(styx_moe *m, uint64_t *out, int64_t max_count, int *nwg,
+                        double *ticks_per_us);
 /* Stage timing (measurement helper, no counterpart in the reference): the
  * launches of one stage ("embed", "qkv", "attn", "o_proj", "router",
  * "gather", "moe_gate_up", "shexp", "moe_down", "reduce", "lm_head") for

@@ -143,6 +143,7 @@ _SIGS = {
     "styx_moe_decode": (i32, [vp, i32, vp]),
     "styx_moe_set_timing": (i32, [vp, i32]),
     "styx_moe_moe_block_trace": (i32, [vp, vp, i64, C.POINTER(i32), C.POINTER(C.c_double)]),
+    "styx_moe_attn_trace": (i32, [vp, vp, i64, C.POINTER(i32), C.POINTER(C.c_double)]),
     "styx_moe_time_stage": (i32, [vp, C.c_char_p, i32, C.POINTER(C.c_double), C.POINTER(i32)]),
     "styx_moe_last_expert_ids": (i32, [vp, vp]),
     "styx_moe_last_hot_cold": (i32, [vp, vp]),

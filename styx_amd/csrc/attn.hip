@@ -125,6 +125,29 @@ __device__ __forceinline__ float sum_rows(float v)
     return __uint_as_float(t[0]) + __uint_as_float(t[1]);
 }
 
+// Phase stamps of a workgroup (AttnArgs::trace): kept by thread 0 in LDS,
+// written out when the workgroup ends.
+struct AtStamps {
+    uint64_t *s;  // LDS slots, or null when not tracing
+    __device__ __forceinline__ void clear() const
+    {
+        if (s && threadIdx.x == 0)
+            for (int i = 0; i < AT_TRACE; i++) s[i] = 0;
+    }
+    __device__ __forceinline__ void at(int i) const
+    {
+        if (s && threadIdx.x == 0) s[i] = wall_clock64();
+    }
+    __device__ __forceinline__ void flush(const AttnArgs &a, int c, int kvh, int n_active) const
+    {
+        if (!s || threadIdx.x != 0) return;
+        s[6] = (uint64_t)n_active;
+        s[7] = ((uint64_t)kvh << 16 | (uint64_t)c) + 1;
+        uint64_t *d = a.trace + ((int64_t)kvh * gridDim.x + c) * AT_TRACE;
+        for (int i = 0; i < AT_TRACE; i++) gst<uint64_t>(d + i, s[i]);
+    }
+};
+
 // ------------------------------------------------------ in-kernel combine --
 // With a.t_part the chunk workgroups publish their partials (m, l, o) as
 // tagged words, and query head g of kv head kvh is merged by the workgroup
@@ -166,7 +189,7 @@ __device__ __forceinline__ unsigned long long attn_ticket(const AttnArgs &a)
 
 template <int EPL>
 __device__ void attn_combine_tail(const AttnArgs &a, int c, int kvh, int n_active, uint32_t tag,
-                                  float *sm)
+                                  float *sm, AtStamps st)
 {
     constexpr int HD = 64 * EPL;
     const int gqa = a.nh / a.nkv, ps = HD + 2;
@@ -232,6 +255,7 @@ __device__ void attn_combine_tail(const AttnArgs &a, int c, int kvh, int n_activ
                     }
                     __builtin_amdgcn_s_sleep(1);
                 }
+                if (r0 == g_begin && c0 == sw) st.at(4);
 #pragma unroll
                 for (int b = 0; b < CT_BATCH; b++) {
                     if (mc[b] == -INFINITY) continue;
@@ -301,6 +325,10 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
 {
     constexpr int HD = 64 * EPL, PPL = (HD / 2 + 63) / 64, SEG = HD / 4;
     const int c = blockIdx.x, kvh = blockIdx.y;
+    __shared__ uint64_t s_tr[AT_TRACE];
+    const AtStamps st{a.trace ? s_tr : nullptr};
+    st.clear();
+    st.at(0);
     const unsigned long long ticket = attn_ticket(a);  // also drawn by chunks past the context
     const int gqa = a.nh / a.nkv, kv_dim = a.nkv * HD;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -395,6 +423,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
 #pragma unroll
     for (int i = 0; i < MAXH; i++)
         if (i < hpw) head_finish<PPL>(hq[i], cs, a.q_norm != nullptr, a.eps, HD, qs + i * HD);
+    st.at(1);
     if (owns_pos) {
         head_finish<PPL>(hk, cs, a.k_norm != nullptr, a.eps, HD, knew);
 #pragma unroll
@@ -484,6 +513,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
+    st.at(2);
     if (owns_pos && wave == 0) {
         const int64_t po = kv_off(a, pos, kvh, kv_dim);
         for (int e = lane; e < HD; e += 64) {
@@ -509,7 +539,10 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
                 part_put(a, pg + HD + 1, tag, l_run[g]);
             }
         }
-        if (a.t_part) attn_combine_tail<EPL>(a, c, kvh, n_active, tag, sm);
+        st.at(3);
+        if (a.t_part) attn_combine_tail<EPL>(a, c, kvh, n_active, tag, sm, st);
+        st.at(5);
+        st.flush(a, c, kvh, n_active);
         return;
     }
     // merge the NTS waves of each head group: M = max m_w, L = sum l_w
@@ -546,7 +579,10 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
             part_put(a, part0 + gg * ps + HD + 1, tag, L);
         }
     }
-    if (a.t_part) attn_combine_tail<EPL>(a, c, kvh, n_active, tag, sm);
+    st.at(3);
+    if (a.t_part) attn_combine_tail<EPL>(a, c, kvh, n_active, tag, sm, st);
+    st.at(5);
+    st.flush(a, c, kvh, n_active);
 }
 
 // ---------------------------------------------------------------------------
@@ -576,6 +612,10 @@ __device__ __forceinline__ constexpr int vcol(int r, int b) { return 64 * (b >> 
 __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
 {
     const int c = blockIdx.x, kvh = blockIdx.y;
+    __shared__ uint64_t s_tr[AT_TRACE];
+    const AtStamps st{a.trace ? s_tr : nullptr};
+    st.clear();
+    st.at(0);
     const unsigned long long ticket = attn_ticket(a);  // also drawn by chunks past the context
     const int gqa = a.nh / a.nkv, kv_dim = a.nkv * MHD;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -684,6 +724,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
         else
             for (int e = lane; e < MHD; e += 64) qs[i * MHD + e] = 0.0f;
     }
+    st.at(1);
     if (owns_pos && wave == 0) {
         head_finish<1>(hk, cs, a.k_norm != nullptr, a.eps, MHD, knew);
 #pragma unroll
@@ -772,6 +813,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 
+    st.at(2);
     // merge the four waves (each covered every head over its own tiles)
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -820,7 +862,11 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
             part_put(a, part0 + h * ps + MHD + 1, tag, mL[h]);
         }
     }
-    if (a.t_part) attn_combine_tail<MHD / 64>(a, c, kvh, (n_t + chunk - 1) / chunk, tag, sm);
+    st.at(3);
+    const int n_active = (n_t + chunk - 1) / chunk;
+    if (a.t_part) attn_combine_tail<MHD / 64>(a, c, kvh, n_active, tag, sm, st);
+    st.at(5);
+    st.flush(a, c, kvh, n_active);
 }
 
 // Merge the per-chunk partials (m, l, o) of one query head: M = max m_c,

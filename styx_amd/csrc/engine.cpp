@@ -152,6 +152,7 @@ struct styx_moe {
     uint64_t *t_xq = nullptr;
     int mb_nwg = -1;
     uint64_t *mb_trace = nullptr;  // [L][mb_nwg][16] phase stamps of the last timed token
+    uint64_t *at_trace = nullptr;  // [L][max_chunks * nkv][AT_TRACE] attention phase stamps
     // arena
     uint8_t *arena[3] = {nullptr, nullptr, nullptr};
     int64_t arena_slab[3] = {0, 0, 0};
@@ -337,6 +338,9 @@ int styx_moe::setup_runtime()
     if (int r = dalloc(&attn_part, (size_t)pf)) return r;
     if (int r = dalloc(&at_part, (size_t)pf)) return r;
     if (int r = dalloc(&at_tickets, 64 * 16)) return r;
+    if (int r = dalloc(&at_trace, (size_t)L * max_chunks * nkv * AT_TRACE)) return r;
+    STYX_HIP(hipMemsetAsync(at_trace, 0, sizeof(uint64_t) * L * max_chunks * nkv * AT_TRACE,
+                            gpu->stream));
     STYX_HIP(hipMemsetAsync(at_part, 0, sizeof(uint64_t) * pf, gpu->stream));
     STYX_HIP(hipMemsetAsync(at_tickets, 0, sizeof(unsigned long long) * 64 * 16, gpu->stream));
     // tagged exchange of the fused MoE block: zero once (tag 0 is never a
@@ -632,8 +636,13 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
         }
         if (!folded)
             tend(e0, "qkv", (double)(ly.wq.bytes() + ly.wk.bytes() + ly.wv.bytes()) + xq_bytes(H));
-        e0 = tstart();
         AttnArgs aa{};
+        if (timing) {
+            // phase stamps of every workgroup (eager timed tokens only)
+            aa.trace = at_trace + (size_t)l * max_chunks * nkv * AT_TRACE;
+            CK(hipMemsetAsync(aa.trace, 0, sizeof(uint64_t) * max_chunks * nkv * AT_TRACE, st));
+        }
+        e0 = tstart();
         aa.q = q;
         aa.k = kk;
         aa.v = vv;
@@ -1852,6 +1861,29 @@ int styx_moe_moe_block_trace(styx_moe *m, uint64_t *out, int64_t max_count, int 
     STYX_HIP(hipSetDevice(m->gpu->device));
     STYX_HIP(hipStreamSynchronize(m->gpu->stream));
     STYX_HIP(hipMemcpy(out, m->mb_trace, sizeof(uint64_t) * n, hipMemcpyDeviceToHost));
+    if (ticks_per_us) {
+        int khz = 0;
+        STYX_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, m->gpu->device));
+        *ticks_per_us = khz / 1000.0;
+    }
+    return STYX_OK;
+}
+
+// Phase stamps of the attention launches from the last timed token
+// (measurement, no reference counterpart): [n_layers][max_chunks * n_kv]
+// [8] wall-clock ticks, 0 for workgroups past the context; slot 7 names the
+// workgroup ((kv head << 16 | chunk) + 1), slot 6 holds the active chunks.
+int styx_moe_attn_trace(styx_moe *m, uint64_t *out, int64_t max_count, int *nwg,
+                        double *ticks_per_us)
+{
+    if (!m || !nwg) return fail(STYX_E_INVALID, "styx_moe_attn_trace: bad argument");
+    *nwg = m->at_trace ? m->max_chunks * m->nkv : 0;
+    if (*nwg == 0 || !out) return STYX_OK;
+    const int64_t n = (int64_t)m->L * *nwg * AT_TRACE;
+    if (max_count < n) return fail(STYX_E_INVALID, "styx_moe_attn_trace: buffer too small");
+    STYX_HIP(hipSetDevice(m->gpu->device));
+    STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+    STYX_HIP(hipMemcpy(out, m->at_trace, sizeof(uint64_t) * n, hipMemcpyDeviceToHost));
     if (ticks_per_us) {
         int khz = 0;
         STYX_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, m->gpu->device));

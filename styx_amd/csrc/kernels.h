@@ -205,7 +205,15 @@ struct AttnArgs {
     unsigned long long *tickets;
     int *abort;
     int max_polls;
+    // Optional phase stamps (measurement): AT_TRACE wall-clock ticks per
+    // workgroup at trace[(kvh * gridDim.x + chunk) * AT_TRACE]; workgroups
+    // past the context write nothing.
+    uint64_t *trace;
 };
+// Stamps: 0 entry, 1 q heads rotated, 2 tiles done, 3 partials stored,
+// 4 partials seen (in-kernel combine), 5 end, 6 active chunks, 7 the
+// workgroup (kvh << 16 | chunk) + 1.
+constexpr int AT_TRACE = 8;
 hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a);
 // Chunks per kv head up to which the partials are merged in-kernel (the
 // caller's choice; with t_part the launch has no more chunk workgroups than

@@ -146,6 +146,18 @@ class MoeModel:
                                                  C.byref(tpu)))
         return out, tpu.value
 
+    def attn_trace(self) -> tuple[np.ndarray, float] | None:
+        """Phase stamps of the attention launches from the last timed token:
+        ([n_layers][nwg][8] ticks, ticks per us), or None."""
+        nwg, tpu = C.c_int(), C.c_double()
+        L.check(self.lib.styx_moe_attn_trace(self.h, None, 0, C.byref(nwg), None))
+        if nwg.value == 0:
+            return None
+        out = np.zeros((self.hp.n_layers, nwg.value, 8), np.uint64)
+        L.check(self.lib.styx_moe_attn_trace(self.h, out.ctypes.data, out.size, C.byref(nwg),
+                                            C.byref(tpu)))
+        return out, tpu.value
+
     def last_expert_ids(self) -> np.ndarray:
         """moe.rs:2387-2402: [n_layers][k]."""
         out = np.empty((self.hp.n_layers, self.hp.n_expert_used), np.uint32)

@@ -188,3 +188,35 @@ def test_repin_swaps_keep_logits_identical(gpu, arena):
     assert hot_last > hot_first
     ref.close()
     m.close()
+
+
+def test_phase_stamps_of_a_timed_token(gpu):
+    """Timing mode leaves the logits unchanged and records, per layer, the
+    phase stamps of the fused MoE block and of the attention workgroups in
+    the context: present, ordered (entry <= q rotated <= tiles done <=
+    partials stored <= end), one workgroup per active chunk and kv head."""
+    from styx_amd import MoeModel
+    cfg = small_cfg(seed=9)
+    a = MoeModel.synth(gpu, cfg, n_ctx=64)
+    b = MoeModel.synth(gpu, cfg, n_ctx=64)
+    for t in range(1, 40):
+        la = a.forward_token(t)
+        b.set_timing(t == 39)
+        lb = b.forward_token(t)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), t
+    st, tpu = b.attn_trace()
+    assert tpu > 0 and st.shape[0] == cfg.n_layers
+    for lay in st:
+        live = lay[lay[:, 7] > 0]
+        n_active = int(live[0, 6])
+        assert n_active >= 1 and len(live) == n_active * cfg.n_kv_heads
+        ids = sorted(int(w) - 1 for w in live[:, 7])
+        assert ids == sorted((h << 16) | c for h in range(cfg.n_kv_heads) for c in range(n_active))
+        for row in live.astype(np.int64):
+            seq = [row[0], row[1], row[2], row[3], row[5]]
+            assert all(x > 0 for x in seq) and seq == sorted(seq), row
+    mb = b.moe_block_trace()
+    if mb is not None:
+        assert (mb[0][:, :, 0] > 0).any()
+    a.close()
+    b.close()
