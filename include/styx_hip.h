@@ -112,8 +112,37 @@ int styx_batch_begin(styx_batch *b);
 int styx_batch_dispatch(styx_batch *b, const styx_kernel *k, const styx_binding *binds,
                         int n_binds, const void *push, uint32_t push_len, uint32_t gx,
                         uint32_t gy, uint32_t gz, int barrier);
-/* Batch::submit (lib.rs:200-231): run the recorded work and wait for it. */
+/* Batch::submit (lib.rs:200-231): run the recorded work and wait for it
+ * (an async batch runs it on its own stream). */
 int styx_batch_submit(styx_batch *b);
+
+/* Asynchronous submission (the reference's M7b-B prefetch path).
+ * A timeline stands in for a Vulkan timeline semaphore: every
+ * styx_batch_submit_async signals one value (values strictly increase), and
+ * a batch submitted with styx_batch_submit_wait_sem starts once the
+ * timeline has reached its value.  Deviation: a wait for a value that no
+ * submit has signalled yet fails with STYX_E_STATE (Vulkan allows
+ * wait-before-signal). */
+typedef struct styx_timeline styx_timeline;
+/* Gpu::create_timeline_semaphore (lib.rs:700-713), initial value 0. */
+int styx_timeline_new(styx_gpu *gpu, styx_timeline **out);
+void styx_timeline_free(styx_timeline *t);
+/* The largest signalled value whose batch has completed
+ * (vkGetSemaphoreCounterValue). */
+int styx_timeline_value(styx_timeline *t, uint64_t *value);
+/* Gpu::create_async_batch (lib.rs:716-754): a batch on a stream of its own
+ * (default priority), beside the gpu's stream; styx_batch_free on it waits
+ * for its in-flight work first (destroy_async_batch, lib.rs:1577-1589). */
+int styx_batch_new_async(styx_gpu *gpu, styx_batch **out);
+/* Batch::submit_async (lib.rs:233-271): run the recorded work on the async
+ * batch's stream and return at once; the timeline reaches `value` when it
+ * completes.  STYX_E_STATE for a batch not made by styx_batch_new_async. */
+int styx_batch_submit_async(styx_batch *b, styx_timeline *t, uint64_t value);
+/* Batch::wait_idle (lib.rs:273-287): wait for the last submit_async. */
+int styx_batch_wait_idle(styx_batch *b);
+/* Batch::submit_wait_sem (lib.rs:289-333): the recorded work starts once
+ * the timeline reaches `value`; returns when it is done. */
+int styx_batch_submit_wait_sem(styx_batch *b, styx_timeline *t, uint64_t value);
 
 /* ------------------------------------------------------- hot-path ops ---- */
 /* Direct entry points of the gfx950 kernels (device pointers, enqueued on

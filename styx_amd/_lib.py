@@ -107,6 +107,13 @@ _SIGS = {
     "styx_batch_begin": (i32, [vp]),
     "styx_batch_dispatch": (i32, [vp, vp, vp, i32, vp, u32, u32, u32, u32, i32]),
     "styx_batch_submit": (i32, [vp]),
+    "styx_batch_new_async": (i32, [vp, C.POINTER(vp)]),
+    "styx_batch_submit_async": (i32, [vp, vp, u64]),
+    "styx_batch_wait_idle": (i32, [vp]),
+    "styx_batch_submit_wait_sem": (i32, [vp, vp, u64]),
+    "styx_timeline_new": (i32, [vp, C.POINTER(vp)]),
+    "styx_timeline_free": (None, [vp]),
+    "styx_timeline_value": (i32, [vp, C.POINTER(u64)]),
     "styx_op_to_split": (i32, [vp, i32, vp, vp, i64, i64]),
     "styx_op_from_split": (i32, [vp, i32, vp, vp, i64, i64]),
     "styx_op_dequant_rows": (i32, [vp, i32, vp, i64, i32, i64, i64, vp]),

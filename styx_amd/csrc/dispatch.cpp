@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cstring>
 #include <string>
+#include <mutex>
 #include <vector>
 
 #include "refk.h"
@@ -25,6 +26,12 @@ struct styx_kernel {
 struct styx_batch {
     styx_gpu *gpu = nullptr;
     bool recording = false;
+    // An async batch (Gpu::create_async_batch) runs on a stream of its own
+    // (the async queue); `done` marks the end of its last submit, which
+    // wait_idle waits for.
+    hipStream_t own = nullptr;
+    hipEvent_t done = nullptr;
+    bool pending = false;
     struct Cmd {
         const styx_kernel *k;
         std::vector<void *> ptr;
@@ -64,6 +71,51 @@ const KDef kdefs[] = {
     {"mul_mat_vec_id_q5_k_f32_f32", RK_MMV_BASE + 6, 6, 48},
     {"mul_mat_vec_id_q6_k_f32_f32", RK_MMV_BASE + 7, 6, 48},
 };
+
+}  // namespace
+
+// Timeline semaphore (Gpu::create_timeline_semaphore, lib.rs:700-713): each
+// signal of value v is an event recorded on the signalling stream; a wait
+// for v waits for the first recorded signal of a value >= v.
+struct styx_timeline {
+    styx_gpu *gpu = nullptr;
+    std::mutex mu;
+    std::vector<std::pair<uint64_t, hipEvent_t>> sig;  // values ascending
+    uint64_t reached = 0;  // largest value whose signal has completed
+};
+
+namespace {
+
+// The recorded work of b, launched in order on stream st.
+int run_cmds(styx_batch *b, hipStream_t st)
+{
+    for (auto &c : b->cmds) {
+        const uint32_t *spec = c.k->spec.empty() ? nullptr : c.k->spec.data();
+        hipError_t e = refk_launch(st, c.k->kid, c.ptr.data(), c.size.data(), c.push.data(), c.gx,
+                                   c.gy, c.gz, spec, (int)c.k->spec.size() / 2);
+        if (e == hipErrorInvalidValue)
+            return fail(STYX_E_INVALID, c.k->name + ": unsupported parameters, or the push "
+                                                    "constants and grid reach past a binding");
+        if (e != hipSuccess) return hip_fail(e, c.k->name.c_str());
+    }
+    b->cmds.clear();
+    return STYX_OK;
+}
+
+// Completed signals are dropped and `reached` advanced (caller holds mu).
+int timeline_poll(styx_timeline *t)
+{
+    size_t n = 0;
+    for (; n < t->sig.size(); n++) {
+        const hipError_t e = hipEventQuery(t->sig[n].second);
+        if (e == hipErrorNotReady) break;
+        if (e != hipSuccess) return hip_fail(e, "hipEventQuery");
+        t->reached = t->sig[n].first;
+        hipEventDestroy(t->sig[n].second);
+    }
+    t->sig.erase(t->sig.begin(), t->sig.begin() + n);
+    return STYX_OK;
+}
 
 }  // namespace
 
@@ -109,6 +161,7 @@ void styx_kernel_free(styx_kernel *k)
     gpu_release(g);
 }
 
+
 int styx_batch_new(styx_gpu *gpu, styx_batch **out)
 {
     if (!gpu || !out) return fail(STYX_E_INVALID, "styx_batch_new: bad argument");
@@ -119,10 +172,38 @@ int styx_batch_new(styx_gpu *gpu, styx_batch **out)
     return STYX_OK;
 }
 
+int styx_batch_new_async(styx_gpu *gpu, styx_batch **out)
+{
+    if (!gpu || !out) return fail(STYX_E_INVALID, "styx_batch_new_async: bad argument");
+    STYX_HIP(hipSetDevice(gpu->device));
+    hipStream_t st = nullptr;
+    STYX_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));  // default priority
+    hipEvent_t ev = nullptr;
+    const hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        hipStreamDestroy(st);
+        return hip_fail(e, "hipEventCreateWithFlags");
+    }
+    styx_batch *b = new styx_batch();
+    b->gpu = gpu;
+    b->own = st;
+    b->done = ev;
+    gpu->live_children++;
+    *out = b;
+    return STYX_OK;
+}
+
 void styx_batch_free(styx_batch *b)
 {
     if (!b) return;
     styx_gpu *g = b->gpu;
+    if (b->own) {
+        // destroy_async_batch waits on any in-flight submit first
+        hipSetDevice(g->device);
+        hipStreamSynchronize(b->own);
+        hipEventDestroy(b->done);
+        hipStreamDestroy(b->own);
+    }
     delete b;
     gpu_release(g);
 }
@@ -176,18 +257,111 @@ int styx_batch_submit(styx_batch *b)
     if (!b->recording) return fail(STYX_E_STATE, "styx_batch_submit: batch not begun");
     b->recording = false;
     STYX_HIP(hipSetDevice(b->gpu->device));
-    for (auto &c : b->cmds) {
-        const uint32_t *spec = c.k->spec.empty() ? nullptr : c.k->spec.data();
-        hipError_t e = refk_launch(b->gpu->stream, c.k->kid, c.ptr.data(), c.size.data(),
-                                   c.push.data(), c.gx, c.gy, c.gz, spec,
-                                   (int)c.k->spec.size() / 2);
-        if (e == hipErrorInvalidValue)
-            return fail(STYX_E_INVALID, c.k->name + ": unsupported parameters, or the push "
-                                                    "constants and grid reach past a binding");
-        if (e != hipSuccess) return hip_fail(e, c.k->name.c_str());
+    hipStream_t st = b->own ? b->own : b->gpu->stream;
+    if (int r = run_cmds(b, st)) return r;
+    STYX_HIP(hipStreamSynchronize(st));
+    return STYX_OK;
+}
+
+int styx_timeline_new(styx_gpu *gpu, styx_timeline **out)
+{
+    if (!gpu || !out) return fail(STYX_E_INVALID, "styx_timeline_new: bad argument");
+    styx_timeline *t = new styx_timeline();
+    t->gpu = gpu;
+    gpu->live_children++;
+    *out = t;
+    return STYX_OK;
+}
+
+void styx_timeline_free(styx_timeline *t)
+{
+    if (!t) return;
+    styx_gpu *g = t->gpu;
+    hipSetDevice(g->device);
+    for (auto &p : t->sig) {
+        hipEventSynchronize(p.second);
+        hipEventDestroy(p.second);
     }
-    b->cmds.clear();
-    STYX_HIP(hipStreamSynchronize(b->gpu->stream));
+    delete t;
+    gpu_release(g);
+}
+
+int styx_timeline_value(styx_timeline *t, uint64_t *value)
+{
+    if (!t || !value) return fail(STYX_E_INVALID, "styx_timeline_value: bad argument");
+    std::lock_guard<std::mutex> lock(t->mu);
+    STYX_HIP(hipSetDevice(t->gpu->device));
+    if (int r = timeline_poll(t)) return r;
+    *value = t->reached;
+    return STYX_OK;
+}
+
+int styx_batch_submit_async(styx_batch *b, styx_timeline *t, uint64_t value)
+{
+    if (!b || !t) return fail(STYX_E_INVALID, "styx_batch_submit_async: NULL batch or timeline");
+    if (!b->recording) return STYX_OK;  // nothing recorded: nothing to submit (lib.rs:243-245)
+    if (!b->own)
+        return fail(STYX_E_STATE, "styx_batch_submit_async: batch was not made by "
+                                  "styx_batch_new_async");
+    if (t->gpu != b->gpu)
+        return fail(STYX_E_INVALID, "styx_batch_submit_async: timeline of another styx_gpu");
+    std::lock_guard<std::mutex> lock(t->mu);
+    const uint64_t last = t->sig.empty() ? t->reached : t->sig.back().first;
+    if (value <= last)
+        return fail(STYX_E_INVALID, "styx_batch_submit_async: a timeline's signal values must "
+                                    "increase (last " + std::to_string(last) + ", got " +
+                                        std::to_string(value) + ")");
+    b->recording = false;
+    STYX_HIP(hipSetDevice(b->gpu->device));
+    if (int r = run_cmds(b, b->own)) return r;
+    hipEvent_t ev = nullptr;
+    STYX_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    hipError_t e = hipEventRecord(ev, b->own);
+    if (e == hipSuccess) e = hipEventRecord(b->done, b->own);
+    if (e != hipSuccess) {
+        hipEventDestroy(ev);
+        return hip_fail(e, "hipEventRecord");
+    }
+    t->sig.emplace_back(value, ev);
+    b->pending = true;
+    return STYX_OK;
+}
+
+int styx_batch_wait_idle(styx_batch *b)
+{
+    if (!b) return fail(STYX_E_INVALID, "styx_batch_wait_idle: NULL batch");
+    if (!b->pending) return STYX_OK;
+    STYX_HIP(hipSetDevice(b->gpu->device));
+    STYX_HIP(hipEventSynchronize(b->done));
+    b->pending = false;
+    return STYX_OK;
+}
+
+int styx_batch_submit_wait_sem(styx_batch *b, styx_timeline *t, uint64_t value)
+{
+    if (!b || !t) return fail(STYX_E_INVALID, "styx_batch_submit_wait_sem: NULL batch or timeline");
+    if (!b->recording) return STYX_OK;
+    if (t->gpu != b->gpu)
+        return fail(STYX_E_INVALID, "styx_batch_submit_wait_sem: timeline of another styx_gpu");
+    STYX_HIP(hipSetDevice(b->gpu->device));
+    hipStream_t st = b->own ? b->own : b->gpu->stream;
+    {
+        std::lock_guard<std::mutex> lock(t->mu);
+        if (int r = timeline_poll(t)) return r;
+        if (t->reached < value) {
+            // the first pending signal that reaches the value; a wait for a
+            // value nobody has submitted yet would never end on one stream
+            size_t i = 0;
+            while (i < t->sig.size() && t->sig[i].first < value) i++;
+            if (i == t->sig.size())
+                return fail(STYX_E_STATE, "styx_batch_submit_wait_sem: no signal of value >= " +
+                                              std::to_string(value) + " has been submitted");
+            STYX_HIP(hipStreamWaitEvent(st, t->sig[i].second, 0));
+        }
+    }
+    b->recording = false;
+    if (int r = run_cmds(b, st)) return r;
+    STYX_HIP(hipStreamSynchronize(st));
     return STYX_OK;
 }
 

@@ -115,13 +115,35 @@ class Kernel:
             self.h = None
 
 
-class Batch:
-    """Batch (lib.rs:44-231): begin, dispatch*, submit."""
+class Timeline:
+    """Timeline semaphore (Gpu::create_timeline_semaphore, lib.rs:700-713)."""
 
     def __init__(self, gpu: Gpu):
         self.gpu, self.lib = gpu, gpu.lib
         h = C.c_void_p()
-        L.check(self.lib.styx_batch_new(gpu.h, C.byref(h)))
+        L.check(self.lib.styx_timeline_new(gpu.h, C.byref(h)))
+        self.h = h
+
+    def value(self) -> int:
+        v = C.c_uint64()
+        L.check(self.lib.styx_timeline_value(self.h, C.byref(v)))
+        return v.value
+
+    def free(self):
+        if self.h:
+            self.lib.styx_timeline_free(self.h)
+            self.h = None
+
+
+class Batch:
+    """Batch (lib.rs:44-333): begin, dispatch*, submit; an async batch
+    (Gpu::create_async_batch) also submit_async / wait_idle."""
+
+    def __init__(self, gpu: Gpu, is_async: bool = False):
+        self.gpu, self.lib = gpu, gpu.lib
+        h = C.c_void_p()
+        new = self.lib.styx_batch_new_async if is_async else self.lib.styx_batch_new
+        L.check(new(gpu.h, C.byref(h)))
         self.h = h
 
     def begin(self):
@@ -139,6 +161,15 @@ class Batch:
 
     def submit(self):
         L.check(self.lib.styx_batch_submit(self.h))
+
+    def submit_async(self, t: Timeline, value: int):
+        L.check(self.lib.styx_batch_submit_async(self.h, t.h, value))
+
+    def wait_idle(self):
+        L.check(self.lib.styx_batch_wait_idle(self.h))
+
+    def submit_wait_sem(self, t: Timeline, value: int):
+        L.check(self.lib.styx_batch_submit_wait_sem(self.h, t.h, value))
 
     def free(self):
         if self.h:

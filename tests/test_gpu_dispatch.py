@@ -327,3 +327,56 @@ def test_dispatch_rejects_reach_past_binding(gpu):
     with pytest.raises(L.StyxError, match="reach past"):
         run(gpu, "moe_reduce_f32", [gpu.zeros(8 * 1024 * 4), gpu.zeros(32), gpu.zeros(512 * 4)],
             struct.pack("<2I", 1024, 8), (4, 1, 1))
+
+
+def test_async_batch_and_timeline(gpu):
+    """The M7b-B surface (lib.rs:233-333, moe.rs:2093,2370-2375): an async
+    batch gathers slabs on its own stream and signals a timeline; the main
+    batch waits for that value, then adds the gathered slab to a vector.
+    The result equals the serial order's; the timeline reaches each
+    signalled value; signal values must increase; a wait for a value no one
+    signalled and submit_async on a plain batch are refused."""
+    from styx_amd import StyxError
+    from styx_amd.runtime import Batch, Kernel, Timeline
+    rng = np.random.default_rng(12)
+    E, k, slab = 4, 1, 1 << 20  # one 1 MiB slab per tensor
+    # finite f32 values as bytes (the add must not meet NaN payloads)
+    src = [rng.standard_normal(E * slab // 4).astype(np.float32).view(np.uint8) for _ in range(3)]
+    bsrc = [gpu.from_numpy(a) for a in src]
+    bdst = [gpu.zeros(k * slab) for _ in range(3)]
+    other = rng.standard_normal(slab // 4).astype(np.float32)
+    bo, bsum = f32buf(gpu, other), gpu.zeros(slab)
+    t = Timeline(gpu)
+    gk = Kernel(gpu, "gather_slabs_f32", [])
+    ak = Kernel(gpu, "add_flat_f32", [])
+    ab, mb = Batch(gpu, is_async=True), Batch(gpu)
+    ne = slab // 4
+    for rnd, e in enumerate([3, 1]):
+        ids = gpu.from_numpy(np.array([e], np.uint32))
+        ab.begin()
+        ab.dispatch(gk, bsrc + bdst + [ids],
+                    struct.pack("<9I", *[slab // 16] * 6, 0, k, 0), (k, 1, 1))
+        ab.submit_async(t, rnd + 1)
+        mb.begin()
+        mb.dispatch(ak, [bdst[0], bo, bsum], struct.pack("<I", ne), ((ne + 255) // 256, 1, 1))
+        mb.submit_wait_sem(t, rnd + 1)
+        ab.wait_idle()
+        assert t.value() == rnd + 1
+        want = src[0][e * slab:(e + 1) * slab].view(np.float32) + other
+        got = bsum.download(np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), rnd
+        for i in range(3):
+            assert np.array_equal(bdst[i].download(), src[i][e * slab:(e + 1) * slab])
+    ab.begin()
+    ab.dispatch(gk, bsrc + bdst + [gpu.from_numpy(np.array([0], np.uint32))],
+                struct.pack("<9I", *[slab // 16] * 6, 0, k, 0), (k, 1, 1))
+    with pytest.raises(StyxError):
+        ab.submit_async(t, 2)  # not above the last signalled value
+    mb.begin()
+    mb.dispatch(ak, [bdst[0], bo, bsum], struct.pack("<I", ne), ((ne + 255) // 256, 1, 1))
+    with pytest.raises(StyxError):
+        mb.submit_wait_sem(t, 9)  # never signalled
+    with pytest.raises(StyxError):
+        mb.submit_async(t, 9)  # a plain batch has no async stream
+    for o in (ab, mb, gk, ak, t):
+        o.free()
