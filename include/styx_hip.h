@@ -34,7 +34,7 @@ enum {
     STYX_E_FORMAT = -5,       /* GGUF / tensor layout rejected */
     STYX_E_STATE = -6,        /* call out of order (e.g. KV full) */
     STYX_E_UNSUPPORTED = -7,
-    STYX_E_DEVICE = -8,       /* a device-side wait gave up; model results invalid */
+    STYX_E_DEVICE = -8,       /* a device-side wait gave up (stage timing; tokens fall back) */
 };
 /* Thread-local message of the last failing call (never NULL). */
 const char *styx_last_error(void);
@@ -281,6 +281,12 @@ typedef struct {
     int no_fold_qkv;         /* 1: keep every layer's q/k/v matvec a kernel of
                                 its own instead of the previous fused MoE
                                 block's tail (same results) */
+    int max_polls;           /* rounds a fused launch's workgroup waits for
+                                another's data before it gives up; 0 =
+                                200000.  A launch that gives up makes the
+                                model fall back to the separate kernels,
+                                which do not wait, and run the token(s)
+                                again (tests lower it to force that) */
 } styx_moe_opts;
 
 typedef struct {
@@ -290,6 +296,8 @@ typedef struct {
     int norm_topk;
     uint64_t slab_bytes;     /* gate+up+down bytes of one (layer,expert) */
     uint64_t expert_bytes_hbm, expert_bytes_host;
+    int unfused_fallbacks;   /* times a fused launch gave up and the model
+                                went over to the separate kernels (0 or 1) */
 } styx_moe_hparams;
 
 typedef struct {
@@ -366,6 +374,9 @@ int styx_moe_generate(styx_moe *m, const uint32_t *prompt, int n_prompt, int n_p
  * each on the previous argmax token (generate_moe.rs:58-67 loop body);
  * out[i] = the token produced by step i. */
 int styx_moe_decode(styx_moe *m, int n_steps, uint32_t *out);
+/* The fused launches' wait bound (styx_moe_opts.max_polls) for the tokens
+ * that follow (test helper, no reference counterpart). */
+int styx_moe_set_wait_limit(styx_moe *m, int max_polls);
 /* Turn HIP-event timing of every kernel launch on or off (launches are then
  * enqueued one by one instead of replayed as a graph). */
 int styx_moe_set_timing(styx_moe *m, int on);

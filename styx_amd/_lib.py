@@ -39,6 +39,7 @@ class MoeOpts(C.Structure):
         ("time_kernels", C.c_int),
         ("no_fuse", C.c_int),
         ("no_fold_qkv", C.c_int),
+        ("max_polls", C.c_int),
     ]
 
 
@@ -50,6 +51,7 @@ class MoeHparams(C.Structure):
         ("n_vocab", C.c_int), ("n_ctx", C.c_int), ("rms_eps", C.c_float),
         ("rope_base", C.c_float), ("norm_topk", C.c_int), ("slab_bytes", C.c_uint64),
         ("expert_bytes_hbm", C.c_uint64), ("expert_bytes_host", C.c_uint64),
+        ("unfused_fallbacks", C.c_int),
     ]
 
 
@@ -150,6 +152,7 @@ _SIGS = {
     "styx_moe_decode": (i32, [vp, i32, vp]),
     "styx_moe_set_timing": (i32, [vp, i32]),
     "styx_moe_moe_block_trace": (i32, [vp, vp, i64, C.POINTER(i32), C.POINTER(C.c_double)]),
+    "styx_moe_set_wait_limit": (i32, [vp, i32]),
     "styx_moe_attn_trace": (i32, [vp, vp, i64, C.POINTER(i32), C.POINTER(C.c_double)]),
     "styx_moe_time_stage": (i32, [vp, C.c_char_p, i32, C.POINTER(C.c_double), C.POINTER(i32)]),
     "styx_moe_last_expert_ids": (i32, [vp, vp]),

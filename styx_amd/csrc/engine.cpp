@@ -185,6 +185,9 @@ struct styx_moe {
     int setup_runtime();
     int size_moe_block();
     int check_abort();
+    int fall_back_unfused();
+    int fallbacks = 0;
+    uint32_t *tok_save = nullptr;  // the pending token at a decode's start
     void queue_abort_read();
     int place_experts(const std::vector<std::vector<std::pair<uint32_t, uint64_t>>> *hist);
     int enqueue_token(bool gen, bool attn_merge_in_kernel);
@@ -350,6 +353,7 @@ int styx_moe::setup_runtime()
     if (int r = dalloc(&t_part, (size_t)(K + 1) * H)) return r;
     if (int r = dalloc(&mb_ticket, 64 * 16)) return r;
     if (int r = dalloc(&mb_abort, 1)) return r;
+    if (int r = dalloc(&tok_save, 1)) return r;
     STYX_HIP(hipMemsetAsync(t_lg, 0, sizeof(uint64_t) * E, gpu->stream));
     STYX_HIP(hipMemsetAsync(t_gu, 0, sizeof(uint64_t) * 2 * (K + 1) * F, gpu->stream));
     STYX_HIP(hipMemsetAsync(t_part, 0, sizeof(uint64_t) * (K + 1) * H, gpu->stream));
@@ -509,6 +513,7 @@ int styx_moe::place_experts(const std::vector<std::vector<std::pair<uint32_t, ui
 int styx_moe::size_moe_block()
 {
     mb_nwg = 0;
+    qkv_fold.assign(L, 0);  // no fold without the fused block
     if (opts.no_fuse || L == 0) return STYX_OK;
     int per_cu = 2;
     for (const Layer &ly : layers) {
@@ -566,6 +571,27 @@ int styx_moe::check_abort()
         return fail(STYX_E_DEVICE, "fused MoE block / attention: a workgroup's wait ran out (not "
                                    "all workgroups resident?); results of this model are invalid");
     return STYX_OK;
+}
+
+// After a fused launch gave up waiting: the model goes over to the separate
+// kernels for good (they never wait on another workgroup), the graphs
+// captured with the fused launches are replaced, and the flag is cleared.
+// The caller then runs the failed token(s) again: a token rewrites every
+// value it reads (the residual from the embedding, its KV row, the ids).
+int styx_moe::fall_back_unfused()
+{
+    opts.no_fuse = 1;
+    fallbacks++;
+    STYX_HIP(hipStreamSynchronize(gpu->stream));
+    for (int i = 0; i < 2; i++) {
+        if (g_fwd[i]) hipGraphExecDestroy(g_fwd[i]);
+        if (g_gen[i]) hipGraphExecDestroy(g_gen[i]);
+        g_fwd[i] = g_gen[i] = nullptr;
+    }
+    if (int r = size_moe_block()) return r;
+    STYX_HIP(hipMemsetAsync(mb_abort, 0, sizeof(int), gpu->stream));
+    h_stage[4] = 0;
+    return build_graphs();
 }
 
 // ------------------------------------------------------------ forward ----
@@ -669,7 +695,7 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
             aa.t_part = at_part;
             aa.tickets = at_tickets;
             aa.abort = mb_abort;
-            aa.max_polls = 200000;
+            aa.max_polls = opts.max_polls > 0 ? opts.max_polls : 200000;
         }
         if (want("attn")) CK(launch_attn_decode(st, aa));
         tend(e0, "attn", (double)(n_past + 1) * nkv * hd * 8.0);
@@ -783,6 +809,7 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
             mb.t_part = t_part;
             mb.ticket = mb_ticket;
             mb.abort = mb_abort;
+            mb.max_polls = opts.max_polls;
             mb.nwg = mb_nwg;
             const bool fold_next = l + 1 < L && qkv_fold[l + 1];
             double qkv_bytes = 0.0;
@@ -1692,6 +1719,7 @@ int styx_moe_get_hparams(const styx_moe *m, styx_moe_hparams *o)
     o->slab_bytes = m->slab_bytes;
     o->expert_bytes_hbm = m->exp_hbm;
     o->expert_bytes_host = m->exp_host;
+    o->unfused_fallbacks = m->fallbacks;
     return STYX_OK;
 }
 
@@ -1717,7 +1745,21 @@ int styx_moe_forward_token(styx_moe *m, uint32_t token, float *logits_out)
                                 m->gpu->stream));
     m->queue_abort_read();
     STYX_HIP(hipStreamSynchronize(m->gpu->stream));
-    if (int r = m->check_abort()) return r;
+    if (m->check_abort()) {
+        // the token again (same token and position, still in the stage), on
+        // the separate kernels
+        if (int r = m->fall_back_unfused()) return r;
+        if (int r = m->collect_stats()) return r;
+        m->n_past--;
+        STYX_HIP(hipMemcpyAsync(m->d_tok, &m->h_stage[0], 4, hipMemcpyHostToDevice, m->gpu->stream));
+        STYX_HIP(hipMemcpyAsync(m->d_pos, &m->h_stage[1], 4, hipMemcpyHostToDevice, m->gpu->stream));
+        if (int r = m->run_token(false)) return r;
+        m->n_past++;
+        if (logits_out)
+            STYX_HIP(hipMemcpyAsync(logits_out, m->logits, sizeof(float) * m->V,
+                                    hipMemcpyDeviceToHost, m->gpu->stream));
+        STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+    }
     return m->collect_stats();
 }
 
@@ -1733,7 +1775,16 @@ int styx_moe_decode(styx_moe *m, int n_steps, uint32_t *out)
     if (int r = m->ensure_pages(start + n_steps - 1)) return r;
     m->h_stage[1] = (uint32_t)start;
     STYX_HIP(hipMemcpyAsync(m->d_pos, &m->h_stage[1], 4, hipMemcpyHostToDevice, m->gpu->stream));
+    // the pending token, for a run again after a fused launch gives up
+    // (every step's argmax overwrites it)
+    if (!m->opts.no_fuse)
+        STYX_HIP(hipMemcpyAsync(m->tok_save, m->d_tok, 4, hipMemcpyDeviceToDevice, m->gpu->stream));
     const bool host_work = (m->opts.repin_interval > 0 && m->any_host) || m->opts.time_kernels;
+    // repin hit counts as they stand, for a run again after a fused launch
+    // gives up (each step adds the previous token's experts)
+    std::vector<std::vector<uint64_t>> hits0;
+    if (!m->opts.no_fuse && m->opts.repin_interval > 0 && m->any_host)
+        for (auto &ly : m->layers) hits0.push_back(ly.hits);
     for (int i = 0; i < n_steps; i++) {
         if (host_work) {
             // host bookkeeping between tokens needs the previous token done
@@ -1749,7 +1800,15 @@ int styx_moe_decode(styx_moe *m, int n_steps, uint32_t *out)
                             hipMemcpyDeviceToHost, m->gpu->stream));
     m->queue_abort_read();
     STYX_HIP(hipStreamSynchronize(m->gpu->stream));
-    if (int r = m->check_abort()) return r;
+    if (m->check_abort()) {
+        // the steps again from the pending token, on the separate kernels
+        if (int r = m->fall_back_unfused()) return r;
+        if (int r = m->collect_stats()) return r;
+        for (size_t l = 0; l < hits0.size(); l++) m->layers[l].hits = hits0[l];
+        m->n_past = start;
+        STYX_HIP(hipMemcpyAsync(m->d_tok, m->tok_save, 4, hipMemcpyDeviceToDevice, m->gpu->stream));
+        return styx_moe_decode(m, n_steps, out);
+    }
     return m->collect_stats();
 }
 
@@ -1890,6 +1949,24 @@ int styx_moe_attn_trace(styx_moe *m, uint64_t *out, int64_t max_count, int *nwg,
         *ticks_per_us = khz / 1000.0;
     }
     return STYX_OK;
+}
+
+// The fused launches' wait bound (styx_moe_opts.max_polls) for the
+// following tokens; the captured graphs are rebuilt with it (test helper, no
+// reference counterpart: a tiny bound forces the fall back to the separate
+// kernels from the host, with every kernel still ending normally).
+int styx_moe_set_wait_limit(styx_moe *m, int max_polls)
+{
+    if (!m || max_polls < 0) return fail(STYX_E_INVALID, "styx_moe_set_wait_limit: bad argument");
+    STYX_HIP(hipSetDevice(m->gpu->device));
+    STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+    m->opts.max_polls = max_polls;
+    for (int i = 0; i < 2; i++) {
+        if (m->g_fwd[i]) hipGraphExecDestroy(m->g_fwd[i]);
+        if (m->g_gen[i]) hipGraphExecDestroy(m->g_gen[i]);
+        m->g_fwd[i] = m->g_gen[i] = nullptr;
+    }
+    return m->build_graphs();
 }
 
 int styx_moe_set_timing(styx_moe *m, int on)

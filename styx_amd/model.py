@@ -57,7 +57,7 @@ CFG_LAYER_Q8 = SynthConfig(n_layers=1, n_vocab=4096)
 
 def make_opts(n_ctx=4096, use_graph=True, expert_budget_mb=-1, expert_hist=None, arena=True,
               repin_interval=0, repin_max=2, record_hidden=False, time_kernels=False,
-              fuse=True, fold_qkv=True):
+              fuse=True, fold_qkv=True, max_polls=0):
     o = L.MoeOpts()
     o.n_ctx, o.use_graph, o.expert_budget_mb = n_ctx, int(use_graph), expert_budget_mb
     o._hist = expert_hist.encode() if expert_hist else None
@@ -66,6 +66,7 @@ def make_opts(n_ctx=4096, use_graph=True, expert_budget_mb=-1, expert_hist=None,
     o.record_hidden, o.time_kernels = int(record_hidden), int(time_kernels)
     o.no_fuse = 0 if fuse else 1
     o.no_fold_qkv = 0 if fold_qkv else 1
+    o.max_polls = max_polls
     return o
 
 
@@ -145,6 +146,17 @@ class MoeModel:
         L.check(self.lib.styx_moe_moe_block_trace(self.h, out.ctypes.data, out.size, C.byref(nwg),
                                                  C.byref(tpu)))
         return out, tpu.value
+
+    def set_wait_limit(self, max_polls: int):
+        """Wait bound of the fused launches for the following tokens."""
+        L.check(self.lib.styx_moe_set_wait_limit(self.h, max_polls))
+
+    def unfused_fallbacks(self) -> int:
+        """Times a fused launch gave up and the model went over to the
+        separate kernels."""
+        hp = L.MoeHparams()
+        L.check(self.lib.styx_moe_get_hparams(self.h, C.byref(hp)))
+        return hp.unfused_fallbacks
 
     def attn_trace(self) -> tuple[np.ndarray, float] | None:
         """Phase stamps of the attention launches from the last timed token:

@@ -220,3 +220,36 @@ def test_phase_stamps_of_a_timed_token(gpu):
         assert (mb[0][:, :, 0] > 0).any()
     a.close()
     b.close()
+
+
+def test_fused_wait_that_gives_up_falls_back_to_separate_kernels(gpu):
+    """A fused launch whose bounded wait runs out (forced from the host with
+    a one-round bound; every kernel still ends normally) makes the model go
+    over to the separate kernels and run the token(s) again: in
+    forward_token the logits equal a model built with the separate kernels
+    bit for bit; inside a graph-replayed decode the steps are rerun from the
+    pending token and give the same greedy tokens."""
+    from styx_amd import MoeModel
+    cfg = small_cfg(seed=13)
+    prompt = [3, 5, 7, 11]
+    ref = MoeModel.synth(gpu, cfg, n_ctx=64, fuse=False)
+    want = [ref.forward_token(t) for t in prompt]
+    want_toks = ref.decode(12).tolist()
+    # in forward_token: the first token falls back
+    m = MoeModel.synth(gpu, cfg, n_ctx=64, max_polls=1)
+    for t, w in zip(prompt, want):
+        assert np.array_equal(m.forward_token(t).view(np.uint32), w.view(np.uint32))
+    assert m.unfused_fallbacks() == 1
+    assert m.decode(12).tolist() == want_toks
+    m.close()
+    # inside decode: the prompt runs fused (within 1e-6 of the separate
+    # kernels), then the bound drops and the decode's first launch gives up
+    m = MoeModel.synth(gpu, cfg, n_ctx=64)
+    for t, w in zip(prompt, want):
+        assert rel_l2(m.forward_token(t), w) < 1e-6
+    assert m.unfused_fallbacks() == 0
+    m.set_wait_limit(1)
+    assert m.decode(12).tolist() == want_toks
+    assert m.unfused_fallbacks() == 1
+    m.close()
+    ref.close()
