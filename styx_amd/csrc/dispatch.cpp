@@ -62,6 +62,8 @@ const KDef kdefs[] = {
     {"axpy_sig_f32", RK_AXPY_SIG, 3, 4},
     {"swiglu_f32", RK_SWIGLU, 3, 108},
     {"rms_norm_f32", RK_RMS_NORM, 3, 116},
+    {"rope_neox_f32", RK_ROPE_NEOX, 5, 116},
+    {"cpy_f32_f32", RK_CPY, 2, 120},
     {"mul_mat_vec_q8_0_f32_f32", RK_MMV_BASE + 0, 5, 52},
     {"mul_mat_vec_q4_k_f32_f32", RK_MMV_BASE + 1, 5, 52},
     {"mul_mat_vec_q5_k_f32_f32", RK_MMV_BASE + 2, 5, 52},

@@ -10,6 +10,7 @@
 #include "topk.h"
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 
 namespace styx {
@@ -183,6 +184,73 @@ __global__ void __launch_bounds__(64) kr_topk(const float *logits, float *w, int
     topk_wave(logits, (int)n, (int)k, (int)renorm, remap, pmap, 0, 0, w, ids);
 }
 
+// rope_neox_f32 with the RopePush of crates/vk-backend/src/ops.rs:385-439
+// for the mode the engine uses (NEOX, no frequency factors, no YaRN:
+// ext_factor 0, freq_scale 1, attn_factor 1): row r = (i3, i2, i1) of
+// (ne01, ne02) rows, pair i < ne00/2 of this thread; pairs (i, i + n/2) of
+// the first n_dims values rotate by pos[i2] * base^(-2i/n_dims), the angle
+// and its sine and cosine in f64 (the reference test's CPU formula,
+// crates/vk-backend/tests/ops2.rs:426-442); values past n_dims are copied.
+struct RopeArgs {
+    const float *src;
+    const int32_t *pos;
+    float *dst;
+    uint32_t nrows, n_dims, ne00, ne01, ne02;
+    uint32_t nb01, nb02, nb03, nb11, nb12, nb13, a_off, d_off;
+    double theta_scale;
+};
+
+__global__ void __launch_bounds__(256) kr_rope_neox(RopeArgs a)
+{
+    const uint32_t r = blockIdx.x, i = blockIdx.y * 256 + threadIdx.x;
+    if (r >= a.nrows || 2 * i >= a.ne00) return;
+    const uint32_t i1 = r % a.ne01, i2 = (r / a.ne01) % a.ne02, i3 = r / (a.ne01 * a.ne02);
+    const int64_t s0 = a.a_off + (int64_t)i3 * a.nb03 + (int64_t)i2 * a.nb02 + (int64_t)i1 * a.nb01;
+    const int64_t d0 = a.d_off + (int64_t)i3 * a.nb13 + (int64_t)i2 * a.nb12 + (int64_t)i1 * a.nb11;
+    if (2 * i >= a.n_dims) {  // past the rotated dims: copied through
+        a.dst[d0 + 2 * i] = a.src[s0 + 2 * i];
+        a.dst[d0 + 2 * i + 1] = a.src[s0 + 2 * i + 1];
+        return;
+    }
+    const uint32_t half = a.n_dims / 2;
+    const double th = (double)a.pos[i2] * pow(a.theta_scale, (double)i);
+    double sn, cs;
+    sincos(th, &sn, &cs);
+    const double x0 = a.src[s0 + i], x1 = a.src[s0 + i + half];
+    a.dst[d0 + i] = (float)(x0 * cs - x1 * sn);
+    a.dst[d0 + i + half] = (float)(x0 * sn + x1 * cs);
+}
+
+// cpy_f32_f32 with the UnaryPush of ops.rs:253-323: element j < ne of the
+// source, at its 4-d index in src0's extents and strides (plus the
+// misalignment offset's high half), goes to the same running index in dst's
+// extents and strides (plus the low half).  512 elements per workgroup
+// (the engine's grid, crates/model/src/moe.rs:1935-1943).
+struct CpyArgs {
+    const float *src;
+    float *dst;
+    uint32_t ne;
+    uint32_t sne[4], snb[4], dne[4], dnb[4];
+    uint32_t a_off, d_off;
+};
+
+__device__ __forceinline__ int64_t elem_at(uint32_t j, const uint32_t *ne, const uint32_t *nb)
+{
+    const uint32_t i0 = j % ne[0], i1 = (j / ne[0]) % ne[1], i2 = (j / (ne[0] * ne[1])) % ne[2],
+                   i3 = j / (ne[0] * ne[1] * ne[2]);
+    return (int64_t)i3 * nb[3] + (int64_t)i2 * nb[2] + (int64_t)i1 * nb[1] + (int64_t)i0 * nb[0];
+}
+
+__global__ void __launch_bounds__(256) kr_cpy(CpyArgs a)
+{
+    const uint64_t wg = ((uint64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    for (uint32_t t = threadIdx.x; t < 512; t += 256) {
+        const uint64_t j = wg * 512 + t;
+        if (j >= a.ne) return;
+        a.dst[a.d_off + elem_at((uint32_t)j, a.dne, a.dnb)] = a.src[a.a_off + elem_at((uint32_t)j, a.sne, a.snb)];
+    }
+}
+
 // Whether n elements of `bytes_each` bytes fit in a binding of `size` bytes
 // (n may be 0).
 static bool fits(uint64_t size, uint64_t n, uint64_t bytes_each)
@@ -259,6 +327,67 @@ hipError_t refk_launch(hipStream_t st, int kid, void *const *ptr, const uint64_t
             return bad;
         hipLaunchKernelGGL(kr_rms_norm, dim3(gx), dim3(256), 0, st, (const float *)ptr[0],
                            (const float *)ptr[1], (float *)ptr[2], pc[1], pc[6], pc[22], eps, mul);
+        break;
+    }
+    case RK_ROPE_NEOX: {
+        float f[29];
+        std::memcpy(f, pc, sizeof(f));
+        RopeArgs a{};
+        a.nrows = pc[1];
+        a.n_dims = pc[2];
+        const float freq_scale = f[3], freq_base = f[4], ext_factor = f[5], attn_factor = f[6];
+        a.ne00 = pc[18], a.ne01 = pc[19], a.ne02 = pc[20];
+        a.nb01 = pc[21], a.nb02 = pc[22], a.nb03 = pc[23];
+        a.nb11 = pc[24], a.nb12 = pc[25], a.nb13 = pc[26];
+        a.a_off = pc[27], a.d_off = pc[28];
+        // the supported mode: NEOX (2), no frequency factors, no YaRN, not
+        // the backward pass, no set_rows, rotation within each row
+        if (pc[0] != 2 || freq_scale != 1.0f || ext_factor != 0.0f || attn_factor != 1.0f ||
+            pc[10] != 0 || pc[15] != 0 || pc[16] != 0 || pc[17] != 0 || a.n_dims == 0 ||
+            a.n_dims % 2 || a.n_dims > a.ne00 || a.ne00 % 2 || a.ne01 == 0 || a.ne02 == 0 ||
+            !(freq_base > 0.0f) || gx < a.nrows || (uint64_t)gy * 256 < a.ne00 / 2)
+            return bad;
+        const uint64_t n3 = ((uint64_t)a.nrows + a.ne01 * a.ne02 - 1) / ((uint64_t)a.ne01 * a.ne02);
+        const uint64_t src_need = a.a_off + (n3 - 1) * a.nb03 + (uint64_t)(a.ne02 - 1) * a.nb02 +
+                                  (uint64_t)(a.ne01 - 1) * a.nb01 + a.ne00;
+        const uint64_t dst_need = a.d_off + (n3 - 1) * a.nb13 + (uint64_t)(a.ne02 - 1) * a.nb12 +
+                                  (uint64_t)(a.ne01 - 1) * a.nb11 + a.ne00;
+        if (!fits(size[0], src_need, 4) || !fits(size[1], a.ne02, 4) || !fits(size[3], dst_need, 4))
+            return bad;
+        a.src = (const float *)ptr[0];
+        a.pos = (const int32_t *)ptr[1];
+        a.dst = (float *)ptr[3];
+        a.theta_scale = std::pow((double)freq_base, -2.0 / (double)a.n_dims);
+        hipLaunchKernelGGL(kr_rope_neox, dim3(a.nrows, (a.ne00 / 2 + 255) / 256), dim3(256), 0, st,
+                           a);
+        break;
+    }
+    case RK_CPY: {
+        CpyArgs a{};
+        a.ne = pc[0];
+        for (int i = 0; i < 4; i++) {
+            a.sne[i] = pc[1 + i];
+            a.snb[i] = pc[5 + i];
+            a.dne[i] = pc[9 + i];
+            a.dnb[i] = pc[13 + i];
+        }
+        a.a_off = pc[17] >> 16;
+        a.d_off = pc[17] & 0xFFFF;
+        uint64_t sn = 1, dn = 1, s_need = a.a_off + 1, d_need = a.d_off + 1;
+        for (int i = 0; i < 4; i++) {
+            if (a.sne[i] == 0 || a.dne[i] == 0) return bad;
+            sn *= a.sne[i];
+            dn *= a.dne[i];
+            s_need += (uint64_t)(a.sne[i] - 1) * a.snb[i];
+            d_need += (uint64_t)(a.dne[i] - 1) * a.dnb[i];
+        }
+        if (a.ne == 0 || sn < a.ne || dn < a.ne || sn > 0xFFFFFFFFull || dn > 0xFFFFFFFFull ||
+            (uint64_t)gx * gy * gz * 512 < a.ne || !fits(size[0], s_need, 4) ||
+            !fits(size[1], d_need, 4))
+            return bad;
+        a.src = (const float *)ptr[0];
+        a.dst = (float *)ptr[1];
+        hipLaunchKernelGGL(kr_cpy, dim3(gx, gy, gz), dim3(256), 0, st, a);
         break;
     }
     case RK_TOPK:

@@ -16,6 +16,8 @@ enum RefKernel {
     RK_AXPY_SIG,
     RK_SWIGLU,
     RK_RMS_NORM,
+    RK_ROPE_NEOX,
+    RK_CPY,
     RK_MMV_BASE = 32,  // +0..3 mul_mat_vec_{q8_0,q4_k,q5_k,q6_k}, +4..7 the _id forms
 };
 

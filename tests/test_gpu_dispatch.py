@@ -380,3 +380,77 @@ def test_async_batch_and_timeline(gpu):
         mb.submit_async(t, 9)  # a plain batch has no async stream
     for o in (ab, mb, gk, ak, t):
         o.free()
+
+
+def rope_push(head_dim, n_heads, n_tokens, base):
+    # RopePush::neox (ops.rs:413-439): 116 bytes
+    ts = np.float32(np.float64(base) ** (-2.0 / head_dim))
+    return struct.pack("<3I4f2ffI4i3I3I3I3I2I", 2, n_heads * n_tokens, head_dim, 1.0, base, 0.0,
+                       1.0, 0.0, 0.0, ts, 0, 0, 0, 0, 0, 0, 0, 0, head_dim, n_heads, n_tokens,
+                       head_dim, head_dim * n_heads, head_dim * n_heads * n_tokens, head_dim,
+                       head_dim * n_heads, head_dim * n_heads * n_tokens, 0, 0)
+
+
+def test_rope_neox(gpu):
+    """rope_neox_f32 (ops2.rs:413-490): head_dim 128, 4 heads, 3 tokens at
+    positions [0, 5, 17], base 1e6, LCG 0x40e0 inputs; against the test's
+    f64 CPU formula within its 1e-4 (and within 1e-6 here), position 0 the
+    identity bit for bit; the rotation composes: rotating by 5 then by 12
+    equals rotating by 17 (1e-6)."""
+    hd, nh, nt = 128, 4, 3
+    pos = np.array([0, 5, 17], np.int32)
+    x = Lcg(0x40E0).f32s(hd * nh * nt)
+    half = hd // 2
+    ts = np.float64(1e6) ** (-2.0 / hd)
+    th = pos[:, None].astype(np.float64) * ts ** np.arange(half, dtype=np.float64)[None, :]
+    xr = x.reshape(nt, nh, hd).astype(np.float64)
+    c, s = np.cos(th)[:, None, :], np.sin(th)[:, None, :]
+    want = np.concatenate([xr[..., :half] * c - xr[..., half:] * s,
+                           xr[..., :half] * s + xr[..., half:] * c], -1).astype(np.float32).ravel()
+    bo = gpu.zeros(x.nbytes)
+    binds = [f32buf(gpu, x), gpu.from_numpy(pos), gpu.zeros(16), bo, gpu.zeros(16)]
+    run(gpu, "rope_neox_f32", binds, rope_push(hd, nh, nt, 1e6), (nh * nt, 1, 1))
+    got = bo.download(np.float32)
+    assert np.max(np.abs(got - want)) < 1e-6
+    assert np.array_equal(got[:hd * nh].view(np.uint32), x[:hd * nh].view(np.uint32))
+    # composition through two dispatches of one token each
+    y = x[:hd * nh]
+    b1, b2 = gpu.zeros(y.nbytes), gpu.zeros(y.nbytes)
+    run(gpu, "rope_neox_f32", [f32buf(gpu, y), gpu.from_numpy(np.array([5], np.int32)),
+                               gpu.zeros(16), b1, gpu.zeros(16)], rope_push(hd, nh, 1, 1e6), (nh, 1, 1))
+    run(gpu, "rope_neox_f32", [b1, gpu.from_numpy(np.array([12], np.int32)), gpu.zeros(16), b2,
+                               gpu.zeros(16)], rope_push(hd, nh, 1, 1e6), (nh, 1, 1))
+    run(gpu, "rope_neox_f32", [f32buf(gpu, y), gpu.from_numpy(np.array([17], np.int32)),
+                               gpu.zeros(16), b1, gpu.zeros(16)], rope_push(hd, nh, 1, 1e6), (nh, 1, 1))
+    assert np.max(np.abs(b2.download(np.float32) - b1.download(np.float32))) < 1e-6
+
+
+def unary_push(ne, src0, dst, misalign):
+    # UnaryPush (ops.rs:253-273): 120 bytes; the fastdiv words are unused here
+    return struct.pack("<I8I8II4f8I", ne, *src0, *dst, misalign, 0, 0, 0, 0, *([0] * 8))
+
+
+def test_cpy_contig_and_strided(gpu):
+    """cpy_f32_f32 with UnaryPush::contig_copy into a KV row at a binding
+    offset (moe.rs:1935-1943: the KV append), and strided_copy(n, stride,
+    off): exact copies, everything else untouched."""
+    rng = np.random.default_rng(21)
+    kvd, pos = 512, 3
+    src = rng.standard_normal(kvd).astype(np.float32)
+    cache0 = rng.standard_normal(8 * kvd).astype(np.float32)
+    bc = f32buf(gpu, cache0)
+    run(gpu, "cpy_f32_f32", [f32buf(gpu, src), (bc, pos * kvd * 4, 2**64 - 1)],
+        unary_push(kvd, [kvd, 1, 1, 1, 1, kvd, kvd, kvd], [kvd, 1, 1, 1, 1, kvd, kvd, kvd], 0),
+        ((kvd + 511) // 512, 1, 1))
+    want = cache0.copy()
+    want[pos * kvd:(pos + 1) * kvd] = src
+    assert np.array_equal(bc.download(np.float32), want)
+    n, stride, off = 100, 3, 7
+    d0 = np.full(off + n * stride + 5, -1.0, np.float32)
+    bd = f32buf(gpu, d0)
+    run(gpu, "cpy_f32_f32", [f32buf(gpu, src[:n]), bd],
+        unary_push(n, [n, 1, 1, 1, 1, n, n, n],
+                   [n, 1, 1, 1, stride, n * stride, n * stride, n * stride], off), (1, 1, 1))
+    want = d0.copy()
+    want[off:off + n * stride:stride] = src[:n]
+    assert np.array_equal(bd.download(np.float32), want)
