@@ -116,6 +116,11 @@ int styx_batch_dispatch(styx_batch *b, const styx_kernel *k, const styx_binding 
  * (an async batch runs it on its own stream). */
 int styx_batch_submit(styx_batch *b);
 
+/* Gpu::dispatch_sync (lib.rs:1415-1515): one dispatch, run and waited for. */
+int styx_dispatch_sync(styx_gpu *gpu, const styx_kernel *k, const styx_binding *binds,
+                       int n_binds, const void *push, uint32_t push_len, uint32_t gx, uint32_t gy,
+                       uint32_t gz);
+
 /* Asynchronous submission (the reference's M7b-B prefetch path).
  * A timeline stands in for a Vulkan timeline semaphore: every
  * styx_batch_submit_async signals one value (values strictly increase), and

@@ -109,6 +109,7 @@ _SIGS = {
     "styx_batch_begin": (i32, [vp]),
     "styx_batch_dispatch": (i32, [vp, vp, vp, i32, vp, u32, u32, u32, u32, i32]),
     "styx_batch_submit": (i32, [vp]),
+    "styx_dispatch_sync": (i32, [vp, vp, vp, i32, vp, u32, u32, u32, u32]),
     "styx_batch_new_async": (i32, [vp, C.POINTER(vp)]),
     "styx_batch_submit_async": (i32, [vp, vp, u64]),
     "styx_batch_wait_idle": (i32, [vp]),

@@ -265,6 +265,19 @@ int styx_batch_submit(styx_batch *b)
     return STYX_OK;
 }
 
+int styx_dispatch_sync(styx_gpu *gpu, const styx_kernel *k, const styx_binding *binds,
+                       int n_binds, const void *push, uint32_t push_len, uint32_t gx, uint32_t gy,
+                       uint32_t gz)
+{
+    if (!gpu || !k) return fail(STYX_E_INVALID, "styx_dispatch_sync: NULL gpu or kernel");
+    if (k->gpu != gpu) return fail(STYX_E_INVALID, "styx_dispatch_sync: kernel of another styx_gpu");
+    styx_batch b;
+    b.gpu = gpu;
+    b.recording = true;
+    if (int r = styx_batch_dispatch(&b, k, binds, n_binds, push, push_len, gx, gy, gz, 1)) return r;
+    return styx_batch_submit(&b);
+}
+
 int styx_timeline_new(styx_gpu *gpu, styx_timeline **out)
 {
     if (!gpu || !out) return fail(STYX_E_INVALID, "styx_timeline_new: bad argument");

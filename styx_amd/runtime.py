@@ -115,6 +115,22 @@ class Kernel:
             self.h = None
 
 
+def _bindings(binds):
+    arr = (L.Binding * len(binds))()
+    for i, b in enumerate(binds):
+        buf, off, rng = (b if isinstance(b, tuple) else (b, 0, 2**64 - 1))
+        arr[i].buf, arr[i].offset, arr[i].range = buf.h, off, rng
+    return arr
+
+
+def dispatch_sync(gpu: "Gpu", k: "Kernel", binds, push: bytes, groups):
+    """Gpu::dispatch_sync (lib.rs:1415-1515): one dispatch, waited for."""
+    pb = C.create_string_buffer(push, len(push))
+    gx, gy, gz = (tuple(groups) + (1, 1))[:3]
+    L.check(gpu.lib.styx_dispatch_sync(gpu.h, k.h, _bindings(binds), len(binds), pb, len(push),
+                                       gx, gy, gz))
+
+
 class Timeline:
     """Timeline semaphore (Gpu::create_timeline_semaphore, lib.rs:700-713)."""
 
@@ -150,10 +166,7 @@ class Batch:
         L.check(self.lib.styx_batch_begin(self.h))
 
     def dispatch(self, k: Kernel, binds, push: bytes, groups, barrier: bool = True):
-        arr = (L.Binding * len(binds))()
-        for i, b in enumerate(binds):
-            buf, off, rng = (b if isinstance(b, tuple) else (b, 0, 2**64 - 1))
-            arr[i].buf, arr[i].offset, arr[i].range = buf.h, off, rng
+        arr = _bindings(binds)
         pb = C.create_string_buffer(push, len(push))
         gx, gy, gz = (tuple(groups) + (1, 1))[:3]
         L.check(self.lib.styx_batch_dispatch(self.h, k.h, arr, len(binds), pb, len(push),

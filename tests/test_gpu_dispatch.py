@@ -413,16 +413,21 @@ def test_rope_neox(gpu):
     got = bo.download(np.float32)
     assert np.max(np.abs(got - want)) < 1e-6
     assert np.array_equal(got[:hd * nh].view(np.uint32), x[:hd * nh].view(np.uint32))
-    # composition through two dispatches of one token each
+    # composition through single dispatches of one token each
+    # (Gpu::dispatch_sync, lib.rs:1415)
+    from styx_amd.runtime import Kernel, dispatch_sync
+    k = Kernel(gpu, "rope_neox_f32", [])
     y = x[:hd * nh]
     b1, b2 = gpu.zeros(y.nbytes), gpu.zeros(y.nbytes)
-    run(gpu, "rope_neox_f32", [f32buf(gpu, y), gpu.from_numpy(np.array([5], np.int32)),
-                               gpu.zeros(16), b1, gpu.zeros(16)], rope_push(hd, nh, 1, 1e6), (nh, 1, 1))
-    run(gpu, "rope_neox_f32", [b1, gpu.from_numpy(np.array([12], np.int32)), gpu.zeros(16), b2,
-                               gpu.zeros(16)], rope_push(hd, nh, 1, 1e6), (nh, 1, 1))
-    run(gpu, "rope_neox_f32", [f32buf(gpu, y), gpu.from_numpy(np.array([17], np.int32)),
-                               gpu.zeros(16), b1, gpu.zeros(16)], rope_push(hd, nh, 1, 1e6), (nh, 1, 1))
+    one = rope_push(hd, nh, 1, 1e6)
+    dispatch_sync(gpu, k, [f32buf(gpu, y), gpu.from_numpy(np.array([5], np.int32)),
+                           gpu.zeros(16), b1, gpu.zeros(16)], one, (nh, 1, 1))
+    dispatch_sync(gpu, k, [b1, gpu.from_numpy(np.array([12], np.int32)), gpu.zeros(16), b2,
+                           gpu.zeros(16)], one, (nh, 1, 1))
+    dispatch_sync(gpu, k, [f32buf(gpu, y), gpu.from_numpy(np.array([17], np.int32)),
+                           gpu.zeros(16), b1, gpu.zeros(16)], one, (nh, 1, 1))
     assert np.max(np.abs(b2.download(np.float32) - b1.download(np.float32))) < 1e-6
+    k.free()
 
 
 def unary_push(ne, src0, dst, misalign):
