@@ -424,9 +424,9 @@ int styx_moe_last_hot_cold(styx_moe *m, uint32_t *out);
 int styx_moe_reset(styx_moe *m);
 /* Synthetic context for long-context measurement (no counterpart in the
  * reference): fill the K and V rows of positions [0, n_t) of every layer
- * with N(0, sigma) values (seeded, deterministic) and continue as if n_t
- * tokens had been forwarded; the next styx_moe_forward_token runs at
- * position n_t. */
+ * (the pages holding them whole) with N(0, sigma) values (seeded,
+ * deterministic) and continue as if n_t tokens had been forwarded; the next
+ * styx_moe_forward_token runs at position n_t. */
 int styx_moe_fill_kv(styx_moe *m, int n_t, uint64_t seed, float sigma);
 /* Copy K and V rows [t0, t0+n) of one layer to the host ([n][n_kv*hd]
  * each), through the page table. */

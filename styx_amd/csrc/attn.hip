@@ -42,10 +42,18 @@ __device__ __forceinline__ int attn_chunk(const AttnArgs &a, int n_t)
     return max(a.chunk, (need + 15) / 16 * 16);
 }
 
+// Offset of the K/V row of kv head kvh at token tp of physical page pg.
+// A page holds page_tokens tokens of every kv head, either token-major
+// ([token][kv_dim], the reference's row layout) or head-major
+// ([kv head][token][hd]: the rows a workgroup reads are contiguous).
+__device__ __forceinline__ int64_t kv_row(const AttnArgs &a, int64_t pg, int tp, int kvh, int kv_dim)
+{
+    return a.kv_head_major ? ((pg * a.nkv + kvh) * a.page_tokens + tp) * (int64_t)a.hd
+                           : (pg * a.page_tokens + tp) * (int64_t)kv_dim + (int64_t)kvh * a.hd;
+}
 __device__ __forceinline__ int64_t kv_off(const AttnArgs &a, int t, int kvh, int kv_dim)
 {
-    const int page = a.page_table[t / a.page_tokens];
-    return ((int64_t)page * a.page_tokens + (t % a.page_tokens)) * kv_dim + (int64_t)kvh * a.hd;
+    return kv_row(a, a.page_table[t / a.page_tokens], t % a.page_tokens, kvh, kv_dim);
 }
 
 // One head's RMSNorm(hd) * w and NEOX rope at pos, split into a load phase
@@ -409,8 +417,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
         // has its minimum size (then tb + tl == t_min)
         const int64_t row =
             spec && chunk == a.chunk
-                ? (tb + tl < t1 ? ((int64_t)pe_min * a.page_tokens + t_min % a.page_tokens) * kv_dim +
-                                      (int64_t)kvh * HD
+                ? (tb + tl < t1 ? kv_row(a, pe_min, t_min % a.page_tokens, kvh, kv_dim)
                                 : 0)
                 : row_of(tb);
         load_k(row, tb);
@@ -673,8 +680,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     float vvr[4][MNB];     // V[tb + 4q + lg][vcol(lr, b)]
     auto kv_at = [&](int t) -> int64_t {
         if (!pt_lds) return kv_off(a, t, kvh, kv_dim);
-        return ((int64_t)s_pt[t / a.page_tokens] * a.page_tokens + t % a.page_tokens) * kv_dim +
-               (int64_t)kvh * MHD;
+        return kv_row(a, s_pt[t / a.page_tokens], t % a.page_tokens, kvh, kv_dim);
     };
     auto row_of = [&](int tbase) -> int64_t { return tbase + lr < t1 ? kv_at(tbase + lr) : 0; };
     auto load_k = [&](int64_t row, int tbase) {
@@ -705,8 +711,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     if (tb < t1) {
         const int64_t row =
             spec && chunk == a.chunk
-                ? (tb + lr < t1 ? ((int64_t)pe_min * a.page_tokens + t_min % a.page_tokens) * kv_dim +
-                                      (int64_t)kvh * MHD
+                ? (tb + lr < t1 ? kv_row(a, pe_min, t_min % a.page_tokens, kvh, kv_dim)
                                 : 0)
                 : row_of(tb);
         load_k(row, tb);

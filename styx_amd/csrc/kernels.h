@@ -184,9 +184,11 @@ struct AttnArgs {
     const float *q_norm, *k_norm;    // [hd] or null
     float eps;
     const double2 *rope;             // [n_pos][hd/2] (cos, sin) of pos * base^(-2i/hd)
-    float *kpool, *vpool;            // [pages][page_tokens][kv_dim]
+    float *kpool, *vpool;            // [pages][page_tokens][kv_dim], or
+                                     // [pages][nkv][page_tokens][hd] (kv_head_major)
     const int32_t *page_table;       // logical page -> physical page
     int page_tokens;
+    int kv_head_major;
     int page_table_len;              // entries of page_table (0: not given)
     const int32_t *pos;              // device scalar
     float *out;                      // [nh*hd]
