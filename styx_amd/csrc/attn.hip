@@ -875,72 +875,80 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
 }
 
 // Merge the per-chunk partials (m, l, o) of one query head: M = max m_c,
-// L = sum l_c e^(m_c-M), out = sum o_c e^(m_c-M) / L; then the limbs of this
-// head's slice of the output.  CB_WG threads = CB_GROUPS chunk groups x 64
-// lanes (each lane hd/64 values).  A group takes its chunks in batches of 8
-// whose loads are all issued before any is merged into the group's running
-// (m, l, o); the groups are merged in LDS.
-constexpr int CB_WG = 1024, CB_GROUPS = CB_WG / 64, CB_BATCH = 8;
+// L = sum l_c e^(m_c-M), out = sum o_c e^(m_c-M) / L; then the limbs of the
+// slice.  One workgroup per (head, 32 output values): at long contexts a
+// head has up to a few hundred chunks, and spreading each head over hd / 32
+// workgroups keeps the reads of one workgroup (and CU) small.  Each half
+// wave takes every eighth chunk, lane l value l % 32, in batches of 8
+// chunks whose loads are all issued before any is merged into the running
+// (m, l, o), the first batch's together with the position's (16-chunk
+// batches, one for the 128 chunks of a long context, measured no faster);
+// the eight half waves are merged in LDS.
+constexpr int CB_WG = 256, CB_DIMS = 32, CB_HALVES = CB_WG / 32, CB_BATCH = 8;
 
 __global__ void __launch_bounds__(CB_WG) k_attn_combine(AttnArgs a)
 {
-    extern __shared__ __align__(16) float xs[];  // [hd] out | [G][hd] o | [G] m | [G] l
+    __shared__ float s_o[CB_HALVES][CB_DIMS], s_m[CB_HALVES], s_l[CB_HALVES], xs[CB_DIMS];
     __shared__ float red[16];
-    const int h = blockIdx.x, gqa = a.nh / a.nkv, hd = a.hd, ps = hd + 2;
-    const int n_t = *a.pos + 1, chunk = attn_chunk(a, n_t);
-    const int n_active = (n_t + chunk - 1) / chunk;
+    const int h = blockIdx.x, d0 = blockIdx.y * CB_DIMS, gqa = a.nh / a.nkv, hd = a.hd, ps = hd + 2;
     const int kvh = h / gqa, g = h - kvh * gqa;
     const int64_t cs = (int64_t)gqa * ps;  // stride between chunks
     const float *pk = a.part + (int64_t)kvh * a.max_chunks * cs + (int64_t)g * ps;
-    const int grp = threadIdx.x >> 6, lane = threadIdx.x & 63, epl = hd / 64;
-    float m = -INFINITY, l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int c0 = grp; c0 < n_active; c0 += CB_GROUPS * CB_BATCH) {
-        float mc[CB_BATCH], lc[CB_BATCH], oc[CB_BATCH][4];
+    const int half = threadIdx.x >> 5, dl = threadIdx.x & 31;
+    // the first batch's loads go out with the position's (every chunk of the
+    // grid; those past the context are dropped once it is known)
+    const int *posp = a.pos;
+    int n_active = -1;
+    float m = -INFINITY, l = 0.0f, o = 0.0f;
+    for (int c0 = half; c0 < a.max_chunks; c0 += CB_HALVES * CB_BATCH) {
+        float mc[CB_BATCH], lc[CB_BATCH], oc[CB_BATCH];
 #pragma unroll
         for (int b = 0; b < CB_BATCH; b++) {
-            const int cc = c0 + CB_GROUPS * b;
-            const bool ok = cc < n_active;
-            const float *pp = pk + (ok ? cc : 0) * cs;
-            mc[b] = ok ? pp[hd] : -INFINITY;
-            lc[b] = ok ? pp[hd + 1] : 0.0f;
-#pragma unroll
-            for (int e = 0; e < 4; e++) oc[b][e] = (ok && e < epl) ? pp[lane * epl + e] : 0.0f;
+            const int cc = c0 + CB_HALVES * b;
+            const float *pp = pk + (cc < a.max_chunks ? cc : 0) * cs;
+            mc[b] = pp[hd];
+            lc[b] = pp[hd + 1];
+            oc[b] = pp[d0 + dl];
+        }
+        if (n_active < 0) {
+            const int n_t = *posp + 1, chunk = attn_chunk(a, n_t);
+            n_active = (n_t + chunk - 1) / chunk;
         }
 #pragma unroll
         for (int b = 0; b < CB_BATCH; b++) {
-            if (mc[b] == -INFINITY) continue;
+            if (c0 + CB_HALVES * b >= n_active || mc[b] == -INFINITY) continue;
             const float mn = fmaxf(m, mc[b]);
             const float fa = expf(m - mn), fb = expf(mc[b] - mn);
             l = l * fa + lc[b] * fb;
-#pragma unroll
-            for (int e = 0; e < 4; e++) o[e] = o[e] * fa + oc[b][e] * fb;
+            o = o * fa + oc[b] * fb;
             m = mn;
         }
     }
-    float *go = xs + hd, *gm = go + CB_GROUPS * hd, *gl = gm + CB_GROUPS;
-    for (int e = 0; e < epl; e++) go[grp * hd + lane * epl + e] = o[e];
-    if (lane == 0) {
-        gm[grp] = m;
-        gl[grp] = l;
+    s_o[half][dl] = o;
+    if (dl == 0) {
+        s_m[half] = m;
+        s_l[half] = l;
     }
     __syncthreads();
-    if (threadIdx.x < hd) {
+    if (threadIdx.x < CB_DIMS) {
         const int i = threadIdx.x;
-        float M = gm[0];
-        for (int q = 1; q < CB_GROUPS; q++) M = fmaxf(M, gm[q]);
+        float M = s_m[0];
+#pragma unroll
+        for (int q = 1; q < CB_HALVES; q++) M = fmaxf(M, s_m[q]);
         float L = 0.0f, O = 0.0f;
-        for (int q = 0; q < CB_GROUPS; q++) {
-            const float f = gm[q] == -INFINITY ? 0.0f : expf(gm[q] - M);
-            L += gl[q] * f;
-            O += go[q * hd + i] * f;
+#pragma unroll
+        for (int q = 0; q < CB_HALVES; q++) {
+            const float f = s_m[q] == -INFINITY ? 0.0f : expf(s_m[q] - M);
+            L += s_l[q] * f;
+            O += s_o[q][i] * f;
         }
         const float v = O / L;
-        a.out[(int64_t)h * hd + i] = v;
+        a.out[(int64_t)h * hd + d0 + i] = v;
         xs[i] = v;
     }
     if (!a.xq.A) return;
     __syncthreads();
-    xq_build(xs, nullptr, 0.0f, false, hd, xq_shift(a.xq, h * hd), red, nullptr);
+    xq_build(xs, nullptr, 0.0f, false, CB_DIMS, xq_shift(a.xq, h * hd + d0), red, nullptr);
 }
 
 template <int MAXH>
@@ -996,8 +1004,7 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.t_part) return e;  // combined inside the kernel
-    hipLaunchKernelGGL(k_attn_combine, dim3(a.nh), dim3(CB_WG),
-                       (size_t)((CB_GROUPS + 1) * a.hd + 2 * CB_GROUPS) * 4, st, am);
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.nh, a.hd / CB_DIMS), dim3(CB_WG), 0, st, am);
     return hipGetLastError();
 }
 
