@@ -296,6 +296,50 @@ def test_attention_paged(gpu, nh, nkv, hd, n_steps, page, max_chunks):
         assert np.array_equal(vp[pt[t // page], t % page], Vv[t]), t
 
 
+@pytest.mark.parametrize("nh,nkv,n_t", [(32, 4, 3001), (64, 4, 8001)])
+def test_attention_many_chunks(gpu, nh, nkv, n_t):
+    """One decode step after a long context written straight into the paged
+    pools: about a hundred chunks per kv head (94 for the VALU kernel's
+    32-token chunks, 126 for the matrix-core kernel's 64), so the combine
+    kernel merges two batches per half wave and drops the grid's chunks past
+    the context (the grid is 128 chunks)."""
+    rng = np.random.default_rng(n_t)
+    hd, page, chunk, max_chunks = 128, 512, 32, 128
+    kvd = nkv * hd
+    npages = -(-n_t // page)
+    pt = rng.permutation(npages).astype(np.int32)
+    K = rng.standard_normal((n_t, kvd)).astype(np.float32)
+    Vv = rng.standard_normal((n_t, kvd)).astype(np.float32)
+    kp = np.zeros((npages, page, kvd), np.float32)
+    vp = np.zeros((npages, page, kvd), np.float32)
+    pos = n_t - 1
+    for t in range(pos):
+        kp[pt[t // page], t % page] = K[t]
+        vp[pt[t // page], t % page] = Vv[t]
+    kpool, vpool = gpu.from_numpy(kp), gpu.from_numpy(vp)
+    base = 1e6
+    rope = np.empty((n_t, hd // 2, 2), np.float64)
+    lib().styx_rope_table(C.c_float(base), hd, n_t, rope.ctypes.data)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(kvd).astype(np.float32)
+    v = rng.standard_normal(kvd).astype(np.float32)
+    part = gpu.buffer(lib().styx_op_attn_part_floats(nh, nkv, hd, max_chunks) * 4)
+    out = gpu.buffer(nh * hd * 4)
+    bufs = [gpu.from_numpy(x) for x in (q, k, v, rope, pt, np.array([pos], np.int32))]
+    qb, kb, vb, invb, ptb, posb = bufs
+    scale = 1.0 / np.sqrt(hd)
+    check(lib().styx_op_attn_decode(gpu.h, qb.ptr, kb.ptr, vb.ptr, None, None, C.c_float(1e-6),
+                                    invb.ptr, kpool.ptr, vpool.ptr, ptb.ptr, page, posb.ptr,
+                                    out.ptr, part.ptr, nh, nkv, hd, chunk, max_chunks,
+                                    C.c_float(scale)))
+    gpu.sync()
+    qr = O.rope_neox(q, hd, nh, pos, base)
+    K[pos] = O.rope_neox(k, hd, nkv, pos, base)
+    Vv[pos] = v
+    ref = O.attn_decode_f64(qr, K, Vv, n_t, hd, kvd, nh // nkv, nh, scale)
+    assert rel_l2(out.download(np.float32), ref) < 2e-6
+
+
 def test_gather_slabs(gpu):
     rng = np.random.default_rng(2)
     E, k, layer = 12, 4, 3
