@@ -307,7 +307,7 @@ __device__ void attn_combine_tail(const AttnArgs &a, int c, int kvh, int n_activ
             }
             if (a.xq.A) {
                 __syncthreads();
-                xq_build(xo, nullptr, 0.0f, false, n, xq_shift(a.xq, (kvh * gqa + r0) * HD), red,
+                xq_build<AT_WG>(xo, nullptr, 0.0f, false, n, xq_shift(a.xq, (kvh * gqa + r0) * HD), red,
                          nullptr);
             }
         };
@@ -948,7 +948,7 @@ __global__ void __launch_bounds__(CB_WG) k_attn_combine(AttnArgs a)
     }
     if (!a.xq.A) return;
     __syncthreads();
-    xq_build(xs, nullptr, 0.0f, false, CB_DIMS, xq_shift(a.xq, h * hd + d0), red, nullptr);
+    xq_build<CB_WG>(xs, nullptr, 0.0f, false, CB_DIMS, xq_shift(a.xq, h * hd + d0), red, nullptr);
 }
 
 template <int MAXH>

@@ -296,7 +296,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
                 const float4 v = gld4(a.x + i);
                 ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
             }
-            ss = block_sum(ss, red);
+            ss = block_sum<WG>(ss, red);
             const float scale = 1.0f / sqrtf(ss / (float)a.H + a.eps);
 #pragma unroll
             for (int j = 0; j < PX; j++) {
@@ -346,7 +346,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     // ---- limbs of xn; shared-expert gate/up rows need no routing
     auto nothing = [] {};
     if (has_x) {
-        xq_build(xs, nullptr, 0.0f, false, a.H, xqx, red, nullptr);
+        xq_build<WG>(xs, nullptr, 0.0f, false, a.H, xqx, red, nullptr);
         __syncthreads();
         stamp(2);
         for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), false, s_ids, xqx, tag, nothing, tr);
@@ -389,7 +389,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         auto build = [&] {
             for (int i = tid; i < F; i += WG) hs[i] = gus[i] / (1.0f + expf(-gus[i])) * gus[F + i];
             __syncthreads();
-            xq_build(hs, nullptr, 0.0f, false, F, xqh, red, nullptr);
+            xq_build<WG>(hs, nullptr, 0.0f, false, F, xqh, red, nullptr);
             __syncthreads();
             stamp(7);
         };
@@ -458,7 +458,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     for (int i = 1; i < WAVES; i++) mx = fmaxf(mx, red[i]);
     float se = 0.0f;
     for (int e = tid; e < a.E; e += WG) se += expf(s_lg[e] - mx);
-    se = block_sum(se, red);
+    se = block_sum<WG>(se, red);
     if (tid < a.k) s_w[tid] = expf(lg_pick - mx) / se;
     __syncthreads();
     if (tid == 0 && a.renorm) {
@@ -473,7 +473,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         if (a.wts_out && w == 0) gst(a.wts_out + tid, wt);
     }
     if (shexp) {
-        const float d = block_sum(shd, red);
+        const float d = block_sum<WG>(shd, red);
         if (tid == 0) s_sg = 1.0f / (1.0f + expf(-d));
     }
     __syncthreads();  // also: gus is reused for the partials
@@ -502,7 +502,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         flush();
         return;
     }
-    const float sq = block_sum(hr ? xv * xv : 0.0f, red);
+    const float sq = block_sum<WG>(hr ? xv * xv : 0.0f, red);
     if (tid == 0) gst(a.ss + w, sq);
     float *xw = hs;  // MB_RR floats; hs is free once the down rows are done
     __syncthreads();

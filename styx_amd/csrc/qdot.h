@@ -75,10 +75,13 @@ __device__ __forceinline__ float wave_max(float v)
 }
 
 // Block-wide sum (blockDim.x multiple of 64, <= 1024).  All threads get it.
-__device__ inline float block_sum(float v, float *red)
+// NT: the workgroup's thread count when the caller knows it (0: read
+// blockDim.x, which in some kernels becomes a vector load of the dispatch
+// packet whose wait also waits for every store in flight).
+template <int NT = 0> __device__ inline float block_sum(float v, float *red)
 {
     v = wave_sum(v);
-    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int w = threadIdx.x >> 6, nw = (NT ? NT : (int)blockDim.x) >> 6;
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[w] = v;
     __syncthreads();
@@ -128,21 +131,24 @@ __device__ __forceinline__ void xq_group(const float *v, bool act, int g, Xq q)
 // Build the limb form of xn = norm ? x * rsqrt(mean(x^2)+eps) * w : x
 // (n a multiple of 32).  If xn_out is non-null the normalised f32 vector is
 // also written there.  Thread t owns 8 consecutive values per pass.
+// NT: the workgroup's thread count if known at compile time (see block_sum).
+template <int NT = 0>
 __device__ inline void xq_build(const float *__restrict__ x, const float *__restrict__ nw,
                                 float eps, bool norm, int n, Xq q, float *red, float *xn_out)
 {
+    const int nt = NT ? NT : (int)blockDim.x;
     float scale = 1.0f;
     if (norm) {
         float ss = 0.0f;
-        for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4) {
+        for (int i = threadIdx.x * 4; i < n; i += nt * 4) {
             const float4 v = *(const float4 *)(x + i);
             ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
-        ss = block_sum(ss, red);
+        ss = block_sum<NT>(ss, red);
         scale = 1.0f / sqrtf(ss / (float)n + eps);
     }
     const int ngroups = n / 8;
-    for (int g0 = 0; g0 < ngroups; g0 += blockDim.x) {
+    for (int g0 = 0; g0 < ngroups; g0 += nt) {
         const int g = g0 + threadIdx.x;
         const bool act = g < ngroups;
         float v[8];

@@ -170,7 +170,7 @@ __device__ inline const int32_t *rank_ids_lds(const Route &r, int32_t *s_ids, co
     __syncthreads();  // also: the caller's logits are in s_lg
     if (E <= 128) {
         // direct: P = 256 / E threads rank each key against a slice of all
-        for (int e = tid; e < E; e += blockDim.x) s_key[e] = rank_key(s_lg[e], e);
+        for (int e = tid; e < E; e += 256) s_key[e] = rank_key(s_lg[e], e);
         __syncthreads();
         const int P = E <= 64 ? 4 : 2, span = E / P;
         const int e = tid / P, part = tid % P;
@@ -240,7 +240,7 @@ __device__ inline const int32_t *rank_ids_lds(const Route &r, int32_t *s_ids, co
 // block index publishes the 64-int id row.
 __device__ inline const int32_t *route_ids_wg(const Route &r, int32_t *s_ids, float *s_lg)
 {
-    for (int e = threadIdx.x; e < r.E / 4; e += blockDim.x)
+    for (int e = threadIdx.x; e < r.E / 4; e += 256)  // blockDim.x == 256
         ((float4 *)s_lg)[e] = ((const float4 *)r.logits)[e];
     return rank_ids_lds(r, s_ids, s_lg, blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0);
 }
