@@ -78,7 +78,7 @@ struct MoeBlockK {
 template <int MAXJ, typename Addr>
 __device__ __forceinline__ bool tpoll(int n, Addr addr, uint32_t tag, float *dst, const MoeBlockK &a)
 {
-    return tpoll_wg<MAXJ>(n, addr, tag, dst, a.max_polls, a.abort);
+    return tpoll_wg<MAXJ, WG>(n, addr, tag, dst, a.max_polls, a.abort);
 }
 
 // Slab of expert e routed to `slot` (null when e is not a valid expert,

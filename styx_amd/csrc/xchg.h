@@ -72,11 +72,13 @@ __device__ __forceinline__ void abort_raise(int *abort)
 // (workgroup-uniform call).  The wait is bounded: after max_polls rounds, or
 // once another workgroup has raised the abort flag, the workgroup raises
 // the flag and returns false.
-template <int MAXJ, typename Addr>
+// NT: the workgroup's thread count when known at compile time (0: read
+// blockDim.x).
+template <int MAXJ, int NT = 0, typename Addr>
 __device__ __forceinline__ bool tpoll_wg(int n, Addr addr, uint32_t tag, float *dst, int max_polls,
                                          int *abort)
 {
-    const int nt = blockDim.x;
+    const int nt = NT ? NT : (int)blockDim.x;
     uint32_t pend = 0;
 #pragma unroll
     for (int j = 0; j < MAXJ; j++) {
@@ -110,7 +112,17 @@ __device__ __forceinline__ bool tpoll_wg(int n, Addr addr, uint32_t tag, float *
         }
         __builtin_amdgcn_s_sleep(1);
     }
-    if (__syncthreads_or(failed)) {
+    // the workgroup's verdict from one flag per wave (failed is uniform in
+    // a wave) in LDS; __syncthreads_or would read the wave count from the
+    // dispatch packet, and that load's wait also waits for every store in
+    // flight
+    __shared__ int s_fail[16];
+    if ((threadIdx.x & 63) == 0) s_fail[threadIdx.x >> 6] = failed;
+    __syncthreads();
+    int any = 0;
+    for (int w = 0; w < nt / 64; w++) any |= s_fail[w];
+    __syncthreads();  // read by every wave before a later call rewrites them
+    if (any) {
         if (threadIdx.x == 0) abort_raise(abort);
         return false;
     }
