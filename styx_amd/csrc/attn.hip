@@ -232,22 +232,30 @@ __device__ void attn_combine_tail(const AttnArgs &a, int c, int kvh, int n_activ
                     if (c0 + wph * b < n_active) pend |= 1u << b;
                 }
                 for (int polls = 0; __any(pend != 0); polls++) {
+                    // every word of the batch is loaded each round, with no
+                    // branch between the loads (a chunk past the context
+                    // reads the batch's first): all of them are then in
+                    // flight together, instead of one chunk per round trip
+                    uint64_t wm[CT_BATCH], wl[CT_BATCH], wo[CT_BATCH][EPL];
 #pragma unroll
                     for (int b = 0; b < CT_BATCH; b++) {
-                        if (!((pend >> b) & 1u)) continue;
-                        const uint64_t *pp = pk + (int64_t)(c0 + wph * b) * cs;
-                        const uint64_t wm = tget(pp + HD), wl = tget(pp + HD + 1);
-                        uint64_t wo[EPL];
+                        const int cc = c0 + wph * b;
+                        const uint64_t *pp = pk + (int64_t)(cc < n_active ? cc : c0) * cs;
+                        wm[b] = tget(pp + HD);
+                        wl[b] = tget(pp + HD + 1);
 #pragma unroll
-                        for (int e = 0; e < EPL; e++) wo[e] = tget(pp + lane * EPL + e);
-                        bool ok = tvalid(wm, tag) && tvalid(wl, tag);
+                        for (int e = 0; e < EPL; e++) wo[b][e] = tget(pp + lane * EPL + e);
+                    }
 #pragma unroll
-                        for (int e = 0; e < EPL; e++) ok = ok && tvalid(wo[e], tag);
+                    for (int b = 0; b < CT_BATCH; b++) {
+                        bool ok = ((pend >> b) & 1u) && tvalid(wm[b], tag) && tvalid(wl[b], tag);
+#pragma unroll
+                        for (int e = 0; e < EPL; e++) ok = ok && tvalid(wo[b][e], tag);
                         if (ok) {
-                            mc[b] = tval(wm);
-                            lc[b] = tval(wl);
+                            mc[b] = tval(wm[b]);
+                            lc[b] = tval(wl[b]);
 #pragma unroll
-                            for (int e = 0; e < EPL; e++) oc[b][e] = tval(wo[e]);
+                            for (int e = 0; e < EPL; e++) oc[b][e] = tval(wo[b][e]);
                             pend &= ~(1u << b);
                         }
                     }
