@@ -272,14 +272,24 @@ __device__ void attn_combine_tail(const AttnArgs &a, int c, int kvh, int n_activ
                     __builtin_amdgcn_s_sleep(1);
                 }
                 if (r0 == g_begin && c0 == sw) st.at(4);
+                // the batch merged at once: its maximum first, then every
+                // chunk's factor (independent exponentials, not a chain of
+                // rescalings)
+                float mn = m;
 #pragma unroll
-                for (int b = 0; b < CT_BATCH; b++) {
-                    if (mc[b] == -INFINITY) continue;
-                    const float mn = fmaxf(m, mc[b]);
-                    const float fa = expf(m - mn), fb = expf(mc[b] - mn);
-                    l = l * fa + lc[b] * fb;
+                for (int b = 0; b < CT_BATCH; b++) mn = fmaxf(mn, mc[b]);
+                if (mn != -INFINITY) {
+                    const float fa = expf(m - mn);  // 0 while nothing is merged (m = -inf)
+                    l *= fa;
 #pragma unroll
-                    for (int e = 0; e < EPL; e++) o[e] = o[e] * fa + oc[b][e] * fb;
+                    for (int e = 0; e < EPL; e++) o[e] *= fa;
+#pragma unroll
+                    for (int b = 0; b < CT_BATCH; b++) {
+                        const float fb = mc[b] == -INFINITY ? 0.0f : expf(mc[b] - mn);
+                        l += lc[b] * fb;
+#pragma unroll
+                        for (int e = 0; e < EPL; e++) o[e] += oc[b][e] * fb;
+                    }
                     m = mn;
                 }
             }
