@@ -932,13 +932,27 @@ __global__ void __launch_bounds__(CB_WG) k_attn_combine(AttnArgs a)
             const int n_t = *posp + 1, chunk = attn_chunk(a, n_t);
             n_active = (n_t + chunk - 1) / chunk;
         }
+        // the batch merged at once (its maximum, then independent factors)
 #pragma unroll
-        for (int b = 0; b < CB_BATCH; b++) {
-            if (c0 + CB_HALVES * b >= n_active || mc[b] == -INFINITY) continue;
-            const float mn = fmaxf(m, mc[b]);
-            const float fa = expf(m - mn), fb = expf(mc[b] - mn);
-            l = l * fa + lc[b] * fb;
-            o = o * fa + oc[b] * fb;
+        for (int b = 0; b < CB_BATCH; b++)
+            if (c0 + CB_HALVES * b >= n_active) {  // a chunk past the context: its words are stale
+                mc[b] = -INFINITY;
+                lc[b] = 0.0f;
+                oc[b] = 0.0f;
+            }
+        float mn = m;
+#pragma unroll
+        for (int b = 0; b < CB_BATCH; b++) mn = fmaxf(mn, mc[b]);
+        if (mn != -INFINITY) {
+            const float fa = expf(m - mn);  // 0 while nothing is merged (m = -inf)
+            l *= fa;
+            o *= fa;
+#pragma unroll
+            for (int b = 0; b < CB_BATCH; b++) {
+                const float fb = mc[b] == -INFINITY ? 0.0f : expf(mc[b] - mn);
+                l += lc[b] * fb;
+                o += oc[b] * fb;
+            }
             m = mn;
         }
     }
