@@ -658,12 +658,12 @@ __global__ void __launch_bounds__(RR_WG) k_reduce_rows(ReduceArgs a)
     xw[tid] = xv * nw;
     __syncthreads();
     const int nrow = min(RR_ROWS, a.H - blockIdx.x * RR_ROWS);
-    if (tid < RR_ROWS / 8) {
-        const bool act = 8 * tid < nrow;
-        float h[8];
+    if (tid < RR_ROWS / 4) {  // four rows per thread: 64 threads at work
+        const bool act = 4 * tid < nrow;
+        float h[4];
 #pragma unroll
-        for (int i = 0; i < 8; i++) h[i] = act ? xw[8 * tid + i] : 0.0f;
-        xq_group(h, act, tid, xq_shift(a.xq, blockIdx.x * RR_ROWS));
+        for (int i = 0; i < 4; i++) h[i] = act ? xw[4 * tid + i] : 0.0f;
+        xq_group4(h, act, tid, xq_shift(a.xq, blockIdx.x * RR_ROWS));
     }
 }
 

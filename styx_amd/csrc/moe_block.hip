@@ -509,23 +509,23 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     xw[tid] = xv * nw;
     __syncthreads();
     if (!a.wqkv[0]) {
-        if (tid < MB_RR / 8) {
-            const bool act = 8 * tid < nrow;
-            float h[8];
+        if (tid < MB_RR / 4) {  // four rows per thread: 64 threads at work
+            const bool act = 4 * tid < nrow;
+            float h[4];
 #pragma unroll
-            for (int i = 0; i < 8; i++) h[i] = act ? xw[8 * tid + i] : 0.0f;
-            xq_group(h, act, tid, xq_shift(a.xq, r0));
+            for (int i = 0; i < 4; i++) h[i] = act ? xw[4 * tid + i] : 0.0f;
+            xq_group4(h, act, tid, xq_shift(a.xq, r0));
         }
     } else {
         // the limbs of these rows built in LDS (gus is free), then written
         // to the limb buffer and as tagged words for the q/k/v workgroups
         const Xq ql = xq_at(gus, MB_RR);
-        if (tid < MB_RR / 8) {
-            const bool act = 8 * tid < nrow;
-            float h[8];
+        if (tid < MB_RR / 4) {  // four rows per thread: 64 threads at work
+            const bool act = 4 * tid < nrow;
+            float h[4];
 #pragma unroll
-            for (int i = 0; i < 8; i++) h[i] = act ? xw[8 * tid + i] : 0.0f;
-            xq_group(h, act, tid, ql);
+            for (int i = 0; i < 4; i++) h[i] = act ? xw[4 * tid + i] : 0.0f;
+            xq_group4(h, act, tid, ql);
         }
         __syncthreads();
         xq_publish(ql, nrow, r0, a.H, a.xq, a.t_xq, tag);

@@ -128,6 +128,41 @@ __device__ __forceinline__ void xq_group(const float *v, bool act, int g, Xq q)
     if ((g & 1) == 0) q.s16[g >> 1] = s16;
 }
 
+// The same for a group of 4 values (group g of the vector q): eight
+// consecutive lanes hold one 32-value block (groups 8-aligned), and all
+// eight must call this together.  Twice the threads of xq_group for half
+// the values each: for vectors of at most 4 values per thread.
+__device__ __forceinline__ void xq_group4(const float *v, bool act, int g, Xq q)
+{
+    float am = 0.0f, s4 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        am = fmaxf(am, fabsf(v[i]));
+        s4 += v[i];
+    }
+    am = bfly<8>(am, [](float a, float b) { return fmaxf(a, b); });
+    const float s16 = bfly_sum<4>(s4);
+    if (!act) return;
+    const float inv = am > 0.0f ? 127.0f / am : 0.0f;
+    uint32_t pa = 0, pb = 0, pc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float y = v[i] * inv;
+        const float a = rintf(y);
+        const float r1 = (y - a) * 254.0f;
+        const float b = rintf(r1);
+        const float c = fminf(fmaxf(rintf((r1 - b) * 254.0f), -127.0f), 127.0f);
+        pa |= ((uint32_t)(int)a & 0xFFu) << (8 * i);
+        pb |= ((uint32_t)(int)b & 0xFFu) << (8 * i);
+        pc |= ((uint32_t)(int)c & 0xFFu) << (8 * i);
+    }
+    *(uint32_t *)(q.A + 4 * g) = pa;
+    *(uint32_t *)(q.B + 4 * g) = pb;
+    *(uint32_t *)(q.C + 4 * g) = pc;
+    if ((g & 7) == 0) q.sx[g >> 3] = am / 127.0f;
+    if ((g & 3) == 0) q.s16[g >> 2] = s16;
+}
+
 // Build the limb form of xn = norm ? x * rsqrt(mean(x^2)+eps) * w : x
 // (n a multiple of 32).  If xn_out is non-null the normalised f32 vector is
 // also written there.  Thread t owns 8 consecutive values per pass.
@@ -146,6 +181,26 @@ __device__ inline void xq_build(const float *__restrict__ x, const float *__rest
         }
         ss = block_sum<NT>(ss, red);
         scale = 1.0f / sqrtf(ss / (float)n + eps);
+    }
+    if (n <= 4 * nt) {
+        // a short vector: four values per thread, more threads at work
+        const int g = threadIdx.x;
+        const bool act = g < n / 4;
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (act) {
+            const float4 a = *(const float4 *)(x + 4 * g);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            if (norm) {
+                const float4 wa = *(const float4 *)(nw + 4 * g);
+                v[0] = (v[0] * scale) * wa.x;
+                v[1] = (v[1] * scale) * wa.y;
+                v[2] = (v[2] * scale) * wa.z;
+                v[3] = (v[3] * scale) * wa.w;
+            }
+            if (xn_out) *(float4 *)(xn_out + 4 * g) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+        xq_group4(v, act, g, q);
+        return;
     }
     const int ngroups = n / 8;
     for (int g0 = 0; g0 < ngroups; g0 += nt) {
