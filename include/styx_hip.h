@@ -85,7 +85,18 @@ int styx_copy_region(styx_gpu *gpu, const styx_buf *src, uint64_t soff, styx_buf
  * grid, so engine code ports call for call.  Names:
  *   topk_softmax_f32, moe_reduce_f32, gather_slabs_f32, attn_decode_f32,
  *   matvec_strided_f32, add_flat_f32, axpy_sig_f32, swiglu_f32,
- *   mul_mat_vec_id_{q8_0,q4_k,q5_k,q6_k}_f32_f32 (weights in GGUF layout).
+ *   rms_norm_f32, rope_neox_f32, cpy_f32_f32,
+ *   mul_mat_vec_{q8_0,q4_k,q5_k,q6_k}_f32_f32 and the _id forms (weights in
+ *   GGUF layout).
+ * and the fused hot-path kernels (no reference pipeline of their own; each
+ * replaces a run of the reference's dispatches, see the push blocks below):
+ *   router_topk, moe_gate_up_silu_{q8_0,q4_k,q5_k,q6_k},
+ *   moe_down_reduce_{q8_0,q4_k,q5_k,q6_k}, attn_decode_paged.
+ * For the fused kernels the grid argument is ignored (the library sizes the
+ * launch; it must still be non-zero), quant weights are in the split layout
+ * of styx_op_to_split, and each dispatch may enqueue more than one kernel.
+ * They use the gpu's op scratch (as the styx_op_* calls do): batches that
+ * use them must not run on two streams at once.
  * styx_kernel_names() lists what this build provides. */
 typedef struct styx_kernel styx_kernel;
 int styx_kernel_get(styx_gpu *gpu, const char *name, const uint32_t *spec, int n_spec,
@@ -115,6 +126,66 @@ int styx_batch_dispatch(styx_batch *b, const styx_kernel *k, const styx_binding 
 /* Batch::submit (lib.rs:200-231): run the recorded work and wait for it
  * (an async batch runs it on its own stream). */
 int styx_batch_submit(styx_batch *b);
+
+/* Push blocks of the fused kernels (no reference counterpart; plain 32-bit
+ * fields, sizes asserted below).
+ *
+ * router_topk replaces moe.rs:1975-2016 (rec_rms of ffn_norm, the
+ * matvec_strided_f32 router, topk_softmax_f32).  10 bindings: 0 x [H] f32,
+ * 1 ffn_norm [H], 2 router W [E][H] f32, 3 bias [E] (read if flags & 1),
+ * 4 remap [E] u32 (flags & 2; else every expert resident at its own index),
+ * 5 pmap [E] u32 (flags & 4), out: 6 xn [H], 7 logits [E], 8 weights [k],
+ * 9 the 256-byte id row (topk_softmax_f32.comp:4-17 layout). */
+typedef struct {
+    uint32_t E, H, k, renorm, arena_mode, layer;
+    float eps;
+    uint32_t flags;
+} styx_push_router_topk;
+/* moe_gate_up_silu_{t}, t the gate type, replaces rec_matvec_id of gate and
+ * of up plus swiglu_f32 (moe.rs:2023-2038): h[s] = silu(Wg[e_s] xn) *
+ * (Wu[e_s] xn) for s < k with e_s = ids[s]; an id at or past n_slabs (SKIP
+ * among them) leaves h[s] untouched, as SKIP does in mul_mat_vec_id.
+ * 5 bindings: 0 gate weights (n_slabs slabs, slab_gate bytes apart), 1 up
+ * weights (slab_up apart), 2 xn [H] f32, 3 ids: k i32 (one row of the id
+ * table: +0 all experts, +64 hot, ...), 4 out h [k][F] f32.  A slab size of
+ * 0 means F*H values of the type (the expert tensor's own stride). */
+typedef struct {
+    uint32_t H, F, k, type_up, n_slabs, slab_gate, slab_up;
+} styx_push_moe_gate_up_silu;
+/* moe_down_reduce_{t} replaces rec_matvec_id of down (ne11 = k) plus
+ * moe_reduce_f32 (moe.rs:2039-2062): x += sum_s w_s Wd[e_s] h[s] in slot
+ * order, skipped slots adding nothing (so hot and cold launches over
+ * disjoint id rows together add every slot).  5 bindings: 0 down weights
+ * (slab_down apart, 0 = H*F values), 1 h [k][F] f32, 2 ids [k] i32,
+ * 3 weights [k] f32, 4 x [H] f32 updated in place. */
+typedef struct {
+    uint32_t H, F, k, n_slabs, slab_down;
+} styx_push_moe_down_reduce;
+/* attn_decode_paged replaces moe.rs:1875-1964 (per-head q/k rms_norm,
+ * rope_neox_f32 of q and k, the two cpy_f32_f32 KV appends at pos and
+ * attn_decode_f32) for one layer at position pos (context pos + 1).
+ * 11 bindings: 0 q [nh*hd], 1 k [nkv*hd], 2 v [nkv*hd] (raw projections),
+ * 3 q_norm [hd] (flags & 1), 4 k_norm [hd] (flags & 2), 5 rope table
+ * [> pos][hd/2][2] f64 (styx_rope_table), 6 K pool, 7 V pool, 8 page table
+ * [i32] (flags & 4: pools of whole pages of page_tokens rows [token][nkv*hd],
+ * logical page i at physical page table[i]; otherwise the pools are the
+ * reference's contiguous [cap][nkv*hd] caches), 9 out [nh*hd] f32, 10 part:
+ * styx_op_attn_part_floats(nh, nkv, hd, max_chunks) floats.  The context
+ * is split over max_chunks workgroups per kv head of at least `chunk`
+ * tokens (a multiple of 16), as in styx_op_attn_decode.  Page-table entries
+ * past the pool are clamped to its last page. */
+typedef struct {
+    float eps;
+    uint32_t page_tokens, nh, nkv, hd, chunk, max_chunks;
+    float scale;
+    uint32_t flags, pos;
+} styx_push_attn_decode_paged;
+#ifdef __cplusplus
+static_assert(sizeof(styx_push_router_topk) == 32, "push layout");
+static_assert(sizeof(styx_push_moe_gate_up_silu) == 28, "push layout");
+static_assert(sizeof(styx_push_moe_down_reduce) == 20, "push layout");
+static_assert(sizeof(styx_push_attn_decode_paged) == 40, "push layout");
+#endif
 
 /* Gpu::dispatch_sync (lib.rs:1415-1515): one dispatch, run and waited for. */
 int styx_dispatch_sync(styx_gpu *gpu, const styx_kernel *k, const styx_binding *binds,

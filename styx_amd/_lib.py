@@ -84,6 +84,30 @@ class Binding(C.Structure):
     _fields_ = [("buf", C.c_void_p), ("offset", C.c_uint64), ("range", C.c_uint64)]
 
 
+# push blocks of the fused dispatch kernels (include/styx_hip.h)
+class PushRouterTopk(C.Structure):
+    _fields_ = [("E", C.c_uint32), ("H", C.c_uint32), ("k", C.c_uint32), ("renorm", C.c_uint32),
+                ("arena_mode", C.c_uint32), ("layer", C.c_uint32), ("eps", C.c_float),
+                ("flags", C.c_uint32)]
+
+
+class PushGateUpSilu(C.Structure):
+    _fields_ = [("H", C.c_uint32), ("F", C.c_uint32), ("k", C.c_uint32), ("type_up", C.c_uint32),
+                ("n_slabs", C.c_uint32), ("slab_gate", C.c_uint32), ("slab_up", C.c_uint32)]
+
+
+class PushDownReduce(C.Structure):
+    _fields_ = [("H", C.c_uint32), ("F", C.c_uint32), ("k", C.c_uint32), ("n_slabs", C.c_uint32),
+                ("slab_down", C.c_uint32)]
+
+
+class PushAttnPaged(C.Structure):
+    _fields_ = [("eps", C.c_float), ("page_tokens", C.c_uint32), ("nh", C.c_uint32),
+                ("nkv", C.c_uint32), ("hd", C.c_uint32), ("chunk", C.c_uint32),
+                ("max_chunks", C.c_uint32), ("scale", C.c_float), ("flags", C.c_uint32),
+                ("pos", C.c_uint32)]
+
+
 vp, i32, i64, u32, u64, f32p = C.c_void_p, C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_void_p
 
 # name: (restype, argtypes)

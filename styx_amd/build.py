@@ -28,6 +28,7 @@ SOURCES = [
     "moe_block.hip",
     "capi.cpp",
     "dispatch.cpp",
+    "dispatch_fused.cpp",
     "engine.cpp",
     "gguf.cpp",
 ]

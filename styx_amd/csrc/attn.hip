@@ -51,9 +51,16 @@ __device__ __forceinline__ int64_t kv_row(const AttnArgs &a, int64_t pg, int tp,
     return a.kv_head_major ? ((pg * a.nkv + kvh) * a.page_tokens + tp) * (int64_t)a.hd
                            : (pg * a.page_tokens + tp) * (int64_t)kv_dim + (int64_t)kvh * a.hd;
 }
+// Page-table entry i; with a.pool_pages set, entries past the pool are
+// clamped to its last page (a caller's table is not trusted to stay inside).
+__device__ __forceinline__ int32_t pt_at(const AttnArgs &a, int i)
+{
+    const int32_t p = a.page_table[i];
+    return a.pool_pages > 0 ? (int32_t)min((uint32_t)p, (uint32_t)(a.pool_pages - 1)) : p;
+}
 __device__ __forceinline__ int64_t kv_off(const AttnArgs &a, int t, int kvh, int kv_dim)
 {
-    return kv_row(a, a.page_table[t / a.page_tokens], t % a.page_tokens, kvh, kv_dim);
+    return kv_row(a, pt_at(a, t / a.page_tokens), t % a.page_tokens, kvh, kv_dim);
 }
 
 // One head's RMSNorm(hd) * w and NEOX rope at pos, split into a load phase
@@ -376,7 +383,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     for (int e = 0; e < EPL; e++) vn[e] = a.v[(int64_t)kvh * HD + lane * EPL + e];
     const int t_min = c * a.chunk + ts * TILE + tl, pg_min = t_min / a.page_tokens;
     const bool spec = pg_min < a.page_table_len;
-    const int32_t pe_min = spec ? a.page_table[pg_min] : 0;
+    const int32_t pe_min = spec ? pt_at(a, pg_min) : 0;
     const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
     const int t0 = c * chunk;
     if (t0 >= n_t) return;
@@ -674,14 +681,14 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     }
     const int t_min = c * a.chunk + wave * 16 + lr, pg_min = t_min / a.page_tokens;
     const bool spec = pg_min < a.page_table_len;
-    const int32_t pe_min = spec ? a.page_table[pg_min] : 0;
+    const int32_t pe_min = spec ? pt_at(a, pg_min) : 0;
     // the whole page table in LDS when it is short: past the minimum chunk
     // size (long contexts) the first tile's page entry then needs no memory
     // trip after the position, nor does any later tile's
     __shared__ int32_t s_pt[ATTN_PT_LDS];
     const bool pt_lds = a.page_table_len > 0 && a.page_table_len <= ATTN_PT_LDS;
     if (pt_lds)
-        for (int i = threadIdx.x; i < a.page_table_len; i += AT_WG) s_pt[i] = a.page_table[i];
+        for (int i = threadIdx.x; i < a.page_table_len; i += AT_WG) s_pt[i] = pt_at(a, i);
 
     const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
     const int t0 = c * chunk;

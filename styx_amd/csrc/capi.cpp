@@ -58,6 +58,7 @@ static void gpu_destroy(styx_gpu *g)
     hipStreamDestroy(g->stream);
     if (g->xq_scratch) hipFree(g->xq_scratch);
     if (g->partial_scratch) hipFree(g->partial_scratch);
+    if (g->fused_scalars) hipFree(g->fused_scalars);
     delete g;
 }
 
@@ -105,8 +106,12 @@ int styx_gpu_new(int device, styx_gpu **out)
     g->partial_bytes = sizeof(float) * MAX_TOPK * XQ_MAX;
     e = hipMalloc(&g->xq_scratch, xq_bytes(XQ_MAX));
     if (e == hipSuccess) e = hipMalloc(&g->partial_scratch, g->partial_bytes);
+    if (e == hipSuccess) e = hipMalloc(&g->fused_scalars, 256);
+    if (e == hipSuccess) e = hipMemset(g->fused_scalars, 0, 256);
     if (e != hipSuccess) {
         if (g->xq_scratch) hipFree(g->xq_scratch);
+        if (g->partial_scratch) hipFree(g->partial_scratch);
+        if (g->fused_scalars) hipFree(g->fused_scalars);
         hipStreamDestroy(g->stream);
         delete g;
         return hip_fail(e, "hipMalloc(op scratch)");

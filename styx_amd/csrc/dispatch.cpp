@@ -72,6 +72,17 @@ const KDef kdefs[] = {
     {"mul_mat_vec_id_q4_k_f32_f32", RK_MMV_BASE + 5, 6, 48},
     {"mul_mat_vec_id_q5_k_f32_f32", RK_MMV_BASE + 6, 6, 48},
     {"mul_mat_vec_id_q6_k_f32_f32", RK_MMV_BASE + 7, 6, 48},
+    // fused hot-path kernels: bindings and push blocks of include/styx_hip.h
+    {"router_topk", RK_F_ROUTER_TOPK, 10, sizeof(styx_push_router_topk)},
+    {"moe_gate_up_silu_q8_0", RK_F_GATE_UP_SILU + 0, 5, sizeof(styx_push_moe_gate_up_silu)},
+    {"moe_gate_up_silu_q4_k", RK_F_GATE_UP_SILU + 1, 5, sizeof(styx_push_moe_gate_up_silu)},
+    {"moe_gate_up_silu_q5_k", RK_F_GATE_UP_SILU + 2, 5, sizeof(styx_push_moe_gate_up_silu)},
+    {"moe_gate_up_silu_q6_k", RK_F_GATE_UP_SILU + 3, 5, sizeof(styx_push_moe_gate_up_silu)},
+    {"moe_down_reduce_q8_0", RK_F_DOWN_REDUCE + 0, 5, sizeof(styx_push_moe_down_reduce)},
+    {"moe_down_reduce_q4_k", RK_F_DOWN_REDUCE + 1, 5, sizeof(styx_push_moe_down_reduce)},
+    {"moe_down_reduce_q5_k", RK_F_DOWN_REDUCE + 2, 5, sizeof(styx_push_moe_down_reduce)},
+    {"moe_down_reduce_q6_k", RK_F_DOWN_REDUCE + 3, 5, sizeof(styx_push_moe_down_reduce)},
+    {"attn_decode_paged", RK_F_ATTN_PAGED, 11, sizeof(styx_push_attn_decode_paged)},
 };
 
 }  // namespace
@@ -93,8 +104,11 @@ int run_cmds(styx_batch *b, hipStream_t st)
 {
     for (auto &c : b->cmds) {
         const uint32_t *spec = c.k->spec.empty() ? nullptr : c.k->spec.data();
-        hipError_t e = refk_launch(st, c.k->kid, c.ptr.data(), c.size.data(), c.push.data(), c.gx,
-                                   c.gy, c.gz, spec, (int)c.k->spec.size() / 2);
+        hipError_t e = c.k->kid >= RK_F_ROUTER_TOPK
+                           ? fused_launch(b->gpu, st, c.k->kid, c.ptr.data(), c.size.data(),
+                                          c.push.data())
+                           : refk_launch(st, c.k->kid, c.ptr.data(), c.size.data(), c.push.data(),
+                                         c.gx, c.gy, c.gz, spec, (int)c.k->spec.size() / 2);
         if (e == hipErrorInvalidValue)
             return fail(STYX_E_INVALID, c.k->name + ": unsupported parameters, or the push "
                                                     "constants and grid reach past a binding");
@@ -104,19 +118,32 @@ int run_cmds(styx_batch *b, hipStream_t st)
     return STYX_OK;
 }
 
-// Completed signals are dropped and `reached` advanced (caller holds mu).
+// Completed signals are dropped and `reached` raised to the largest
+// completed value (caller holds mu).  Every pending signal is queried:
+// signals of async batches on different streams may complete out of
+// submission order, and a timeline's value is the largest one reached
+// (vkGetSemaphoreCounterValue).
 int timeline_poll(styx_timeline *t)
 {
-    size_t n = 0;
-    for (; n < t->sig.size(); n++) {
-        const hipError_t e = hipEventQuery(t->sig[n].second);
-        if (e == hipErrorNotReady) break;
-        if (e != hipSuccess) return hip_fail(e, "hipEventQuery");
-        t->reached = t->sig[n].first;
-        hipEventDestroy(t->sig[n].second);
+    std::vector<std::pair<uint64_t, hipEvent_t>> keep;
+    keep.reserve(t->sig.size());
+    int r = STYX_OK;
+    for (auto &sg : t->sig) {
+        const hipError_t e = r ? hipErrorNotReady : hipEventQuery(sg.second);
+        if (e == hipErrorNotReady) {
+            keep.push_back(sg);
+            continue;
+        }
+        if (e != hipSuccess) {
+            r = hip_fail(e, "hipEventQuery");
+            keep.push_back(sg);
+            continue;
+        }
+        t->reached = std::max(t->reached, sg.first);
+        hipEventDestroy(sg.second);
     }
-    t->sig.erase(t->sig.begin(), t->sig.begin() + n);
-    return STYX_OK;
+    t->sig.swap(keep);
+    return r;
 }
 
 }  // namespace

@@ -90,6 +90,20 @@ hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, c
                               int H, int F, int k, const uint8_t *sh_gate = nullptr,
                               const uint8_t *sh_up = nullptr, int filter = SLOTS_ALL);
 
+// h[s] = swiglu(Wg[e_s] xn, Wu[e_s] xn) for the k slots, e_s = ids[s] (one
+// id per slot; an id at or past n_slabs, SKIP among them, leaves h[s]
+// untouched); wg / wu hold n_slabs split-layout slabs slab_g / slab_u bytes
+// apart; xn given by its limbs; h is [k][F].
+hipError_t launch_moe_gate_up_silu(hipStream_t st, int tg, int tu, const uint8_t *wg,
+                                   int64_t slab_g, const uint8_t *wu, int64_t slab_u,
+                                   const int32_t *ids, uint32_t n_slabs, const Xq &xq, float *h,
+                                   int H, int F, int k);
+// partial[s] = Wd[e_s] h[s] with e_s = ids[s] as above (a skipped slot's
+// partial is zeros); partial is [k][H].
+hipError_t launch_moe_down_h(hipStream_t st, int td, const uint8_t *wd, int64_t slab_d,
+                             const int32_t *ids, uint32_t n_slabs, const float *h, float *partial,
+                             int H, int F, int k);
+
 // partial[s] = Wd[e_s] swiglu(gu[0][s], gu[1][s]) for the k routed slots
 // (and the shared expert's down matrix as slot k if sh_down); gu is
 // [2][nslots][F], partial [nslots][H].
@@ -190,6 +204,8 @@ struct AttnArgs {
     int page_tokens;
     int kv_head_major;
     int page_table_len;              // entries of page_table (0: not given)
+    int pool_pages;                  // pages in kpool / vpool: entries past them are
+                                     // clamped (0: entries trusted, no clamp)
     const int32_t *pos;              // device scalar
     float *out;                      // [nh*hd]
     Xq xq;                           // optional limbs of out (o-proj input)

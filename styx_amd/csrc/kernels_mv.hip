@@ -356,6 +356,13 @@ hipError_t launch_router_topk(hipStream_t st, const RouterArgs &a)
 }
 
 // ------------------------------------------------------------ gate / up ---
+// Whether a slot with hot id h (SKIP: not hot) passes the launch's filter
+// (SlotFilter); the shared expert slot counts as hot.
+__device__ __forceinline__ bool slot_passes(int filter, bool hot)
+{
+    return filter == SLOTS_ALL || (filter == SLOTS_HOT) == hot;
+}
+
 struct GateUpK {
     ExpSrc src[2];
     const uint8_t *sh[2];  // shared expert gate/up matrices (slot k) or null
@@ -365,13 +372,27 @@ struct GateUpK {
     Xq xq;
     float *gu;  // [2][nslots][F]
     int F, k, nslots, nb, rpw, filter;
+    // one expert id per slot (a single row of the id table), or null: slot
+    // s reads slab id_one[s] of src[m].hot; an id at or past n_slabs (SKIP
+    // among them) leaves the slot's outputs untouched
+    const int32_t *id_one;
+    uint32_t n_slabs;
+    float *h;  // k_gate_up_silu: [nslots][F] = silu(gate rows) * up rows
 };
 
-// Whether a slot with hot id h (SKIP: not hot) passes the launch's filter
-// (SlotFilter); the shared expert slot counts as hot.
-__device__ __forceinline__ bool slot_passes(int filter, bool hot)
+// Slab of matrix m (0 gate, 1 up) for slot s < k from an id row in memory
+// (the id_one row, or the hot / arena / host rows), or null when the slot
+// is skipped (by its ids or the launch's filter).
+__device__ __forceinline__ const uint8_t *gu_slab_of_ids(const GateUpK &a, int m, int s)
 {
-    return filter == SLOTS_ALL || (filter == SLOTS_HOT) == hot;
+    if (a.id_one) {
+        const uint32_t e = (uint32_t)a.id_one[s];
+        return e < a.n_slabs ? a.src[m].hot + (int64_t)e * a.src[m].hot_slab : nullptr;
+    }
+    uint32_t r3[3];
+    for (int j = 0; j < 3; j++) r3[j] = (uint32_t)a.ids[16 * (j + 1) + s];
+    if (!slot_passes(a.filter, r3[0] != SKIP)) return nullptr;
+    return slab_pick(a.src[m], r3[0], r3[1], r3[2]);
 }
 
 // Routing first (one trip for the logits, then LDS work), then the slot's
@@ -381,15 +402,15 @@ __device__ inline void gate_up_body(const GateUpK &a, int m, int s, int32_t *s_i
 {
     const uint8_t *slab;
     if (s < a.k) {
-        uint32_t r3[3];
         if (a.route.logits) {
+            uint32_t r3[3];
             const int32_t *ids = route_ids_wg(a.route, s_ids, s_lg);
             route_row(a.route, ids[s], s, r3);
+            if (!slot_passes(a.filter, r3[0] != SKIP)) return;
+            slab = slab_pick(a.src[m], r3[0], r3[1], r3[2]);
         } else {
-            for (int j = 0; j < 3; j++) r3[j] = (uint32_t)a.ids[16 * (j + 1) + s];
+            slab = gu_slab_of_ids(a, m, s);
         }
-        if (!slot_passes(a.filter, r3[0] != SKIP)) return;
-        slab = slab_pick(a.src[m], r3[0], r3[1], r3[2]);
     } else {
         if (!slot_passes(a.filter, true)) return;
         slab = a.sh[m];  // the shared expert needs no routing
@@ -419,6 +440,43 @@ __global__ void __launch_bounds__(WG) k_gate_up(GateUpK a)
         gate_up_body<TG, UPL>(a, 0, s, s_ids, s_lg);
     else
         gate_up_body<TU, UPL>(a, 1, s, s_ids, s_lg);
+}
+
+// Gate and up rows [r0, r1) of one slot in one workgroup, then
+// h = swiglu_f32(g, u) (ops2.rs:305-309) of those rows: the gate rows' first
+// weights are issued, then the up rows are walked, then the gate rows; both
+// land in LDS.  Ids from an id row in memory (no in-kernel routing).  A
+// skipped slot writes nothing.
+template <int TG, int TU, int UPL>
+__global__ void __launch_bounds__(WG) k_gate_up_silu(GateUpK a)
+{
+    extern __shared__ __align__(16) float s_gu[];  // gate rows | up rows of the block
+    const int s = blockIdx.y;
+    const uint8_t *sg = s < a.k ? gu_slab_of_ids(a, 0, s) : a.sh[0];
+    const uint8_t *su = s < a.k ? gu_slab_of_ids(a, 1, s) : a.sh[1];
+    if (!sg || !su) return;
+    const int r_begin = blockIdx.x * a.rpw, r_end = min(a.F, r_begin + a.rpw);
+    float *gs = s_gu, *us = s_gu + a.rpw;
+    walk_rows_pipelined<TG, UPL, 1>(
+        OneMat{mat_at(sg, TG, (int64_t)a.F * a.nb), a.nb}, a.nb, a.G, r_begin, r_end,
+        [&](UX<TG>(&x)[UPL], const LaneU<UPL> &lu) {
+            walk_rows_pipelined<TU, UPL, 1>(
+                OneMat{mat_at(su, TU, (int64_t)a.F * a.nb), a.nb}, a.nb, a.G, r_begin, r_end,
+                [&](UX<TU>(&xu)[UPL], const LaneU<UPL> &luu) {
+                    XFrom<TU, UPL>{a.xq}(xu, luu);
+                    return true;
+                },
+                [&](int r, float v) { us[r - r_begin] = v; });
+            XFrom<TG, UPL>{a.xq}(x, lu);
+            return true;
+        },
+        [&](int r, float v) { gs[r - r_begin] = v; });
+    __syncthreads();
+    float *h = a.h + (int64_t)s * a.F;
+    for (int i = threadIdx.x; i < r_end - r_begin; i += WG) {
+        const float g = gs[i];
+        h[r_begin + i] = g / (1.0f + expf(-g)) * us[i];
+    }
 }
 
 // gate and up share the block size, so one geometry serves both
@@ -477,6 +535,65 @@ hipError_t launch_moe_gate_up(hipStream_t st, int tg, int tu, const ExpSrc &g, c
     }
 }
 
+template <int TG, int TU>
+static void launch_gus(hipStream_t st, int upl, const GateUpK &a, dim3 grid, size_t lds)
+{
+    upl_dispatch<TG>(upl, [&](auto u) {
+        hipLaunchKernelGGL((k_gate_up_silu<TG, TU, decltype(u)::value>), grid, dim3(WG), lds, st, a);
+    });
+}
+
+hipError_t launch_moe_gate_up_silu(hipStream_t st, int tg, int tu, const uint8_t *wg,
+                                   int64_t slab_g, const uint8_t *wu, int64_t slab_u,
+                                   const int32_t *ids, uint32_t n_slabs, const Xq &xq, float *h,
+                                   int H, int F, int k)
+{
+    const Geo gg = pick_geo(tg, H), gu = pick_geo(tu, H);
+    if (!gg.G || gu.G != gg.G || gu.UPL != gg.UPL || blk_elems(tg) != blk_elems(tu) || k < 1 ||
+        k > MAX_TOPK || !xq.A || !wg || !wu || !ids || !h || F < 1)
+        return hipErrorInvalidValue;
+    GateUpK a{};
+    a.src[0].hot = wg;
+    a.src[0].hot_slab = slab_g;
+    a.src[1].hot = wu;
+    a.src[1].hot_slab = slab_u;
+    a.nslots = k;
+    a.G = gg.G;
+    a.id_one = ids;
+    a.n_slabs = n_slabs;
+    a.xq = xq;
+    a.h = h;
+    a.F = F;
+    a.k = k;
+    a.nb = H / blk_elems(tg);
+    // ~512 workgroups, each a row block of one slot's gate and up
+    a.rpw = rows_per_wg(a.nslots * F, gg.G, 512);
+    const dim3 grid((F + a.rpw - 1) / a.rpw, a.nslots, 1);
+    const size_t lds = (size_t)8 * a.rpw;
+    auto with_tu = [&](auto tgc) {
+        constexpr int TG = decltype(tgc)::value;
+        if constexpr (TG == T_Q8_0) {
+            if (tu != T_Q8_0) return hipErrorInvalidValue;
+            launch_gus<TG, T_Q8_0>(st, gg.UPL, a, grid, lds);
+        } else {
+            switch (tu) {
+            case T_Q4_K: launch_gus<TG, T_Q4_K>(st, gg.UPL, a, grid, lds); break;
+            case T_Q5_K: launch_gus<TG, T_Q5_K>(st, gg.UPL, a, grid, lds); break;
+            case T_Q6_K: launch_gus<TG, T_Q6_K>(st, gg.UPL, a, grid, lds); break;
+            default: return hipErrorInvalidValue;
+            }
+        }
+        return hipGetLastError();
+    };
+    switch (tg) {
+    case T_Q8_0: return with_tu(IC<T_Q8_0>{});
+    case T_Q4_K: return with_tu(IC<T_Q4_K>{});
+    case T_Q5_K: return with_tu(IC<T_Q5_K>{});
+    case T_Q6_K: return with_tu(IC<T_Q6_K>{});
+    default: return hipErrorInvalidValue;
+    }
+}
+
 // ------------------------------------------------------------- down -------
 // partial[s] = Wd[e_s] . swiglu(g_s, u_s) for every routed slot s; the
 // weighted combine into the residual is k_reduce_rows.
@@ -488,6 +605,11 @@ struct DownK {
     const float *gu;    // [2][nslots][F]
     float *partial;     // [nslots][H]
     int H, F, k, nslots, nb, rpw, filter;
+    // one expert id per slot, or null (as GateUpK::id_one): slab id_one[s]
+    // of src.hot; a skipped slot's partial is written as zeros
+    const int32_t *id_one;
+    uint32_t n_slabs;
+    const float *h;     // [nslots][F] already silu(g) * u (gu unused), or null
 };
 
 template <int T, int UPL>
@@ -502,22 +624,30 @@ __global__ void __launch_bounds__(WG) k_down(DownK a)
     // (ops2.rs:305-309) with the limbs of its output is built in LDS while
     // they are in flight
     int32_t idr[3] = {(int32_t)SKIP, (int32_t)SKIP, (int32_t)SKIP};
-    if (s < a.k) {
+    if (s < a.k && !a.id_one) {
 #pragma unroll
         for (int j = 0; j < 3; j++) idr[j] = a.ids[16 * (j + 1) + s];
     }
-    if (!slot_passes(a.filter, s >= a.k || (uint32_t)idr[0] != SKIP)) return;
+    if (!a.id_one && !slot_passes(a.filter, s >= a.k || (uint32_t)idr[0] != SKIP)) return;
     constexpr int PG = 4;  // gate/up values per thread held in registers
-    const float *g = a.gu + (int64_t)s * a.F, *u = a.gu + ((int64_t)a.nslots + s) * a.F;
+    const float *g = a.h ? a.h + (int64_t)s * a.F : a.gu + (int64_t)s * a.F;
+    const float *u = a.h ? g : a.gu + ((int64_t)a.nslots + s) * a.F;
     float gv[PG], uv[PG];
 #pragma unroll
     for (int j = 0; j < PG; j++) {
         const int i = threadIdx.x + WG * j;
         gv[j] = i < a.F ? g[i] : 0.0f;
-        uv[j] = i < a.F ? u[i] : 0.0f;
+        uv[j] = (i < a.F && !a.h) ? u[i] : 0.0f;
     }
-    const uint8_t *slab =
-        s < a.k ? slab_pick(a.src, (uint32_t)idr[0], (uint32_t)idr[1], (uint32_t)idr[2]) : a.sh;
+    const uint8_t *slab = a.sh;
+    if (s < a.k) {
+        if (a.id_one) {
+            const uint32_t e = (uint32_t)a.id_one[s];
+            slab = e < a.n_slabs ? a.src.hot + (int64_t)e * a.src.hot_slab : nullptr;
+        } else {
+            slab = slab_pick(a.src, (uint32_t)idr[0], (uint32_t)idr[1], (uint32_t)idr[2]);
+        }
+    }
     float *part = a.partial + (int64_t)s * a.H;
     if (!slab) {
         for (int r = r_begin + threadIdx.x; r < r_end; r += WG) part[r] = 0.0f;
@@ -527,12 +657,21 @@ __global__ void __launch_bounds__(WG) k_down(DownK a)
     float *hs = (float *)lds;
     const Xq q = xq_at(lds + (size_t)a.F * 4, a.F);
     auto build = [&](UX<T> (&x)[UPL], const LaneU<UPL> &lu) {
+        if (a.h) {
 #pragma unroll
-        for (int j = 0; j < PG; j++) {
-            const int i = threadIdx.x + WG * j;
-            if (i < a.F) hs[i] = gv[j] / (1.0f + expf(-gv[j])) * uv[j];
+            for (int j = 0; j < PG; j++) {
+                const int i = threadIdx.x + WG * j;
+                if (i < a.F) hs[i] = gv[j];
+            }
+            for (int i = threadIdx.x + WG * PG; i < a.F; i += WG) hs[i] = g[i];
+        } else {
+#pragma unroll
+            for (int j = 0; j < PG; j++) {
+                const int i = threadIdx.x + WG * j;
+                if (i < a.F) hs[i] = gv[j] / (1.0f + expf(-gv[j])) * uv[j];
+            }
+            for (int i = threadIdx.x + WG * PG; i < a.F; i += WG) hs[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
         }
-        for (int i = threadIdx.x + WG * PG; i < a.F; i += WG) hs[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
         __syncthreads();
         xq_build(hs, nullptr, 0.0f, false, a.F, q, red, nullptr);
         __syncthreads();
@@ -541,6 +680,33 @@ __global__ void __launch_bounds__(WG) k_down(DownK a)
     };
     walk_rows_pipelined<T, UPL, 1>(OneMat{mat, a.nb}, a.nb, a.G, r_begin, r_end, build,
                                    [=](int r, float v) { part[r] = v; });  // (as k_gate_up)
+}
+
+static hipError_t launch_down_k(hipStream_t st, int td, const DownK &a, const Geo &g);
+
+hipError_t launch_moe_down_h(hipStream_t st, int td, const uint8_t *wd, int64_t slab_d,
+                             const int32_t *ids, uint32_t n_slabs, const float *h, float *partial,
+                             int H, int F, int k)
+{
+    const Geo g = pick_geo(td, F);
+    if (!g.G || k < 1 || k > MAX_TOPK || F > XQ_MAX / 2 || !wd || !ids || !h || !partial)
+        return hipErrorInvalidValue;
+    DownK a{};
+    a.src.hot = wd;
+    a.src.hot_slab = slab_d;
+    a.nslots = k;
+    a.G = g.G;
+    a.UPL = g.UPL;
+    a.id_one = ids;
+    a.n_slabs = n_slabs;
+    a.h = h;
+    a.partial = partial;
+    a.H = H;
+    a.F = F;
+    a.k = k;
+    a.nb = F / blk_elems(td);
+    a.rpw = rows_per_wg(a.nslots * H, g.G, 1024);
+    return launch_down_k(st, td, a, g);
 }
 
 hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_t *ids,
@@ -564,6 +730,12 @@ hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_
     a.filter = filter;
     a.nb = F / blk_elems(td);
     a.rpw = rows_per_wg(a.nslots * H, g.G, 1024);
+    return launch_down_k(st, td, a, g);
+}
+
+static hipError_t launch_down_k(hipStream_t st, int td, const DownK &a, const Geo &g)
+{
+    const int H = a.H, F = a.F;
     const dim3 grid((H + a.rpw - 1) / a.rpw, a.nslots, 1);
     const size_t lds = (size_t)F * 4 + xq_bytes(F);
     switch (td) {

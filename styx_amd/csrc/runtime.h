@@ -27,6 +27,10 @@ struct styx_gpu {
     // array of styx_op_attn_decode_noalloc (capi.cpp), looked up at
     // styx_gpu_new with the device current.
     float *noalloc_part = nullptr;
+    // Device scalars of the fused dispatch kernels: [0] the position of an
+    // attn_decode_paged dispatch (written in stream order by a fill kernel),
+    // [1] = 0, the one-entry page table of a contiguous KV cache.
+    int32_t *fused_scalars = nullptr;
 };
 
 struct styx_buf {

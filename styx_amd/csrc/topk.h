@@ -146,8 +146,11 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
 // Top-k ids of the router logits inside a workgroup, by ranking: the rank
 // of a key is the number of larger keys, and ranks 0..k-1 are exactly the
 // reference's selection order (keys of rank_key: larger value first, equal
-// values by lower index).  Up to 128 experts every key is ranked against all
-// (2 or 4 threads per logit, one 64-bit compare per pair).  Above that each
+// values by lower index).  Up to 128 experts (a power-of-two quarter) each
+// wave ranks the keys of its quarter among themselves and keeps the top k as
+// candidates, which are then ranked among themselves (16x fewer compares
+// than ranking every key against all, the cost of which was VALU-bound);
+// other counts up to 128 rank every key against all.  Above 128 each
 // wave takes a quarter of the experts (at most two keys per lane) and draws
 // its quarter's top min(k, E/4) keys one at a time -- the wave's largest key
 // (wave_max_u64), which its owner then drops -- and, every global top-k key
@@ -168,7 +171,41 @@ __device__ inline const int32_t *rank_ids_lds(const Route &r, int32_t *s_ids, co
     if (tid < IDS_ROW) s_ids[tid] = (int32_t)SKIP;
     if (tid < 4 * MAX_TOPK) c_key[tid] = 0;
     __syncthreads();  // also: the caller's logits are in s_lg
-    if (E <= 128) {
+    if (E <= 128 && (Q & (Q - 1)) == 0) {
+        // two stages: every key ranked within its wave's quarter (P = 64 / Q
+        // lanes per key, at least two keys each), the quarter's top min(k, Q)
+        // kept as candidates; then the <= 4k candidates ranked among
+        // themselves.  A key of the global top k has fewer than k larger keys
+        // in its quarter, so it is a candidate, and every key larger than it
+        // is a candidate too: its rank among the candidates is its rank.
+        for (int e = tid; e < E; e += 256) s_key[e] = rank_key(s_lg[e], e);
+        __syncthreads();
+        const int P = min(64 / Q, Q / 2), span = Q / P;  // span >= 2, even
+        const int e = lane / P, part = lane - e * P;
+        int cnt = 0;
+        uint64_t mk = 0;
+        if (e < Q) {
+            mk = s_key[q0 + e];
+            const ulonglong2 *q = (const ulonglong2 *)(s_key + q0 + part * span);
+            for (int j2 = 0; j2 < span / 2; j2++) {
+                const ulonglong2 u = q[j2];
+                cnt += (int)(u.x > mk) + (int)(u.y > mk);
+            }
+        }
+        for (int sh = 1; sh < P; sh <<= 1) cnt += __shfl_xor(cnt, sh);
+        if (e < Q && part == 0 && cnt < k) c_key[wave * k + cnt] = mk;
+        __syncthreads();
+        if (tid < 4 * k) {
+            const uint64_t ck = c_key[tid];
+            int c2 = 0;
+            const ulonglong2 *q = (const ulonglong2 *)c_key;
+            for (int j2 = 0; j2 < 2 * k; j2++) {
+                const ulonglong2 u = q[j2];
+                c2 += (int)(u.x > ck) + (int)(u.y > ck);
+            }
+            if (ck != 0 && c2 < k) s_ids[c2] = (int32_t)(0xFFFFFFFFu - (uint32_t)ck);
+        }
+    } else if (E <= 128) {
         // direct: P = 256 / E threads rank each key against a slice of all
         for (int e = tid; e < E; e += 256) s_key[e] = rank_key(s_lg[e], e);
         __syncthreads();

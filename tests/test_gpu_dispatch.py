@@ -459,3 +459,223 @@ def test_cpy_contig_and_strided(gpu):
     want = d0.copy()
     want[off:off + n * stride:stride] = src[:n]
     assert np.array_equal(bd.download(np.float32), want)
+
+
+# ------------------------------------------------------------ fused names --
+# The fused kernels registered under SURVEY 8(b)'s names, dispatched through
+# styx_batch_dispatch with their push blocks (include/styx_hip.h), checked
+# against the oracle's MoE block and attention.  Quant weights in the split
+# layout (styx_op_to_split), as the fused path reads them.
+
+def _push(cls, **kw) -> bytes:
+    import ctypes
+    from styx_amd import _lib as L
+    p = getattr(L, cls)(**kw)
+    return ctypes.string_at(ctypes.addressof(p), ctypes.sizeof(p))
+
+
+def _experts(gpu, t, E, rows, cols, seed):
+    """E seeded slabs of type t: (split-layout device buffer, GGUF host bytes)."""
+    import ctypes
+    from styx_amd import _lib as L
+    from styx_amd.runtime import to_split
+    be, bb = BLK[t]
+    b = gpu.buffer(E * rows * cols // be * bb)
+    L.check(gpu.lib.styx_op_gen_quant(gpu.h, t, seed, ctypes.c_float(0.02), b.ptr, E * rows * cols))
+    host = b.download()
+    sp = to_split(gpu, t, b, rows, cols, E)
+    b.free()
+    return sp, host
+
+
+@pytest.mark.parametrize("types,H,F,E,k", [((12, 13, 14), 2048, 768, 32, 8),
+                                           ((8, 8, 8), 1024, 512, 16, 4),
+                                           ((12, 12, 14), 2048, 512, 64, 10)])
+def test_fused_moe_block_dispatch(gpu, types, H, F, E, k):
+    """router_topk -> moe_gate_up_silu_{t} -> moe_down_reduce_{t} as three
+    dispatches of one batch (moe.rs:1975-2062 in three calls) against the
+    oracle: ids bit-exact, h and the updated residual within 1e-5 relative
+    L2; a SKIP id leaves its h row untouched; two down launches over
+    disjoint id rows (hot then cold) add what one launch over all slots adds."""
+    from styx_amd.runtime import Batch, Kernel
+    tg, tu, td = types
+    rng = np.random.default_rng(H + F + E)
+    x = rng.standard_normal(H).astype(np.float32)
+    nw = (1 + 0.05 * rng.standard_normal(H)).astype(np.float32)
+    W = (0.02 * rng.standard_normal((E, H))).astype(np.float32)
+    gsp, gh = _experts(gpu, tg, E, F, H, 11 * E + 1)
+    usp, uh = _experts(gpu, tu, E, F, H, 11 * E + 2)
+    dsp, dh = _experts(gpu, td, E, H, F, 11 * E + 3)
+    xb, nwb, Wb = f32buf(gpu, x), f32buf(gpu, nw), f32buf(gpu, W)
+    xn, lg, wts, ids = gpu.buffer(H * 4), gpu.buffer(E * 4), gpu.buffer(64), gpu.buffer(256)
+    sentinel = np.full(k * F, 3.0, np.float32)
+    hb = f32buf(gpu, sentinel)
+    dummy = gpu.zeros(256)
+    kr = Kernel(gpu, "router_topk", [])
+    kg = Kernel(gpu, f"moe_gate_up_silu_{NAME[tg]}", [])
+    kd = Kernel(gpu, f"moe_down_reduce_{NAME[td]}", [])
+    b = Batch(gpu)
+    b.begin()
+    b.dispatch(kr, [xb, nwb, Wb, dummy, dummy, dummy, xn, lg, wts, ids],
+               _push("PushRouterTopk", E=E, H=H, k=k, renorm=1, arena_mode=0, layer=0, eps=1e-6,
+                     flags=0), (1, 1, 1))
+    b.dispatch(kg, [gsp, usp, xn, (ids, 0, 4 * k), hb],
+               _push("PushGateUpSilu", H=H, F=F, k=k, type_up=tu, n_slabs=E), (1, 1, 1))
+    b.submit()
+    # oracle on the same routing
+    xn_ref = O.rms_norm(x, nw, H, 1, 1e-6)
+    w_ref, ids_ref = O.topk_softmax(lg.download(np.float32), k, True)
+    idh = ids.download(np.int32)
+    assert np.array_equal(idh[:k], ids_ref[:k]) and np.array_equal(idh[16:16 + k], ids_ref[:k])
+    sel = ids_ref[:k].astype(np.uint32)
+    g = O.matvec_id(tg, gh, F, H, len(gh) // E, sel, xn_ref, 1)
+    u = O.matvec_id(tu, uh, F, H, len(uh) // E, sel, xn_ref, 1)
+    h_ref = O.swiglu(g, u)
+    h = hb.download(np.float32)
+    assert rel_l2(h, h_ref) < 1e-5
+    d = O.matvec_id(td, dh, H, F, len(dh) // E, sel, h_ref, k)
+    x_ref = O.moe_reduce(d, w_ref, H, k, x)
+    b.begin()
+    b.dispatch(kd, [dsp, hb, (ids, 0, 4 * k), wts, xb],
+               _push("PushDownReduce", H=H, F=F, k=k, n_slabs=E), (1, 1, 1))
+    b.submit()
+    assert rel_l2(xb.download(np.float32) - x, x_ref - x) < 1e-5
+    # hot / cold split over disjoint id rows adds the same
+    half = k // 2
+    hot = np.where(np.arange(k) < half, idh[:k], -1).astype(np.int32)
+    cold = np.where(np.arange(k) >= half, idh[:k], -1).astype(np.int32)
+    hotb, coldb = gpu.from_numpy(hot), gpu.from_numpy(cold)
+    xb.upload(x)
+    b.begin()
+    for rowb in (hotb, coldb):
+        b.dispatch(kd, [dsp, hb, rowb, wts, xb],
+                   _push("PushDownReduce", H=H, F=F, k=k, n_slabs=E), (1, 1, 1))
+    b.submit()
+    assert rel_l2(xb.download(np.float32) - x, x_ref - x) < 1e-5
+    # a SKIP (and an id past n_slabs) leaves h untouched
+    skip = idh[:k].copy()
+    skip[1] = -1
+    skip[k - 1] = E + 5
+    sb = gpu.from_numpy(skip.astype(np.int32))
+    hb.upload(sentinel)
+    b.begin()
+    b.dispatch(kg, [gsp, usp, xn, sb, hb],
+               _push("PushGateUpSilu", H=H, F=F, k=k, type_up=tu, n_slabs=E), (1, 1, 1))
+    b.submit()
+    h2 = hb.download(np.float32).reshape(k, F)
+    assert (h2[1] == 3.0).all() and (h2[k - 1] == 3.0).all()
+    assert rel_l2(h2[0], h_ref.reshape(k, F)[0]) < 1e-5
+    b.free()
+    for kk in (kr, kg, kd):
+        kk.free()
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_fused_attn_decode_paged(gpu, paged):
+    """attn_decode_paged (moe.rs:1875-1964 in one dispatch: q/k norm, rope,
+    K/V append at pos, split-context attention) over the reference's
+    contiguous caches or a scrambled page table, 40 positions, against the
+    f64 oracle at 2e-6 relative L2; the appended rows land at their
+    addresses."""
+    import ctypes
+    from styx_amd.runtime import Batch, Kernel
+    nh, nkv, hd, n_steps, page, max_chunks = 32, 4, 128, 40, 16, 4
+    rng = np.random.default_rng(77 + paged)
+    kvd, n_ctx, base = nkv * hd, 64, 1e6
+    npages = n_ctx // page
+    pt = rng.permutation(npages).astype(np.int32)
+    kpool, vpool = gpu.zeros(n_ctx * kvd * 4), gpu.zeros(n_ctx * kvd * 4)
+    rope = np.empty((n_ctx, hd // 2, 2), np.float64)
+    gpu.lib.styx_rope_table(ctypes.c_float(base), hd, n_ctx, rope.ctypes.data)
+    ropeb, ptb = gpu.from_numpy(rope), gpu.from_numpy(pt)
+    qn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    qnb, knb = f32buf(gpu, qn), f32buf(gpu, kn)
+    part = gpu.buffer(gpu.lib.styx_op_attn_part_floats(nh, nkv, hd, max_chunks) * 4)
+    out = gpu.buffer(nh * hd * 4)
+    kern = Kernel(gpu, "attn_decode_paged", [])
+    b = Batch(gpu)
+    K = np.zeros((n_ctx, kvd), np.float32)
+    V = np.zeros((n_ctx, kvd), np.float32)
+    scale = 1.0 / np.sqrt(hd)
+
+    def nr(v, w, n, pos):
+        return O.rope_neox(O.rms_norm(v, w, hd, n, 1e-6), hd, n, pos, base)
+    for pos in range(n_steps):
+        q = rng.standard_normal(nh * hd).astype(np.float32)
+        k = rng.standard_normal(kvd).astype(np.float32)
+        v = rng.standard_normal(kvd).astype(np.float32)
+        b.begin()
+        b.dispatch(kern, [f32buf(gpu, q), f32buf(gpu, k), f32buf(gpu, v), qnb, knb, ropeb, kpool,
+                          vpool, ptb, out, part],
+                   _push("PushAttnPaged", eps=1e-6, page_tokens=page, nh=nh, nkv=nkv, hd=hd,
+                         chunk=16, max_chunks=max_chunks, scale=scale,
+                         flags=3 | (4 if paged else 0), pos=pos), (1, 1, 1))
+        b.submit()
+        K[pos] = nr(k, kn, nkv, pos)
+        V[pos] = v
+        ref = O.attn_decode_f64(nr(q, qn, nh, pos), K, V, pos + 1, hd, kvd, nh // nkv, nh, scale)
+        assert rel_l2(out.download(np.float32), ref) < 2e-6, pos
+    kp = kpool.download(np.float32).reshape(n_ctx, kvd)
+    vp = vpool.download(np.float32).reshape(n_ctx, kvd)
+    for t in range(n_steps):
+        row = pt[t // page] * page + t % page if paged else t
+        np.testing.assert_allclose(kp[row], K[t], rtol=2e-6, atol=2e-6)
+        assert np.array_equal(vp[row], V[t]), t
+    b.free()
+    kern.free()
+
+
+def test_fused_attn_page_entries_clamped_to_pool(gpu):
+    """A page-table entry past the pool reads (and appends to) the pool's
+    last page instead of memory outside it: the result equals the table
+    with that entry replaced by the last page."""
+    import ctypes
+    from styx_amd.runtime import Batch, Kernel
+    nh, nkv, hd, page = 8, 2, 64, 16
+    kvd, n_ctx, base = nkv * hd, 32, 1e6
+    rng = np.random.default_rng(5)
+    rope = np.empty((n_ctx, hd // 2, 2), np.float64)
+    gpu.lib.styx_rope_table(ctypes.c_float(base), hd, n_ctx, rope.ctypes.data)
+    ropeb = gpu.from_numpy(rope)
+    q, k, v = (rng.standard_normal(n).astype(np.float32) for n in (nh * hd, kvd, kvd))
+    pools = rng.standard_normal(n_ctx * kvd).astype(np.float32)
+    kern = Kernel(gpu, "attn_decode_paged", [])
+    outs = []
+    for table in ([0, 2 ** 31 - 1], [0, 1]):
+        kp, vp = f32buf(gpu, pools), f32buf(gpu, pools[::-1].copy())
+        out, part = gpu.buffer(nh * hd * 4), gpu.buffer(
+            gpu.lib.styx_op_attn_part_floats(nh, nkv, hd, 2) * 4)
+        b = Batch(gpu)
+        b.begin()
+        b.dispatch(kern, [f32buf(gpu, q), f32buf(gpu, k), f32buf(gpu, v), gpu.zeros(256),
+                          gpu.zeros(256), ropeb, kp, vp, gpu.from_numpy(np.array(table, np.int32)),
+                          out, part],
+                   _push("PushAttnPaged", eps=1e-6, page_tokens=page, nh=nh, nkv=nkv, hd=hd,
+                         chunk=16, max_chunks=2, scale=0.125, flags=4, pos=20), (1, 1, 1))
+        b.submit()
+        b.free()
+        outs.append(out.download(np.float32))
+    assert np.array_equal(outs[0], outs[1])
+    kern.free()
+
+
+def test_fused_rejects_reach_past_binding(gpu):
+    """A fused dispatch whose push block implies more bytes than a binding
+    makes visible is refused before anything launches."""
+    from styx_amd import _lib as L
+    from styx_amd.runtime import Batch, Kernel
+    H, E, k = 512, 16, 4
+    small = gpu.zeros(64)
+    big = gpu.zeros(E * H * 4)
+    kr = Kernel(gpu, "router_topk", [])
+    b = Batch(gpu)
+    b.begin()
+    b.dispatch(kr, [small, big, big, big, big, big, big, big, big, big],
+               _push("PushRouterTopk", E=E, H=H, k=k, renorm=1, arena_mode=0, layer=0, eps=1e-6,
+                     flags=0), (1, 1, 1))
+    with pytest.raises(L.StyxError) as ei:
+        b.submit()
+    assert ei.value.status == -1
+    b.free()
+    kr.free()
