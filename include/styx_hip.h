@@ -323,7 +323,8 @@ int styx_op_argmax(styx_gpu *gpu, const float *v, int n, uint32_t *out, float *s
  * achievable HBM streaming-read bandwidth of the device. */
 int styx_op_read_probe(styx_gpu *gpu, const void *p, int64_t bytes, uint32_t *out, int grid);
 /* Seeded synthetic data: N(0, sigma) values quantized to GGUF blocks of
- * `type` (n values), or f32 N(mean, sigma). */
+ * `type` (n values; STYX_F16: each value rounded to f16), or f32
+ * N(mean, sigma). */
 int styx_op_gen_quant(styx_gpu *gpu, int type, uint64_t seed, float sigma, void *dst, int64_t n);
 int styx_op_gen_f32(styx_gpu *gpu, uint64_t seed, float mean, float sigma, float *dst, int64_t n);
 

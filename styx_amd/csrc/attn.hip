@@ -38,6 +38,7 @@ constexpr int TILE = 16;
 // the live context length inside one captured graph.
 __device__ __forceinline__ int attn_chunk(const AttnArgs &a, int n_t)
 {
+    if (n_t <= a.solo_max) return max(a.chunk, (n_t + 15) / 16 * 16);  // one chunk
     const int need = (n_t + a.max_chunks - 1) / a.max_chunks;
     return max(a.chunk, (need + 15) / 16 * 16);
 }
@@ -51,16 +52,9 @@ __device__ __forceinline__ int64_t kv_row(const AttnArgs &a, int64_t pg, int tp,
     return a.kv_head_major ? ((pg * a.nkv + kvh) * a.page_tokens + tp) * (int64_t)a.hd
                            : (pg * a.page_tokens + tp) * (int64_t)kv_dim + (int64_t)kvh * a.hd;
 }
-// Page-table entry i; with a.pool_pages set, entries past the pool are
-// clamped to its last page (a caller's table is not trusted to stay inside).
-__device__ __forceinline__ int32_t pt_at(const AttnArgs &a, int i)
-{
-    const int32_t p = a.page_table[i];
-    return a.pool_pages > 0 ? (int32_t)min((uint32_t)p, (uint32_t)(a.pool_pages - 1)) : p;
-}
 __device__ __forceinline__ int64_t kv_off(const AttnArgs &a, int t, int kvh, int kv_dim)
 {
-    return kv_row(a, pt_at(a, t / a.page_tokens), t % a.page_tokens, kvh, kv_dim);
+    return kv_row(a, a.page_table[t / a.page_tokens], t % a.page_tokens, kvh, kv_dim);
 }
 
 // One head's RMSNorm(hd) * w and NEOX rope at pos, split into a load phase
@@ -345,6 +339,21 @@ __device__ void attn_combine_tail(const AttnArgs &a, int c, int kvh, int n_activ
     }
 }
 
+// A context of one chunk per kv head (n_active == 1): the workgroup's merged
+// (m, l, o) already is the output, O / L (the in-kernel merge of a single
+// chunk computes the same quotient: its factor is exactly 1), so it is
+// written directly with no exchange.  xo holds the kv head's gqa * HD output
+// values in LDS; this builds their limbs (the o-proj input).
+template <int HD>
+__device__ __forceinline__ void attn_solo_limbs(const AttnArgs &a, int kvh, int gqa, const float *xo)
+{
+    __shared__ float red[16];
+    if (!a.xq.A) return;
+    __syncthreads();
+    xq_build<AT_WG>(xo, nullptr, 0.0f, false, gqa * HD, xq_shift(a.xq, kvh * gqa * HD), red,
+                    nullptr);
+}
+
 // Wave roles: the four waves of a workgroup split the gqa query heads into
 // NHG head groups of HPW heads (HPW <= MAXH) and, when fewer than four
 // groups exist, also split the chunk's 16-token tiles NTS = 4 / NHG ways.
@@ -383,7 +392,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     for (int e = 0; e < EPL; e++) vn[e] = a.v[(int64_t)kvh * HD + lane * EPL + e];
     const int t_min = c * a.chunk + ts * TILE + tl, pg_min = t_min / a.page_tokens;
     const bool spec = pg_min < a.page_table_len;
-    const int32_t pe_min = spec ? pt_at(a, pg_min) : 0;
+    const int32_t pe_min = spec ? a.page_table[pg_min] : 0;
     const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
     const int t0 = c * chunk;
     if (t0 >= n_t) return;
@@ -558,6 +567,27 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     const int64_t part0 = ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
     const uint32_t tag = a.t_part ? attn_tag(a, ticket) : 0u;
     const int n_active = (n_t + chunk - 1) / chunk;
+    const bool solo = a.t_part && n_active == 1;
+    if (nts == 1 && solo) {
+        // every wave owns distinct heads: its running state is the output
+        float *xo = sm + AT_WAVES * PWF;  // [gqa][HD] (the merge area, unused here)
+#pragma unroll
+        for (int g = 0; g < MAXH; g++) {
+            if (g >= hpw) break;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) {
+                const int i = (g0 + g) * HD + lane * EPL + e;
+                const float v = o[g][e] / l_run[g];
+                gst(a.out + (int64_t)kvh * gqa * HD + i, v);
+                xo[i] = v;
+            }
+        }
+        st.at(3);
+        attn_solo_limbs<HD>(a, kvh, gqa, xo);
+        st.at(5);
+        st.flush(a, c, kvh, n_active);
+        return;
+    }
     if (nts == 1) {
         // every wave owns distinct heads: its running state is the partial
 #pragma unroll
@@ -605,6 +635,12 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
             O += mo[wi * HD + e] * f;
             L += ml[wi] * f;
         }
+        if (solo) {
+            const float v = O / L;
+            gst(a.out + (int64_t)kvh * gqa * HD + idx, v);
+            sm[idx] = v;  // the per-wave areas are free after the barrier
+            continue;
+        }
         part_put(a, part0 + gg * ps + e, tag, O);
         if (e == 0) {
             part_put(a, part0 + gg * ps + HD, tag, M);
@@ -612,7 +648,10 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
         }
     }
     st.at(3);
-    if (a.t_part) attn_combine_tail<EPL>(a, c, kvh, n_active, tag, sm, st);
+    if (solo)
+        attn_solo_limbs<HD>(a, kvh, gqa, sm);
+    else if (a.t_part)
+        attn_combine_tail<EPL>(a, c, kvh, n_active, tag, sm, st);
     st.at(5);
     st.flush(a, c, kvh, n_active);
 }
@@ -681,14 +720,14 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     }
     const int t_min = c * a.chunk + wave * 16 + lr, pg_min = t_min / a.page_tokens;
     const bool spec = pg_min < a.page_table_len;
-    const int32_t pe_min = spec ? pt_at(a, pg_min) : 0;
+    const int32_t pe_min = spec ? a.page_table[pg_min] : 0;
     // the whole page table in LDS when it is short: past the minimum chunk
     // size (long contexts) the first tile's page entry then needs no memory
     // trip after the position, nor does any later tile's
     __shared__ int32_t s_pt[ATTN_PT_LDS];
     const bool pt_lds = a.page_table_len > 0 && a.page_table_len <= ATTN_PT_LDS;
     if (pt_lds)
-        for (int i = threadIdx.x; i < a.page_table_len; i += AT_WG) s_pt[i] = pt_at(a, i);
+        for (int i = threadIdx.x; i < a.page_table_len; i += AT_WG) s_pt[i] = a.page_table[i];
 
     const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
     const int t0 = c * chunk;
@@ -881,11 +920,19 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     __syncthreads();
     const int ps = MHD + 2;
     const int64_t part0 = ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
+    const int n_active = (n_t + chunk - 1) / chunk;
+    const bool solo = a.t_part && n_active == 1;
     for (int idx = threadIdx.x; idx < gqa * MHD; idx += AT_WG) {
         const int h = idx / MHD, e = idx - h * MHD;
         float O = 0.0f;
 #pragma unroll
         for (int w = 0; w < AT_WAVES; w++) O += mo[(w * MH + h) * MHD + e] * mf[w * MH + h];
+        if (solo) {
+            const float v = O / mL[h];
+            gst(a.out + (int64_t)kvh * gqa * MHD + idx, v);
+            qs[idx] = v;  // q is no longer read
+            continue;
+        }
         part_put(a, part0 + h * ps + e, tag, O);
         if (e == 0) {
             part_put(a, part0 + h * ps + MHD, tag, mM[h]);
@@ -893,8 +940,10 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
         }
     }
     st.at(3);
-    const int n_active = (n_t + chunk - 1) / chunk;
-    if (a.t_part) attn_combine_tail<MHD / 64>(a, c, kvh, n_active, tag, sm, st);
+    if (solo)
+        attn_solo_limbs<MHD>(a, kvh, gqa, qs);
+    else if (a.t_part)
+        attn_combine_tail<MHD / 64>(a, c, kvh, n_active, tag, sm, st);
     st.at(5);
     st.flush(a, c, kvh, n_active);
 }
@@ -925,7 +974,8 @@ __global__ void __launch_bounds__(CB_WG) k_attn_combine(AttnArgs a)
     const int *posp = a.pos;
     int n_active = -1;
     float m = -INFINITY, l = 0.0f, o = 0.0f;
-    for (int c0 = half; c0 < a.max_chunks; c0 += CB_HALVES * CB_BATCH) {
+    // the batches past the first stop at the live context (known from then on)
+    for (int c0 = half; c0 < (n_active < 0 ? a.max_chunks : n_active); c0 += CB_HALVES * CB_BATCH) {
         float mc[CB_BATCH], lc[CB_BATCH], oc[CB_BATCH];
 #pragma unroll
         for (int b = 0; b < CB_BATCH; b++) {

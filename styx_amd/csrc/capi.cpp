@@ -59,6 +59,7 @@ static void gpu_destroy(styx_gpu *g)
     if (g->xq_scratch) hipFree(g->xq_scratch);
     if (g->partial_scratch) hipFree(g->partial_scratch);
     if (g->fused_scalars) hipFree(g->fused_scalars);
+    if (g->fused_pt) hipFree(g->fused_pt);
     delete g;
 }
 
@@ -108,10 +109,12 @@ int styx_gpu_new(int device, styx_gpu **out)
     if (e == hipSuccess) e = hipMalloc(&g->partial_scratch, g->partial_bytes);
     if (e == hipSuccess) e = hipMalloc(&g->fused_scalars, 256);
     if (e == hipSuccess) e = hipMemset(g->fused_scalars, 0, 256);
+    if (e == hipSuccess) e = hipMalloc(&g->fused_pt, sizeof(uint32_t) * styx_gpu::FUSED_PT_MAX);
     if (e != hipSuccess) {
         if (g->xq_scratch) hipFree(g->xq_scratch);
         if (g->partial_scratch) hipFree(g->partial_scratch);
         if (g->fused_scalars) hipFree(g->fused_scalars);
+        if (g->fused_pt) hipFree(g->fused_pt);
         hipStreamDestroy(g->stream);
         delete g;
         return hip_fail(e, "hipMalloc(op scratch)");
@@ -427,8 +430,10 @@ int styx_op_attn_decode_noalloc(styx_gpu *g, const float *q, const float *k, con
                         " floats (nh, nkv, hd, max_chunks) exceed the static scratch of " +
                         std::to_string((long long)STYX_NOALLOC_ATTN_PART_FLOATS) +
                         " floats; lower max_chunks or use styx_op_attn_decode");
-    // every chunk the combine reads is written by the same launch first, so
-    // the shared array needs no clearing between calls
+    // the shared array needs no clearing between calls: the combine masks
+    // every chunk past the context (its first batch of loads may read such
+    // stale words before the position is known, and discards them), and
+    // every chunk inside the context is written by the same launch first
     return styx_op_attn_decode(g, q, k, v, q_norm, k_norm, eps, rope, kpool, vpool, page_table,
                                page_tokens, pos, out, g->noalloc_part, nh, nkv, hd, chunk,
                                max_chunks, scale);

@@ -141,16 +141,21 @@ hipError_t attn_paged(styx_gpu *g, hipStream_t st, void *const *ptr, const uint6
         return bad;
     AttnArgs a{};
     const uint64_t pool = std::min(size[6], size[7]);
+    hipError_t e = hipSuccess;
     if (p.flags & 4) {
-        // whole pages of page_tokens rows; the table covers the context
-        const uint64_t pt = p.page_tokens;
-        if (pt < 1 || !fits(size[8], pos / pt + 1, 4)) return bad;
+        // whole pages of page_tokens rows; the table covers the context and
+        // is read through a copy whose entries are clamped to the pool
+        const uint64_t pt = p.page_tokens, need = pos / pt + 1;
+        if (pt < 1 || !fits(size[8], need, 4) || need > (uint64_t)styx_gpu::FUSED_PT_MAX)
+            return bad;
         const uint64_t pages = pool / (pt * row);
         if (pages < 1 || pages > 0x7FFFFFFF) return bad;
-        a.page_table = (const int32_t *)ptr[8];
+        e = launch_clamp_copy_u32(st, (const uint32_t *)ptr[8], g->fused_pt, (uint32_t)(pages - 1),
+                                  (int64_t)need);
+        if (e != hipSuccess) return e;
+        a.page_table = (const int32_t *)g->fused_pt;
         a.page_tokens = (int)pt;
-        a.page_table_len = (int)std::min<uint64_t>(size[8] / 4, 0x7FFFFFFF);
-        a.pool_pages = (int)pages;
+        a.page_table_len = (int)need;
     } else {
         // the reference's contiguous caches: one page of the whole capacity
         const uint64_t cap = pool / row;
@@ -158,10 +163,9 @@ hipError_t attn_paged(styx_gpu *g, hipStream_t st, void *const *ptr, const uint6
         a.page_table = g->fused_scalars + 1;  // a single entry 0
         a.page_tokens = (int)cap;
         a.page_table_len = 1;
-        a.pool_pages = 1;
     }
     // the position: written to the gpu's scalar in stream order
-    hipError_t e = launch_fill_u32(st, (uint32_t *)g->fused_scalars, (uint32_t)pos, 1);
+    e = launch_fill_u32(st, (uint32_t *)g->fused_scalars, (uint32_t)pos, 1);
     if (e != hipSuccess) return e;
     a.q = (const float *)ptr[0];
     a.k = (const float *)ptr[1];

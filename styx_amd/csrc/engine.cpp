@@ -139,6 +139,13 @@ struct styx_moe {
     int32_t *d_pt = nullptr;
     std::vector<int32_t> h_pt;
     int pages_per_layer = 0, next_page = 0, chunk = 64, max_chunks = 1;
+    // contexts of up to this many tokens run as one chunk per kv head (the
+    // chunk's workgroup then writes the output itself, no exchange between
+    // chunks, as every context of one chunk does).  Off: measured on
+    // configs[1] at 57 tokens, one workgroup walking its 4 tiles one after
+    // another (about 2 us each, latency-bound) took 13.3 us against 9.2 us
+    // for 16-token chunks merged in-kernel.
+    int attn_solo_max = 0;
     double *rope = nullptr;  // [n_ctx][hd/2] (cos, sin)
     // fused MoE block (moe_block.hip): tagged exchange buffers, ticket,
     // abort flag; mb_nwg = its grid (0: the separate kernels run), -1 until
@@ -695,6 +702,7 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
         aa.hd = hd;
         aa.chunk = chunk;
         aa.max_chunks = max_chunks;
+        aa.solo_max = attn_solo_max;
         aa.scale = 1.0f / std::sqrt((float)hd);
         if (merge_in_kernel) {
             aa.t_part = at_part;
@@ -1070,6 +1078,9 @@ struct Builder {
             STYX_HIP(hipMemcpyAsync(tmp, src.values->data(), bytes, hipMemcpyHostToDevice, st));
         } else if (type == T_F32) {
             CK(launch_gen_f32(st, src.seed, src.mean, src.sigma, (float *)tmp, n));
+        } else if (type == T_F16) {
+            // f16 values of the same seeded N(0, sigma) draws
+            CK(launch_gen_quant(st, T_F16, src.seed, src.sigma, tmp, n));
         } else {
             CK(launch_gen_quant(st, type, src.seed, src.sigma, tmp, n));
         }
@@ -1089,9 +1100,10 @@ struct Builder {
 
     // 2-D matrix or 3-D expert tensor into split layout; host_copy: keep the
     // split bytes in pinned host memory instead of HBM.
-    int mat(const TensorSpec &t, const Source &src, Mat &o, bool host_copy)
+    int mat(const TensorSpec &t, const Source &src, Mat &o, bool host_copy, bool allow_float = false)
     {
-        if (!is_quant(t.type)) return fail(STYX_E_FORMAT, t.name + ": matrix type must be q8_0/q4_K/q5_K/q6_K");
+        if (!is_quant(t.type) && !(allow_float && (t.type == T_F32 || t.type == T_F16)))
+            return fail(STYX_E_FORMAT, t.name + ": matrix type must be q8_0/q4_K/q5_K/q6_K");
         if (t.dims.size() < 2) return fail(STYX_E_FORMAT, t.name + ": not a matrix");
         o.name = t.name;
         o.type = t.type;
@@ -1179,9 +1191,11 @@ int check_specs(const styx_moe_synth_cfg &c, std::vector<TensorSpec> &specs)
     const int64_t H = c.n_embd, qd = (int64_t)c.n_heads * c.head_dim,
                   kvd = (int64_t)c.n_kv_heads * c.head_dim, E = c.n_expert, F = c.n_ff_exp,
                   Fs = c.n_ff_shexp, V = c.n_vocab, hd = c.head_dim;
-    struct Want { std::vector<int64_t> dims; bool quant; bool required; };
+    struct Want { std::vector<int64_t> dims; bool quant; bool required; bool flt = false; };
     std::map<std::string, Want> want;
-    want["token_embd.weight"] = {{H, V}, true, true};
+    // the embedding table: a quant type, or f32/f16, as MoeModel::load admits
+    // (moe.rs:1107-1112, f32/f16/q8_0/q4_K; q5_K/q6_K decode here as well)
+    want["token_embd.weight"] = {{H, V}, true, true, true};
     want["output.weight"] = {{H, V}, true, true};
     want["output_norm.weight"] = {{H}, false, true};
     for (int l = 0; l < c.n_layers; l++) {
@@ -1211,9 +1225,12 @@ int check_specs(const styx_moe_synth_cfg &c, std::vector<TensorSpec> &specs)
         used.push_back(t);
         if (seen[t.name]++) return fail(STYX_E_FORMAT, t.name + ": tensor listed twice");
         const Want &w = it->second;
-        if (w.quant ? !is_quant(t.type) : t.type != T_F32)
-            return fail(STYX_E_FORMAT, t.name + (w.quant ? ": matrix type must be q8_0/q4_K/q5_K/q6_K"
-                                                         : ": expected f32"));
+        if (w.quant ? !(is_quant(t.type) || (w.flt && (t.type == T_F32 || t.type == T_F16)))
+                    : t.type != T_F32)
+            return fail(STYX_E_FORMAT,
+                        t.name + (w.quant ? (w.flt ? ": type must be f32/f16/q8_0/q4_K/q5_K/q6_K"
+                                                   : ": matrix type must be q8_0/q4_K/q5_K/q6_K")
+                                          : ": expected f32"));
         if (t.dims != w.dims) {
             std::string d, e;
             for (auto v : t.dims) d += (d.empty() ? "" : ",") + std::to_string(v);
@@ -1306,7 +1323,7 @@ int build_model(styx_moe *m, const styx_moe_synth_cfg &c, std::vector<TensorSpec
             else if (r == "ffn_down_shexp") rc = b.mat(t, src, ly.dsh, false);
             if (rc) return rc;
         } else if (n == "token_embd.weight") {
-            if (int r = b.mat(t, src, m->embd, false)) return r;
+            if (int r = b.mat(t, src, m->embd, false, true)) return r;
         } else if (n == "output.weight") {
             if (int r = b.mat(t, src, m->head, false)) return r;
         } else if (n == "output_norm.weight") {
@@ -1785,21 +1802,40 @@ int styx_moe_decode(styx_moe *m, int n_steps, uint32_t *out)
     if (!m->opts.no_fuse)
         STYX_HIP(hipMemcpyAsync(m->tok_save, m->d_tok, 4, hipMemcpyDeviceToDevice, m->gpu->stream));
     const bool host_work = (m->opts.repin_interval > 0 && m->any_host) || m->opts.time_kernels;
-    // repin hit counts as they stand, for a run again after a fused launch
-    // gives up (each step adds the previous token's experts)
-    std::vector<std::vector<uint64_t>> hits0;
-    if (!m->opts.no_fuse && m->opts.repin_interval > 0 && m->any_host)
-        for (auto &ly : m->layers) hits0.push_back(ly.hits);
+    // With host work between tokens every step is waited for anyway, so a
+    // fused launch that gives up is caught at its own step: the steps before
+    // it stand (with the repins and hit counts they made), and that step
+    // runs again on the separate kernels without repinning a second time --
+    // host state then matches a run that never fell back.
+    bool again = false;
     for (int i = 0; i < n_steps; i++) {
         if (host_work) {
             // host bookkeeping between tokens needs the previous token done
             // (as forward_token, the first step repins for the token before)
             STYX_HIP(hipStreamSynchronize(m->gpu->stream));
-            if (int r = m->maybe_repin()) return r;
+            if (!again)
+                if (int r = m->maybe_repin()) return r;
             if (int r = m->collect_stats()) return r;
         }
+        again = false;
         if (int r = m->run_token(true)) return r;
         m->n_past++;
+        if (host_work && !m->opts.no_fuse) {
+            m->queue_abort_read();
+            STYX_HIP(hipStreamSynchronize(m->gpu->stream));
+            if (m->check_abort()) {
+                if (int r = m->fall_back_unfused()) return r;
+                m->n_past--;
+                m->h_stage[1] = (uint32_t)m->n_past;
+                STYX_HIP(hipMemcpyAsync(m->d_pos, &m->h_stage[1], 4, hipMemcpyHostToDevice,
+                                        m->gpu->stream));
+                // the step's input token: the pending one, or the previous step's
+                STYX_HIP(hipMemcpyAsync(m->d_tok, i == 0 ? m->tok_save : m->hist + start + i, 4,
+                                        hipMemcpyDeviceToDevice, m->gpu->stream));
+                again = true;
+                i--;
+            }
+        }
     }
     STYX_HIP(hipMemcpyAsync(out, m->hist + start + 1, sizeof(uint32_t) * n_steps,
                             hipMemcpyDeviceToHost, m->gpu->stream));
@@ -1807,9 +1843,9 @@ int styx_moe_decode(styx_moe *m, int n_steps, uint32_t *out)
     STYX_HIP(hipStreamSynchronize(m->gpu->stream));
     if (m->check_abort()) {
         // the steps again from the pending token, on the separate kernels
+        // (no host work ran between them, so no host state to restore)
         if (int r = m->fall_back_unfused()) return r;
         if (int r = m->collect_stats()) return r;
-        for (size_t l = 0; l < hits0.size(); l++) m->layers[l].hits = hits0[l];
         m->n_past = start;
         STYX_HIP(hipMemcpyAsync(m->d_tok, m->tok_save, 4, hipMemcpyDeviceToDevice, m->gpu->stream));
         return styx_moe_decode(m, n_steps, out);

@@ -204,8 +204,8 @@ struct AttnArgs {
     int page_tokens;
     int kv_head_major;
     int page_table_len;              // entries of page_table (0: not given)
-    int pool_pages;                  // pages in kpool / vpool: entries past them are
-                                     // clamped (0: entries trusted, no clamp)
+    int solo_max;                    // contexts of up to this many tokens are one chunk
+                                     // per kv head (no exchange between chunks); 0: off
     const int32_t *pos;              // device scalar
     float *out;                      // [nh*hd]
     Xq xq;                           // optional limbs of out (o-proj input)
@@ -289,6 +289,9 @@ hipError_t launch_gen_f32(hipStream_t st, uint64_t seed, float mean, float sigma
                           int64_t n);
 
 hipError_t launch_fill_u32(hipStream_t st, uint32_t *p, uint32_t v, int64_t n);
+// dst[i] = min(src[i], maxv) (unsigned) for i < n.
+hipError_t launch_clamp_copy_u32(hipStream_t st, const uint32_t *src, uint32_t *dst, uint32_t maxv,
+                                 int64_t n);
 
 // Streaming-read probe over bytes (multiple of 16); out gets 4*grid words.
 hipError_t launch_read_probe(hipStream_t st, const void *p, int64_t bytes, uint32_t *out,

@@ -369,6 +369,12 @@ __device__ __forceinline__ uint16_t to_f16(float f)
 
 __device__ void quant_block(int t, const float *x, uint8_t *o)
 {
+    if (t == T_F16) {  // one value, rounded to nearest even
+        const uint16_t h = to_f16(x[0]);
+        o[0] = h & 0xFF;
+        o[1] = h >> 8;
+        return;
+    }
     if (t == T_Q8_0) {
         float am = 0.0f;
         for (int i = 0; i < 32; i++) am = fmaxf(am, fabsf(x[i]));
@@ -485,7 +491,7 @@ __global__ void __launch_bounds__(64) k_gen_quant(int t, uint64_t seed, float si
 hipError_t launch_gen_quant(hipStream_t st, int t, uint64_t seed, float sigma, uint8_t *dst,
                             int64_t n)
 {
-    if (!is_quant(t) || n % blk_elems(t)) return hipErrorInvalidValue;
+    if ((!is_quant(t) && t != T_F16) || n % blk_elems(t)) return hipErrorInvalidValue;
     const int64_t nb = n / blk_elems(t);
     const int64_t nwg = std::min<int64_t>((nb + 63) / 64, 16384);
     hipLaunchKernelGGL(k_gen_quant, dim3((unsigned)std::max<int64_t>(nwg, 1)), dim3(64), 0, st, t,
@@ -514,6 +520,13 @@ __global__ void k_fill_u32(uint32_t *p, uint32_t v, int64_t n)
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
         p[i] = v;
+}
+
+__global__ void k_clamp_copy_u32(const uint32_t *src, uint32_t *dst, uint32_t maxv, int64_t n)
+{
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = min(src[i], maxv);
 }
 
 // Streaming-read probe: every 16-byte word of [p, p + n16*16) is loaded
@@ -560,6 +573,15 @@ hipError_t launch_fill_u32(hipStream_t st, uint32_t *p, uint32_t v, int64_t n)
     const int64_t nwg = std::min<int64_t>((n + 255) / 256, 4096);
     hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::max<int64_t>(nwg, 1)), dim3(256), 0, st, p, v,
                        n);
+    return hipGetLastError();
+}
+
+hipError_t launch_clamp_copy_u32(hipStream_t st, const uint32_t *src, uint32_t *dst, uint32_t maxv,
+                                 int64_t n)
+{
+    const int64_t nwg = std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_clamp_copy_u32, dim3((unsigned)std::max<int64_t>(nwg, 1)), dim3(256), 0, st,
+                       src, dst, maxv, n);
     return hipGetLastError();
 }
 

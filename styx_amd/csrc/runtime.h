@@ -31,6 +31,11 @@ struct styx_gpu {
     // attn_decode_paged dispatch (written in stream order by a fill kernel),
     // [1] = 0, the one-entry page table of a contiguous KV cache.
     int32_t *fused_scalars = nullptr;
+    // attn_decode_paged's copy of a caller's page table, its entries clamped
+    // to the pool (FUSED_PT_MAX entries): the kernel then reads nothing
+    // outside the pools whatever the table holds.
+    static constexpr int FUSED_PT_MAX = 65536;
+    uint32_t *fused_pt = nullptr;
 };
 
 struct styx_buf {

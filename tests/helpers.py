@@ -56,3 +56,27 @@ def export_all(m) -> dict:
 
 def oracle_from_model(m, n_ctx: int) -> O.OracleModel:
     return O.OracleModel(model_hparams(m), export_all(m), n_ctx)
+
+
+class Tally:
+    """Routed-id checks done and skipped as near-ties (k-th vs k+1-th logit
+    within 1e-4 in the oracle): ids are compared bit for bit wherever the
+    oracle's routing margin leaves no doubt, and the skips are counted so
+    that a test can bound them."""
+
+    def __init__(self):
+        self.checked = self.skipped = 0
+
+    def ids(self, gpu_ids, oracle_ids, margins, where):
+        for l in range(gpu_ids.shape[0]):
+            if margins[l] > 1e-4:
+                assert np.array_equal(gpu_ids[l], oracle_ids[l].astype(np.uint32)), (where, l)
+                self.checked += 1
+            else:
+                self.skipped += 1
+
+    def bound(self, frac: float = 0.1):
+        """At most frac of the (layer, step) pairs skipped, and at least one
+        skip allowed however few pairs there are."""
+        n = self.checked + self.skipped
+        assert self.skipped <= max(1, int(frac * n)), (self.checked, self.skipped)

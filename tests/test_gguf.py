@@ -163,7 +163,7 @@ def tiny_qwen3moe(overrides=None, drop=()):
         if name in drop:
             continue
         n = int(np.prod(dims))
-        nbytes = n * 4 if typ == 0 else n // 32 * 34
+        nbytes = n * 4 if typ == 0 else n * 2 if typ == 1 else n // 32 * 34
         tens.append((name, typ, dims, np.zeros(nbytes, np.uint8)))
     return hp, tens
 
@@ -207,6 +207,23 @@ def test_model_file_shape_mismatch_rejected(tmp_path, name, typ, dims, needle):
     with pytest.raises(ValueError) as e:
         check_file(write_model(tmp_path, "bad", hp, tens))
     assert needle in str(e.value) and name in str(e.value)
+
+
+@pytest.mark.parametrize("typ", [0, 1])
+def test_float_token_embd_accepted(tmp_path, typ):
+    """MoeModel::load admits f32 and f16 embedding tables (moe.rs:1107-1112)
+    as well as the quant types."""
+    hp, tens = tiny_qwen3moe({"token_embd.weight": (typ, [256, 64])})
+    got = check_file(write_model(tmp_path, f"embd{typ}", hp, tens))
+    assert got.n_vocab == 64
+
+
+def test_float_type_refused_for_other_matrices(tmp_path):
+    """f32/f16 are for the embedding table only: an f16 attention matrix is
+    refused before anything is uploaded, with the type named."""
+    hp, tens = tiny_qwen3moe({"blk.0.attn_q.weight": (1, [256, 256])})
+    with pytest.raises(ValueError, match="attn_q.weight: matrix type must be q8_0/q4_K/q5_K/q6_K"):
+        check_file(write_model(tmp_path, "f16q", hp, tens))
 
 
 def test_model_file_missing_tensor_rejected(tmp_path):

@@ -16,7 +16,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from helpers import oracle_from_model, rel_l2
+from helpers import Tally, oracle_from_model, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -32,7 +32,10 @@ def gpu():
 
 
 def check_forward(m, orc, toks, pos0=0):
-    """Per-token logits and per-layer residuals within 1e-4 relative L2."""
+    """Per-token logits and per-layer residuals within 1e-4 relative L2;
+    routed ids bit-exact where the oracle's routing margin exceeds 1e-4,
+    the near-tie skips counted and bounded (Tally)."""
+    tally = Tally()
     for i, t in enumerate(toks):
         lg = m.forward_token(t)
         hid = m.last_hidden()
@@ -40,10 +43,9 @@ def check_forward(m, orc, toks, pos0=0):
         assert rel_l2(lg, ol) < 1e-4, i
         for l in range(hid.shape[0]):
             assert rel_l2(hid[l], oh[l]) < 1e-4, (i, l)
-        ids = m.last_expert_ids()
-        for l in range(ids.shape[0]):
-            if margins[l] > 1e-4:
-                assert np.array_equal(ids[l], oids[l].astype(np.uint32)), (i, l)
+        tally.ids(m.last_expert_ids(), oids, margins, i)
+    tally.bound()
+    return tally
 
 
 @pytest.mark.parametrize("ff_shexp", [512, 256])

@@ -24,7 +24,7 @@ from dataclasses import replace
 import numpy as np
 import pytest
 
-from helpers import oracle_from_model, rel_l2
+from helpers import Tally, oracle_from_model, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -37,22 +37,6 @@ def gpu():
     g = Gpu(0)
     yield g
     g.close()
-
-
-class Tally:
-    """Routed-id checks done and skipped as near-ties (k-th vs k+1-th logit
-    within 1e-4 in the oracle)."""
-
-    def __init__(self):
-        self.checked = self.skipped = 0
-
-    def ids(self, gpu_ids, oracle_ids, margins, where):
-        for l in range(gpu_ids.shape[0]):
-            if margins[l] > 1e-4:
-                assert np.array_equal(gpu_ids[l], oracle_ids[l].astype(np.uint32)), (where, l)
-                self.checked += 1
-            else:
-                self.skipped += 1
 
 
 @pytest.mark.timeout(900)
