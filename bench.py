@@ -25,14 +25,26 @@ pass of one token, device-side argmax, no host round trip per token).
 
 The JSON line carries:
   value      decode tok/s over the K timed steps
-  roofline   the dominant kernel (expert gate/up dequant-matvec, k_gate_up):
+  roofline   the dominant kernel, the fused MoE block k_moe_block (router,
+             top-k, expert gate/up/down dequant-matvec, combine; k_gate_up
+             when the block runs as separate kernels, --no-fuse):
              algorithmic bytes per launch / average launch time, measured
              with HIP events on the engine's stream around graph replays of
-             the k_gate_up launches of every layer (each reading its own
+             that kernel's launches for every layer (each reading its own
              slabs, as a token does), against 8 TB/s
   cpu_baseline  the C oracle (a restatement of the reference's CPU
              dequant-then-dot path, -O2 -ffp-contract=off) decoding the same
              model on the host's cores for a bounded sample
+  cpu_block  (configs 1 and 2) one MoE block of layer 0 on the oracle:
+             cpu_ref_1t (1 thread) and cpu_ref_mt (16 threads), us per block
+             and GB/s of its algorithmic bytes, beside the GPU block
+  baseline_rows  (config 1) each BASELINE.md section 2 row of config 1 --
+             the whole MoE block, gate+up+SiLU, down+reduce -- with its
+             algorithmic bytes, the measured kernel time, GB/s, fraction of
+             8 TB/s and the 70% target time; the fused block reports the
+             first row, --no-fuse the other two
+  unfused_fallbacks  times a fused launch gave up waiting and the model went
+             over to the separate kernels (0 in a clean run)
 """
 from __future__ import annotations
 
@@ -180,6 +192,64 @@ def cpu_baseline(m, prompt, seconds: float, threads: int) -> dict:
             "sample": f"{n} full forward passes (prompt then greedy) of the same model, "
                       f"{el:.1f}s, C oracle with {threads} OpenMP threads",
             "host": host_info(threads)}, gen
+
+
+def cpu_block_baseline(m, seconds: float) -> dict:
+    """One MoE block (ffn norm, router, top-k, k expert gate/up/SiLU/down,
+    weighted combine) of layer 0 on the oracle, single-threaded (cpu_ref_1t)
+    and with 16 threads (cpu_ref_mt): us per block over a bounded number of
+    repetitions (about `seconds` each), and GB/s of its algorithmic bytes
+    (router, the routed slabs, the vectors)."""
+    from oracle import oracle as O
+    sys.path.insert(0, str(ROOT / "tests"))
+    from helpers import oracle_from_model
+    orc = oracle_from_model(m, n_ctx=8)
+    hp = m.hp
+    rng = np.random.default_rng(0x1234)
+    x = rng.standard_normal(hp.n_embd).astype(np.float32)
+    _, _, _, ids, _ = orc.moe_block(0, x)
+    names = ("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps")
+    slab = sum(orc.t[f"blk.0.{n}.weight"][2].nbytes // hp.n_expert for n in names)
+    H, F, E, k = hp.n_embd, hp.n_ff_exp, hp.n_expert, hp.n_expert_used
+    nbytes = k * slab + E * H * 4 + 4 * (2 * H + 2 * k * F + 2 * H)
+    out = {"bytes_per_block": int(nbytes), "experts": ids.tolist()}
+    for label, thr in (("cpu_ref_1t", 1), ("cpu_ref_mt", 16)):
+        O.set_threads(thr)
+        orc.moe_block(0, x)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            orc.moe_block(0, x)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+        us = el / n * 1e6
+        out[label] = {"us_per_block": round(us, 1), "GB/s": round(nbytes / us / 1e3, 3),
+                      "threads": thr, "blocks": n}
+    out["host"] = host_info(16)
+    out["kind"] = "port: C++ restatement of the reference's CPU dequant+matvec path"
+    return out
+
+
+def baseline_rows(table: dict) -> dict:
+    """BASELINE.md section 2's config-1 rows: the kernel time measured here
+    beside the algorithmic bytes, the fraction of 8 TB/s and the 70% target."""
+    rows = {}
+
+    def row(label, stages):
+        got = [table[s] for s in stages if s in table]
+        if len(got) != len(stages):
+            return
+        by = sum(g["bytes_per_launch"] for g in got)
+        us = sum(g["avg_us"] for g in got)
+        rows[label] = {"kernels": list(stages), "bytes": by, "avg_us": round(us, 3),
+                       "GB/s": round(by / us / 1e3, 1), "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 4),
+                       "target_70pct_us": round(by / (0.7 * HBM_PEAK_GBS) / 1e3, 3)}
+    row("moe_block", ["moe_block"])
+    row("moe_block_separate", ["router", "moe_gate_up", "moe_down", "reduce"])
+    row("gate_up_silu", ["moe_gate_up"])
+    row("down_reduce", ["moe_down", "reduce"])
+    return rows
 
 
 def host_info(threads: int) -> dict:
@@ -512,6 +582,9 @@ def main() -> int:
     ap.add_argument("--timing-steps", type=int, default=16,
                     help="extra decode steps run with per-launch HIP event timing")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--cpu-block-seconds", type=float, default=3.0,
+                    help="configs 1-2: seconds of each single-block oracle timing (1 and 16 "
+                         "threads)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layers", type=int, default=None, help="(testing only) fewer layers")
     ap.add_argument("--contexts", default="512,4096,32768",
@@ -650,6 +723,18 @@ def main() -> int:
         extra["greedy_identical"] = bool(np.array_equal(np.asarray(gen[1:1 + n_cmp], np.uint32),
                                                         toks[:n_cmp]))
         log(f"greedy stream vs oracle: {n_cmp} tokens, identical={extra['greedy_identical']}")
+
+    if args.config in (1, 2) and not args.no_cpu_baseline:
+        extra["cpu_block"] = cpu_block_baseline(m, args.cpu_block_seconds)
+        stg = table.get("moe_block") or table.get("moe_gate_up")
+        if stg and args.config == 1:
+            extra["cpu_block"]["gpu_us_per_block"] = sum(
+                table[s]["avg_us"] for s in ("moe_block", "moe_gate_up", "moe_down", "reduce",
+                                             "router") if s in table)
+        log(f"cpu block: {extra['cpu_block']}")
+    if args.config == 1:
+        extra["baseline_rows"] = baseline_rows(table)
+    extra["unfused_fallbacks"] = m.unfused_fallbacks()
 
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "tok/s", "n_gpus": 1,

@@ -360,13 +360,13 @@ int styx_moe::setup_runtime()
     // tagged exchange of the fused MoE block: zero once (tag 0 is never a
     // launch's), never cleared again
     if (int r = dalloc(&t_lg, E)) return r;
-    if (int r = dalloc(&t_gu, (size_t)2 * (K + 1) * F)) return r;
+    if (int r = dalloc(&t_gu, (size_t)(K + 1) * F)) return r;
     if (int r = dalloc(&t_part, (size_t)(K + 1) * H)) return r;
     if (int r = dalloc(&mb_ticket, 64 * 16)) return r;
     if (int r = dalloc(&mb_abort, 1)) return r;
     if (int r = dalloc(&tok_save, 1)) return r;
     STYX_HIP(hipMemsetAsync(t_lg, 0, sizeof(uint64_t) * E, gpu->stream));
-    STYX_HIP(hipMemsetAsync(t_gu, 0, sizeof(uint64_t) * 2 * (K + 1) * F, gpu->stream));
+    STYX_HIP(hipMemsetAsync(t_gu, 0, sizeof(uint64_t) * (K + 1) * F, gpu->stream));
     STYX_HIP(hipMemsetAsync(t_part, 0, sizeof(uint64_t) * (K + 1) * H, gpu->stream));
     STYX_HIP(hipMemsetAsync(mb_ticket, 0, sizeof(unsigned long long) * 64 * 16, gpu->stream));
     STYX_HIP(hipMemsetAsync(mb_abort, 0, sizeof(int), gpu->stream));

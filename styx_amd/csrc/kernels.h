@@ -116,7 +116,8 @@ hipError_t launch_moe_down(hipStream_t st, int td, const ExpSrc &d, const int32_
 // the weighted combine into x and the next RMSNorm's limbs -- the results of
 // launch_router + launch_moe_gate_up + launch_moe_down + launch_reduce_rows,
 // bit for bit.  Workgroups exchange data through the tagged buffers t_lg
-// [E], t_gu [2][k+1][F], t_part [k+1][H] (64-bit words, zeroed once at
+// [E], t_gu [k+1][F] (each slot's swiglu of its gate and up rows), t_part
+// [k+1][H] (64-bit words, zeroed once at
 // allocation) and draw a ticket at entry from one of 64 counters (ticket
 // points at 64 x 16 zeroed u64; nwg a multiple of 64); a wait that exceeds
 // max_polls rounds sets *abort.  trace (optional): [nwg][8] wall-clock

@@ -8,9 +8,10 @@
 // top-k weights before the partials, and each phase's weights issued as
 // soon as its rows are known.
 //
-// Cross-workgroup data (router logits, gate/up outputs, per-slot down
-// partials) travels as tagged 64-bit words (xchg.h): no fence and no
-// counter is needed, and no buffer has to be cleared between launches.
+// Cross-workgroup data (router logits, each slot's SwiGLU of its gate and
+// up rows, per-slot down partials) travels as tagged 64-bit words (xchg.h):
+// no fence and no counter is needed, and no buffer has to be cleared between
+// launches.
 //
 // Every wait is bounded: after max_polls rounds, or once another workgroup
 // has given up, a workgroup sets *abort and exits.  The grid is sized to be
@@ -53,7 +54,7 @@ struct MoeBlockK {
     Xq xq;
     float *ss;
     float *wts_out;
-    uint64_t *t_lg, *t_gu, *t_part;  // tagged [E], [2][nslots][F], [nslots][H]
+    uint64_t *t_lg, *t_gu, *t_part;  // tagged [E], h [nslots][F], [nslots][H]
     unsigned long long *ticket;  // MB_TICKETS counters, 128 bytes apart
     int *abort;
     int max_polls;
@@ -92,19 +93,19 @@ __device__ __forceinline__ const uint8_t *routed_slab(const MoeBlockK &a, const 
     return slab_pick(src, r3[0], r3[1], r3[2]);
 }
 
-// Rows [r0, r1) of matrix m (0 gate, 1 up) of slot s against the limbs of
-// xn in LDS, published tagged; a missing slab publishes zeros.
+// Rows [r0, r1) of one expert matrix (gate or up) against the limbs of xn
+// in LDS, walked by the lane groups of waves [wave0, wave0 + 2); row r's
+// dot goes to dst[r - r0] (LDS).  A missing slab gives zeros.
 // `between` runs once the rows' first weights are issued (the caller
 // issues further loads there).
 template <int T, typename Between>
-__device__ __forceinline__ void gu_rows(const MoeBlockK &a, const uint8_t *slab, const Xq &xqx, int m,
-                               int s, int r0, int r1, uint32_t tag, Between between,
+__device__ __forceinline__ void gu_rows(const MoeBlockK &a, const uint8_t *slab, const Xq &xqx,
+                               int r0, int r1, int wave0, float *dst, Between between,
                                uint64_t *tr)
 {
-    uint64_t *y = a.t_gu + ((size_t)m * a.nslots + s) * a.F;
     if (!slab) {
         between();
-        for (int r = r0 + (int)threadIdx.x; r < r1; r += WG) tput(y + r, tag, 0.0f);
+        for (int r = r0 + (int)threadIdx.x - 64 * wave0; r < r1; r += 128) dst[r - r0] = 0.0f;
         return;
     }
     auto stamp = [&](int i) {
@@ -119,38 +120,52 @@ __device__ __forceinline__ void gu_rows(const MoeBlockK &a, const uint8_t *slab,
             stamp(12);
             return true;
         },
-        [&](int r, float v) { tput(y + r, tag, v); });
+        [&](int r, float v) { dst[r - r0] = v; }, 2, wave0);
     stamp(13);
 }
 
-// Gate/up block b: matrix m, slot s, rows [r0, r1).
+// Gate/up block b: rows [r0, r1) of slot s, of both matrices.
 struct GuPos {
-    int m, s, r0, r1;
+    int s, r0, r1;
 };
 __device__ __forceinline__ GuPos gu_pos(const MoeBlockK &a, int b)
 {
-    const int per_m = a.nslots * a.bps_gu;
-    const int m = b / per_m, rem = b - m * per_m, s = rem / a.bps_gu;
-    const int r0 = (rem - s * a.bps_gu) * a.rpw_gu;
-    return {m, s, r0, min(a.F, r0 + a.rpw_gu)};
+    const int s = b / a.bps_gu;
+    const int r0 = (b - s * a.bps_gu) * a.rpw_gu;
+    return {s, r0, min(a.F, r0 + a.rpw_gu)};
 }
 
+// Gate/up block bp: waves 0-1 walk its gate rows and waves 2-3 the same up
+// rows, side by side (each matrix at its own type); then the block's
+// h = swiglu_f32(g, u) (ops2.rs:305-309) is published, one tagged word per
+// row, so a down workgroup waits for F words of its slot instead of 2F and
+// every gate/up workgroup carries the same mix of the two matrices' bytes.
+// gl holds 2 * rpw_gu floats of LDS.
 template <typename Between>
 __device__ __forceinline__ void gu_block(const MoeBlockK &a, const GuPos &bp, bool routed_phase,
                                 const int32_t *s_ids, const Xq &xqx, uint32_t tag,
-                                Between between, uint64_t *tr)
+                                float *gl, Between between, uint64_t *tr)
 {
-    const int m = bp.m, s = bp.s, r0 = bp.r0, r1 = bp.r1;
+    const int s = bp.s, r0 = bp.r0, r1 = bp.r1;
     if ((s < a.k) != routed_phase) return;
+    const int m = (int)(threadIdx.x >> 7);  // 0: gate (waves 0, 1), 1: up (waves 2, 3)
     if (routed_phase && tr && threadIdx.x == 0) tr[14] = wall_clock64();
     const uint8_t *slab = s < a.k ? routed_slab(a, a.src[m], s_ids[s], s) : a.sh[m];
     if (routed_phase && tr && threadIdx.x == 0) tr[15] = wall_clock64();
+    float *dst = gl + m * a.rpw_gu;
     switch (m == 0 ? a.tg : a.tu) {
-    case T_Q8_0: gu_rows<T_Q8_0>(a, slab, xqx, m, s, r0, r1, tag, between, tr); break;
-    case T_Q4_K: gu_rows<T_Q4_K>(a, slab, xqx, m, s, r0, r1, tag, between, tr); break;
-    case T_Q5_K: gu_rows<T_Q5_K>(a, slab, xqx, m, s, r0, r1, tag, between, tr); break;
-    default: gu_rows<T_Q6_K>(a, slab, xqx, m, s, r0, r1, tag, between, tr); break;
+    case T_Q8_0: gu_rows<T_Q8_0>(a, slab, xqx, r0, r1, 2 * m, dst, between, tr); break;
+    case T_Q4_K: gu_rows<T_Q4_K>(a, slab, xqx, r0, r1, 2 * m, dst, between, tr); break;
+    case T_Q5_K: gu_rows<T_Q5_K>(a, slab, xqx, r0, r1, 2 * m, dst, between, tr); break;
+    default: gu_rows<T_Q6_K>(a, slab, xqx, r0, r1, 2 * m, dst, between, tr); break;
     }
+    __syncthreads();
+    uint64_t *y = a.t_gu + (size_t)s * a.F;
+    for (int r = r0 + (int)threadIdx.x; r < r1; r += WG) {
+        const float g = gl[r - r0];
+        tput(y + r, tag, g / (1.0f + expf(-g)) * gl[a.rpw_gu + r - r0]);
+    }
+    __syncthreads();  // gl is rewritten by the next block
 }
 
 // The next layer's q/k/v rows [r0, r1) (of the three matrices stacked):
@@ -216,9 +231,9 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     float *xs = (float *)lds;                         // x, then xn = rmsnorm(x) * w
     const Xq xqx = xq_at(lds + a.off_xq, a.H);        // limbs of xn
     float *s_lg = (float *)(lds + a.off_lg);          // router logits
-    float *gus = (float *)(lds + a.off_gu);           // g[F] | u[F]; reduce: partials
-    float *hs = (float *)(lds + a.off_hs);            // swiglu(g, u)
-    const Xq xqh = xq_at(lds + a.off_xqh, a.F);       // limbs of hs
+    float *gus = (float *)(lds + a.off_gu);           // gate/up rows; then h[F]; reduce: partials
+    float *hs = (float *)(lds + a.off_hs);            // the reduce's rows of x (.) w_next
+    const Xq xqh = xq_at(lds + a.off_xqh, a.F);       // limbs of the slot's h
     __shared__ int32_t s_ids[IDS_ROW];
     __shared__ float red[16];
     __shared__ uint32_t s_tag;
@@ -349,7 +364,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         xq_build<WG>(xs, nullptr, 0.0f, false, a.H, xqx, red, nullptr);
         __syncthreads();
         stamp(2);
-        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), false, s_ids, xqx, tag, nothing, tr);
+        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), false, s_ids, xqx, tag, gus, nothing, tr);
     }
 
     // ---- routing: every workgroup ranks the logits (topk_softmax_f32 order)
@@ -366,30 +381,27 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
 
     // ---- routed gate/up rows
     if (has_x)
-        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), true, s_ids, xqx, tag, nothing, tr);
+        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), true, s_ids, xqx, tag, gus, nothing, tr);
     stamp(5);
 
-    // ---- down: swiglu_f32 (ops2.rs:305-309) of the slot's g and u and its
+    // ---- down: the slot's h (published by its gate/up workgroups) and its
     // limbs in LDS, then the rows whose weights are already in flight
     if (has_d) {
         const int F = a.F;
-        const uint64_t *g = a.t_gu + (size_t)ds * F, *u = a.t_gu + ((size_t)a.nslots + ds) * F;
+        const uint64_t *hw = a.t_gu + (size_t)ds * F;
         auto wait_gu = [&] {
-            const bool ok = tpoll<2 * MB_MAX_F / WG>(
-                2 * F, [&](int i) { return i < F ? g + i : u + (i - F); }, tag, gus, a);
+            const bool ok = tpoll<MB_MAX_F / WG>(F, [&](int i) { return hw + i; }, tag, gus, a);
             stamp(6);
             return ok;
         };
         // the down weights go out first (two batches of rows per lane
         // group: of two rows each with one unit per lane, of one row with
-        // more, as the registers allow), before the wait for the slot's g
-        // and u: they stream while the slowest gate/up rows are finished,
-        // and the SwiGLU limbs are built once g and u are in
+        // more, as the registers allow), before the wait for the slot's h:
+        // they stream while the slowest gate/up rows are finished, and the
+        // limbs of h are built once it is in
         uint64_t *part = a.t_part + (size_t)ds * a.H;
         auto build = [&] {
-            for (int i = tid; i < F; i += WG) hs[i] = gus[i] / (1.0f + expf(-gus[i])) * gus[F + i];
-            __syncthreads();
-            xq_build<WG>(hs, nullptr, 0.0f, false, F, xqh, red, nullptr);
+            xq_build<WG>(gus, nullptr, 0.0f, false, F, xqh, red, nullptr);
             __syncthreads();
             stamp(7);
         };
@@ -504,7 +516,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     }
     const float sq = block_sum<WG>(hr ? xv * xv : 0.0f, red);
     if (tid == 0) gst(a.ss + w, sq);
-    float *xw = hs;  // MB_RR floats; hs is free once the down rows are done
+    float *xw = hs;  // MB_RR floats
     __syncthreads();
     xw[tid] = xv * nw;
     __syncthreads();
@@ -572,13 +584,14 @@ static bool moe_geometry(const MoeBlockArgs &h, int nwg, MoeBlockK &a, size_t &l
     a.nslots = h.k + (h.sh[0] ? 1 : 0);
     a.nR = (h.E + MB_ROUTER_ROWS - 1) / MB_ROUTER_ROWS;
     a.nRed = (h.H + MB_RR - 1) / MB_RR;
-    // one gate/up block per workgroup: the walker keeps the next
-    // MB_GU_ROWS rows per lane group in flight while a batch is consumed
-    const int ngrp_gu = WAVES * (64 / gg.G), ngrp_d = WAVES * (64 / gd.G);
-    int rpw = (2 * a.nslots * h.F + nwg - 1) / nwg;
+    // one gate/up block per workgroup, its rows of both matrices (half the
+    // waves each): the walker keeps the next MB_GU_ROWS rows per lane group
+    // in flight while a batch is consumed
+    const int ngrp_gu = (WAVES / 2) * (64 / gg.G), ngrp_d = WAVES * (64 / gd.G);
+    int rpw = (a.nslots * h.F + nwg - 1) / nwg;
     a.rpw_gu = (rpw + ngrp_gu - 1) / ngrp_gu * ngrp_gu;
     a.bps_gu = (h.F + a.rpw_gu - 1) / a.rpw_gu;
-    a.n_gu = 2 * a.nslots * a.bps_gu;
+    a.n_gu = a.nslots * a.bps_gu;
     if (nwg % MB_TICKETS) return false;
     const int per_slot = nwg / a.nslots;
     if (per_slot < 1) return false;
@@ -614,8 +627,10 @@ static bool moe_geometry(const MoeBlockArgs &h, int nwg, MoeBlockK &a, size_t &l
     a.off_xq = align16((size_t)4 * h.H);
     a.off_lg = a.off_xq + align16(xq_bytes(h.H));
     a.off_gu = a.off_lg + align16((size_t)4 * h.E);
-    a.off_hs = a.off_gu + align16(std::max((size_t)8 * h.F, (size_t)4 * a.nslots * MB_RR));
-    a.off_xqh = a.off_hs + align16((size_t)4 * std::max(h.F, MB_RR));
+    // gate/up rows of a block (2 rpw) | h (F) | the reduce's partials
+    a.off_hs = a.off_gu + align16(std::max({(size_t)8 * a.rpw_gu, (size_t)4 * h.F,
+                                            (size_t)4 * a.nslots * MB_RR}));
+    a.off_xqh = a.off_hs + align16((size_t)4 * MB_RR);
     lds = (size_t)a.off_xqh + align16(xq_bytes(h.F));
     return true;
 }

@@ -33,11 +33,13 @@ struct LaneMap {
     bool ok;
 };
 
-__device__ __forceinline__ LaneMap lane_map(int G, int nwaves = WAVES)
+// Lane groups of G lanes over the waves [wave0, wave0 + nwaves) of the
+// workgroup (the calling wave must be one of them).
+__device__ __forceinline__ LaneMap lane_map(int G, int nwaves = WAVES, int wave0 = 0)
 {
     LaneMap m;
     m.lane = threadIdx.x & 63;
-    m.wave = threadIdx.x >> 6;
+    m.wave = (int)(threadIdx.x >> 6) - wave0;
     m.gpw = 64 / G;
     m.grp = m.lane / G;
     m.gl = m.lane - m.grp * G;
@@ -149,11 +151,14 @@ struct Mat3 {
 // exactly the other batch's loads may still be in flight and waits for
 // this batch's alone; with conditional issues it has to wait for all of
 // them, and the walk degrades to one round trip per batch.
+// The rows are spread over the lane groups of waves [wave0, wave0 + nwaves)
+// (all four by default); only those waves call the walker.
 template <int T, int UPL, int NR, typename RowAt, typename XLoad, typename Emit>
 __device__ __forceinline__ bool walk_rows_pipelined(RowAt at, int nb, int G, int r_begin,
-                                                    int r_end, XLoad xload, Emit emit)
+                                                    int r_end, XLoad xload, Emit emit,
+                                                    int nwaves = WAVES, int wave0 = 0)
 {
-    const LaneMap lm = lane_map(G);
+    const LaneMap lm = lane_map(G, nwaves, wave0);
     const LaneU<UPL> lu = lane_units<T, UPL>(lm, nb, G);
     const int step = NR * lm.ngrp;
     const int nbat = (r_end - r_begin + step - 1) / step;
