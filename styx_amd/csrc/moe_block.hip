@@ -82,6 +82,63 @@ __device__ __forceinline__ bool tpoll(int n, Addr addr, uint32_t tag, float *dst
     return tpoll_wg<MAXJ, WG>(n, addr, tag, dst, a.max_polls, a.abort);
 }
 
+// Routing for E <= 128 experts with a power-of-two quarter Q = E / 4:
+// wave w polls the tagged logits of its quarter [w Q, (w + 1) Q) and ranks
+// them among themselves as soon as they are in (rank_quarter, no workgroup
+// barrier between the poll and that stage), then the 4k candidates are
+// ranked (rank_candidates): the ids of rank_ids_lds with two workgroup
+// barriers instead of six.  The logits land in s_lg for the reduce's
+// weights.  Returns false when the wait was abandoned (*abort set).
+__device__ __forceinline__ bool route_by_quarters(const MoeBlockK &a, uint32_t tag, float *s_lg,
+                                                  int32_t *s_ids, bool publish, uint64_t *tr)
+{
+    __shared__ __align__(16) uint64_t q_key[128];
+    __shared__ __align__(16) uint64_t c_key[4 * MAX_TOPK];
+    __shared__ int q_fail[WAVES];
+    const int Q = a.E / 4, k = a.k;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, e = wave * Q + lane;
+    if (tid < IDS_ROW) s_ids[tid] = (int32_t)SKIP;  // read after the barrier below
+    bool pend = lane < Q;
+    int failed = 0;
+    for (int polls = 0; __any(pend); polls++) {
+        if (pend) {
+            const uint64_t v = tget(a.t_lg + e);
+            if (tvalid(v, tag)) {
+                const float f = tval(v);
+                s_lg[e] = f;
+                q_key[e] = rank_key(f, e);
+                pend = false;
+            }
+        }
+        if (!__any(pend)) break;
+        if (polls >= a.max_polls || ((polls & 31) == 31 && __any(abort_seen(a.abort)))) {
+            failed = 1;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (tr && tid == 0) tr[3] = wall_clock64();
+    // this wave's candidate slots (a quarter of fewer than k keys leaves
+    // some unwritten), then its ranking: all the wave's own LDS words
+    if (lane < k) c_key[wave * k + lane] = 0;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (!failed) rank_quarter(q_key + wave * Q, Q, k, c_key + wave * k);
+    if (lane == 0) q_fail[wave] = failed;
+    __syncthreads();
+    int any = 0;
+    for (int i = 0; i < WAVES; i++) any |= q_fail[i];
+    if (any) {
+        if (tid == 0) abort_raise(a.abort);
+        return false;
+    }
+    rank_candidates(c_key, k, s_ids);
+    __syncthreads();
+    if (publish) publish_id_row(a.route, s_ids);
+    return true;
+}
+
 // Slab of expert e routed to `slot` (null when e is not a valid expert,
 // which only non-finite logits can cause: the rows then publish zeros).
 __device__ __forceinline__ const uint8_t *routed_slab(const MoeBlockK &a, const ExpSrc &src, int e,
@@ -368,9 +425,14 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     }
 
     // ---- routing: every workgroup ranks the logits (topk_softmax_f32 order)
-    if (!tpoll<MAX_EXPERTS / WG>(a.E, [&](int i) { return a.t_lg + i; }, tag, s_lg, a)) return;
-    stamp(3);
-    rank_ids_lds(a.route, s_ids, s_lg, w == 0);
+    const int Qr = a.E / 4;
+    if (a.E <= 128 && (Qr & (Qr - 1)) == 0) {
+        if (!route_by_quarters(a, tag, s_lg, s_ids, w == 0, tr)) return;
+    } else {
+        if (!tpoll<MAX_EXPERTS / WG>(a.E, [&](int i) { return a.t_lg + i; }, tag, s_lg, a)) return;
+        stamp(3);
+        rank_ids_lds(a.route, s_ids, s_lg, w == 0);
+    }
     stamp(4);
 
     // ---- this workgroup's down rows (their weights are issued after the

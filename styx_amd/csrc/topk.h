@@ -143,6 +143,70 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
     return v;
 }
 
+// Stage 1 of the two-stage ranking for one wave: the Q keys of its quarter
+// (q[0..Q), in LDS, Q a power of two <= 32) ranked among themselves, P =
+// min(64 / Q, Q / 2) lanes per key; a key of quarter rank below k goes to
+// cand[rank] (cand: this wave's k candidate slots, zeroed by the caller).
+__device__ __forceinline__ void rank_quarter(const uint64_t *q, int Q, int k, uint64_t *cand)
+{
+    const int lane = threadIdx.x & 63;
+    const int P = min(64 / Q, Q / 2), span = Q / P;  // span >= 2, even
+    const int e = lane / P, part = lane - e * P;
+    int cnt = 0;
+    uint64_t mk = 0;
+    if (e < Q) {
+        mk = q[e];
+        const ulonglong2 *qq = (const ulonglong2 *)(q + part * span);
+        for (int j2 = 0; j2 < span / 2; j2++) {
+            const ulonglong2 u = qq[j2];
+            cnt += (int)(u.x > mk) + (int)(u.y > mk);
+        }
+    }
+    for (int sh = 1; sh < P; sh <<= 1) cnt += __shfl_xor(cnt, sh);
+    if (e < Q && part == 0 && cnt < k) cand[cnt] = mk;
+}
+
+// Stage 2: the 4k candidate slots (unused ones hold key 0) ranked among
+// themselves by the workgroup's first 4k threads; ranks below k give
+// s_ids.  A key of the global top k has fewer than k larger keys in its
+// quarter, so it is a candidate, and every key larger than it is a
+// candidate too: its rank among the candidates is its rank.
+__device__ __forceinline__ void rank_candidates(const uint64_t *c_key, int k, int32_t *s_ids)
+{
+    const int tid = threadIdx.x;
+    if (tid < 4 * k) {
+        const uint64_t ck = c_key[tid];
+        int c2 = 0;
+        const ulonglong2 *q = (const ulonglong2 *)c_key;
+        for (int j2 = 0; j2 < 2 * k; j2++) {
+            const ulonglong2 u = q[j2];
+            c2 += (int)(u.x > ck) + (int)(u.y > ck);
+        }
+        if (ck != 0 && c2 < k) s_ids[c2] = (int32_t)(0xFFFFFFFFu - (uint32_t)ck);
+    }
+}
+
+// The whole 64-int id row of the routed slots s_ids[0..k) to r.ids_out
+// (orig | hot | arena | host, topk_softmax_f32.comp:4-17) by threads < 64.
+__device__ __forceinline__ void publish_id_row(const Route &r, const int32_t *s_ids)
+{
+    const int tid = threadIdx.x;
+    if (!r.ids_out || tid >= IDS_ROW) return;
+    const int row = tid >> 4, slot = tid & 15;
+    int32_t v = (int32_t)SKIP;
+    if (slot < r.k) {
+        const int e = s_ids[slot];
+        if (row == 0) {
+            v = e;
+        } else {
+            uint32_t ids3[3];
+            route_row(r, e, slot, ids3);
+            v = (int32_t)ids3[row - 1];
+        }
+    }
+    *(int32_t STYX_GLOBAL *)(r.ids_out + tid) = v;
+}
+
 // Top-k ids of the router logits inside a workgroup, by ranking: the rank
 // of a key is the number of larger keys, and ranks 0..k-1 are exactly the
 // reference's selection order (keys of rank_key: larger value first, equal
@@ -172,39 +236,13 @@ __device__ inline const int32_t *rank_ids_lds(const Route &r, int32_t *s_ids, co
     if (tid < 4 * MAX_TOPK) c_key[tid] = 0;
     __syncthreads();  // also: the caller's logits are in s_lg
     if (E <= 128 && (Q & (Q - 1)) == 0) {
-        // two stages: every key ranked within its wave's quarter (P = 64 / Q
-        // lanes per key, at least two keys each), the quarter's top min(k, Q)
-        // kept as candidates; then the <= 4k candidates ranked among
-        // themselves.  A key of the global top k has fewer than k larger keys
-        // in its quarter, so it is a candidate, and every key larger than it
-        // is a candidate too: its rank among the candidates is its rank.
+        // two stages: every wave ranks the keys of its quarter, then the
+        // candidates are ranked among themselves
         for (int e = tid; e < E; e += 256) s_key[e] = rank_key(s_lg[e], e);
         __syncthreads();
-        const int P = min(64 / Q, Q / 2), span = Q / P;  // span >= 2, even
-        const int e = lane / P, part = lane - e * P;
-        int cnt = 0;
-        uint64_t mk = 0;
-        if (e < Q) {
-            mk = s_key[q0 + e];
-            const ulonglong2 *q = (const ulonglong2 *)(s_key + q0 + part * span);
-            for (int j2 = 0; j2 < span / 2; j2++) {
-                const ulonglong2 u = q[j2];
-                cnt += (int)(u.x > mk) + (int)(u.y > mk);
-            }
-        }
-        for (int sh = 1; sh < P; sh <<= 1) cnt += __shfl_xor(cnt, sh);
-        if (e < Q && part == 0 && cnt < k) c_key[wave * k + cnt] = mk;
+        rank_quarter(s_key + q0, Q, k, c_key + wave * k);
         __syncthreads();
-        if (tid < 4 * k) {
-            const uint64_t ck = c_key[tid];
-            int c2 = 0;
-            const ulonglong2 *q = (const ulonglong2 *)c_key;
-            for (int j2 = 0; j2 < 2 * k; j2++) {
-                const ulonglong2 u = q[j2];
-                c2 += (int)(u.x > ck) + (int)(u.y > ck);
-            }
-            if (ck != 0 && c2 < k) s_ids[c2] = (int32_t)(0xFFFFFFFFu - (uint32_t)ck);
-        }
+        rank_candidates(c_key, k, s_ids);
     } else if (E <= 128) {
         // direct: P = 256 / E threads rank each key against a slice of all
         for (int e = tid; e < E; e += 256) s_key[e] = rank_key(s_lg[e], e);
@@ -255,21 +293,7 @@ __device__ inline const int32_t *rank_ids_lds(const Route &r, int32_t *s_ids, co
         }
     }
     __syncthreads();
-    if (r.ids_out && publish && tid < IDS_ROW) {
-        const int row = tid >> 4, slot = tid & 15;
-        int32_t v = (int32_t)SKIP;
-        if (slot < k) {
-            const int e = s_ids[slot];
-            if (row == 0) {
-                v = e;
-            } else {
-                uint32_t ids3[3];
-                route_row(r, e, slot, ids3);
-                v = (int32_t)ids3[row - 1];
-            }
-        }
-        *(int32_t STYX_GLOBAL *)(r.ids_out + tid) = v;
-    }
+    if (publish) publish_id_row(r, s_ids);
     return s_ids;
 }
 
