@@ -567,7 +567,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     const int64_t part0 = ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
     const uint32_t tag = a.t_part ? attn_tag(a, ticket) : 0u;
     const int n_active = (n_t + chunk - 1) / chunk;
-    const bool solo = a.t_part && n_active == 1;
+    const bool solo = (a.t_part || a.solo_max > 0) && n_active == 1;
     if (nts == 1 && solo) {
         // every wave owns distinct heads: its running state is the output
         float *xo = sm + AT_WAVES * PWF;  // [gqa][HD] (the merge area, unused here)
@@ -921,7 +921,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     const int ps = MHD + 2;
     const int64_t part0 = ((int64_t)kvh * a.max_chunks + c) * gqa * ps;
     const int n_active = (n_t + chunk - 1) / chunk;
-    const bool solo = a.t_part && n_active == 1;
+    const bool solo = (a.t_part || a.solo_max > 0) && n_active == 1;
     for (int idx = threadIdx.x; idx < gqa * MHD; idx += AT_WG) {
         const int h = idx / MHD, e = idx - h * MHD;
         float O = 0.0f;
@@ -1058,11 +1058,13 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
     const int gqa = a.nkv > 0 ? a.nh / a.nkv : 0;
     if (gqa < 1 || gqa > 16 || a.nh % a.nkv || (a.hd != 64 && a.hd != 128 && a.hd != 256) ||
         a.chunk < TILE || a.chunk % TILE || a.page_tokens < 1 || a.max_chunks < 1 ||
-        (a.t_part && (!a.tickets || !a.abort || a.max_polls < 1)))
+        (a.t_part && (!a.tickets || !a.abort || a.max_polls < 1)) ||
+        (a.solo_max > 0 && !a.t_part && a.max_chunks != 1))
         return hipErrorInvalidValue;
-    // the matrix-core variant serves 16 query heads per kv head; its waves
-    // split tokens, so its chunks hold at least one 16-token tile per wave
-    const bool use_mfma = a.hd == MHD && gqa == MH;
+    // the matrix-core variant serves 16 query heads per kv head, and a
+    // single-chunk context (solo_max) of 4 to 16; its waves split tokens, so
+    // its chunks hold at least one 16-token tile per wave
+    const bool use_mfma = a.hd == MHD && (gqa == MH || (a.solo_max > 0 && gqa >= 4));
     AttnArgs am = a;
     if (use_mfma) {
         am.chunk = std::max(a.chunk, AT_WAVES * TILE);
@@ -1092,7 +1094,8 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
         return hipErrorInvalidValue;  // gqa of 5, 7, 9.. above 4 heads per wave
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.t_part) return e;  // combined inside the kernel
+    // combined inside the kernel, or a single chunk written directly
+    if (e != hipSuccess || a.t_part || a.solo_max > 0) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nh, a.hd / CB_DIMS), dim3(CB_WG), 0, st, am);
     return hipGetLastError();
 }

@@ -99,6 +99,9 @@ struct KStat {
 
 }  // namespace
 
+// Attention variants of a token (styx_moe::attn_mode).
+enum AttnMode { AT_SOLO = 0, AT_MERGE = 1, AT_COMBINE = 2 };
+
 struct styx_moe {
     styx_gpu *gpu = nullptr;
     styx_moe_opts opts{};
@@ -139,13 +142,15 @@ struct styx_moe {
     int32_t *d_pt = nullptr;
     std::vector<int32_t> h_pt;
     int pages_per_layer = 0, next_page = 0, chunk = 64, max_chunks = 1;
-    // contexts of up to this many tokens run as one chunk per kv head (the
-    // chunk's workgroup then writes the output itself, no exchange between
-    // chunks, as every context of one chunk does).  Off: measured on
-    // configs[1] at 57 tokens, one workgroup walking its 4 tiles one after
-    // another (about 2 us each, latency-bound) took 13.3 us against 9.2 us
-    // for 16-token chunks merged in-kernel.
-    int attn_solo_max = 0;
+    // contexts of up to this many tokens run as one chunk per kv head on the
+    // matrix-core attention kernel (AT_SOLO; head_dim 128, 4-16 query heads
+    // per kv head): its four waves take one 16-token tile each at once and
+    // the chunk's workgroup writes the output itself, with no exchange
+    // between chunks.  Measured on configs[1] at up to 57 tokens: 497
+    // against 474 tok/s with 16-token chunks merged in-kernel.  Past 64
+    // tokens the waves would walk tiles one after another, slower than
+    // splitting the context.
+    int attn_solo_max = 64;
     double *rope = nullptr;  // [n_ctx][hd/2] (cos, sin)
     // fused MoE block (moe_block.hip): tagged exchange buffers, ticket,
     // abort flag; mb_nwg = its grid (0: the separate kernels run), -1 until
@@ -170,7 +175,9 @@ struct styx_moe {
     bool any_host = false;
     // graphs
     // [short context: attention partials merged in-kernel, long: combine kernel]
-    hipGraphExec_t g_fwd[2] = {nullptr, nullptr}, g_gen[2] = {nullptr, nullptr};
+    // one graph per attention mode (AT_SOLO, AT_MERGE, AT_COMBINE), forward
+    // and generate
+    hipGraphExec_t g_fwd[3] = {nullptr, nullptr, nullptr}, g_gen[3] = {nullptr, nullptr, nullptr};
     // arena placement: the cold-slab gather runs on a second stream (same
     // priority), forked after the router and joined before the cold slots'
     // expert kernels, so that it overlaps the hot slots' gate/up and down
@@ -201,9 +208,10 @@ struct styx_moe {
     uint32_t *tok_save = nullptr;  // the pending token at a decode's start
     void queue_abort_read();
     int place_experts(const std::vector<std::vector<std::pair<uint32_t, uint64_t>>> *hist);
-    int enqueue_token(bool gen, bool attn_merge_in_kernel);
+    int enqueue_token(bool gen, int attn_mode);
     int run_token(bool gen);
     bool attn_merge_in_kernel(int n_t) const;
+    int attn_mode(int n_t) const;
     int ensure_pages(int upto_pos);
     int build_graphs();
     int maybe_repin();
@@ -219,7 +227,7 @@ styx_moe::~styx_moe()
         hipSetDevice(gpu->device);
         hipStreamSynchronize(gpu->stream);
     }
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < 3; i++) {
         if (g_fwd[i]) hipGraphExecDestroy(g_fwd[i]);
         if (g_gen[i]) hipGraphExecDestroy(g_gen[i]);
     }
@@ -594,7 +602,7 @@ int styx_moe::fall_back_unfused()
     opts.no_fuse = 1;
     fallbacks++;
     STYX_HIP(hipStreamSynchronize(gpu->stream));
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < 3; i++) {
         if (g_fwd[i]) hipGraphExecDestroy(g_fwd[i]);
         if (g_gen[i]) hipGraphExecDestroy(g_gen[i]);
         g_fwd[i] = g_gen[i] = nullptr;
@@ -624,7 +632,18 @@ bool styx_moe::attn_merge_in_kernel(int n_t) const
     return (n_t + ch - 1) / ch <= ATTN_MERGE_MAX_CHUNKS;
 }
 
-int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
+// Attention variant of a token at context n_t: one chunk on the matrix-core
+// kernel (short contexts), chunks merged in the attention kernel, or merged
+// by the combine kernel (the only variant with no_fuse, whose kernels never
+// wait on another workgroup).
+int styx_moe::attn_mode(int n_t) const
+{
+    if (!opts.no_fuse && hd == 128 && nh / nkv >= 4 && nh / nkv <= 16 && n_t <= attn_solo_max)
+        return AT_SOLO;
+    return attn_merge_in_kernel(n_t) ? AT_MERGE : AT_COMBINE;
+}
+
+int styx_moe::enqueue_token(bool gen, int mode)
 {
     hipStream_t st = gpu->stream;
     const int q_dim = nh * hd;
@@ -701,10 +720,13 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
         aa.nkv = nkv;
         aa.hd = hd;
         aa.chunk = chunk;
-        aa.max_chunks = max_chunks;
-        aa.solo_max = attn_solo_max;
+        aa.max_chunks = mode == AT_SOLO ? 1 : max_chunks;
+        aa.solo_max = mode == AT_SOLO ? attn_solo_max : 0;
         aa.scale = 1.0f / std::sqrt((float)hd);
-        if (merge_in_kernel) {
+        // the single-chunk mode exchanges nothing: no tagged words, and no
+        // ticket draws (a launch of another grid drawing from the counters
+        // would break the launch numbering the merged mode's tags rely on)
+        if (mode == AT_MERGE) {
             aa.t_part = at_part;
             aa.tickets = at_tickets;
             aa.abort = mb_abort;
@@ -921,14 +943,17 @@ int styx_moe::enqueue_token(bool gen, bool merge_in_kernel)
 int styx_moe::build_graphs()
 {
     if (!opts.use_graph) return STYX_OK;
-    // forward / generate x attention merged in the kernel (short contexts)
-    // or by the combine kernel (long ones; the only variant with no_fuse)
-    for (int gm = 0; gm < 4; gm++) {
-        const bool gen = gm / 2 == 1, merge = gm % 2 == 0;
-        if (merge && opts.no_fuse) continue;
+    // forward / generate x the attention modes (attn_mode): one chunk
+    // (short contexts), merged in the kernel, or by the combine kernel (long
+    // ones; the only variant with no_fuse)
+    for (int gm = 0; gm < 6; gm++) {
+        const bool gen = gm / 3 == 1;
+        const int mode = gm % 3;
+        if (mode != AT_COMBINE && opts.no_fuse) continue;
+        if (mode == AT_SOLO && attn_mode(1) != AT_SOLO) continue;  // shapes without it
         hipGraph_t g;
         STYX_HIP(hipStreamBeginCapture(gpu->stream, hipStreamCaptureModeThreadLocal));
-        int r = enqueue_token(gen, merge);
+        int r = enqueue_token(gen, mode);
         hipError_t e = hipStreamEndCapture(gpu->stream, &g);
         if (r) return r;
         if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
@@ -936,7 +961,7 @@ int styx_moe::build_graphs()
         e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
         hipGraphDestroy(g);
         if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
-        (gen ? g_gen : g_fwd)[merge ? 0 : 1] = ex;
+        (gen ? g_gen : g_fwd)[mode] = ex;
     }
     return STYX_OK;
 }
@@ -944,13 +969,13 @@ int styx_moe::build_graphs()
 // The token at position n_past (context n_past + 1).
 int styx_moe::run_token(bool gen)
 {
-    const bool merge = attn_merge_in_kernel(n_past + 1);
-    hipGraphExec_t g = (gen ? g_gen : g_fwd)[merge ? 0 : 1];
+    const int mode = attn_mode(n_past + 1);
+    hipGraphExec_t g = (gen ? g_gen : g_fwd)[mode];
     if (g && !opts.time_kernels) {
         STYX_HIP(hipGraphLaunch(g, gpu->stream));
         return STYX_OK;
     }
-    return enqueue_token(gen, merge);
+    return enqueue_token(gen, mode);
 }
 
 // Repin choice for one layer (moe.rs:1465-1497): residents ranked coldest
@@ -1906,8 +1931,8 @@ int styx_moe_time_stage(styx_moe *m, const char *stage, int reps, double *us_per
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
     int r = STYX_OK;
-    const bool merge = m->attn_merge_in_kernel(m->n_past);  // the last token's context
-    for (int i = 0; i < nrep && e == hipSuccess && !r; i++) r = m->enqueue_token(false, merge);
+    const int mode = m->attn_mode(m->n_past);  // the last token's context
+    for (int i = 0; i < nrep && e == hipSuccess && !r; i++) r = m->enqueue_token(false, mode);
     hipError_t e2 = e == hipSuccess ? hipStreamEndCapture(st, &g) : e;
     m->stage_only.clear();
     m->opts.time_kernels = saved;
@@ -2002,7 +2027,7 @@ int styx_moe_set_wait_limit(styx_moe *m, int max_polls)
     STYX_HIP(hipSetDevice(m->gpu->device));
     STYX_HIP(hipStreamSynchronize(m->gpu->stream));
     m->opts.max_polls = max_polls;
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < 3; i++) {
         if (m->g_fwd[i]) hipGraphExecDestroy(m->g_fwd[i]);
         if (m->g_gen[i]) hipGraphExecDestroy(m->g_gen[i]);
         m->g_fwd[i] = m->g_gen[i] = nullptr;

@@ -206,7 +206,12 @@ struct AttnArgs {
     int kv_head_major;
     int page_table_len;              // entries of page_table (0: not given)
     int solo_max;                    // contexts of up to this many tokens are one chunk
-                                     // per kv head (no exchange between chunks); 0: off
+                                     // per kv head (no exchange between chunks; on the
+                                     // matrix-core kernel when head_dim is 128 and 4 to 16
+                                     // query heads share a kv head); 0: off.  Without
+                                     // t_part it needs max_chunks == 1: every context is
+                                     // then one chunk, written directly (no tickets drawn,
+                                     // no combine kernel)
     const int32_t *pos;              // device scalar
     float *out;                      // [nh*hd]
     Xq xq;                           // optional limbs of out (o-proj input)
