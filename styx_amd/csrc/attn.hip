@@ -81,6 +81,22 @@ __device__ __forceinline__ void head_load(HeadIn<PPL> &h, const float *src, cons
     }
 }
 
+// head_load for head_dim 128 with one pair per lane: every load issued
+// unconditionally (without norm weights, the weights' loads read the head
+// itself and are replaced by 1)
+template <int PPL>
+__device__ __forceinline__ void head_load_all(HeadIn<PPL> &h, const float *src, const float *w, int hd)
+{
+    static_assert(PPL == 1, "one rope pair per lane");
+    const int lane = threadIdx.x & 63, half = hd / 2;
+    const float *ws = w ? w : src;
+    h.x0[0] = src[lane];
+    h.x1[0] = src[lane + half];
+    const float w0 = ws[lane], w1 = ws[lane + half];
+    h.w0[0] = w ? w0 : 1.0f;
+    h.w1[0] = w ? w1 : 1.0f;
+}
+
 template <int PPL>
 __device__ __forceinline__ void cs_load(double2 *cs, const double2 *row, int hd)
 {
@@ -362,7 +378,9 @@ __device__ __forceinline__ void attn_solo_limbs(const AttnArgs &a, int kvh, int 
 // first tile's before the q heads are normalised and rotated, the next
 // tile's K as soon as this tile's scores are formed and its V as soon as this
 // tile's PV is done, with the page-table entries one tile further ahead.
-template <int MAXH, int EPL>
+// RR: the rope row of the position is given (AttnArgs::rope_row) and loaded
+// at entry with the q heads.
+template <int MAXH, int EPL, bool RR>
 __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
 {
     constexpr int HD = 64 * EPL, PPL = (HD / 2 + 63) / 64, SEG = HD / 4;
@@ -371,6 +389,11 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     const AtStamps st{a.trace ? s_tr : nullptr};
     st.clear();
     st.at(0);
+    // the position through the scalar cache (the kernel never writes it):
+    // its wait counts scalar loads only, not the vector loads below
+    const int pos = *(const __attribute__((address_space(4))) int32_t *)a.pos;
+    double2 cs[PPL];
+    if constexpr (RR) cs_load<PPL>(cs, a.rope_row, HD);
     const unsigned long long ticket = attn_ticket(a);  // also drawn by chunks past the context
     const int gqa = a.nh / a.nkv, kv_dim = a.nkv * HD;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -393,7 +416,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     const int t_min = c * a.chunk + ts * TILE + tl, pg_min = t_min / a.page_tokens;
     const bool spec = pg_min < a.page_table_len;
     const int32_t pe_min = spec ? a.page_table[pg_min] : 0;
-    const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
+    const int n_t = pos + 1, chunk = attn_chunk(a, n_t);
     const int t0 = c * chunk;
     if (t0 >= n_t) return;
     const int t1 = min(n_t, t0 + chunk);
@@ -410,8 +433,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     // the new k/v head (in the chunk that holds pos), the first tile's
     // page-table entry
     const bool owns_pos = t1 == n_t;
-    double2 cs[PPL];
-    cs_load<PPL>(cs, a.rope + (int64_t)pos * (HD / 2), HD);
+    if constexpr (!RR) cs_load<PPL>(cs, a.rope + (int64_t)pos * (HD / 2), HD);
     int tb = t0 + ts * TILE;
     // K quarter-row of token tb+tl (this lane) and all 16 V rows of the tile
     // at [tb, tb+16): rows are pool offsets of each lane's token (lane i of
@@ -675,11 +697,20 @@ constexpr int MH = 16;      // padded heads per kv head
 constexpr int MHD = 128;    // head_dim of this variant
 constexpr int MNB = MHD / 16;
 constexpr int ATTN_PT_LDS = 256;  // page-table entries kept in LDS (128K tokens of 512)
+// page-table entries copied to LDS by a FAST launch (1M tokens of 512)
+constexpr int ATTN_PT_FAST = 2048;
+static_assert(ATTN_PT_FAST % AT_WG == 0, "whole entries per thread");
 // Column of Q and K that lane group g supplies at k-step m (m < 32), and
 // the output column of lane r's accumulator block b (b < 8).
 __device__ __forceinline__ constexpr int kcol(int g, int m) { return 16 * (m >> 2) + 4 * g + (m & 3); }
 __device__ __forceinline__ constexpr int vcol(int r, int b) { return 64 * (b >> 2) + 4 * r + (b & 3); }
 
+// FAST: the launch gives the rope row of the position (AttnArgs::rope_row)
+// and a page table of 1 to ATTN_PT_FAST entries (page_table_len).  The
+// table is then copied to LDS with the first loads and every K/V address
+// comes from LDS; otherwise the position's rope row and the page entries
+// past the minimum chunk size are read after the position.
+template <bool FAST>
 __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
 {
     const int c = blockIdx.x, kvh = blockIdx.y;
@@ -687,10 +718,37 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     const AtStamps st{a.trace ? s_tr : nullptr};
     st.clear();
     st.at(0);
-    const unsigned long long ticket = attn_ticket(a);  // also drawn by chunks past the context
-    const int gqa = a.nh / a.nkv, kv_dim = a.nkv * MHD;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;  // row-lane, k-group
+    const int gqa = a.nh / a.nkv, kv_dim = a.nkv * MHD;
+    // The position goes through the scalar cache (the kernel never writes
+    // it), so its wait counts scalar loads only.  The vector loads are
+    // issued in the order they are needed, each of them on every path (a
+    // head past gqa reads head gqa - 1, every wave reads the new k/v head,
+    // a table entry past the end reads the last one): gfx950 counts vector
+    // loads in order, and a wait for one then leaves the later ones in
+    // flight.
+    const int pos = *(const __attribute__((address_space(4))) int32_t *)a.pos;
+    const int pt_n = a.page_table_len;
+    constexpr int PT_CAP = FAST ? ATTN_PT_FAST : ATTN_PT_LDS;
+    constexpr int PT_PER = FAST ? ATTN_PT_FAST / AT_WG : 1;
+    __shared__ int32_t s_pt[PT_CAP];
+    int32_t pte[PT_PER];
+    int32_t pe_min = 0;
+    const int t_min = c * a.chunk + wave * 16 + lr, pg_min = t_min / a.page_tokens;
+    const bool spec = pg_min < pt_n;
+    double2 cs[1];
+    if constexpr (FAST) {
+#pragma unroll
+        for (int j = 0; j < PT_PER; j++)
+            pte[j] = a.page_table[min((int)threadIdx.x + AT_WG * j, pt_n - 1)];
+        cs_load<1>(cs, a.rope_row, MHD);
+    } else {
+        // the page entry of this lane's first token at the minimum chunk
+        // size, the chunk size of every short context
+        pe_min = a.page_table[spec ? pg_min : 0];
+    }
+    const unsigned long long ticket = attn_ticket(a);  // also drawn by chunks past the context
 
     extern __shared__ __align__(16) float sm[];
     float *qs = sm;                      // [MH][MHD] normalised, rotated q (zero rows past gqa)
@@ -701,42 +759,38 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     float *mm = mo + AT_WAVES * MH * MHD;
     float *ml = mm + AT_WAVES * MH;
 
-    // loads that do not depend on the position go out first: this wave's q
-    // heads (heads wave + 4 j) and norm weights, the new k/v head (wave 0),
-    // and the page-table entry of this lane's first token for the minimum
-    // chunk size (the chunk size of every short context)
+    // this wave's q heads (heads wave + 4 j) and norm weights, and the new
+    // k/v head
     constexpr int HPW = MH / AT_WAVES;
     HeadIn<1> hq[HPW], hk;
 #pragma unroll
     for (int j = 0; j < HPW; j++) {
-        const int i = wave + AT_WAVES * j;
-        if (i < gqa) head_load<1>(hq[j], a.q + (int64_t)(kvh * gqa + i) * MHD, a.q_norm, MHD);
+        const int i = min(wave + AT_WAVES * j, gqa - 1);
+        head_load_all<1>(hq[j], a.q + (int64_t)(kvh * gqa + i) * MHD, a.q_norm, MHD);
     }
     float vn[MHD / 64];
-    if (wave == 0) {
-        head_load<1>(hk, a.k + (int64_t)kvh * MHD, a.k_norm, MHD);
+    head_load_all<1>(hk, a.k + (int64_t)kvh * MHD, a.k_norm, MHD);
 #pragma unroll
-        for (int e = 0; e < MHD / 64; e++) vn[e] = a.v[(int64_t)kvh * MHD + lane + 64 * e];
+    for (int e = 0; e < MHD / 64; e++) vn[e] = a.v[(int64_t)kvh * MHD + lane + 64 * e];
+    // the page table in LDS: the whole of it (FAST), or when it is short:
+    // past the minimum chunk size (long contexts) the first tile's page
+    // entry then needs no memory trip after the position, nor does any
+    // later tile's
+    const bool pt_lds = FAST || (pt_n > 0 && pt_n <= ATTN_PT_LDS);
+    if constexpr (FAST) {
+#pragma unroll
+        for (int j = 0; j < PT_PER; j++) s_pt[threadIdx.x + AT_WG * j] = pte[j];
+    } else if (pt_lds) {
+        for (int i = threadIdx.x; i < pt_n; i += AT_WG) s_pt[i] = a.page_table[i];
     }
-    const int t_min = c * a.chunk + wave * 16 + lr, pg_min = t_min / a.page_tokens;
-    const bool spec = pg_min < a.page_table_len;
-    const int32_t pe_min = spec ? a.page_table[pg_min] : 0;
-    // the whole page table in LDS when it is short: past the minimum chunk
-    // size (long contexts) the first tile's page entry then needs no memory
-    // trip after the position, nor does any later tile's
-    __shared__ int32_t s_pt[ATTN_PT_LDS];
-    const bool pt_lds = a.page_table_len > 0 && a.page_table_len <= ATTN_PT_LDS;
-    if (pt_lds)
-        for (int i = threadIdx.x; i < a.page_table_len; i += AT_WG) s_pt[i] = a.page_table[i];
 
-    const int pos = *a.pos, n_t = pos + 1, chunk = attn_chunk(a, n_t);
+    const int n_t = pos + 1, chunk = attn_chunk(a, n_t);
     const int t0 = c * chunk;
     if (t0 >= n_t) return;
     __syncthreads();  // s_pt
     const int t1 = min(n_t, t0 + chunk);
     const bool owns_pos = t1 == n_t;
-    double2 cs[1];
-    cs_load<1>(cs, a.rope + (int64_t)pos * (MHD / 2), MHD);
+    if constexpr (!FAST) cs_load<1>(cs, a.rope + (int64_t)pos * (MHD / 2), MHD);
 
     const int step = AT_WAVES * 16;
     int tb = t0 + wave * 16;
@@ -746,38 +800,46 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
         if (!pt_lds) return kv_off(a, t, kvh, kv_dim);
         return kv_row(a, s_pt[t / a.page_tokens], t % a.page_tokens, kvh, kv_dim);
     };
+    // Every tile issues the same loads on every lane, with nothing done to
+    // their results before use, so that the waits for the q heads and for
+    // each tile count only older loads: a token past the chunk reads the
+    // new k and v heads of the launch (finite values: its score is masked
+    // and its probability 0), and the token at pos reads V from the new v
+    // head (its pool row is written at the end) and has its K replaced by
+    // the rotated head from LDS
+    const float *k_in = a.k + (int64_t)kvh * MHD, *v_in = a.v + (int64_t)kvh * MHD;
+    // the early page entries apply to a table in memory at the minimum
+    // chunk size
+    const bool early = !FAST && chunk == a.chunk && !pt_lds && pt_n > 0;
     auto row_of = [&](int tbase) -> int64_t { return tbase + lr < t1 ? kv_at(tbase + lr) : 0; };
     auto load_k = [&](int64_t row, int tbase) {
-        const bool ok = tbase + lr < t1;
+        const float *src = tbase + lr < t1 ? a.kpool + row : k_in;
 #pragma unroll
         for (int m = 0; m < MHD / 4; m += 4) {
-            const float4 v = ok ? *(const float4 *)(a.kpool + row + kcol(lg, m))
-                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 v = *(const float4 *)(src + kcol(lg, m));
             kv[m] = v.x; kv[m + 1] = v.y; kv[m + 2] = v.z; kv[m + 3] = v.w;
         }
     };
     auto load_v = [&](int64_t row, int tbase) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int t = 4 * q + lg;  // token in tile of this k-step
-            const int64_t rq = __shfl(row, t);
-            const bool ok = tbase + t < t1;
+            const int t = tbase + 4 * q + lg;  // token of this k-step
+            const int64_t rq = __shfl(row, 4 * q + lg);
+            const float *src = t < t1 && t != pos ? a.vpool + rq : v_in;
 #pragma unroll
             for (int b = 0; b < MNB; b += 4) {
-                const float4 v = ok ? *(const float4 *)(a.vpool + rq + vcol(lr, b))
-                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                const float4 v = *(const float4 *)(src + vcol(lr, b));
                 vvr[q][b] = v.x; vvr[q][b + 1] = v.y; vvr[q][b + 2] = v.z; vvr[q][b + 3] = v.w;
             }
         }
     };
-    // the first tile's loads, from the early page entry when the chunk has
-    // its minimum size (then tb + lr == t_min)
-    if (tb < t1) {
-        const int64_t row =
-            spec && chunk == a.chunk
-                ? (tb + lr < t1 ? kv_row(a, pe_min, t_min % a.page_tokens, kvh, kv_dim)
-                                : 0)
-                : row_of(tb);
+    // the first tile's loads (every wave has one; t0 + 16 wave may be past
+    // the chunk), from the early page entry when the table is in memory and
+    // the chunk has its minimum size (then tb + lr == t_min)
+    {
+        const int64_t row = early && spec && tb + lr < t1
+                                ? kv_row(a, pe_min, t_min % a.page_tokens, kvh, kv_dim)
+                                : row_of(tb);
         load_k(row, tb);
         load_v(row, tb);
     }
@@ -800,13 +862,6 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
         for (int e = 0; e < MHD / 64; e++) vnew[lane + 64 * e] = vn[e];
     }
     __syncthreads();
-    if (owns_pos && wave == 0) {
-        const int64_t po = kv_at(pos);
-        for (int e = lane; e < MHD; e += 64) {
-            a.kpool[po + e] = knew[e];
-            a.vpool[po + e] = vnew[e];
-        }
-    }
     // this lane's Q operand: Q[lr][kcol(lg, m)], m < 32
     float qv[MHD / 4];
 #pragma unroll
@@ -828,19 +883,11 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     for (; tb < t1; tb += step) {
         const int tn = tb + step;
         const bool tv = tb + lr < t1;
-        // the token at pos comes from LDS (its pool row is written above by
-        // wave 0 of this workgroup, possibly after these loads)
+        // the K of the token at pos comes from LDS (its pool row is written
+        // at the end of the kernel)
         if (tb + lr == pos) {
 #pragma unroll
             for (int m = 0; m < MHD / 4; m++) kv[m] = knew[kcol(lg, m)];
-        }
-        if (pos >= tb && pos < tb + 16) {
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                if (tb + 4 * q + lg == pos) {
-#pragma unroll
-                    for (int b = 0; b < MNB; b++) vvr[q][b] = vnew[vcol(lr, b)];
-                }
         }
         // four independent accumulation chains over the k-steps
         f4v sc4[4];
@@ -850,7 +897,10 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
         for (int m = 0; m < MHD / 4; m++)
             sc4[m & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[m], kv[m], sc4[m & 3], 0, 0, 0);
         const f4v sacc = (sc4[0] + sc4[1]) + (sc4[2] + sc4[3]);
-        if (tn < t1) load_k(row_n, tn);  // kv is free
+        // kv is free: the next tile's K (issued also after the last tile, as
+        // loads of the new k head, so that every trip issues the same loads
+        // and the wait for this tile's V leaves them in flight)
+        load_k(row_n, tn);
         // online softmax; lane holds heads 4 lg + r, token lr
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -875,7 +925,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
             for (int b = 0; b < MNB; b++)
                 o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vvr[q][b], o[b], 0, 0, 0);
         }
-        if (tn < t1) load_v(row_n, tn);  // vvr is free
+        load_v(row_n, tn);  // vvr is free
         row_n = row_of(tn + step);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -944,6 +994,16 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
         attn_solo_limbs<MHD>(a, kvh, gqa, qs);
     else if (a.t_part)
         attn_combine_tail<MHD / 64>(a, c, kvh, n_active, tag, sm, st);
+    // the new k/v rows go to the pool last (the tiles took them from LDS):
+    // gfx950 counts stores with the loads, so a store issued earlier would
+    // hold up every later wait for a load until it is acknowledged
+    if (owns_pos && wave == 0) {
+        const int64_t po = kv_at(pos);
+        for (int e = lane; e < MHD; e += 64) {
+            a.kpool[po + e] = knew[e];
+            a.vpool[po + e] = vnew[e];
+        }
+    }
     st.at(5);
     st.flush(a, c, kvh, n_active);
 }
@@ -1040,16 +1100,16 @@ __global__ void __launch_bounds__(CB_WG) k_attn_combine(AttnArgs a)
     xq_build<CB_WG>(xs, nullptr, 0.0f, false, CB_DIMS, xq_shift(a.xq, h * hd + d0), red, nullptr);
 }
 
-template <int MAXH>
+template <int MAXH, bool RR>
 static void launch_k_attn(hipStream_t st, const AttnArgs &a, int nhg, int hpw)
 {
     const dim3 grid(a.max_chunks, a.nkv);
     const size_t lds = sizeof(float) * (AT_WAVES * ((size_t)MAXH * a.hd + 2 * a.hd + MAXH * TILE) +
                                         (size_t)AT_WAVES * MAXH * a.hd + 2 * AT_WAVES * MAXH);
     switch (a.hd) {
-    case 64: hipLaunchKernelGGL((k_attn<MAXH, 1>), grid, dim3(AT_WG), lds, st, a, nhg, hpw); break;
-    case 128: hipLaunchKernelGGL((k_attn<MAXH, 2>), grid, dim3(AT_WG), lds, st, a, nhg, hpw); break;
-    default: hipLaunchKernelGGL((k_attn<MAXH, 4>), grid, dim3(AT_WG), lds, st, a, nhg, hpw); break;
+    case 64: hipLaunchKernelGGL((k_attn<MAXH, 1, RR>), grid, dim3(AT_WG), lds, st, a, nhg, hpw); break;
+    case 128: hipLaunchKernelGGL((k_attn<MAXH, 2, RR>), grid, dim3(AT_WG), lds, st, a, nhg, hpw); break;
+    default: hipLaunchKernelGGL((k_attn<MAXH, 4, RR>), grid, dim3(AT_WG), lds, st, a, nhg, hpw); break;
     }
 }
 
@@ -1079,17 +1139,20 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
     if (use_mfma) {
         const size_t lds = sizeof(float) * ((size_t)MH * MHD + 2 * MHD + AT_WAVES * MH * 16 +
                                             (size_t)AT_WAVES * MH * MHD + 2 * AT_WAVES * MH);
-        hipLaunchKernelGGL(k_attn_mfma, dim3(am.max_chunks, am.nkv), dim3(AT_WG), lds, st, am);
+        if (a.rope_row && a.page_table_len >= 1 && a.page_table_len <= ATTN_PT_FAST)
+            hipLaunchKernelGGL(k_attn_mfma<true>, dim3(am.max_chunks, am.nkv), dim3(AT_WG), lds, st, am);
+        else
+            hipLaunchKernelGGL(k_attn_mfma<false>, dim3(am.max_chunks, am.nkv), dim3(AT_WG), lds, st, am);
     } else {
     // head groups: the largest of 4, 2, 1 dividing gqa
     const int nhg = gqa % 4 == 0 ? 4 : gqa % 2 == 0 ? 2 : 1;
     const int hpw = gqa / nhg;
     if (hpw <= 1)
-        launch_k_attn<1>(st, am, nhg, hpw);
+        a.rope_row ? launch_k_attn<1, true>(st, am, nhg, hpw) : launch_k_attn<1, false>(st, am, nhg, hpw);
     else if (hpw <= 2)
-        launch_k_attn<2>(st, am, nhg, hpw);
+        a.rope_row ? launch_k_attn<2, true>(st, am, nhg, hpw) : launch_k_attn<2, false>(st, am, nhg, hpw);
     else if (hpw <= 4)
-        launch_k_attn<4>(st, am, nhg, hpw);
+        a.rope_row ? launch_k_attn<4, true>(st, am, nhg, hpw) : launch_k_attn<4, false>(st, am, nhg, hpw);
     else
         return hipErrorInvalidValue;  // gqa of 5, 7, 9.. above 4 heads per wave
     }

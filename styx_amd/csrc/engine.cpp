@@ -152,6 +152,7 @@ struct styx_moe {
     // splitting the context.
     int attn_solo_max = 64;
     double *rope = nullptr;  // [n_ctx][hd/2] (cos, sin)
+    double *rope_cur = nullptr;  // [hd/2] (cos, sin) of the token's position (k_embed)
     // fused MoE block (moe_block.hip): tagged exchange buffers, ticket,
     // abort flag; mb_nwg = its grid (0: the separate kernels run), -1 until
     // first sized
@@ -383,6 +384,7 @@ int styx_moe::setup_runtime()
         std::vector<double> cs((size_t)n_ctx * hd);
         styx_rope_table(rope_base, hd, n_ctx, cs.data());
         if (int r = dalloc(&rope, cs.size())) return r;
+        if (int r = dalloc(&rope_cur, (size_t)hd)) return r;
         STYX_HIP(hipMemcpyAsync(rope, cs.data(), sizeof(double) * cs.size(), hipMemcpyHostToDevice,
                                 gpu->stream));
         STYX_HIP(hipStreamSynchronize(gpu->stream));
@@ -670,7 +672,11 @@ int styx_moe::enqueue_token(bool gen, int mode)
     // the first layer's q/k/v input: limbs of attn_norm_0(x) (or of the LM
     // head's output_norm(x) for a model without layers)
     const float *norm0 = L > 0 ? layers[0].attn_norm : out_norm;
-    if (want("embed")) CK(launch_embed(st, embd.type, embd.dev, V, H, d_tok, x, norm0, xq_a, ss_a));
+    // (and the rope row of the token's position, which every layer's
+    // attention then loads without waiting for the position)
+    if (want("embed"))
+        CK(launch_embed(st, embd.type, embd.dev, V, H, d_tok, x, norm0, xq_a, ss_a,
+                        (const double2 *)rope, d_pos, (double2 *)rope_cur, hd / 2));
     // every consumer of xq_a applies the RMSNorm scale from the x^2 partials
     const NormScale ns_a{ss_a, (H + 255) / 256, H, eps};
     if (opts.record_hidden && stage_only.empty()) CK(hipMemcpyAsync(hidden, x, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
@@ -706,6 +712,7 @@ int styx_moe::enqueue_token(bool gen, int mode)
         aa.k_norm = ly.k_norm;
         aa.eps = eps;
         aa.rope = (const double2 *)rope;
+        aa.rope_row = (const double2 *)rope_cur;
         aa.kpool = kpool;
         aa.vpool = vpool;
         aa.page_table = d_pt + (size_t)l * pages_per_layer;

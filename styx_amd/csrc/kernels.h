@@ -199,6 +199,9 @@ struct AttnArgs {
     const float *q_norm, *k_norm;    // [hd] or null
     float eps;
     const double2 *rope;             // [n_pos][hd/2] (cos, sin) of pos * base^(-2i/hd)
+    const double2 *rope_row;         // [hd/2]: the row of *pos, written before the launch
+                                     // in stream order (the engine's embedding kernel),
+                                     // loaded without waiting for the position; or null
     float *kpool, *vpool;            // [pages][page_tokens][kv_dim], or
                                      // [pages][nkv][page_tokens][hd] (kv_head_major)
     const int32_t *page_table;       // logical page -> physical page
@@ -246,10 +249,13 @@ constexpr int ATTN_MERGE_MAX_CHUNKS = 32;
 
 // x = dequant(token_embd[tok]) for the token held in device memory, and
 // (if q.A) the limbs of x ⊙ norm_w (of x if norm_w is null) with ss[0] =
-// sum x^2 for the consumer's RMSNorm scale.
+// sum x^2 for the consumer's RMSNorm scale.  With rope_row, also copies the
+// rope table's row of *pos ([half] (cos, sin)) there, for the attention
+// kernels of the token (AttnArgs::rope_row).
 hipError_t launch_embed(hipStream_t st, int t, const uint8_t *w, int64_t nrows, int ncols,
                         const uint32_t *tok, float *x, const float *norm_w, const Xq &q,
-                        float *ss);
+                        float *ss, const double2 *rope = nullptr, const int32_t *pos = nullptr,
+                        double2 *rope_row = nullptr, int half = 0);
 
 // Greedy argmax over logits (ties -> highest index, generate_moe.rs:29),
 // in two kernels through part_val/part_idx (64 entries each).  Writes

@@ -85,13 +85,19 @@ hipError_t launch_dequant_rows(hipStream_t st, int t, const uint8_t *w, int64_t 
 // ----------------------------------------------------------- embedding ----
 // x = dequant(token_embd[tok]); the limbs of x ⊙ norm_w for the first
 // layer's q/k/v matvec, which applies the RMSNorm scale from ss[0] = sum x^2
-// (ss[1..nss) = 0); one workgroup.
+// (ss[1..nss) = 0); one workgroup.  With rope_row, the (cos, sin) row of
+// *pos copied from the rope table.
 __global__ void __launch_bounds__(256) k_embed(int t, const uint8_t *w, int64_t nrows, int ncols,
                                                const uint32_t *tok, float *x, const float *nw,
-                                               Xq q, float *ss, int nss)
+                                               Xq q, float *ss, int nss, const double2 *rope,
+                                               const int32_t *pos, double2 *rope_row, int half)
 {
     extern __shared__ __align__(16) float xs[];  // [ncols]
     __shared__ float red[16];
+    if (rope_row) {
+        const int64_t p = *pos;
+        for (int i = threadIdx.x; i < half; i += blockDim.x) rope_row[i] = rope[p * half + i];
+    }
     const int be = blk_elems(t), nb = ncols / be;
     const Mat m = mat_at(w, t, nrows * nb);
     const int64_t r = *tok;
@@ -118,11 +124,13 @@ __global__ void __launch_bounds__(256) k_embed(int t, const uint8_t *w, int64_t 
 
 hipError_t launch_embed(hipStream_t st, int t, const uint8_t *w, int64_t nrows, int ncols,
                         const uint32_t *tok, float *x, const float *norm_w, const Xq &q,
-                        float *ss)
+                        float *ss, const double2 *rope, const int32_t *pos, double2 *rope_row,
+                        int half)
 {
     if (ncols % 32 || ncols > XQ_MAX || ncols % blk_elems(t)) return hipErrorInvalidValue;
+    if (rope_row && (!rope || !pos || half < 1)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), (size_t)ncols * 4, st, t, w, nrows, ncols,
-                       tok, x, norm_w, q, ss, ncols / 32);
+                       tok, x, norm_w, q, ss, ncols / 32, rope, pos, rope_row, half);
     return hipGetLastError();
 }
 
