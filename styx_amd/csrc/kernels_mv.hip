@@ -27,6 +27,7 @@
 // fence or counter anywhere on the path.
 #include "kernels.h"
 #include "qdot.h"
+#include "router.h"
 #include "topk.h"
 #include "walk.h"
 
@@ -262,87 +263,57 @@ hipError_t launch_topk_softmax(hipStream_t st, const float *logits, int n, int k
 // (shaders/matvec_strided_f32.comp); one row per wave.  The top-k ids are
 // ranked by each consumer workgroup from these logits (route_ids_wg) and the
 // weights by k_reduce_norm, so no workgroup ever waits on another.
-constexpr int ROUTER_ROWS = 4;
 
 __global__ void __launch_bounds__(WG) k_router(RouterArgs a)
 {
     extern __shared__ __align__(16) uint8_t lds[];
-    float *xs = (float *)lds;          // normalised x, H floats
-    float *red = xs + a.H;             // 16 floats
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = blockIdx.x * ROUTER_ROWS + wave;
-    // the router row, x and the norm weights do not depend on each other:
-    // load the first 2048 columns of all three before any reduction
-    constexpr int PW = 8, PX = 2;  // float4 per lane of W, per thread of x
-    float4 wv[PW], xv[PX], nv[PX];
-    const float *w = a.W + (int64_t)min(r, a.E - 1) * a.H;
+    float *xs = (float *)lds;          // x (.) w, H floats
+    __shared__ float red[RT_RED];
+    const int r0 = blockIdx.x * RT_ROWS;
+    // x, the norm weight and the workgroup's RT_ROWS rows at columns
+    // 4 t + 1024 j of thread t (router.h; the fused MoE block's order)
+    const float *wr[RT_ROWS];
 #pragma unroll
-    for (int j = 0; j < PW; j++) {
-        const int c = lane * 4 + 256 * j;
-        wv[j] = c < a.H ? *(const float4 *)(w + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
+    for (int r = 0; r < RT_ROWS; r++) wr[r] = a.W + (int64_t)min(r0 + r, a.E - 1) * a.H;
+    float ss = 0.0f, p[RT_ROWS] = {};
+    for (int i = threadIdx.x * 4; i < a.H; i += WG * 4) {
+        const float4 xv = *(const float4 *)(a.x + i);
+        const float4 nv = *(const float4 *)(a.norm_w + i);
+        float4 wv[RT_ROWS];
 #pragma unroll
-    for (int j = 0; j < PX; j++) {
-        const int i = threadIdx.x * 4 + WG * 4 * j;
-        xv[j] = i < a.H ? *(const float4 *)(a.x + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        nv[j] = i < a.H ? *(const float4 *)(a.norm_w + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int r = 0; r < RT_ROWS; r++) wv[r] = *(const float4 *)(wr[r] + i);
+        *(float4 *)(xs + i) = router_acc(xv, nv, wv, RT_ROWS, ss, p);
     }
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < PX; j++)
-        ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
-    for (int i = threadIdx.x * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {
-        const float4 v = *(const float4 *)(a.x + i);
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    router_wave_part(ss, p, RT_ROWS, red);
+    __syncthreads();
+    const float scale = router_scale(red, a.H, a.eps);
+    if ((int)threadIdx.x < RT_ROWS && r0 + (int)threadIdx.x < a.E) {
+        const int r = r0 + threadIdx.x;
+        const float lg = scale * router_dot(red, threadIdx.x);
+        a.logits[r] = a.bias ? lg + a.bias[r] : lg;
     }
-    ss = block_sum(ss, red);
-    const float scale = 1.0f / sqrtf(ss / (float)a.H + a.eps);
-#pragma unroll
-    for (int j = 0; j < PX; j++) {
-        const int i = threadIdx.x * 4 + WG * 4 * j;
-        if (i < a.H)
-            *(float4 *)(xs + i) = make_float4((xv[j].x * scale) * nv[j].x, (xv[j].y * scale) * nv[j].y,
-                                              (xv[j].z * scale) * nv[j].z, (xv[j].w * scale) * nv[j].w);
-    }
-    for (int i = threadIdx.x * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {
-        const float4 v = *(const float4 *)(a.x + i);
-        const float4 nw = *(const float4 *)(a.norm_w + i);
-        *(float4 *)(xs + i) = make_float4((v.x * scale) * nw.x, (v.y * scale) * nw.y,
-                                          (v.z * scale) * nw.z, (v.w * scale) * nw.w);
+    if (blockIdx.x != 0 || (!a.xq.A && !a.xn)) return;
+    // the first workgroup: xn = rmsnorm(x) * w (the reference's (x s) w)
+    // for the separate expert kernels, and its limbs
+    for (int i = threadIdx.x * 4; i < a.H; i += WG * 4) {
+        const float4 xv = *(const float4 *)(a.x + i);
+        const float4 nv = *(const float4 *)(a.norm_w + i);
+        *(float4 *)(xs + i) = make_float4((xv.x * scale) * nv.x, (xv.y * scale) * nv.y,
+                                          (xv.z * scale) * nv.z, (xv.w * scale) * nv.w);
     }
     __syncthreads();
-    if (r < a.E) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < PW; j++) {
-            const int c = lane * 4 + 256 * j;
-            if (c < a.H) {
-                const float4 xv4 = *(const float4 *)(xs + c);
-                acc += wv[j].x * xv4.x + wv[j].y * xv4.y + wv[j].z * xv4.z + wv[j].w * xv4.w;
-            }
-        }
-        for (int c = lane * 4 + 256 * PW; c < a.H; c += 256) {
-            const float4 wq = *(const float4 *)(w + c);
-            const float4 xv4 = *(const float4 *)(xs + c);
-            acc += wq.x * xv4.x + wq.y * xv4.y + wq.z * xv4.z + wq.w * xv4.w;
-        }
-        acc = wave_sum(acc);
-        if (lane == 0) a.logits[r] = a.bias ? acc + a.bias[r] : acc;
-    }
-    if (blockIdx.x == 0) {
-        if (a.xq.A)
-            xq_build(xs, nullptr, 0.0f, false, a.H, a.xq, red, a.xn);
-        else if (a.xn)
-            for (int i = threadIdx.x * 4; i < a.H; i += WG * 4)
-                *(float4 *)(a.xn + i) = *(const float4 *)(xs + i);
-    }
+    if (a.xq.A)
+        xq_build(xs, nullptr, 0.0f, false, a.H, a.xq, red, a.xn);
+    else
+        for (int i = threadIdx.x * 4; i < a.H; i += WG * 4)
+            *(float4 *)(a.xn + i) = *(const float4 *)(xs + i);
 }
 
 hipError_t launch_router(hipStream_t st, const RouterArgs &a)
 {
     if (a.E < 1 || a.E > MAX_EXPERTS || a.H % 32 || a.H > XQ_MAX) return hipErrorInvalidValue;
-    const int nwg = (a.E + ROUTER_ROWS - 1) / ROUTER_ROWS;
-    hipLaunchKernelGGL(k_router, dim3(nwg), dim3(WG), (size_t)a.H * 4 + 64, st, a);
+    const int nwg = (a.E + RT_ROWS - 1) / RT_ROWS;
+    hipLaunchKernelGGL(k_router, dim3(nwg), dim3(WG), (size_t)a.H * 4, st, a);
     return hipGetLastError();
 }
 

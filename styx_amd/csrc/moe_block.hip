@@ -19,6 +19,7 @@
 // ever approaches the bound; the host checks *abort after each token.
 #include "kernels.h"
 #include "qdot.h"
+#include "router.h"
 #include "topk.h"
 #include "walk.h"
 #include "xchg.h"
@@ -28,7 +29,6 @@
 
 namespace styx {
 
-constexpr int MB_ROUTER_ROWS = 4;  // router rows per workgroup (one per wave), as k_router
 constexpr int MB_RR = 256;         // reduce rows per workgroup, as k_reduce_rows
 constexpr int MB_MAX_F = 2048;     // gate/up width handled here (g and u of a slot in LDS)
 constexpr int MB_TICKETS = 64;     // ticket counters (workgroup w draws from counter w % 64)
@@ -65,7 +65,7 @@ struct MoeBlockK {
     int qkv_rows[3];
     uint64_t *t_xq;          // tagged limbs of x (.) w_next + the x^2 partials
     int G_q, UPL_q, nb_q, rpw_q, n_q;  // rows per workgroup, workgroups [nRed, nRed + n_q)
-    int nR;                                  // router workgroups
+    int nR, rt_rows;                         // router workgroups, rows per router workgroup
     int G_gu, nb_gu, rpw_gu, bps_gu, n_gu;   // gate/up blocks: [2][nslots][bps_gu]
     int G_d, nb_d, rpw_d, bps_d, n_d;        // down blocks: [nslots][bps_d]
     int nRed;                                // reduce workgroups
@@ -150,14 +150,15 @@ __device__ __forceinline__ const uint8_t *routed_slab(const MoeBlockK &a, const 
     return slab_pick(src, r3[0], r3[1], r3[2]);
 }
 
-// Rows [r0, r1) of one expert matrix (gate or up) against the limbs of xn
-// in LDS, walked by the lane groups of waves [wave0, wave0 + 2); row r's
-// dot goes to dst[r - r0] (LDS).  A missing slab gives zeros.
+// Rows [r0, r1) of one expert matrix (gate or up) against the limbs of
+// x (.) w in LDS, walked by the lane groups of waves [wave0, wave0 + 2); row
+// r's dot times the RMSNorm scale xscale goes to dst[r - r0] (LDS).  A
+// missing slab gives zeros.
 // `between` runs once the rows' first weights are issued (the caller
 // issues further loads there).
 template <int T, typename Between>
 __device__ __forceinline__ void gu_rows(const MoeBlockK &a, const uint8_t *slab, const Xq &xqx,
-                               int r0, int r1, int wave0, float *dst, Between between,
+                               float xscale, int r0, int r1, int wave0, float *dst, Between between,
                                uint64_t *tr)
 {
     if (!slab) {
@@ -177,7 +178,7 @@ __device__ __forceinline__ void gu_rows(const MoeBlockK &a, const uint8_t *slab,
             stamp(12);
             return true;
         },
-        [&](int r, float v) { dst[r - r0] = v; }, 2, wave0);
+        [&](int r, float v) { dst[r - r0] = v * xscale; }, 2, wave0);
     stamp(13);
 }
 
@@ -200,7 +201,7 @@ __device__ __forceinline__ GuPos gu_pos(const MoeBlockK &a, int b)
 // gl holds 2 * rpw_gu floats of LDS.
 template <typename Between>
 __device__ __forceinline__ void gu_block(const MoeBlockK &a, const GuPos &bp, bool routed_phase,
-                                const int32_t *s_ids, const Xq &xqx, uint32_t tag,
+                                const int32_t *s_ids, const Xq &xqx, float xscale, uint32_t tag,
                                 float *gl, Between between, uint64_t *tr)
 {
     const int s = bp.s, r0 = bp.r0, r1 = bp.r1;
@@ -211,10 +212,10 @@ __device__ __forceinline__ void gu_block(const MoeBlockK &a, const GuPos &bp, bo
     if (routed_phase && tr && threadIdx.x == 0) tr[15] = wall_clock64();
     float *dst = gl + m * a.rpw_gu;
     switch (m == 0 ? a.tg : a.tu) {
-    case T_Q8_0: gu_rows<T_Q8_0>(a, slab, xqx, r0, r1, 2 * m, dst, between, tr); break;
-    case T_Q4_K: gu_rows<T_Q4_K>(a, slab, xqx, r0, r1, 2 * m, dst, between, tr); break;
-    case T_Q5_K: gu_rows<T_Q5_K>(a, slab, xqx, r0, r1, 2 * m, dst, between, tr); break;
-    default: gu_rows<T_Q6_K>(a, slab, xqx, r0, r1, 2 * m, dst, between, tr); break;
+    case T_Q8_0: gu_rows<T_Q8_0>(a, slab, xqx, xscale, r0, r1, 2 * m, dst, between, tr); break;
+    case T_Q4_K: gu_rows<T_Q4_K>(a, slab, xqx, xscale, r0, r1, 2 * m, dst, between, tr); break;
+    case T_Q5_K: gu_rows<T_Q5_K>(a, slab, xqx, xscale, r0, r1, 2 * m, dst, between, tr); break;
+    default: gu_rows<T_Q6_K>(a, slab, xqx, xscale, r0, r1, 2 * m, dst, between, tr); break;
     }
     __syncthreads();
     uint64_t *y = a.t_gu + (size_t)s * a.F;
@@ -285,8 +286,8 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     __syncthreads();
     const MoeBlockK &a = s_args;
     extern __shared__ __align__(16) uint8_t lds[];
-    float *xs = (float *)lds;                         // x, then xn = rmsnorm(x) * w
-    const Xq xqx = xq_at(lds + a.off_xq, a.H);        // limbs of xn
+    float *xs = (float *)lds;                         // x (.) w (the RMSNorm scale apart)
+    const Xq xqx = xq_at(lds + a.off_xq, a.H);        // limbs of x (.) w
     float *s_lg = (float *)(lds + a.off_lg);          // router logits
     float *gus = (float *)(lds + a.off_gu);           // gate/up rows; then h[F]; reduce: partials
     float *hs = (float *)(lds + a.off_hs);            // the reduce's rows of x (.) w_next
@@ -334,94 +335,72 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     }
 
     // ---- entry (workgroups with gate/up work; the router and reduce
-    // workgroups are among them): router row, x and the ffn norm weight are
-    // independent loads, issued before any reduction (k_router's order)
+    // workgroups are among them)
     const bool has_x = w < a.n_gu;
-    const bool router = w < a.nR;
-    const int rr = w * MB_ROUTER_ROWS + wave;
-    // x and the router row in registers in one trip: PX float4 of x per
-    // thread and PW of the row per lane (H <= 4 * WG * PX); a short row does
-    // not pay for the registers and predicated loads of a long one
+    const int nrt = w < a.nR ? a.rt_rows : 0;  // router rows of this workgroup
     uint32_t tag = 0;
-    auto entry = [&](auto pw, auto px) {
-        constexpr int PW = decltype(pw)::value, PX = decltype(px)::value;
-        float4 wv[PW];
+    float xscale = 1.0f;  // the ffn RMSNorm scale (xs holds x (.) w unscaled)
+    // x, the norm weight and (router workgroups) the workgroup's router rows
+    // at columns 4 t + 1024 j of thread t, all issued before any reduction;
+    // xs gets x (.) w, whose limbs need no sum of squares, and the router
+    // dots and the x^2 sum are reduced together (router.h)
+    __shared__ float s_rt[RT_RED];
+    auto entry = [&](auto px) {
+        constexpr int PX = decltype(px)::value;
         if (has_x) {
-            const float *wr = a.W + (int64_t)min(rr, a.E - 1) * a.H;
-#pragma unroll
-            for (int j = 0; j < PW; j++) {
-                const int c = lane * 4 + 256 * j;
-                wv[j] = (router && c < a.H) ? gld4(wr + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            }
-            float4 xv[PX], nv[PX];
+            float4 xv[PX], nv[PX], wv[PX][RT_ROWS];
 #pragma unroll
             for (int j = 0; j < PX; j++) {
                 const int i = tid * 4 + WG * 4 * j;
-                xv[j] = i < a.H ? gld4(a.x + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                nv[j] = i < a.H ? gld4(a.ffn_norm + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            }
-            float ss = 0.0f;
+                const int ic = i < a.H ? i : 0;
+                xv[j] = gld4(a.x + ic);
+                nv[j] = gld4(a.ffn_norm + ic);
 #pragma unroll
-            for (int j = 0; j < PX; j++)
-                ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
-            for (int i = tid * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {
-                const float4 v = gld4(a.x + i);
-                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                for (int r = 0; r < RT_ROWS; r++)
+                    if (r < nrt) wv[j][r] = gld4(a.W + (int64_t)min(w * a.rt_rows + r, a.E - 1) * a.H + ic);
             }
-            ss = block_sum<WG>(ss, red);
-            const float scale = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+            float ss = 0.0f, p[RT_ROWS] = {};
 #pragma unroll
             for (int j = 0; j < PX; j++) {
                 const int i = tid * 4 + WG * 4 * j;
-                if (i < a.H)
-                    *(float4 *)(xs + i) = make_float4((xv[j].x * scale) * nv[j].x, (xv[j].y * scale) * nv[j].y,
-                                                      (xv[j].z * scale) * nv[j].z, (xv[j].w * scale) * nv[j].w);
+                if (i < a.H) *(float4 *)(xs + i) = router_acc(xv[j], nv[j], wv[j], nrt, ss, p);
             }
-            for (int i = tid * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {
-                const float4 v = gld4(a.x + i);
-                const float4 nw = gld4(a.ffn_norm + i);
-                *(float4 *)(xs + i) = make_float4((v.x * scale) * nw.x, (v.y * scale) * nw.y,
-                                                  (v.z * scale) * nw.z, (v.w * scale) * nw.w);
+            for (int i = tid * 4 + WG * 4 * PX; i < a.H; i += WG * 4) {  // rows past MB_MAX_H
+                float4 wt[RT_ROWS];
+#pragma unroll
+                for (int r = 0; r < RT_ROWS; r++)
+                    wt[r] = r < nrt ? gld4(a.W + (int64_t)min(w * a.rt_rows + r, a.E - 1) * a.H + i)
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                *(float4 *)(xs + i) = router_acc(gld4(a.x + i), gld4(a.ffn_norm + i), wt, nrt, ss, p);
             }
+            router_wave_part(ss, p, nrt, s_rt);
         }
         if (tid == 0) s_tag = ticket_tag(ticket, nwg, MB_TICKETS);
-        __syncthreads();
+        __syncthreads();  // s_rt, s_tag, xs
         tag = s_tag;
+        if (has_x) xscale = router_scale(s_rt, a.H, a.eps);
         stamp(1);
-
-        // ---- router logits (matvec_strided_f32, one row per wave)
-        if (router && rr < a.E) {
-            const float *wr = a.W + (int64_t)rr * a.H;
-            float acc = 0.0f;
-#pragma unroll
-            for (int j = 0; j < PW; j++) {
-                const int c = lane * 4 + 256 * j;
-                if (c < a.H) {
-                    const float4 xv4 = *(const float4 *)(xs + c);
-                    acc += wv[j].x * xv4.x + wv[j].y * xv4.y + wv[j].z * xv4.z + wv[j].w * xv4.w;
-                }
-            }
-            for (int c = lane * 4 + 256 * PW; c < a.H; c += 256) {
-                const float4 wq = gld4(wr + c);
-                const float4 xv4 = *(const float4 *)(xs + c);
-                acc += wq.x * xv4.x + wq.y * xv4.y + wq.z * xv4.z + wq.w * xv4.w;
-            }
-            acc = wave_sum(acc);
-            if (lane == 0) tput(a.t_lg + rr, tag, a.bias ? acc + gld(a.bias + rr) : acc);
+        // ---- router logits: thread r publishes row w * rt_rows + r
+        const int rr = w * a.rt_rows + tid;
+        if (tid < nrt && rr < a.E) {
+            const float lg = xscale * router_dot(s_rt, tid);
+            tput(a.t_lg + rr, tag, a.bias ? lg + gld(a.bias + rr) : lg);
         }
     };
     if (a.H <= 2048)
-        entry(std::integral_constant<int, 8>{}, std::integral_constant<int, 2>{});
+        entry(std::integral_constant<int, 2>{});
     else
-        entry(std::integral_constant<int, MB_MAX_H / 256>{}, std::integral_constant<int, MB_MAX_H / (4 * WG)>{});
+        entry(std::integral_constant<int, MB_MAX_H / (4 * WG)>{});
 
-    // ---- limbs of xn; shared-expert gate/up rows need no routing
+    // ---- limbs of x (.) w (before the routing wait: polling the logits
+    // while the router workgroups still load their rows slows those loads);
+    // the shared-expert gate/up rows need no routing
     auto nothing = [] {};
     if (has_x) {
         xq_build<WG>(xs, nullptr, 0.0f, false, a.H, xqx, red, nullptr);
         __syncthreads();
         stamp(2);
-        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), false, s_ids, xqx, tag, gus, nothing, tr);
+        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), false, s_ids, xqx, xscale, tag, gus, nothing, tr);
     }
 
     // ---- routing: every workgroup ranks the logits (topk_softmax_f32 order)
@@ -443,7 +422,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
 
     // ---- routed gate/up rows
     if (has_x)
-        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), true, s_ids, xqx, tag, gus, nothing, tr);
+        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), true, s_ids, xqx, xscale, tag, gus, nothing, tr);
     stamp(5);
 
     // ---- down: the slot's h (published by its gate/up workgroups) and its
@@ -491,7 +470,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     if (a.wqkv[0] && w >= a.nRed && w < a.nRed + a.n_q) {
         const int q0 = (w - a.nRed) * a.rpw_q;
         const int q1 = min(a.qkv_rows[0] + a.qkv_rows[1] + a.qkv_rows[2], q0 + a.rpw_q);
-        __syncthreads();  // the limbs of xn are no longer read (their LDS is reused)
+        __syncthreads();  // the limbs of x (.) w are no longer read (their LDS is reused)
         // rows per lane group in flight: all of them at the shapes served
         // (a single memory round trip), as the registers allow
         const bool ok = a.UPL_q == 1 ? qkv_rows<1, 3>(a, q0, q1, tag, lds + a.off_xq, tr)
@@ -547,7 +526,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         if (a.wts_out && w == 0) gst(a.wts_out + tid, wt);
     }
     if (shexp) {
-        const float d = block_sum<WG>(shd, red);
+        const float d = block_sum<WG>(shd, red) * xscale;  // xs is x (.) w unscaled
         if (tid == 0) s_sg = 1.0f / (1.0f + expf(-d));
     }
     __syncthreads();  // also: gus is reused for the partials
@@ -644,7 +623,6 @@ static bool moe_geometry(const MoeBlockArgs &h, int nwg, MoeBlockK &a, size_t &l
         h.k < 1 || h.k > MAX_TOPK || h.k > h.E || h.route.arena_mode)
         return false;
     a.nslots = h.k + (h.sh[0] ? 1 : 0);
-    a.nR = (h.E + MB_ROUTER_ROWS - 1) / MB_ROUTER_ROWS;
     a.nRed = (h.H + MB_RR - 1) / MB_RR;
     // one gate/up block per workgroup, its rows of both matrices (half the
     // waves each): the walker keeps the next MB_GU_ROWS rows per lane group
@@ -661,6 +639,12 @@ static bool moe_geometry(const MoeBlockArgs &h, int nwg, MoeBlockK &a, size_t &l
     a.rpw_d = std::max(ngrp_d, (rpw + ngrp_d - 1) / ngrp_d * ngrp_d);
     a.bps_d = (h.H + a.rpw_d - 1) / a.rpw_d;
     a.n_d = a.nslots * a.bps_d;
+    // one router row per workgroup while there are enough gate/up
+    // workgroups (each extra row lengthens its workgroup's entry loads),
+    // else up to RT_ROWS
+    a.rt_rows = (h.E + a.n_gu - 1) / a.n_gu;
+    if (a.rt_rows > RT_ROWS) return false;
+    a.nR = (h.E + a.rt_rows - 1) / a.rt_rows;
     // every workgroup that reads x at entry has gate/up work, whose outputs
     // the reduce (which rewrites x) waits on
     if (a.n_d > nwg || a.nR > a.n_gu || a.nRed > a.n_gu) return false;
