@@ -42,14 +42,20 @@ Geo pick_geo(int t, int ncols)
     if (!is_quant(t) || ncols % blk_elems(t) != 0) return g;
     const int units = ncols / blk_elems(t) * units_per_blk(t);
     const int max_upl = t == T_Q8_0 ? 4 : 2;
-    int best_waste = 1 << 30;
+    // lane groups of a power of two (a row's sum is then a butterfly of
+    // lane permutes within a DPP row; a group of 12 needed dependent LDS
+    // permutes), lanes past the row's units idle; the most lanes with units
+    // per wave wins, then the fewest units per lane
+    int best_used = -1;
     for (int upl = 1; upl <= max_upl; upl++) {
         if (units % upl) continue;
-        const int G = units / upl;
-        if (G > 64) continue;
-        const int waste = 64 - (64 / G) * G;
-        if (waste < best_waste) {
-            best_waste = waste;
+        const int Gu = units / upl;
+        if (Gu > 64) continue;
+        int G = 1;
+        while (G < Gu) G *= 2;
+        const int used = (64 / G) * Gu;
+        if (used > best_used) {
+            best_used = used;
             g.G = G;
             g.UPL = upl;
         }
