@@ -199,16 +199,36 @@ __device__ __forceinline__ GuPos gu_pos(const MoeBlockK &a, int b)
 // row, so a down workgroup waits for F words of its slot instead of 2F and
 // every gate/up workgroup carries the same mix of the two matrices' bytes.
 // gl holds 2 * rpw_gu floats of LDS.
+// With every expert in HBM (no remap), the slab of expert e is hot +
+// e * stride: the two are read from the arguments before the routing wait,
+// so only the id read stands between the ranking and the first loads.
+struct HotSlab {
+    const uint8_t *hot;
+    int64_t stride;
+};
+__device__ __forceinline__ HotSlab hot_slab(const MoeBlockK &a, int m)
+{
+    return a.route.remap ? HotSlab{nullptr, 0} : HotSlab{a.src[m].hot, a.src[m].hot_slab};
+}
+__device__ __forceinline__ const uint8_t *slot_slab(const MoeBlockK &a, const HotSlab &hs, int m,
+                                                    const int32_t *s_ids, int s)
+{
+    if (s >= a.k) return a.sh[m];
+    const int e = s_ids[s];
+    if (hs.hot) return (unsigned)e < (unsigned)a.E ? hs.hot + (int64_t)e * hs.stride : nullptr;
+    return routed_slab(a, a.src[m], e, s);
+}
+
 template <typename Between>
 __device__ __forceinline__ void gu_block(const MoeBlockK &a, const GuPos &bp, bool routed_phase,
-                                const int32_t *s_ids, const Xq &xqx, float xscale, uint32_t tag,
-                                float *gl, Between between, uint64_t *tr)
+                                const int32_t *s_ids, const HotSlab &hs, const Xq &xqx, float xscale,
+                                uint32_t tag, float *gl, Between between, uint64_t *tr)
 {
     const int s = bp.s, r0 = bp.r0, r1 = bp.r1;
     if ((s < a.k) != routed_phase) return;
     const int m = (int)(threadIdx.x >> 7);  // 0: gate (waves 0, 1), 1: up (waves 2, 3)
     if (routed_phase && tr && threadIdx.x == 0) tr[14] = wall_clock64();
-    const uint8_t *slab = s < a.k ? routed_slab(a, a.src[m], s_ids[s], s) : a.sh[m];
+    const uint8_t *slab = slot_slab(a, hs, m, s_ids, s);
     if (routed_phase && tr && threadIdx.x == 0) tr[15] = wall_clock64();
     float *dst = gl + m * a.rpw_gu;
     switch (m == 0 ? a.tg : a.tu) {
@@ -392,6 +412,9 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     else
         entry(std::integral_constant<int, MB_MAX_H / (4 * WG)>{});
 
+    // the slab rules of this workgroup's gate/up matrix and down rows
+    const HotSlab hs_gu = hot_slab(a, tid >> 7), hs_d = hot_slab(a, 2);
+
     // ---- limbs of x (.) w (before the routing wait: polling the logits
     // while the router workgroups still load their rows slows those loads);
     // the shared-expert gate/up rows need no routing
@@ -400,7 +423,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         xq_build<WG>(xs, nullptr, 0.0f, false, a.H, xqx, red, nullptr);
         __syncthreads();
         stamp(2);
-        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), false, s_ids, xqx, xscale, tag, gus, nothing, tr);
+        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), false, s_ids, hs_gu, xqx, xscale, tag, gus, nothing, tr);
     }
 
     // ---- routing: every workgroup ranks the logits (topk_softmax_f32 order)
@@ -417,12 +440,11 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
     // ---- this workgroup's down rows (their weights are issued after the
     // workgroup's own gate/up rows and before the wait for the slot's
     // outputs; issuing them during the gate/up phase delays that stream)
-    const uint8_t *dslab = nullptr;
-    if (has_d) dslab = ds < a.k ? routed_slab(a, a.src[2], s_ids[ds], ds) : a.sh[2];
+    const uint8_t *dslab = has_d ? slot_slab(a, hs_d, 2, s_ids, ds) : nullptr;
 
     // ---- routed gate/up rows
     if (has_x)
-        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), true, s_ids, xqx, xscale, tag, gus, nothing, tr);
+        for (int b = w; b < a.n_gu; b += nwg) gu_block(a, b == w ? gp0 : gu_pos(a, b), true, s_ids, hs_gu, xqx, xscale, tag, gus, nothing, tr);
     stamp(5);
 
     // ---- down: the slot's h (published by its gate/up workgroups) and its
