@@ -577,12 +577,16 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         flush();
         return;
     }
-    const float sq = block_sum<WG>(hr ? xv * xv : 0.0f, red);
-    if (tid == 0) gst(a.ss + w, sq);
+    // x (.) w_next for the limbs and the x^2 sums of the waves, behind one
+    // barrier (red and hs are free: the partials' wait has passed barriers
+    // since their last use); the four sums in block_sum's order
     float *xw = hs;  // MB_RR floats
-    __syncthreads();
     xw[tid] = xv * nw;
+    const float sqw = wave_sum(hr ? xv * xv : 0.0f);
+    if (lane == 0) red[wave] = sqw;
     __syncthreads();
+    const float sq = ((red[0] + red[1]) + red[2]) + red[3];
+    if (tid == 0) gst(a.ss + w, sq);
     if (!a.wqkv[0]) {
         if (tid < MB_RR / 4) {  // four rows per thread: 64 threads at work
             const bool act = 4 * tid < nrow;
@@ -592,18 +596,17 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
             xq_group4(h, act, tid, xq_shift(a.xq, r0));
         }
     } else {
-        // the limbs of these rows built in LDS (gus is free), then written
-        // to the limb buffer and as tagged words for the q/k/v workgroups
-        const Xq ql = xq_at(gus, MB_RR);
+        // the limbs of these rows, written to the limb buffer and published
+        // as tagged words for the q/k/v workgroups by the threads that form
+        // them
         if (tid < MB_RR / 4) {  // four rows per thread: 64 threads at work
             const bool act = 4 * tid < nrow;
             float h[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) h[i] = act ? xw[4 * tid + i] : 0.0f;
-            xq_group4(h, act, tid, ql);
+            xq_group4_put(h, act, tid, xq_shift(a.xq, r0), a.H, r0,
+                          [&](int i, uint32_t v) { tput(a.t_xq + i, tag, __uint_as_float(v)); });
         }
-        __syncthreads();
-        xq_publish(ql, nrow, r0, a.H, a.xq, a.t_xq, tag);
         if (tid == 0) tput(a.t_xq + xq_bytes(a.H) / 4 + w, tag, sq);
     }
     stamp(10);

@@ -163,6 +163,55 @@ __device__ __forceinline__ void xq_group4(const float *v, bool act, int g, Xq q)
     if ((g & 3) == 0) q.s16[g >> 2] = s16;
 }
 
+// xq_group4 with the group's limbs written straight to the limb buffer q
+// (shifted to the vector's element e0) and published as tagged words in t,
+// laid out as the 32-bit words of xq_at(., N): A | B | C | sx | s16 (the
+// layout of xq_publish), with no LDS pass.  tput is the caller's tagged
+// store (xchg.h).
+template <typename Put>
+__device__ __forceinline__ void xq_group4_put(const float *v, bool act, int g, Xq q, int N, int e0,
+                                              Put tput)
+{
+    float am = 0.0f, s4 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        am = fmaxf(am, fabsf(v[i]));
+        s4 += v[i];
+    }
+    am = bfly<8>(am, [](float a, float b) { return fmaxf(a, b); });
+    const float s16 = bfly_sum<4>(s4);
+    if (!act) return;
+    const float inv = am > 0.0f ? 127.0f / am : 0.0f;
+    uint32_t pa = 0, pb = 0, pc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float y = v[i] * inv;
+        const float a = rintf(y);
+        const float r1 = (y - a) * 254.0f;
+        const float b = rintf(r1);
+        const float c = fminf(fmaxf(rintf((r1 - b) * 254.0f), -127.0f), 127.0f);
+        pa |= ((uint32_t)(int)a & 0xFFu) << (8 * i);
+        pb |= ((uint32_t)(int)b & 0xFFu) << (8 * i);
+        pc |= ((uint32_t)(int)c & 0xFFu) << (8 * i);
+    }
+    const int N4 = N / 4, o = e0 / 4 + g;
+    *(uint32_t *)(q.A + 4 * g) = pa;
+    *(uint32_t *)(q.B + 4 * g) = pb;
+    *(uint32_t *)(q.C + 4 * g) = pc;
+    tput(o, pa);
+    tput(N4 + o, pb);
+    tput(2 * N4 + o, pc);
+    if ((g & 7) == 0) {
+        const float sx = am / 127.0f;
+        q.sx[g >> 3] = sx;
+        tput(3 * N4 + e0 / 32 + (g >> 3), __float_as_uint(sx));
+    }
+    if ((g & 3) == 0) {
+        q.s16[g >> 2] = s16;
+        tput(3 * N4 + N / 32 + e0 / 16 + (g >> 2), __float_as_uint(s16));
+    }
+}
+
 // Build the limb form of xn = norm ? x * rsqrt(mean(x^2)+eps) * w : x
 // (n a multiple of 32).  If xn_out is non-null the normalised f32 vector is
 // also written there.  Thread t owns 8 consecutive values per pass.
