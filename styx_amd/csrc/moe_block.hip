@@ -124,7 +124,7 @@ __device__ __forceinline__ bool route_by_quarters(const MoeBlockK &a, uint32_t t
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (!failed) rank_quarter(q_key + wave * Q, Q, k, c_key + wave * k);
+    if (!failed) rank_quarter_any(q_key + wave * Q, Q, k, c_key + wave * k);
     if (lane == 0) q_fail[wave] = failed;
     __syncthreads();
     int any = 0;
@@ -133,7 +133,7 @@ __device__ __forceinline__ bool route_by_quarters(const MoeBlockK &a, uint32_t t
         if (tid == 0) abort_raise(a.abort);
         return false;
     }
-    rank_candidates(c_key, k, s_ids);
+    rank_candidates_any(c_key, k, s_ids);
     __syncthreads();
     if (publish) publish_id_row(a.route, s_ids);
     return true;

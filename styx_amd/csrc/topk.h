@@ -186,6 +186,73 @@ __device__ __forceinline__ void rank_candidates(const uint64_t *c_key, int k, in
     }
 }
 
+// The two stages with the quarter Q (a power of two <= 32) and k <= 8 known
+// at compile time: every LDS read of a thread's compares is issued before
+// the first compare (in the loops above each read waited in turn), and the
+// P lanes of a key sum their counts with DPP quad permutes.  Same compares,
+// same results.
+template <int Q>
+__device__ __forceinline__ void rank_quarter_q(const uint64_t *q, int k, uint64_t *cand)
+{
+    constexpr int P = (64 / Q < Q / 2) ? 64 / Q : Q / 2, SPAN = Q / P;
+    static_assert(P >= 2 && P <= 4 && SPAN % 2 == 0, "quarter geometry");
+    const int lane = threadIdx.x & 63;
+    const int e = lane / P, part = lane - e * P;
+    int cnt = 0;
+    uint64_t mk = 0;
+    if (e < Q) {
+        mk = q[e];
+        const ulonglong2 *qq = (const ulonglong2 *)(q + part * SPAN);
+        ulonglong2 u[SPAN / 2];
+#pragma unroll
+        for (int j2 = 0; j2 < SPAN / 2; j2++) u[j2] = qq[j2];
+#pragma unroll
+        for (int j2 = 0; j2 < SPAN / 2; j2++) cnt += (int)(u[j2].x > mk) + (int)(u[j2].y > mk);
+    }
+    cnt += (int)dpp_u<0xB1>((uint32_t)cnt);  // lane ^ 1
+    if constexpr (P == 4) cnt += (int)dpp_u<0x4E>((uint32_t)cnt);  // lane ^ 2
+    if (e < Q && part == 0 && cnt < k) cand[cnt] = mk;
+}
+template <int K>
+__device__ __forceinline__ void rank_candidates_k(const uint64_t *c_key, int32_t *s_ids)
+{
+    const int tid = threadIdx.x;
+    if (tid < 4 * K) {
+        const uint64_t ck = c_key[tid];
+        ulonglong2 u[2 * K];
+#pragma unroll
+        for (int j2 = 0; j2 < 2 * K; j2++) u[j2] = ((const ulonglong2 *)c_key)[j2];
+        int c2 = 0;
+#pragma unroll
+        for (int j2 = 0; j2 < 2 * K; j2++) c2 += (int)(u[j2].x > ck) + (int)(u[j2].y > ck);
+        if (ck != 0 && c2 < K) s_ids[c2] = (int32_t)(0xFFFFFFFFu - (uint32_t)ck);
+    }
+}
+__device__ __forceinline__ void rank_quarter_any(const uint64_t *q, int Q, int k, uint64_t *cand)
+{
+    switch (Q) {
+    case 32: rank_quarter_q<32>(q, k, cand); break;
+    case 16: rank_quarter_q<16>(q, k, cand); break;
+    case 8: rank_quarter_q<8>(q, k, cand); break;
+    case 4: rank_quarter_q<4>(q, k, cand); break;
+    default: rank_quarter(q, Q, k, cand); break;
+    }
+}
+__device__ __forceinline__ void rank_candidates_any(const uint64_t *c_key, int k, int32_t *s_ids)
+{
+    switch (k) {
+    case 1: rank_candidates_k<1>(c_key, s_ids); break;
+    case 2: rank_candidates_k<2>(c_key, s_ids); break;
+    case 3: rank_candidates_k<3>(c_key, s_ids); break;
+    case 4: rank_candidates_k<4>(c_key, s_ids); break;
+    case 5: rank_candidates_k<5>(c_key, s_ids); break;
+    case 6: rank_candidates_k<6>(c_key, s_ids); break;
+    case 7: rank_candidates_k<7>(c_key, s_ids); break;
+    case 8: rank_candidates_k<8>(c_key, s_ids); break;
+    default: rank_candidates(c_key, k, s_ids); break;
+    }
+}
+
 // The whole 64-int id row of the routed slots s_ids[0..k) to r.ids_out
 // (orig | hot | arena | host, topk_softmax_f32.comp:4-17) by threads < 64.
 __device__ __forceinline__ void publish_id_row(const Route &r, const int32_t *s_ids)
@@ -240,9 +307,9 @@ __device__ inline const int32_t *rank_ids_lds(const Route &r, int32_t *s_ids, co
         // candidates are ranked among themselves
         for (int e = tid; e < E; e += 256) s_key[e] = rank_key(s_lg[e], e);
         __syncthreads();
-        rank_quarter(s_key + q0, Q, k, c_key + wave * k);
+        rank_quarter_any(s_key + q0, Q, k, c_key + wave * k);
         __syncthreads();
-        rank_candidates(c_key, k, s_ids);
+        rank_candidates_any(c_key, k, s_ids);
     } else if (E <= 128) {
         // direct: P = 256 / E threads rank each key against a slice of all
         for (int e = tid; e < E; e += 256) s_key[e] = rank_key(s_lg[e], e);
