@@ -13,6 +13,7 @@ placement invariance of scripts/verify.sh:57-78).
   pinned host memory under a 6 GiB HBM budget, cold slabs read in place or
   gathered into the arena: logits bit-identical to all-in-HBM, hot + cold
   = tokens x 48 x 8.
+  The same routing and placement at 4 layers against the oracle.
 * the 235B-A22B layer shape (H 4096, 64/4 heads, E 128 top-8,
   F 1536, q4_K experts; 2 of its 94 layers) at 512 and 32768 tokens of
   context: per-layer hidden states and logits against the oracle.
@@ -149,6 +150,60 @@ def test_config3_host_pinned_6gib_identical(gpu, tmp_path, arena):
     print("\n".join(hud))
     assert sum(int(v) for v in re.findall(r"\((\d+)\)", hud[0])) == 12672
     assert re.match(r"^hud: cold/layer \[[.0-9]{48}\]", hud[1])
+    m.close()
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("arena", [False, True])
+def test_config3_zipf_host_pinned_against_oracle(gpu, tmp_path, arena):
+    """configs[2]'s routing and placement at configs[1]'s layer shape on 4
+    layers, against the oracle (the tests above hold the full-size run to
+    the all-in-HBM one): Zipf(1.1) router bias, experts in pinned host
+    memory under a 160 MiB HBM budget (about a tenth of the 512 (layer,
+    expert) slabs hot, by the bias ranking), cold slabs read in place by the fused block or
+    gathered into the arena; at every position each layer's residual and
+    the logits within 1e-4 of the oracle with the same bias, routed ids
+    identical outside counted near-ties, and both hot and cold slabs used."""
+    from oracle import oracle as O
+    from styx_amd import CFG_30B_A3B, MoeModel
+    O.set_threads(16)
+    cfg = replace(CFG_30B_A3B, n_layers=4, router_zipf_s=1.1)
+    rng = np.random.default_rng(0x21BF)
+    prompt = rng.integers(0, cfg.n_vocab, 6).astype(np.uint32).tolist()
+    n_ctx = 32
+    ref = MoeModel.synth(gpu, cfg, n_ctx=n_ctx)
+    rows = ["layer,expert,hits"]
+    for l in range(cfg.n_layers):
+        b = ref.export_tensor(f"blk.{l}.ffn_gate_inp.bias")[2].view(np.float32)
+        rows += [f"{l},{e},{int(round(1e6 * np.exp(b[e])))}" for e in range(len(b))]
+    hist = tmp_path / "zipf_hist.csv"
+    hist.write_text("\n".join(rows) + "\n")
+    orc = oracle_from_model(ref, n_ctx)
+    ref.close()
+    m = MoeModel.synth(gpu, cfg, n_ctx=n_ctx, record_hidden=True, expert_budget_mb=160,
+                       expert_hist=str(hist), arena=arena, fuse=not arena)
+    assert m.hp.expert_bytes_host > 0 and m.hp.expert_bytes_hbm > 0
+    tally = Tally()
+    hot = cold = 0
+    feed = list(prompt)
+    for pos in range(len(prompt) + 6):
+        t = feed[pos]
+        lg = m.forward_token(t)
+        hid = m.last_hidden()
+        ol, oh, oids, margins = orc.forward(pos, t, want_hidden=True)
+        assert rel_l2(lg, ol) < TOL, pos
+        for l in range(hid.shape[0]):
+            assert rel_l2(hid[l], oh[l]) < TOL, (pos, l)
+        tally.ids(m.last_expert_ids(), oids, margins, pos)
+        hc = m.last_hot_cold()
+        hot += int(hc[:, 0].sum())
+        cold += int(hc[:, 1].sum())
+        if pos >= len(prompt) - 1:
+            feed.append(int(np.argmax(ol)))
+    tally.bound()
+    print(f"\nconfigs[2] routing, 4 layers, arena={arena}: hit rate {hot / (hot + cold):.3f}, "
+          f"ids checked {tally.checked}, near-ties skipped {tally.skipped}")
+    assert hot > 0 and cold > 0
     m.close()
 
 
