@@ -252,7 +252,9 @@ __device__ __forceinline__ void gu_block(const MoeBlockK &a, const GuPos &bp, bo
 // reduce workgroups' tagged words into LDS, then the rows are formed as
 // k_mv_dense forms them (dot times the RMSNorm scale) and stored for the
 // next kernel.  Returns false when the wait was abandoned.
-template <int UPL, int NR>
+// GC: the lane-group width when known at compile time (the rows' sums
+// and lane map then fold to constants), 0: a.G_q.
+template <int UPL, int NR, int GC>
 __device__ __forceinline__ bool qkv_rows(const MoeBlockK &a, int r0, int r1, uint32_t tag, uint8_t *xq_lds,
                          uint64_t *tr)
 {
@@ -262,7 +264,7 @@ __device__ __forceinline__ bool qkv_rows(const MoeBlockK &a, int r0, int r1, uin
                   mat_at(a.wqkv[2], T_Q8_0, (int64_t)a.qkv_rows[2] * a.nb_q), b1, b2, a.nb_q);
     float scale = 0.0f;
     return walk_rows_pipelined<T_Q8_0, UPL, NR>(
-        at, a.nb_q, a.G_q, r0, r1,
+        at, a.nb_q, GC ? GC : a.G_q, r0, r1,
         [&](UX<T_Q8_0>(&x)[UPL], const LaneU<UPL> &lu) {
             // the limbs (A | B | C | sx | s16, the layout of xq_at) and the
             // partials
@@ -495,8 +497,11 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         __syncthreads();  // the limbs of x (.) w are no longer read (their LDS is reused)
         // rows per lane group in flight: all of them at the shapes served
         // (a single memory round trip), as the registers allow
-        const bool ok = a.UPL_q == 1 ? qkv_rows<1, 3>(a, q0, q1, tag, lds + a.off_xq, tr)
-                                     : qkv_rows<2, 3>(a, q0, q1, tag, lds + a.off_xq, tr);
+        const bool ok =
+            a.G_q == 64 ? (a.UPL_q == 1 ? qkv_rows<1, 3, 64>(a, q0, q1, tag, lds + a.off_xq, tr)
+                                        : qkv_rows<2, 3, 64>(a, q0, q1, tag, lds + a.off_xq, tr))
+                        : (a.UPL_q == 1 ? qkv_rows<1, 3, 0>(a, q0, q1, tag, lds + a.off_xq, tr)
+                                        : qkv_rows<2, 3, 0>(a, q0, q1, tag, lds + a.off_xq, tr));
         if (!ok) return;
         stamp(10);
         flush();
