@@ -34,16 +34,18 @@ struct LaneMap {
 };
 
 // Lane groups of G lanes over the waves [wave0, wave0 + nwaves) of the
-// workgroup (the calling wave must be one of them).
+// workgroup (the calling wave must be one of them).  G is a power of two
+// (pick_geo): shifts and masks, no integer division.
 __device__ __forceinline__ LaneMap lane_map(int G, int nwaves = WAVES, int wave0 = 0)
 {
     LaneMap m;
+    const int lg = __builtin_ctz((unsigned)G);
     m.lane = threadIdx.x & 63;
     m.wave = (int)(threadIdx.x >> 6) - wave0;
-    m.gpw = 64 / G;
-    m.grp = m.lane / G;
-    m.gl = m.lane - m.grp * G;
-    m.ok = m.grp < m.gpw;
+    m.gpw = 64 >> lg;
+    m.grp = m.lane >> lg;
+    m.gl = m.lane & (G - 1);
+    m.ok = true;
     m.gid = m.wave * m.gpw + m.grp;
     m.ngrp = nwaves * m.gpw;
     return m;
