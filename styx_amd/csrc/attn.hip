@@ -54,7 +54,12 @@ __device__ __forceinline__ int64_t kv_row(const AttnArgs &a, int64_t pg, int tp,
 }
 __device__ __forceinline__ int64_t kv_off(const AttnArgs &a, int t, int kvh, int kv_dim)
 {
-    return kv_row(a, a.page_table[t / a.page_tokens], t % a.page_tokens, kvh, kv_dim);
+    const int pt = a.page_tokens;
+    if ((pt & (pt - 1)) == 0) {  // a power of two (the engine's pages): no division
+        const int sh = __builtin_ctz((unsigned)pt);
+        return kv_row(a, a.page_table[t >> sh], t & (pt - 1), kvh, kv_dim);
+    }
+    return kv_row(a, a.page_table[t / pt], t % pt, kvh, kv_dim);
 }
 
 // One head's RMSNorm(hd) * w and NEOX rope at pos, split into a load phase
@@ -705,8 +710,9 @@ static_assert(ATTN_PT_FAST % AT_WG == 0, "whole entries per thread");
 __device__ __forceinline__ constexpr int kcol(int g, int m) { return 16 * (m >> 2) + 4 * g + (m & 3); }
 __device__ __forceinline__ constexpr int vcol(int r, int b) { return 64 * (b >> 2) + 4 * r + (b & 3); }
 
-// FAST: the launch gives the rope row of the position (AttnArgs::rope_row)
-// and a page table of 1 to ATTN_PT_FAST entries (page_table_len).  The
+// FAST: the launch gives the rope row of the position (AttnArgs::rope_row),
+// a page table of 1 to ATTN_PT_FAST entries (page_table_len) and pages of a
+// power of two of tokens.  The
 // table is then copied to LDS with the first loads and every K/V address
 // comes from LDS; otherwise the position's rope row and the page entries
 // past the minimum chunk size are read after the position.
@@ -735,7 +741,8 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     __shared__ int32_t s_pt[PT_CAP];
     int32_t pte[PT_PER];
     int32_t pe_min = 0;
-    const int t_min = c * a.chunk + wave * 16 + lr, pg_min = t_min / a.page_tokens;
+    const int t_min = c * a.chunk + wave * 16 + lr;
+    const int pg_min = FAST ? 0 : t_min / a.page_tokens;  // (the early entry: generic launches)
     const bool spec = pg_min < pt_n;
     double2 cs[1];
     if constexpr (FAST) {
@@ -796,7 +803,11 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     int tb = t0 + wave * 16;
     float kv[MHD / 4];     // K[tb + lr][kcol(lg, m)]
     float vvr[4][MNB];     // V[tb + 4q + lg][vcol(lr, b)]
+    // (FAST: page_tokens is a power of two, so the page and the row within
+    // it are a shift and a mask)
+    const int pshift = FAST ? __builtin_ctz((unsigned)a.page_tokens) : 0;
     auto kv_at = [&](int t) -> int64_t {
+        if (FAST) return kv_row(a, s_pt[t >> pshift], t & (a.page_tokens - 1), kvh, kv_dim);
         if (!pt_lds) return kv_off(a, t, kvh, kv_dim);
         return kv_row(a, s_pt[t / a.page_tokens], t % a.page_tokens, kvh, kv_dim);
     };
@@ -1139,7 +1150,8 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
     if (use_mfma) {
         const size_t lds = sizeof(float) * ((size_t)MH * MHD + 2 * MHD + AT_WAVES * MH * 16 +
                                             (size_t)AT_WAVES * MH * MHD + 2 * AT_WAVES * MH);
-        if (a.rope_row && a.page_table_len >= 1 && a.page_table_len <= ATTN_PT_FAST)
+        if (a.rope_row && a.page_table_len >= 1 && a.page_table_len <= ATTN_PT_FAST &&
+            (a.page_tokens & (a.page_tokens - 1)) == 0)
             hipLaunchKernelGGL(k_attn_mfma<true>, dim3(am.max_chunks, am.nkv), dim3(AT_WG), lds, st, am);
         else
             hipLaunchKernelGGL(k_attn_mfma<false>, dim3(am.max_chunks, am.nkv), dim3(AT_WG), lds, st, am);
