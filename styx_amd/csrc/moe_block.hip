@@ -470,17 +470,27 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
             __syncthreads();
             stamp(7);
         };
+        // the walk with the lane-group width a compile-time constant for the
+        // widths of the configs' down rows (16: F 768 and 512 at one unit
+        // per lane; 32: F 1536), so that its lane map and row sums fold
+        auto down_walk = [&](auto gc) {
+            constexpr int GC = decltype(gc)::value;
+            return walk_rows_pipelined<TD, UD, UD == 1 ? 2 : 1>(
+                OneMat{mat_at(dslab, TD, (int64_t)a.H * a.nb_d), a.nb_d}, a.nb_d, GC ? GC : a.G_d,
+                d0, d1,
+                [&](UX<TD>(&x)[UD], const LaneU<UD> &lu) {
+                    if (!wait_gu()) return false;
+                    build();
+                    XFrom<TD, UD>{xqh}(x, lu);
+                    return true;
+                },
+                [&](int r, float v) { tput(part + r, tag, v); });
+        };
         if (dslab) {
-            if (!walk_rows_pipelined<TD, UD, UD == 1 ? 2 : 1>(
-                    OneMat{mat_at(dslab, TD, (int64_t)a.H * a.nb_d), a.nb_d}, a.nb_d, a.G_d, d0, d1,
-                    [&](UX<TD>(&x)[UD], const LaneU<UD> &lu) {
-                        if (!wait_gu()) return false;
-                        build();
-                        XFrom<TD, UD>{xqh}(x, lu);
-                        return true;
-                    },
-                    [&](int r, float v) { tput(part + r, tag, v); }))
-                return;
+            const bool ok = a.G_d == 16   ? down_walk(std::integral_constant<int, 16>{})
+                            : a.G_d == 32 ? down_walk(std::integral_constant<int, 32>{})
+                                          : down_walk(std::integral_constant<int, 0>{});
+            if (!ok) return;
         } else {
             if (!wait_gu()) return;
             build();
