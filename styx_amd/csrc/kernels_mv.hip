@@ -137,7 +137,10 @@ struct DenseK {
 // flight, of more rows where a lane holds fewer units.
 template <int UPL> constexpr int dense_nr() { return UPL <= 2 ? 2 : 1; }
 
-template <int T, int UPL>
+// GC: the lane-group width when it is 64 (a whole wave per row: q/k/v,
+// o-proj and LM head of the configs), known at compile time so that the
+// walk's lane map and row sums fold; 0: a.G.
+template <int T, int UPL, int GC>
 __global__ void __launch_bounds__(WG) k_mv_dense(DenseK a)
 {
     const int r_begin = blockIdx.x * a.rpw, r_end = min(a.total, r_begin + a.rpw);
@@ -185,10 +188,10 @@ __global__ void __launch_bounds__(WG) k_mv_dense(DenseK a)
         if (a.amax) best = max(best, argmax_key(v, (uint32_t)r));
     };
     if (a.nseg == 1)
-        walk_rows_pipelined<T, UPL, dense_nr<UPL>()>(OneMat{m0, a.nb}, a.nb, a.G, r_begin, r_end,
+        walk_rows_pipelined<T, UPL, dense_nr<UPL>()>(OneMat{m0, a.nb}, a.nb, GC ? GC : a.G, r_begin, r_end,
                                                       xload, emit);
     else
-        walk_rows_pipelined<T, UPL, dense_nr<UPL>()>(Mat3(m0, m1, m2, b1, b2, a.nb), a.nb, a.G,
+        walk_rows_pipelined<T, UPL, dense_nr<UPL>()>(Mat3(m0, m1, m2, b1, b2, a.nb), a.nb, GC ? GC : a.G,
                                                       r_begin, r_end, xload, emit);
     if (early) {
         __syncthreads();
@@ -237,10 +240,18 @@ hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, 
     a.rpw = rows_per_wg(a.total, g.G, 1024);
     const dim3 grid((a.total + a.rpw - 1) / a.rpw);
     switch (t) {
-    case T_Q8_0: upl_dispatch<T_Q8_0>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_mv_dense<T_Q8_0, decltype(u)::value>), grid, dim3(WG), 0, st, a); }); break;
-    case T_Q4_K: upl_dispatch<T_Q4_K>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_mv_dense<T_Q4_K, decltype(u)::value>), grid, dim3(WG), 0, st, a); }); break;
-    case T_Q5_K: upl_dispatch<T_Q5_K>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_mv_dense<T_Q5_K, decltype(u)::value>), grid, dim3(WG), 0, st, a); }); break;
-    case T_Q6_K: upl_dispatch<T_Q6_K>(g.UPL, [&](auto u) { hipLaunchKernelGGL((k_mv_dense<T_Q6_K, decltype(u)::value>), grid, dim3(WG), 0, st, a); }); break;
+    case T_Q8_0: upl_dispatch<T_Q8_0>(g.UPL, [&](auto u) {
+        if (g.G == 64) hipLaunchKernelGGL((k_mv_dense<T_Q8_0, decltype(u)::value, 64>), grid, dim3(WG), 0, st, a);
+        else hipLaunchKernelGGL((k_mv_dense<T_Q8_0, decltype(u)::value, 0>), grid, dim3(WG), 0, st, a); }); break;
+    case T_Q4_K: upl_dispatch<T_Q4_K>(g.UPL, [&](auto u) {
+        if (g.G == 64) hipLaunchKernelGGL((k_mv_dense<T_Q4_K, decltype(u)::value, 64>), grid, dim3(WG), 0, st, a);
+        else hipLaunchKernelGGL((k_mv_dense<T_Q4_K, decltype(u)::value, 0>), grid, dim3(WG), 0, st, a); }); break;
+    case T_Q5_K: upl_dispatch<T_Q5_K>(g.UPL, [&](auto u) {
+        if (g.G == 64) hipLaunchKernelGGL((k_mv_dense<T_Q5_K, decltype(u)::value, 64>), grid, dim3(WG), 0, st, a);
+        else hipLaunchKernelGGL((k_mv_dense<T_Q5_K, decltype(u)::value, 0>), grid, dim3(WG), 0, st, a); }); break;
+    case T_Q6_K: upl_dispatch<T_Q6_K>(g.UPL, [&](auto u) {
+        if (g.G == 64) hipLaunchKernelGGL((k_mv_dense<T_Q6_K, decltype(u)::value, 64>), grid, dim3(WG), 0, st, a);
+        else hipLaunchKernelGGL((k_mv_dense<T_Q6_K, decltype(u)::value, 0>), grid, dim3(WG), 0, st, a); }); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
