@@ -716,7 +716,10 @@ __device__ __forceinline__ constexpr int vcol(int r, int b) { return 64 * (b >> 
 // table is then copied to LDS with the first loads and every K/V address
 // comes from LDS; otherwise the position's rope row and the page entries
 // past the minimum chunk size are read after the position.
-template <bool FAST>
+// GQ: the query heads per kv head when known at compile time (8 or 16 on
+// FAST launches: the merge and output loops then have constant bounds), 0:
+// a.nh / a.nkv.
+template <bool FAST, int GQ>
 __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
 {
     const int c = blockIdx.x, kvh = blockIdx.y;
@@ -726,7 +729,7 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
     st.at(0);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;  // row-lane, k-group
-    const int gqa = a.nh / a.nkv, kv_dim = a.nkv * MHD;
+    const int gqa = GQ ? GQ : a.nh / a.nkv, kv_dim = a.nkv * MHD;
     // The position goes through the scalar cache (the kernel never writes
     // it), so its wait counts scalar loads only.  The vector loads are
     // issued in the order they are needed, each of them on every path (a
@@ -1150,11 +1153,18 @@ hipError_t launch_attn_decode(hipStream_t st, const AttnArgs &a)
     if (use_mfma) {
         const size_t lds = sizeof(float) * ((size_t)MH * MHD + 2 * MHD + AT_WAVES * MH * 16 +
                                             (size_t)AT_WAVES * MH * MHD + 2 * AT_WAVES * MH);
+        const dim3 grid(am.max_chunks, am.nkv);
         if (a.rope_row && a.page_table_len >= 1 && a.page_table_len <= ATTN_PT_FAST &&
-            (a.page_tokens & (a.page_tokens - 1)) == 0)
-            hipLaunchKernelGGL(k_attn_mfma<true>, dim3(am.max_chunks, am.nkv), dim3(AT_WG), lds, st, am);
-        else
-            hipLaunchKernelGGL(k_attn_mfma<false>, dim3(am.max_chunks, am.nkv), dim3(AT_WG), lds, st, am);
+            (a.page_tokens & (a.page_tokens - 1)) == 0) {
+            if (gqa == 8)
+                hipLaunchKernelGGL((k_attn_mfma<true, 8>), grid, dim3(AT_WG), lds, st, am);
+            else if (gqa == 16)
+                hipLaunchKernelGGL((k_attn_mfma<true, 16>), grid, dim3(AT_WG), lds, st, am);
+            else
+                hipLaunchKernelGGL((k_attn_mfma<true, 0>), grid, dim3(AT_WG), lds, st, am);
+        } else {
+            hipLaunchKernelGGL((k_attn_mfma<false, 0>), grid, dim3(AT_WG), lds, st, am);
+        }
     } else {
     // head groups: the largest of 4, 2, 1 dividing gqa
     const int nhg = gqa % 4 == 0 ? 4 : gqa % 2 == 0 ? 2 : 1;
