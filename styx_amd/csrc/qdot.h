@@ -90,6 +90,43 @@ template <int NT = 0> __device__ inline float block_sum(float v, float *red)
     return t;
 }
 
+// The three int8 limbs of four values v scaled by inv, packed four to a
+// dword (value i in byte i):
+//   a = rint(v inv), d = v inv - a (one fused rounding),
+//   b = rint(254 d), c = rint(254 (254 d - b)) (the inner one fused).
+// Every rounding adds 1.5 * 2^23: the sum is the value rounded to the
+// nearest integer, ties to even (as rintf), and its low byte is that
+// integer as an int8; subtracting 1.5 * 2^23 again gives the rounded value
+// exactly.  |v inv| <= 127 (inv = 127 / max |v|) and |d|, |254 d - b| are
+// within 1/2 of a unit, so every limb lies in [-127, 127].  Contraction is
+// off: only the two fmaf calls fuse.
+__device__ __forceinline__ uint32_t pack_low_bytes(const uint32_t (&t)[4])
+{
+    const uint32_t lo = __builtin_amdgcn_perm(t[1], t[0], 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(t[3], t[2], 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+__device__ __forceinline__ void limbs3x4(const float *v, float inv, uint32_t &pa, uint32_t &pb,
+                                         uint32_t &pc)
+{
+#pragma clang fp contract(off)
+    constexpr float M = 12582912.0f;
+    uint32_t ta[4], tb[4], tc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float t1 = v[i] * inv + M;
+        const float d = fmaf(v[i], inv, -(t1 - M));
+        const float t2 = d * 254.0f + M;
+        const float t3 = fmaf(d, 254.0f, -(t2 - M)) * 254.0f + M;
+        ta[i] = __float_as_uint(t1);
+        tb[i] = __float_as_uint(t2);
+        tc[i] = __float_as_uint(t3);
+    }
+    pa = pack_low_bytes(ta);
+    pb = pack_low_bytes(tb);
+    pc = pack_low_bytes(tc);
+}
+
 // Limbs of one group of 8 consecutive values (group g of the vector q).
 // Four consecutive lanes hold the four groups of one 32-value block (groups
 // are 4-aligned); all four must call this together.  Inactive groups pass
@@ -108,19 +145,9 @@ __device__ __forceinline__ void xq_group(const float *v, bool act, int g, Xq q)
     const float s16 = s8 + dpp_f<0xB1>(s8);
     if (!act) return;
     const float inv = am > 0.0f ? 127.0f / am : 0.0f;
-    uint32_t pa[2] = {0, 0}, pb[2] = {0, 0}, pc[2] = {0, 0};
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float y = v[i] * inv;
-        const float a = rintf(y);
-        const float r1 = (y - a) * 254.0f;
-        const float b = rintf(r1);
-        const float c = fminf(fmaxf(rintf((r1 - b) * 254.0f), -127.0f), 127.0f);
-        const int sh = 8 * (i & 3);
-        pa[i >> 2] |= ((uint32_t)(int)a & 0xFFu) << sh;
-        pb[i >> 2] |= ((uint32_t)(int)b & 0xFFu) << sh;
-        pc[i >> 2] |= ((uint32_t)(int)c & 0xFFu) << sh;
-    }
+    uint32_t pa[2], pb[2], pc[2];
+    limbs3x4(v, inv, pa[0], pb[0], pc[0]);
+    limbs3x4(v + 4, inv, pa[1], pb[1], pc[1]);
     *(uint2 *)(q.A + 8 * g) = make_uint2(pa[0], pa[1]);
     *(uint2 *)(q.B + 8 * g) = make_uint2(pb[0], pb[1]);
     *(uint2 *)(q.C + 8 * g) = make_uint2(pc[0], pc[1]);
@@ -144,18 +171,8 @@ __device__ __forceinline__ void xq_group4(const float *v, bool act, int g, Xq q)
     const float s16 = bfly_sum<4>(s4);
     if (!act) return;
     const float inv = am > 0.0f ? 127.0f / am : 0.0f;
-    uint32_t pa = 0, pb = 0, pc = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float y = v[i] * inv;
-        const float a = rintf(y);
-        const float r1 = (y - a) * 254.0f;
-        const float b = rintf(r1);
-        const float c = fminf(fmaxf(rintf((r1 - b) * 254.0f), -127.0f), 127.0f);
-        pa |= ((uint32_t)(int)a & 0xFFu) << (8 * i);
-        pb |= ((uint32_t)(int)b & 0xFFu) << (8 * i);
-        pc |= ((uint32_t)(int)c & 0xFFu) << (8 * i);
-    }
+    uint32_t pa, pb, pc;
+    limbs3x4(v, inv, pa, pb, pc);
     *(uint32_t *)(q.A + 4 * g) = pa;
     *(uint32_t *)(q.B + 4 * g) = pb;
     *(uint32_t *)(q.C + 4 * g) = pc;
@@ -182,18 +199,8 @@ __device__ __forceinline__ void xq_group4_put(const float *v, bool act, int g, X
     const float s16 = bfly_sum<4>(s4);
     if (!act) return;
     const float inv = am > 0.0f ? 127.0f / am : 0.0f;
-    uint32_t pa = 0, pb = 0, pc = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float y = v[i] * inv;
-        const float a = rintf(y);
-        const float r1 = (y - a) * 254.0f;
-        const float b = rintf(r1);
-        const float c = fminf(fmaxf(rintf((r1 - b) * 254.0f), -127.0f), 127.0f);
-        pa |= ((uint32_t)(int)a & 0xFFu) << (8 * i);
-        pb |= ((uint32_t)(int)b & 0xFFu) << (8 * i);
-        pc |= ((uint32_t)(int)c & 0xFFu) << (8 * i);
-    }
+    uint32_t pa, pb, pc;
+    limbs3x4(v, inv, pa, pb, pc);
     const int N4 = N / 4, o = e0 / 4 + g;
     *(uint32_t *)(q.A + 4 * g) = pa;
     *(uint32_t *)(q.B + 4 * g) = pb;
