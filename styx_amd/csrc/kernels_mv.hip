@@ -140,10 +140,28 @@ template <int UPL> constexpr int dense_nr() { return UPL <= 2 ? 2 : 1; }
 // GC: the lane-group width when it is 64 (a whole wave per row: q/k/v,
 // o-proj and LM head of the configs), known at compile time so that the
 // walk's lane map and row sums fold; 0: a.G.
-template <int T, int UPL, int GC>
+// STAGE (q8_0 rows of 64-lane groups whose limb buffer is one xq_at block
+// of a multiple of 128 values): every wave reads the whole limb vector, so
+// the workgroup loads it once, 2 UPL 16-byte pieces per thread issued before
+// the weights, and the waves read it from LDS -- a quarter of the limb
+// traffic through the CU's memory pipeline.  Taken for workgroups of many
+// rows (the launcher's choice).
+template <int T, int UPL, int GC, bool STAGE>
 __global__ void __launch_bounds__(WG) k_mv_dense(DenseK a)
 {
     const int r_begin = blockIdx.x * a.rpw, r_end = min(a.total, r_begin + a.rpw);
+    constexpr int XC = STAGE ? 2 * UPL : 1;
+    extern __shared__ __align__(16) uint8_t s_xq[];
+    const int ncols = a.nb * blk_elems(T);
+    const int nxc = STAGE ? (int)(xq_bytes(ncols) / 16) : 0;
+    styx_u4 xc[XC];
+    if constexpr (STAGE) {
+        // unconditional loads (a piece past the end reads the last one), so
+        // that the wait for them leaves the weights issued after in flight
+        const styx_u4 STYX_GLOBAL *src = (const styx_u4 STYX_GLOBAL *)a.xq.A;
+#pragma unroll
+        for (int j = 0; j < XC; j++) xc[j] = src[min((int)threadIdx.x + WG * j, nxc - 1)];
+    }
     unsigned long long best = 0;  // argmax_key of the best row this lane emitted
     // the segments are walked as one stack of rows, so that a workgroup's
     // rows that span two segments stream in one pass
@@ -155,7 +173,15 @@ __global__ void __launch_bounds__(WG) k_mv_dense(DenseK a)
     // the RMSNorm scale is summed while the first weights are in flight
     float scale = 1.0f;
     auto xload = [&](UX<T> (&x)[UPL], const LaneU<UPL> &lu) {
-        XFrom<T, UPL>{a.xq}(x, lu);
+        if constexpr (STAGE) {
+#pragma unroll
+            for (int j = 0; j < XC; j++)
+                if ((int)threadIdx.x + WG * j < nxc) ((styx_u4 *)s_xq)[threadIdx.x + WG * j] = xc[j];
+            __syncthreads();
+            XFrom<T, UPL>{xq_at(s_xq, ncols)}(x, lu);
+        } else {
+            XFrom<T, UPL>{a.xq}(x, lu);
+        }
         if (a.ns.ss) {
             float t = 0.0f;
             for (int i = threadIdx.x & 63; i < a.ns.n_ss; i += 64) t += a.ns.ss[i];
@@ -239,19 +265,31 @@ hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, 
     a.amax = amax;
     a.rpw = rows_per_wg(a.total, g.G, 1024);
     const dim3 grid((a.total + a.rpw - 1) / a.rpw);
+    // the limb buffer as one xq_at block, staged in LDS by q8_0 64-lane walks
+    // of one unit per lane and many rows per workgroup (the LM head of
+    // 60.4 -> 58.0 us).  With a few rows the barrier costs more
+    // than the repeated reads, which hit the CU's cache (o-proj 4.3 -> 4.5
+    // us staged); with two units per lane the staging registers cost
+    // occupancy (the LM head of configs[3]: 108 -> 113 us staged)
+    const Xq xc = xq_at(xq.A, ncols);
+    const bool stage = g.UPL == 1 && a.rpw >= 32 && ncols % 128 == 0 && ((uintptr_t)xq.A & 15) == 0 && xq.B == xc.B &&
+                       xq.C == xc.C && xq.sx == xc.sx && xq.s16 == xc.s16;
+    const size_t lds_xq = stage ? xq_bytes(ncols) : 0;
     switch (t) {
     case T_Q8_0: upl_dispatch<T_Q8_0>(g.UPL, [&](auto u) {
-        if (g.G == 64) hipLaunchKernelGGL((k_mv_dense<T_Q8_0, decltype(u)::value, 64>), grid, dim3(WG), 0, st, a);
-        else hipLaunchKernelGGL((k_mv_dense<T_Q8_0, decltype(u)::value, 0>), grid, dim3(WG), 0, st, a); }); break;
+        constexpr int U = decltype(u)::value;
+        if (g.G == 64 && stage) hipLaunchKernelGGL((k_mv_dense<T_Q8_0, U, 64, true>), grid, dim3(WG), lds_xq, st, a);
+        else if (g.G == 64) hipLaunchKernelGGL((k_mv_dense<T_Q8_0, U, 64, false>), grid, dim3(WG), 0, st, a);
+        else hipLaunchKernelGGL((k_mv_dense<T_Q8_0, U, 0, false>), grid, dim3(WG), 0, st, a); }); break;
     case T_Q4_K: upl_dispatch<T_Q4_K>(g.UPL, [&](auto u) {
-        if (g.G == 64) hipLaunchKernelGGL((k_mv_dense<T_Q4_K, decltype(u)::value, 64>), grid, dim3(WG), 0, st, a);
-        else hipLaunchKernelGGL((k_mv_dense<T_Q4_K, decltype(u)::value, 0>), grid, dim3(WG), 0, st, a); }); break;
+        if (g.G == 64) hipLaunchKernelGGL((k_mv_dense<T_Q4_K, decltype(u)::value, 64, false>), grid, dim3(WG), 0, st, a);
+        else hipLaunchKernelGGL((k_mv_dense<T_Q4_K, decltype(u)::value, 0, false>), grid, dim3(WG), 0, st, a); }); break;
     case T_Q5_K: upl_dispatch<T_Q5_K>(g.UPL, [&](auto u) {
-        if (g.G == 64) hipLaunchKernelGGL((k_mv_dense<T_Q5_K, decltype(u)::value, 64>), grid, dim3(WG), 0, st, a);
-        else hipLaunchKernelGGL((k_mv_dense<T_Q5_K, decltype(u)::value, 0>), grid, dim3(WG), 0, st, a); }); break;
+        if (g.G == 64) hipLaunchKernelGGL((k_mv_dense<T_Q5_K, decltype(u)::value, 64, false>), grid, dim3(WG), 0, st, a);
+        else hipLaunchKernelGGL((k_mv_dense<T_Q5_K, decltype(u)::value, 0, false>), grid, dim3(WG), 0, st, a); }); break;
     case T_Q6_K: upl_dispatch<T_Q6_K>(g.UPL, [&](auto u) {
-        if (g.G == 64) hipLaunchKernelGGL((k_mv_dense<T_Q6_K, decltype(u)::value, 64>), grid, dim3(WG), 0, st, a);
-        else hipLaunchKernelGGL((k_mv_dense<T_Q6_K, decltype(u)::value, 0>), grid, dim3(WG), 0, st, a); }); break;
+        if (g.G == 64) hipLaunchKernelGGL((k_mv_dense<T_Q6_K, decltype(u)::value, 64, false>), grid, dim3(WG), 0, st, a);
+        else hipLaunchKernelGGL((k_mv_dense<T_Q6_K, decltype(u)::value, 0, false>), grid, dim3(WG), 0, st, a); }); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
