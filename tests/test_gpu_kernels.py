@@ -90,6 +90,23 @@ def test_matvec_dense(gpu, t, ncols):
     assert np.max(np.abs(got - ref)) < 1e-5 * np.abs(ref).max()
 
 
+def test_matvec_dense_many_rows(gpu):
+    """q8_0 rows of 2048 values, 40,960 of them: every workgroup takes 40
+    rows, the walk that loads the activation limbs into LDS once per
+    workgroup (as the LM head of configs[1] does)."""
+    t, rows, ncols = 8, 40960, 2048
+    b, host = gen_quant(gpu, t, rows * ncols, seed=77)
+    s = split(gpu, t, b, rows, ncols)
+    rng = np.random.default_rng(78)
+    x = rng.standard_normal(ncols).astype(np.float32)
+    xb, yb = gpu.from_numpy(x), gpu.buffer(rows * 4)
+    check(lib().styx_op_matvec(gpu.h, t, s.ptr, rows, ncols, xb.ptr, None, C.c_float(0), yb.ptr, 0))
+    got = yb.download(np.float32)
+    ref = O.matvec_f64(t, host, rows, ncols, x)
+    assert rel_l2(got, ref) < 2e-6
+    assert np.max(np.abs(got - ref)) < 1e-5 * np.abs(ref).max()
+
+
 @pytest.mark.parametrize("t", [8, 14])
 def test_matvec_norm_add(gpu, t):
     rows, ncols, eps = 96, 2048, 1e-6
