@@ -36,6 +36,7 @@ constexpr int MB_GU_ROWS = 4;      // gate/up rows per lane group in flight at o
 constexpr int MB_TRACE = 16;       // trace slots per workgroup
 constexpr int MB_MAX_H = 4096;     // residual width when the next q/k/v is folded in
 constexpr int MB_QJ = 7;           // tagged words per thread and poll round, q/k/v phase
+constexpr int MB_SHJ = 8;          // shared-expert gate inputs per thread loaded before the partials' wait
 
 struct MoeBlockK {
     const float *x;         // residual [H]: read at entry, updated by the reduce
@@ -538,9 +539,14 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         const int e = s_ids[tid];
         lg_pick = (e >= 0 && e < a.E) ? s_lg[e] : -INFINITY;
     }
-    float shd = 0.0f;
-    if (shexp)
-        for (int i = tid; i < a.H; i += WG) shd += gld(a.sh_ginp + i) * xs[i];
+    // the shared expert's gate input (columns tid + 256 j): loaded here,
+    // reduced after the partials' wait, so that its memory round trip runs
+    // during that wait instead of before it
+    float shg[MB_SHJ];
+    if (shexp) {
+#pragma unroll
+        for (int j = 0; j < MB_SHJ; j++) shg[j] = gld(a.sh_ginp + min(tid + WG * j, a.H - 1));
+    }
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
@@ -562,11 +568,7 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
         s_w[tid] = wt;
         if (a.wts_out && w == 0) gst(a.wts_out + tid, wt);
     }
-    if (shexp) {
-        const float d = block_sum<WG>(shd, red) * xscale;  // xs is x (.) w unscaled
-        if (tid == 0) s_sg = 1.0f / (1.0f + expf(-d));
-    }
-    __syncthreads();  // also: gus is reused for the partials
+    __syncthreads();  // gus is reused for the partials
     float *pl = gus;  // [nslots][MB_RR]
     if (!tpoll<MAX_TOPK + 1>(a.nslots * MB_RR,
                              [&](int i) -> const uint64_t * {
@@ -576,6 +578,16 @@ __global__ void __launch_bounds__(WG, 2) k_moe_block(MoeBlockK args)
                              tag, pl, a))
         return;
     stamp(9);
+    if (shexp) {
+        float shd = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MB_SHJ; j++)
+            if (tid + WG * j < a.H) shd += shg[j] * xs[tid + WG * j];
+        for (int i = tid + WG * MB_SHJ; i < a.H; i += WG) shd += gld(a.sh_ginp + i) * xs[i];
+        const float d = block_sum<WG>(shd, red) * xscale;  // xs is x (.) w unscaled
+        if (tid == 0) s_sg = 1.0f / (1.0f + expf(-d));
+        __syncthreads();  // s_sg; red is read by every wave before it is rewritten below
+    }
     float p[MAX_TOPK];
 #pragma unroll
     for (int s = 0; s < MAX_TOPK; s++) p[s] = (s < a.k && hr) ? pl[s * MB_RR + tid] : 0.0f;
