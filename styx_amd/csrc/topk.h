@@ -115,32 +115,46 @@ __device__ __forceinline__ uint64_t rank_key(float v, int e)
     return ((uint64_t)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
 }
 
-// Maximum of a 64-bit key over the wave, every lane getting it: the
-// butterfly of bfly() on both 32-bit halves, the larger key kept at each
-// step.
 template <int CTRL> __device__ __forceinline__ uint32_t dpp_u(uint32_t v)
 {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
 }
 __device__ __forceinline__ uint64_t join64(uint32_t hi, uint32_t lo) { return ((uint64_t)hi << 32) | lo; }
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
+
+// Maximum of a 32-bit value over the wave, every lane getting it: a
+// butterfly of DPP moves within rows, then lane swaps across rows.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
 {
-    auto mx = [](uint64_t a, uint64_t b) { return a > b ? a : b; };
-    v = mx(v, join64(dpp_u<0xB1>((uint32_t)(v >> 32)), dpp_u<0xB1>((uint32_t)v)));
-    v = mx(v, join64(dpp_u<0x4E>((uint32_t)(v >> 32)), dpp_u<0x4E>((uint32_t)v)));
-    v = mx(v, join64(dpp_u<0x141>((uint32_t)(v >> 32)), dpp_u<0x141>((uint32_t)v)));
-    v = mx(v, join64(dpp_u<0x140>((uint32_t)(v >> 32)), dpp_u<0x140>((uint32_t)v)));
+    v = max(v, dpp_u<0xB1>(v));
+    v = max(v, dpp_u<0x4E>(v));
+    v = max(v, dpp_u<0x141>(v));
+    v = max(v, dpp_u<0x140>(v));
     {
-        const auto h = __builtin_amdgcn_permlane16_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
-        const auto l = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
-        v = mx(join64(h[0], l[0]), join64(h[1], l[1]));
+        const auto s = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        v = max(s[0], s[1]);
     }
     {
-        const auto h = __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
-        const auto l = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
-        v = mx(join64(h[0], l[0]), join64(h[1], l[1]));
+        const auto s = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        v = max(s[0], s[1]);
     }
     return v;
+}
+
+// Maximum of a 64-bit rank key over the wave, every lane getting it: the
+// maximum of the high halves (the logit's order bits), then the low half
+// (the expert) of the one lane holding it -- or, when several lanes hold
+// that high half (equal logits), the maximum of their low halves.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t v)
+{
+    const uint32_t hi = (uint32_t)(v >> 32);
+    const uint32_t mh = wave_max_u32(hi);
+    const uint64_t ball = __ballot(hi == mh);
+    uint32_t ml;
+    if ((ball & (ball - 1)) == 0)
+        ml = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, (int)__builtin_ctzll(ball));
+    else
+        ml = wave_max_u32(hi == mh ? (uint32_t)v : 0u);
+    return join64(mh, ml);
 }
 
 // Stage 1 of the two-stage ranking for one wave: the Q keys of its quarter
@@ -284,7 +298,7 @@ __device__ __forceinline__ void publish_id_row(const Route &r, const int32_t *s_
 // other counts up to 128 rank every key against all.  Above 128 each
 // wave takes a quarter of the experts (at most two keys per lane) and draws
 // its quarter's top min(k, E/4) keys one at a time -- the wave's largest key
-// (wave_max_u64), which its owner then drops -- and, every global top-k key
+// (wave_max_key), which its owner then drops -- and, every global top-k key
 // being in its quarter's top k, the <= 4k candidates are ranked among
 // themselves.  Integer compares only.
 // Fills s_ids[0..k) with the routed experts (route_row gives a slot's other
@@ -339,7 +353,7 @@ __device__ inline const int32_t *rank_ids_lds(const Route &r, int32_t *s_ids, co
         }
         const int kk = min(k, Q);
         for (int it = 0; it < kk; it++) {
-            const uint64_t m = wave_max_u64(k0);
+            const uint64_t m = wave_max_key(k0);
             if (lane == 0) c_key[wave * k + it] = m;
             if (k0 == m) {  // keys are distinct: one lane
                 k0 = k1;
