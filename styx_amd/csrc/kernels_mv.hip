@@ -267,12 +267,15 @@ hipError_t launch_dense(hipStream_t st, int t, int ncols, const DenseSeg *segs, 
     const dim3 grid((a.total + a.rpw - 1) / a.rpw);
     // the limb buffer as one xq_at block, staged in LDS by q8_0 64-lane walks
     // of one unit per lane and many rows per workgroup (the LM head of
-    // 60.4 -> 58.0 us).  With a few rows the barrier costs more
-    // than the repeated reads, which hit the CU's cache (o-proj 4.3 -> 4.5
-    // us staged); with two units per lane the staging registers cost
-    // occupancy (the LM head of configs[3]: 108 -> 113 us staged)
+    // 60.4 -> 58.0 us) and of four units per lane (the 8192
+    // columns of configs[3]'s o-proj: 9.5 -> 8.3 us, its 27 KB of limbs
+    // read by each of eight waves per CU otherwise).  With two units per
+    // lane it measured slower: configs[1]'s o-proj (few rows: the barrier
+    // costs more than the repeated reads, which hit the CU's cache; 4.3 ->
+    // 4.5 us) and configs[3]'s LM head (the staging registers cost
+    // occupancy; 108 -> 113 us)
     const Xq xc = xq_at(xq.A, ncols);
-    const bool stage = g.UPL == 1 && a.rpw >= 32 && ncols % 128 == 0 && ((uintptr_t)xq.A & 15) == 0 && xq.B == xc.B &&
+    const bool stage = ((g.UPL == 1 && a.rpw >= 32) || g.UPL == 4) && ncols % 128 == 0 && ((uintptr_t)xq.A & 15) == 0 && xq.B == xc.B &&
                        xq.C == xc.C && xq.sx == xc.sx && xq.s16 == xc.s16;
     const size_t lds_xq = stage ? xq_bytes(ncols) : 0;
     switch (t) {

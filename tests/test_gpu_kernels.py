@@ -72,7 +72,7 @@ def test_dequant_bit_exact(gpu, t):
 
 
 @pytest.mark.parametrize("t", TYPES)
-@pytest.mark.parametrize("ncols", [512, 768, 2048, 4096])
+@pytest.mark.parametrize("ncols", [512, 768, 2048, 4096, 8192])
 def test_matvec_dense(gpu, t, ncols):
     if ncols % BLOCK[t][0]:
         pytest.skip("not a block multiple")
