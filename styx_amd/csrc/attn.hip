@@ -399,7 +399,6 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     const int pos = *(const __attribute__((address_space(4))) int32_t *)a.pos;
     double2 cs[PPL];
     if constexpr (RR) cs_load<PPL>(cs, a.rope_row, HD);
-    const unsigned long long ticket = attn_ticket(a);  // also drawn by chunks past the context
     const int gqa = a.nh / a.nkv, kv_dim = a.nkv * HD;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nts = AT_WAVES / nhg, hg = wave % nhg, ts = wave / nhg;
@@ -423,7 +422,10 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
     const int32_t pe_min = spec ? a.page_table[pg_min] : 0;
     const int n_t = pos + 1, chunk = attn_chunk(a, n_t);
     const int t0 = c * chunk;
-    if (t0 >= n_t) return;
+    if (t0 >= n_t) {
+        attn_ticket(a);  // every workgroup draws, also a chunk past the context
+        return;
+    }
     const int t1 = min(n_t, t0 + chunk);
 
     extern __shared__ __align__(16) float sm[];
@@ -485,6 +487,10 @@ __global__ void __launch_bounds__(AT_WG) k_attn(AttnArgs a, int nhg, int hpw)
         load_v(row, tb);
     }
     int64_t row_n = row_of(tb + step);  // the next tile's rows, one tile ahead
+    // the ticket (thread 0's atomic) after the q heads and the first tile:
+    // vector loads and atomics are counted in order, so drawn before them
+    // it would make the waits for the q heads wait for its round trip too
+    const unsigned long long ticket = attn_ticket(a);
 
     // q heads (and the new k head) normalised and rotated into this wave's
     // LDS while the first tile's loads are in flight
@@ -758,7 +764,6 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
         // size, the chunk size of every short context
         pe_min = a.page_table[spec ? pg_min : 0];
     }
-    const unsigned long long ticket = attn_ticket(a);  // also drawn by chunks past the context
 
     extern __shared__ __align__(16) float sm[];
     float *qs = sm;                      // [MH][MHD] normalised, rotated q (zero rows past gqa)
@@ -796,7 +801,10 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
 
     const int n_t = pos + 1, chunk = attn_chunk(a, n_t);
     const int t0 = c * chunk;
-    if (t0 >= n_t) return;
+    if (t0 >= n_t) {
+        attn_ticket(a);  // every workgroup draws, also a chunk past the context
+        return;
+    }
     __syncthreads();  // s_pt
     const int t1 = min(n_t, t0 + chunk);
     const bool owns_pos = t1 == n_t;
@@ -858,6 +866,8 @@ __global__ void __launch_bounds__(AT_WG) k_attn_mfma(AttnArgs a)
         load_v(row, tb);
     }
     int64_t row_n = row_of(tb + step);
+    // the ticket after the q heads and the first tile (as in k_attn)
+    const unsigned long long ticket = attn_ticket(a);
 
     // the q heads and, in the chunk holding pos, the new k/v head,
     // normalised and rotated into LDS while the first tile is in flight
