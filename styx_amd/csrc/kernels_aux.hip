@@ -94,9 +94,12 @@ __global__ void __launch_bounds__(256) k_embed(int t, const uint8_t *w, int64_t 
 {
     extern __shared__ __align__(16) float xs[];  // [ncols]
     __shared__ float red[16];
-    if (rope_row) {
+    // the rope row of the position by the last wave, whose threads have no
+    // embedding blocks at the shapes served (nb <= 192): its two dependent
+    // loads then run beside the token's, not before them
+    if (rope_row && threadIdx.x >= blockDim.x - 64) {
         const int64_t p = *pos;
-        for (int i = threadIdx.x; i < half; i += blockDim.x) rope_row[i] = rope[p * half + i];
+        for (int i = threadIdx.x - (blockDim.x - 64); i < half; i += 64) rope_row[i] = rope[p * half + i];
     }
     const int be = blk_elems(t), nb = ncols / be;
     const Mat m = mat_at(w, t, nrows * nb);
