@@ -219,11 +219,12 @@ __global__ void __launch_bounds__(64) k_argmax_word(unsigned long long *amax, ui
                                                     int32_t *pos, int advance, uint32_t *hist)
 {
     if (threadIdx.x != 0) return;
+    // both loads before any store (one memory round trip, not two)
     const uint32_t idx = (uint32_t)*amax;
+    const int32_t p = advance ? *pos + 1 : 0;
     *amax = 0ull;
     *out_tok = idx;
     if (advance) {
-        const int32_t p = *pos + 1;
         *pos = p;
         if (hist) hist[p] = idx;
     }
