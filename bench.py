@@ -11,7 +11,7 @@ in [0, 151936) (seed 0xC0FFEE) is prefilled, W warmup tokens are decoded,
 then exactly K greedy decode steps are timed (one step = one full forward
 pass of one token, device-side argmax, no host round trip per token).
 
---config k runs BASELINE.json configs[k-1] instead (SURVEY numbering):
+--config k runs BASELINE.json configs[k-1] instead (numbered from 1):
   1  one qwen3moe layer, q8_0 experts (H 2048, E 128, k 8, F 768): the
      per-kernel table is the measurement (gate+up, down, reduce)
   2  the default above
@@ -38,7 +38,7 @@ The JSON line carries:
   cpu_block  (configs 1 and 2) one MoE block of layer 0 on the oracle:
              cpu_ref_1t (1 thread) and cpu_ref_mt (16 threads), us per block
              and GB/s of its algorithmic bytes, beside the GPU block
-  baseline_rows  (config 1) each BASELINE.md section 2 row of config 1 --
+  baseline_rows  (config 1) each of the reference's published rows of config 1 --
              the whole MoE block, gate+up+SiLU, down+reduce -- with its
              algorithmic bytes, the measured kernel time, GB/s, fraction of
              8 TB/s and the 70% target time; the fused block reports the
@@ -232,7 +232,7 @@ def cpu_block_baseline(m, seconds: float) -> dict:
 
 
 def baseline_rows(table: dict) -> dict:
-    """BASELINE.md section 2's config-1 rows: the kernel time measured here
+    """The reference's published config-1 rows: the kernel time measured here
     beside the algorithmic bytes, the fraction of 8 TB/s and the 70% target."""
     rows = {}
 
@@ -576,7 +576,7 @@ def measure(m, args, prompt):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--config", type=int, default=2, help="SURVEY config number, 1-5 (default 2)")
+    ap.add_argument("--config", type=int, default=2, help="config number k, 1-5: BASELINE.json configs[k-1] (default 2)")
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--timing-steps", type=int, default=16,
@@ -620,7 +620,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build measures one GPU only (the MoE decode path is "
-              "single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "single-GPU; its sharding across GPUs is a design, not built here)", file=sys.stderr)
         return 2
 
     from styx_amd import Gpu, MoeModel

@@ -1,5 +1,5 @@
 """The C ABI's three mirrors cannot drift from include/styx_hip.h: the Rust
-binding written out in INTEGRATION.md (the -sys crate a maintainer adds to
+binding written out in the integration guide (the -sys crate a maintainer adds to
 the reference) and the ctypes tables of styx_amd/_lib.py.  For every struct
 the header declares, the field names and order, and the offsets and size of
 the C layout (printed by a gcc build of the header itself), must match the

@@ -462,7 +462,8 @@ def test_cpy_contig_and_strided(gpu):
 
 
 # ------------------------------------------------------------ fused names --
-# The fused kernels registered under SURVEY 8(b)'s names, dispatched through
+# The fused kernels registered under their own names (moe_gate_up_silu_{t},
+# moe_down_reduce_{t}, router_topk, attn_decode_paged), dispatched through
 # styx_batch_dispatch with their push blocks (include/styx_hip.h), checked
 # against the oracle's MoE block and attention.  Quant weights in the split
 # layout (styx_op_to_split), as the fused path reads them.

@@ -1,5 +1,5 @@
 """GPU parity at BASELINE.json's full shapes, against the CPU oracle or the
-all-in-HBM run (SURVEY north star: greedy tokens identical over 256 tokens,
+all-in-HBM run (the parity bar: greedy tokens identical over 256 tokens,
 per-layer hidden states within 1e-4 relative L2, top-k ids bit-exact,
 placement invariance of scripts/verify.sh:57-78).
 

@@ -41,7 +41,7 @@ def test_fixture_shape():
 
 def test_6gib_budget_pins_the_hottest_slabs():
     """config 3: a 6 GiB budget over 3,256,320-byte slabs holds
-    floor(6 GiB / slab) = 1978 slabs (~41 of 128 per layer)."""
+    floor(6 GiB / slab) = 1978 slabs (about 41 of 128 per layer)."""
     remap, n = plan(HIST, 48, 128, SLAB_30B, 6144)
     assert n == (6144 << 20) // SLAB_30B == 1978
     hot = remap != SKIP
